@@ -1,0 +1,65 @@
+// Error text, device queries and the library identity entry points.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+
+#include "abi_util.hpp"
+
+namespace asdsl {
+
+namespace {
+thread_local char g_error[512] = "";
+
+struct DeviceShape {
+    int cus = -1;
+};
+std::mutex g_shape_mu;
+DeviceShape g_shape[64];
+}  // namespace
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, ap);
+    va_end(ap);
+}
+
+void clear_error() { g_error[0] = '\0'; }
+
+int cu_count_current() {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("no usable HIP device: %s", hipGetErrorString(e));
+        return -1;
+    }
+    std::lock_guard<std::mutex> lock(g_shape_mu);
+    if (g_shape[dev].cus < 0) {
+        int cus = 0;
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess || cus <= 0) {
+            set_error("hipDeviceGetAttribute(MultiprocessorCount) failed: %s", hipGetErrorString(e));
+            return -1;
+        }
+        g_shape[dev].cus = cus;
+    }
+    return g_shape[dev].cus;
+}
+
+asdsl_status launch_status(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+        return ASDSL_ERR_HIP;
+    }
+    return ASDSL_OK;
+}
+
+}  // namespace asdsl
+
+extern "C" int asdsl_abi_version(void) { return ASDSL_ABI_VERSION; }
+
+extern "C" const char* asdsl_last_error(void) { return asdsl::g_error; }
+
+extern "C" int asdsl_device_cu_count(void) { return asdsl::cu_count_current(); }

@@ -1,0 +1,114 @@
+/*
+ * asdsl_hip.h — C ABI of the MI355X (gfx950) Q4 GEMV family.
+ *
+ * Every entry point is stream-ordered and asynchronous: pointers are DEVICE
+ * pointers, nothing is allocated, and the call returns as soon as the kernel
+ * is queued on `stream` (0 = the null stream).  Buffers are owned by the
+ * caller, exactly as in the reference kernels, which take caller-owned
+ * host buffers (asdsl/kernels/native/gemv_q4_kernel.h:25-121).
+ *
+ * Byte layouts are the reference's, unchanged:
+ *   preq    20-byte block per (row, 32-group): fp16 scale | fp16 zero | 16 B nibbles
+ *           (asdsl/quantization/repack_q4_32.py:1-7)
+ *   preq2   meta[M][G][4] (fp16 scale, fp16 zero) + quant[ceil(M/4)][G][64]
+ *           4-row bands, slot r%4 at byte 16*(r%4) (asdsl/quantization/repack_preq2.py:1-9)
+ *   Q4_128  66-byte block per (row, 128-group): fp16 scale=amax/7 | 64 B nibbles,
+ *           implicit zero 8 (asdsl/quantization/repack_q4_128.py:1-6)
+ *   nibbles low nibble = even element (asdsl/quantization/core.py:556-563)
+ *
+ * Return value: ASDSL_OK, or an error code; asdsl_last_error() then holds a
+ * message for the calling thread.  Argument errors are detected before any
+ * HIP call, so they are reported even on a machine without a GPU.
+ */
+#ifndef ASDSL_HIP_H
+#define ASDSL_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as hipStream_t (hip/hip_runtime_api.h), so a hipStream_t, or
+ * torch.cuda.current_stream().cuda_stream, is passed unchanged. */
+struct ihipStream_t;
+typedef struct ihipStream_t* asdsl_stream_t;
+
+typedef enum asdsl_status {
+    ASDSL_OK = 0,
+    ASDSL_ERR_INVALID_ARGUMENT = 1, /* reference: std::invalid_argument -> ValueError */
+    ASDSL_ERR_HIP = 2,              /* a HIP runtime call or kernel launch failed */
+    ASDSL_ERR_UNSUPPORTED = 3       /* valid request outside what the kernels handle */
+} asdsl_status;
+
+#define ASDSL_ABI_VERSION 1
+
+/* Library identity and error text. No reference counterpart (pybind11 raises). */
+int asdsl_abi_version(void);
+const char* asdsl_last_error(void);
+
+/* Number of compute units of the current device, or -1 (and an error) when
+ * no HIP device is usable.  Replaces the reference's thread-count probes
+ * get_num_threads/has_openmp (asdsl/kernels/native/gemv_q4_avx2.cpp:1490-1505). */
+int asdsl_device_cu_count(void);
+
+/* ------------------------------------------------------------------ A1 ---
+ * Per-group int8 activation quantizer.
+ * Replaces quantize_activation_avx2
+ *   (asdsl/kernels/native/gemv_q4_preq_restored.cpp:505-549;
+ *    pybind asdsl/kernels/native/gemv_q4_avx2.cpp:1352-1365).
+ * amax=max|x|; amax<1e-9 -> q=0, scale=1; else scale=amax*(1/127),
+ * q=sat8(rne(x*(127/amax))).  x[in_features] -> x_q8[in_features],
+ * x_scales[in_features/group_size].  group_size in {32, 64, 128}. */
+asdsl_status asdsl_quantize_activation(const float* x, int8_t* x_q8, float* x_scales,
+                                       int in_features, int group_size,
+                                       asdsl_stream_t stream);
+
+/* ------------------------------------------------------------------ A3 ---
+ * preq g32 GEMV on 20-byte blocks, activation already quantized.
+ * Replaces gemv_q4_32_preq_avx2 (asdsl/kernels/native/gemv_q4_preq_restored.cpp:551-573).
+ * y[r] = sum_g s*xs*D_g - z*s*xs*X_g (D_g = sum q*xq, X_g = sum xq).  y overwritten. */
+asdsl_status asdsl_gemv_q4_32_preq(const uint8_t* blocks, const int8_t* x_q8,
+                                   const float* x_scales, float* y,
+                                   int out_features, int in_features, int group_size,
+                                   asdsl_stream_t stream);
+
+/* Same, quantizing the fp32 activation inside the call.
+ * Replaces gemv_q4_32_preq_fused_avx2 / _4row_avx2 / _8row_avx2
+ *   (asdsl/kernels/native/gemv_q4_preq_restored.cpp:575-669); the 4/8-row
+ *   unroll of the reference is a CPU scheduling choice with identical math. */
+asdsl_status asdsl_gemv_q4_32_preq_fused(const uint8_t* blocks, const float* x, float* y,
+                                         int out_features, int in_features, int group_size,
+                                         asdsl_stream_t stream);
+
+/* ------------------------------------------------------------------ A5 ---
+ * preq2 GEMV (4-row band quant + sidecar meta), fp32 activation quantized inside.
+ * Replaces gemv_preq2_fused_avx2 (asdsl/kernels/native/gemv_preq2_avx2.cpp:301-319).
+ * group_size 32 is the reference layout.  group_size 128 selects the
+ * asymmetric preq2-g128 layout, which the reference does not have:
+ * meta[M][K/128][4] + quant[ceil(M/4)][K/128][256] (4 rows x 64 B per band),
+ * activation quantized per 128. */
+asdsl_status asdsl_gemv_preq2_fused(const uint8_t* meta, const uint8_t* quant,
+                                    const float* x, float* y,
+                                    int out_features, int in_features, int group_size,
+                                    asdsl_stream_t stream);
+
+/* preq2 GEMV on a pre-quantized activation.
+ * Replaces gemv_preq2_avx2 (asdsl/kernels/native/gemv_preq2_avx2.cpp:321-337).
+ * group_size as for asdsl_gemv_preq2_fused; x_scales has in_features/group_size entries. */
+asdsl_status asdsl_gemv_preq2(const uint8_t* meta, const uint8_t* quant,
+                              const int8_t* x_q8, const float* x_scales, float* y,
+                              int out_features, int in_features, int group_size,
+                              asdsl_stream_t stream);
+
+/* Debug dequantization of a preq2 matrix to fp32 W[M][K]: w = (q - z) * s,
+ * bit-exact with the reference's dequant (experiments/phi4_cpu_run.py:3450-3467). */
+asdsl_status asdsl_dequant_preq2(const uint8_t* meta, const uint8_t* quant, float* w,
+                                 int out_features, int in_features, int group_size,
+                                 asdsl_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASDSL_HIP_H */

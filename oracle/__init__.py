@@ -1,0 +1,149 @@
+"""CPU oracle for the Q4 GEMV hot path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
+may import this package.  It is the parity checker, never the thing measured
+or shipped: the product path (``asdsl`` under ``asdsl-framework_amd/``) never
+imports it and fails loudly when its HIP library is missing.
+
+Two checkers live here:
+
+* ``liboracle.so`` — a scalar C restatement of the reference formulas
+  (``asdsl_oracle.c``), wrapped below with numpy in/out.
+* ``_ref/`` — the reference's own AVX2 kernels compiled unchanged from its
+  sources by ``make -C oracle ref`` (only where the reference tree is mounted;
+  the built modules travel with the repository).  :func:`load_reference`
+  imports them as the pybind11 modules the reference exposes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import importlib.machinery
+import importlib.util
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "lib" / "liboracle.so"
+REF_DIR = ORACLE_DIR / "_ref"
+REFERENCE_TREE = Path("/root/reference")
+
+_lib = None
+_c_f32p = ctypes.POINTER(ctypes.c_float)
+_c_i8p = ctypes.POINTER(ctypes.c_int8)
+_c_u8p = ctypes.POINTER(ctypes.c_uint8)
+
+
+def build(with_reference: bool | None = None) -> None:
+    """Compile liboracle.so and, when the reference tree is present, oracle/_ref."""
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+    if with_reference is None:
+        with_reference = REFERENCE_TREE.is_dir()
+    if with_reference:
+        subprocess.run(["make", "-s", "-C", str(ORACLE_DIR), "ref"], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build(with_reference=False)
+        _lib = ctypes.CDLL(str(LIB_PATH))
+    return _lib
+
+
+def _p(a: np.ndarray, ctype):
+    return a.ctypes.data_as(ctype)
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint8).reshape(-1)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i8(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int8).reshape(-1)
+
+
+# --------------------------------------------------------------- restatement
+def quantize_activation(x, group_size: int = 32) -> tuple[np.ndarray, np.ndarray]:
+    x = _f32(x).reshape(-1)
+    K = x.shape[0]
+    xq = np.empty(K, np.int8)
+    xs = np.empty(K // group_size, np.float32)
+    lib().oracle_quantize_activation(_p(x, _c_f32p), _p(xq, _c_i8p), _p(xs, _c_f32p), K, group_size)
+    return xq, xs
+
+
+def gemv_preq(blocks, x_q8, x_scales, M: int, K: int) -> np.ndarray:
+    blocks, xq, xs = _u8(blocks), _i8(x_q8), _f32(x_scales)
+    y = np.empty(M, np.float32)
+    lib().oracle_gemv_preq(_p(blocks, _c_u8p), _p(xq, _c_i8p), _p(xs, _c_f32p), _p(y, _c_f32p), M, K)
+    return y
+
+
+def gemv_preq_fused(blocks, x, M: int, K: int) -> np.ndarray:
+    xq, xs = quantize_activation(x, 32)
+    return gemv_preq(blocks, xq, xs, M, K)
+
+
+def gemv_preq2(meta, quant, x_q8, x_scales, M: int, K: int, group_size: int = 32) -> np.ndarray:
+    meta, quant, xq, xs = _u8(meta), _u8(quant), _i8(x_q8), _f32(x_scales)
+    y = np.empty(M, np.float32)
+    lib().oracle_gemv_preq2(_p(meta, _c_u8p), _p(quant, _c_u8p), _p(xq, _c_i8p), _p(xs, _c_f32p),
+                            _p(y, _c_f32p), M, K, group_size)
+    return y
+
+
+def gemv_preq2_fused(meta, quant, x, M: int, K: int, group_size: int = 32) -> np.ndarray:
+    xq, xs = quantize_activation(x, group_size)
+    return gemv_preq2(meta, quant, xq, xs, M, K, group_size)
+
+
+def dequant_preq2(meta, quant, M: int, K: int, group_size: int = 32) -> np.ndarray:
+    meta, quant = _u8(meta), _u8(quant)
+    w = np.empty((M, K), np.float32)
+    lib().oracle_dequant_preq2(_p(meta, _c_u8p), _p(quant, _c_u8p), _p(w, _c_f32p), M, K, group_size)
+    return w
+
+
+def dequant_preq(blocks, M: int, K: int) -> np.ndarray:
+    blocks = _u8(blocks)
+    w = np.empty((M, K), np.float32)
+    lib().oracle_dequant_preq(_p(blocks, _c_u8p), _p(w, _c_f32p), M, K)
+    return w
+
+
+def half_to_float(bits: int) -> float:
+    f = lib().oracle_half_to_float
+    f.restype = ctypes.c_float
+    f.argtypes = [ctypes.c_uint16]
+    return float(f(bits))
+
+
+# ------------------------------------------------------ compiled reference
+_ref_modules: dict[str, object] = {}
+
+
+def reference_available(name: str = "_native_gemv") -> bool:
+    return (REF_DIR / f"{name}.so").exists()
+
+
+def load_reference(name: str = "_native_gemv"):
+    """Import one of the reference's pybind11 modules built under oracle/_ref."""
+    if name in _ref_modules:
+        return _ref_modules[name]
+    path = REF_DIR / f"{name}.so"
+    if not path.exists():
+        raise FileNotFoundError(f"{path} not built (make -C oracle ref needs the reference tree)")
+    loader = importlib.machinery.ExtensionFileLoader(name, str(path))
+    spec = importlib.util.spec_from_file_location(name, str(path), loader=loader)
+    mod = importlib.util.module_from_spec(spec)
+    loader.exec_module(mod)
+    _ref_modules[name] = mod
+    return mod

@@ -1,0 +1,88 @@
+"""The C-ABI library: loads, exports every declared entry point, and rejects
+bad arguments before touching HIP (so these run without a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from conftest import REPO
+
+HEADER = REPO / "include" / "asdsl_hip.h"
+
+
+def declared_entry_points() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(asdsl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_entry_points()
+    assert "asdsl_gemv_preq2_fused" in names and len(names) >= 8
+
+
+def test_library_exports_every_declared_symbol():
+    from asdsl import _hip
+
+    missing = [n for n in declared_entry_points() if not _hip.exported(n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert _hip.LIB.asdsl_abi_version() == 1
+
+
+def test_python_signatures_cover_header():
+    from asdsl import _hip
+
+    assert set(declared_entry_points()) <= set(_hip.SIGNATURES)
+
+
+def test_invalid_arguments_rejected_without_gpu():
+    from asdsl import _hip
+
+    lib = _hip.LIB
+    one = ctypes.c_void_p(16)
+    # null pointers
+    assert lib.asdsl_gemv_preq2_fused(None, None, None, None, 4, 64, 32, None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+    assert "null" in _hip.last_error()
+    # group size / divisibility / size limits, as the reference checks
+    assert lib.asdsl_gemv_preq2_fused(one, one, one, one, 4, 64, 64, None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+    assert "group_size" in _hip.last_error()
+    assert lib.asdsl_gemv_preq2_fused(one, one, one, one, 4, 48, 32, None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+    assert lib.asdsl_gemv_preq2_fused(one, one, one, one, 4, 32 * 641, 32, None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+    assert "exceeds" in _hip.last_error()
+    assert lib.asdsl_gemv_q4_32_preq_fused(one, one, one, 0, 64, 32, None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+    assert lib.asdsl_quantize_activation(one, one, one, 100, 32, None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+
+
+def test_python_wrapper_validates_sizes():
+    from asdsl.kernels import _native_gemv as ng
+
+    with pytest.raises(ValueError, match="meta"):
+        ng.gemv_preq2_fused_avx2(np.zeros(10, np.uint8), np.zeros(1 << 12, np.uint8),
+                                 np.zeros(64, np.float32), np.zeros(4, np.float32), 4, 64, 32)
+    with pytest.raises(ValueError, match="group_size"):
+        ng.gemv_q4_32_preq_fused_avx2(np.zeros(1 << 12, np.uint8), np.zeros(64, np.float32),
+                                      np.zeros(4, np.float32), 4, 64, 16)
+    with pytest.raises(ValueError, match="y"):
+        ng.gemv_preq2_fused_avx2(np.zeros(32, np.uint8), np.zeros(1 << 12, np.uint8),
+                                 np.zeros(64, np.float32), np.zeros(3, np.float32), 4, 64, 32)
+
+
+def test_no_cpu_fallback():
+    """Valid arguments on a machine without a GPU must fail loudly, not compute."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from asdsl import _hip
+
+    one = ctypes.c_void_p(16)
+    assert _hip.LIB.asdsl_gemv_preq2_fused(one, one, one, one, 4, 64, 32, None) == _hip.ASDSL_ERR_HIP
+    from asdsl.kernels import _native_gemv as ng
+
+    with pytest.raises(RuntimeError):
+        ng.gemv_preq2_fused_avx2(np.zeros(32, np.uint8), np.zeros(128, np.uint8),
+                                 np.zeros(64, np.float32), np.zeros(4, np.float32), 4, 64, 32)

@@ -1,0 +1,167 @@
+"""HIP parity for the preq / preq2 family (gs=32 and the g128 extension).
+
+Bars (written here as in the task statement): activation quantization and
+dequantized weights bit-exact; GEMV outputs within 1e-4 relative L2 of the
+oracle (itself pinned to the reference's compiled kernels).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from asdsl.quantization import synthetic as syn
+from asdsl.quantization.repack import repack_preq_blocks_to_preq2
+from conftest import GOLDEN, rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+SHAPES = [(1, 32), (3, 64), (4, 256), (70, 512), (129, 3072), (66, 8192), (257, 5120), (8, 20480)]
+
+
+def _dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def test_golden_fixtures(gpu):
+    from asdsl.kernels import _native_gemv as ng
+
+    d = np.load(GOLDEN / "gemv_q4_reference.npz")
+    for gs in (32, 128):
+        x = d[f"qa{gs}_x"]
+        xq = np.zeros(x.size, np.int8)
+        xs = np.zeros(x.size // gs, np.float32)
+        ng.quantize_activation_avx2(x, xq, xs, x.size, gs)
+        assert np.array_equal(xq, d[f"qa{gs}_xq"])
+        assert np.array_equal(xs.view(np.uint32), d[f"qa{gs}_xs"].view(np.uint32))
+    M, K = map(int, d["preq_shape"])
+    y = np.zeros(M, np.float32)
+    ng.gemv_q4_32_preq_fused_avx2(d["preq_blocks"], d["preq_x"], y, M, K, 32)
+    assert rel_l2(y, d["preq_y_fused"]) < TOL
+    y2 = np.zeros(M, np.float32)
+    ng.gemv_preq2_fused_avx2(d["preq2_meta"], d["preq2_quant"], d["preq_x"], y2, M, K, 32)
+    assert rel_l2(y2, d["preq2_y"]) < TOL
+
+
+@pytest.mark.parametrize("gs", [32, 128])
+def test_quantize_activation_bitexact(gpu, gs):
+    from asdsl.kernels import _native_gemv as ng
+
+    rng = np.random.default_rng(3)
+    K = 8192
+    x = (rng.standard_normal(K) * 10.0 ** rng.uniform(-5, 5, K // gs).repeat(gs)).astype(np.float32)
+    x[:gs] = 0.0
+    xq = np.zeros(K, np.int8)
+    xs = np.zeros(K // gs, np.float32)
+    ng.quantize_activation_avx2(x, xq, xs, K, gs)
+    oq, os_ = oracle.quantize_activation(x, gs)
+    assert np.array_equal(xq, oq)
+    assert np.array_equal(xs.view(np.uint32), os_.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K", SHAPES)
+def test_preq_fused_vs_oracle(gpu, M, K):
+    from asdsl.kernels import _native_gemv as ng
+
+    blocks = syn.preq_blocks(syn.gaussian_weights(M, K, M + K))
+    x = syn.activation(K, K)
+    y = np.full(M, np.nan, np.float32)
+    ng.gemv_q4_32_preq_fused_avx2(blocks, x, y, M, K, 32)
+    assert rel_l2(y, oracle.gemv_preq_fused(blocks, x, M, K)) < TOL
+
+
+@pytest.mark.parametrize("M,K", [(70, 512), (129, 3072)])
+def test_preq_preq8_vs_oracle(gpu, M, K):
+    from asdsl.kernels import _native_gemv as ng
+
+    blocks = syn.preq_blocks(syn.gaussian_weights(M, K, 5))
+    xq, xs = oracle.quantize_activation(syn.activation(K, 6), 32)
+    y = np.full(M, np.nan, np.float32)
+    ng.gemv_q4_32_preq_avx2(blocks, xq, xs, y, M, K, 32)
+    assert rel_l2(y, oracle.gemv_preq(blocks, xq, xs, M, K)) < TOL
+
+
+@pytest.mark.parametrize("gs", [32, 128])
+@pytest.mark.parametrize("M,K", SHAPES)
+def test_preq2_fused_vs_oracle(gpu, gs, M, K):
+    if K % gs:
+        pytest.skip("K not a multiple of the group size")
+    from asdsl.kernels import _native_gemv as ng
+
+    meta, quant = syn.preq2(syn.gaussian_weights(M, K, M * 7 + K), gs)
+    x = syn.activation(K, K + 1)
+    y = np.full(M, np.nan, np.float32)
+    ng.gemv_preq2_fused_avx2(meta, quant, x, y, M, K, gs)
+    assert rel_l2(y, oracle.gemv_preq2_fused(meta, quant, x, M, K, gs)) < TOL
+
+
+@pytest.mark.parametrize("gs", [32, 128])
+def test_preq2_preq8_and_dequant_bitexact(gpu, gs):
+    from asdsl.kernels import _native_gemv as ng
+
+    M, K = 70, 1024
+    meta, quant = syn.preq2(syn.gaussian_weights(M, K, 77), gs)
+    xq, xs = oracle.quantize_activation(syn.activation(K, 78), gs)
+    y = np.full(M, np.nan, np.float32)
+    ng.gemv_preq2_avx2(meta, quant, xq, xs, y, M, K, gs)
+    assert rel_l2(y, oracle.gemv_preq2(meta, quant, xq, xs, M, K, gs)) < TOL
+    w = ng.dequant_preq2(meta, quant, M, K, gs)
+    assert np.array_equal(w.view(np.uint32), oracle.dequant_preq2(meta, quant, M, K, gs).view(np.uint32))
+
+
+def test_preq2_matches_preq_reference_shapes(gpu):
+    """The reference's own invariant (benchmarks/test_preq2_correctness.py:25-37):
+    preq2 == preq at 512x3072, 3072x8192, 16384x3072."""
+    from asdsl.kernels import _native_gemv as ng
+
+    for rows, cols in [(512, 3072), (3072, 8192), (16384, 3072)]:
+        blocks = syn.preq_blocks(syn.gaussian_weights(rows, cols, 42))
+        x = syn.activation(cols, 43)
+        meta, quant = repack_preq_blocks_to_preq2(blocks, rows, cols, 32)
+        y1 = np.zeros(rows, np.float32)
+        y2 = np.zeros(rows, np.float32)
+        ng.gemv_q4_32_preq_fused_avx2(blocks, x, y1, rows, cols, 32)
+        ng.gemv_preq2_fused_avx2(meta, quant, x, y2, rows, cols, 32)
+        np.testing.assert_allclose(y2, y1, rtol=1e-4, atol=1e-3)
+        assert rel_l2(y2, oracle.gemv_preq2_fused(meta, quant, x, rows, cols, 32)) < TOL
+
+
+def test_device_tensors_zero_copy_and_deterministic(gpu):
+    import torch
+    from asdsl.kernels import _native_gemv as ng
+
+    M, K = 16384, 3072
+    meta, quant = syn.preq2(syn.gaussian_weights(M, K, 42), 32)
+    x = syn.activation(K, 43)
+    dm, dq, dx = _dev(meta), _dev(quant), _dev(x)
+    y1 = torch.empty(M, dtype=torch.float32, device="cuda")
+    y2 = torch.empty(M, dtype=torch.float32, device="cuda")
+    ng.gemv_preq2_fused_avx2(dm, dq, dx, y1, M, K, 32)
+    ng.gemv_preq2_fused_avx2(dm, dq, dx, y2, M, K, 32)
+    torch.cuda.synchronize()
+    a, b = y1.cpu().numpy(), y2.cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), "repeat runs must be bitwise identical"
+    assert rel_l2(a, oracle.gemv_preq2_fused(meta, quant, x, M, K, 32)) < TOL
+
+
+def test_lm_head_preq2_g128_full_size(gpu):
+    """Config 2 shape 200064x3072 preq2-g128, quantized on the device by the
+    torch mirror of the reference quantizer, checked against the oracle."""
+    import torch
+    from asdsl.kernels import _native_gemv as ng
+
+    M, K = 200064, 3072
+    g = torch.Generator(device="cuda").manual_seed(42)
+    w = torch.randn((M, K), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    meta, quant = syn.preq2_from_weights_torch(w, 128)
+    del w
+    x = syn.activation(K, 43)
+    y = torch.empty(M, dtype=torch.float32, device="cuda")
+    ng.gemv_preq2_fused_avx2(meta, quant, _dev(x), y, M, K, 128)
+    torch.cuda.synchronize()
+    want = oracle.gemv_preq2_fused(meta.cpu().numpy(), quant.cpu().numpy(), x, M, K, 128)
+    assert rel_l2(y.cpu().numpy(), want) < TOL
