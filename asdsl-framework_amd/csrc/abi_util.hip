@@ -1,6 +1,7 @@
 // Error text, device queries and the library identity entry points.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <mutex>
 
@@ -45,6 +46,13 @@ int cu_count_current() {
         g_shape[dev].cus = cus;
     }
     return g_shape[dev].cus;
+}
+
+int env_knob(const char* name) {
+    const char* v = getenv(name);
+    if (!v || !*v) return 0;
+    const int n = atoi(v);
+    return n > 0 ? n : 0;
 }
 
 asdsl_status launch_status(const char* what) {

@@ -19,10 +19,18 @@ asdsl_status launch_status(const char* what);
 
 inline hipStream_t as_hip(asdsl_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Integer tuning knob from the environment, read once (0 = unset).  Knobs
+// only change launch shapes (and with them the fp32 summation order), never
+// the formula: ASDSL_HIP_WG_PER_CU caps workgroups per compute unit,
+// ASDSL_HIP_KSPLIT forces the K split of the preq2 kernels.
+int env_knob(const char* name);
+
 // Workgroups for a streaming kernel: enough tiles for every wave, capped at
 // `per_cu` workgroups per compute unit (waves then loop over tiles).
 inline int stream_grid(long long tiles, int waves_per_wg, int per_cu, int cus) {
     long long wgs = (tiles + waves_per_wg - 1) / waves_per_wg;
+    static const int knob = env_knob("ASDSL_HIP_WG_PER_CU");
+    if (knob > 0) per_cu = knob;
     const long long cap = static_cast<long long>(per_cu) * (cus > 0 ? cus : 256);
     if (wgs > cap) wgs = cap;
     if (wgs < 1) wgs = 1;

@@ -50,10 +50,70 @@ __device__ __forceinline__ int unit_dot(const uint4 w, const uint32_t* __restric
     return d;
 }
 
-// Same dot with weights centred at 8 ((q-8)*x), used by the symmetric
-// kernels whose reference sums (q-8)*xq directly.  Computed as D - 8*X by the
-// caller instead; kept here only as documentation of the identity.
+// ------------------------------------------------------------ lane exchange
+// DPP controls (GCN/CDNA encoding): quad permutes, and row (16-lane) mirrors
+// and rotations.
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+// ds_swizzle bit mode: and_mask 0x1F, xor_mask 0x10 -> lane ^ 16 within 32.
+constexpr int kSwizzleXor16 = 0x401F;
 
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ float swz_xor16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), kSwizzleXor16));
+}
+
+// max over aligned groups of kLanes consecutive lanes (kLanes in {1,2,4,8,16}),
+// result in every lane of the group.
+template <int kLanes>
+__device__ __forceinline__ float group_max(float v) {
+    if (kLanes >= 2) v = fmaxf(v, dpp<kDppQuadXor1>(v));
+    if (kLanes >= 4) v = fmaxf(v, dpp<kDppQuadXor2>(v));
+    if (kLanes >= 8) v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+    if (kLanes >= 16) v = fmaxf(v, dpp<kDppRowMirror>(v));
+    return v;
+}
+
+template <int kLanes, typename T>
+__device__ __forceinline__ T group_sum(T v) {
+    if (kLanes >= 2) v += dpp<kDppQuadXor1>(v);
+    if (kLanes >= 4) v += dpp<kDppQuadXor2>(v);
+    if (kLanes >= 8) v += dpp<kDppRowHalfMirror>(v);
+    if (kLanes >= 16) v += dpp<kDppRowMirror>(v);
+    return v;
+}
+
+// Sum over all lanes that agree with this lane in the two "slot" bits
+// [SB, SB+2) of the lane index; every lane gets the sum for its slot.
+template <int SB>
+__device__ __forceinline__ float slot_sum(float v) {
+    static_assert(SB == 0 || SB == 2, "slot bits at 0 or 2");
+    if (SB == 0) {               // reduce lane bits 2,3 (in-row), 4, 5
+        v += dpp<kDppRowRor4>(v);
+        v += dpp<kDppRowRor8>(v);
+    } else {                     // reduce lane bits 0,1 (quad), 4, 5
+        v += dpp<kDppQuadXor1>(v);
+        v += dpp<kDppQuadXor2>(v);
+    }
+    v += swz_xor16(v);
+    v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+// ------------------------------------------------------------ int8 helpers
 // Round-to-nearest-even float -> int, saturated to int8 (cvtps_epi32 +
 // packs_epi32 + packs_epi16 in the reference: both packs saturate).
 __device__ __forceinline__ int sat_rne_i8(float v) {
@@ -73,57 +133,41 @@ __device__ __forceinline__ int sum4_i8(uint32_t v) {
     return __builtin_amdgcn_sdot4(static_cast<int>(v), 0x01010101, 0, false);
 }
 
-template <int kLanes>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int m = 1; m < kLanes; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-    return v;
+// ------------------------------------------------------------ activation
+// LDS image of the int8 activation: split-order int8 (K/4 dwords), per-group
+// scale (K/GS floats), per-unit (float)sum(xq)*scale (K/32 floats).
+struct XImage {
+    uint32_t* xq;
+    float* scale;
+    float* usum;
+};
+
+__device__ __forceinline__ XImage x_image(uint32_t* lds, int K, int gs) {
+    XImage im;
+    im.xq = lds;
+    im.scale = reinterpret_cast<float*>(lds + (K >> 2));
+    im.usum = im.scale + K / gs;
+    return im;
 }
 
-template <int kLanes>
-__device__ __forceinline__ int group_sum_i(int v) {
-#pragma unroll
-    for (int m = 1; m < kLanes; m <<= 1) v += __shfl_xor(v, m, kWave);
-    return v;
+inline size_t x_image_bytes(int K, int gs) {
+    return static_cast<size_t>(K) + static_cast<size_t>(K / gs) * 4 + static_cast<size_t>(K / 32) * 4;
 }
 
 // Activation quantizer of the reference (quantize_activation_avx2,
 // asdsl/kernels/native/gemv_q4_preq_restored.cpp:505-549) as built with
 // -O3 -ffast-math (setup.py:56-65): the compiler turns amax/127.0f into
 // amax*(1/127.0f); 127.0f/amax stays a true division; cvtps_epi32 rounds
-// half to even.  Each thread owns one 8-element chunk; the GS/8 threads of a
-// group are consecutive lanes of one wave.
-//
-// Writes, for the whole vector:
-//   xq_split[K/4]  int8 in split order (dwords, see file header)
-//   xscale[K/GS]   per-group scale
-//   xsum_sc[K/32]  per-unit (float)sum(xq) * scale
-//   xq_nat         optional natural-order int8 copy (global, may be null)
-//   xscale_out     optional copy of the scales (global, may be null)
+// half to even; packs saturate.  One thread owns one 8-element chunk; the GS/8
+// threads of a group are consecutive, aligned lanes of one wave.
 template <int GS>
-__device__ __forceinline__ void quantize_chunk_q8(const float* __restrict__ x, int chunk, bool active,
-                                                  uint32_t* __restrict__ xq_split,
-                                                  float* __restrict__ xscale,
-                                                  float* __restrict__ xsum_sc,
-                                                  int8_t* __restrict__ xq_nat,
-                                                  float* __restrict__ xscale_out) {
-    static_assert(GS % 32 == 0 || GS == 64, "group size");
+__device__ __forceinline__ void quantize_chunk(const float (&v)[8], int chunk, bool active, XImage im,
+                                               int8_t* __restrict__ xq_nat, float* __restrict__ xscale_out) {
     constexpr int kLanes = GS / 8;
-    float v[8];
-    if (active) {
-        const float4 a = reinterpret_cast<const float4*>(x)[2 * chunk];
-        const float4 b = reinterpret_cast<const float4*>(x)[2 * chunk + 1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    }
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
     const float amax = group_max<kLanes>(m);
-
     int q[8];
     float scale;
     if (amax < 1e-9f) {
@@ -138,45 +182,78 @@ __device__ __forceinline__ void quantize_chunk_q8(const float* __restrict__ x, i
     }
     const uint32_t even = pack4_i8(q[0], q[2], q[4], q[6]);
     const uint32_t odd = pack4_i8(q[1], q[3], q[5], q[7]);
-    // unit (32 elements) sum: 4 consecutive chunks
-    const int usum = group_sum_i<4>(sum4_i8(even) + sum4_i8(odd));
+    const int usum = group_sum<4>(sum4_i8(even) + sum4_i8(odd));  // 4 chunks = 1 unit
     if (active) {
-        xq_split[2 * chunk] = even;
-        xq_split[2 * chunk + 1] = odd;
+        reinterpret_cast<uint2*>(im.xq)[chunk] = make_uint2(even, odd);
         if (xq_nat) {
             reinterpret_cast<uint2*>(xq_nat)[chunk] =
                 make_uint2(pack4_i8(q[0], q[1], q[2], q[3]), pack4_i8(q[4], q[5], q[6], q[7]));
         }
         if ((chunk & (kLanes - 1)) == 0) {
-            xscale[chunk / kLanes] = scale;
+            im.scale[chunk / kLanes] = scale;
             if (xscale_out) xscale_out[chunk / kLanes] = scale;
         }
-        if ((chunk & 3) == 0) xsum_sc[chunk >> 2] = static_cast<float>(usum) * scale;
+        if ((chunk & 3) == 0) im.usum[chunk >> 2] = static_cast<float>(usum) * scale;
     }
 }
 
-// Loads a caller-quantized activation (natural int8 order + per-group scales)
-// into the split-order LDS image.  Same outputs as quantize_chunk_q8.
+// Caller-quantized activation (natural int8 order + per-group scales).
 template <int GS>
-__device__ __forceinline__ void load_chunk_q8(const int8_t* __restrict__ xq, const float* __restrict__ xsc_in,
-                                              int chunk, bool active,
-                                              uint32_t* __restrict__ xq_split,
-                                              float* __restrict__ xscale,
-                                              float* __restrict__ xsum_sc) {
+__device__ __forceinline__ void load_q8_chunk(uint2 n, float scale, int chunk, bool active, XImage im) {
     constexpr int kLanes = GS / 8;
-    uint2 n = make_uint2(0u, 0u);
-    if (active) n = reinterpret_cast<const uint2*>(xq)[chunk];
     // natural bytes b0..b7 -> even (b0,b2,b4,b6), odd (b1,b3,b5,b7)
     const uint32_t even = __builtin_amdgcn_perm(n.y, n.x, 0x06040200u);
     const uint32_t odd = __builtin_amdgcn_perm(n.y, n.x, 0x07050301u);
-    const int usum = group_sum_i<4>(sum4_i8(even) + sum4_i8(odd));
+    const int usum = group_sum<4>(sum4_i8(even) + sum4_i8(odd));
     if (active) {
-        const float scale = xsc_in[chunk / kLanes];
-        xq_split[2 * chunk] = even;
-        xq_split[2 * chunk + 1] = odd;
-        if ((chunk & (kLanes - 1)) == 0) xscale[chunk / kLanes] = scale;
-        if ((chunk & 3) == 0) xsum_sc[chunk >> 2] = static_cast<float>(usum) * scale;
+        reinterpret_cast<uint2*>(im.xq)[chunk] = make_uint2(even, odd);
+        if ((chunk & (kLanes - 1)) == 0) im.scale[chunk / kLanes] = scale;
+        if ((chunk & 3) == 0) im.usum[chunk >> 2] = static_cast<float>(usum) * scale;
     }
 }
+
+// Activation staging in two phases so that its global loads can be issued
+// BEFORE the weight loads: vmcnt retires in order, so a load issued after the
+// weights could only be consumed once every weight load had landed.
+//   ActStage::load()    issues this thread's NCH chunk loads (clamped, in bounds)
+//   ActStage::process() quantizes them into the LDS image (no global loads)
+// One workgroup of NT threads covers K <= 8*NT*NCH; lanes past the end form
+// whole groups of their own and never store.
+template <int GS, int NT, int NCH, bool Q8>
+struct ActStage {
+    float v[Q8 ? 1 : NCH][8];
+    uint2 n[Q8 ? NCH : 1];
+    float s[Q8 ? NCH : 1];
+
+    __device__ __forceinline__ void load(const float* __restrict__ x, const int8_t* __restrict__ xq8,
+                                         const float* __restrict__ xsc, int K) {
+        const int nchunk = K >> 3;
+        const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = min(i * NT + tid, nchunk - 1);
+            if constexpr (Q8) {
+                n[i] = reinterpret_cast<const uint2*>(xq8)[c];
+                s[i] = xsc[c / (GS / 8)];
+            } else {
+                const float4 a = reinterpret_cast<const float4*>(x)[2 * c];
+                const float4 b = reinterpret_cast<const float4*>(x)[2 * c + 1];
+                v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+                v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void process(int K, XImage im) {
+        const int nchunk = K >> 3;
+        const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = i * NT + tid;
+            if constexpr (Q8) load_q8_chunk<GS>(n[i], s[i], c, c < nchunk, im);
+            else quantize_chunk<GS>(v[i], c, c < nchunk, im, nullptr, nullptr);
+        }
+    }
+};
 
 }  // namespace asdsl

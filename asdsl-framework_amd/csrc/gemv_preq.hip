@@ -23,7 +23,7 @@ constexpr int kWavesPerWg = kThreads / kWave;
 
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
-template <int LPR, int UNROLL>
+template <int LPR, int UNROLL, int NCH, bool Q8>
 __global__ __launch_bounds__(kThreads) void preq_gemv_kernel(const uint8_t* __restrict__ blocks,
                                                             const float* __restrict__ x,
                                                             const int8_t* __restrict__ xq8,
@@ -32,9 +32,7 @@ __global__ __launch_bounds__(kThreads) void preq_gemv_kernel(const uint8_t* __re
     extern __shared__ __align__(16) uint32_t lds[];
     constexpr int RPW = kWave / LPR;  // rows per wave step
     const int G = K >> 5;
-    uint32_t* s_xq = lds;
-    float* s_xs = reinterpret_cast<float*>(lds + (K >> 2));
-    float* s_xsum = s_xs + G;
+    const XImage im = x_image(lds, K, 32);
 
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int wave = static_cast<int>(threadIdx.x) >> 6;
@@ -47,34 +45,23 @@ __global__ __launch_bounds__(kThreads) void preq_gemv_kernel(const uint8_t* __re
 
     u32x4_a4 h[UNROLL];
     uint32_t t[UNROLL];
+    // Unconditional loads at clamped, in-bounds indices; values of groups
+    // >= G or rows >= M are never used.
     auto load_batch = [&](int tl, int k0) {
-        const int row = tl * RPW + rin;
-        const bool row_ok = row < M;
-        const uint8_t* rb = blocks + static_cast<size_t>(row_ok ? row : 0) * G * 20;
+        const int row = min(tl * RPW + rin, M - 1);
+        const uint8_t* rb = blocks + static_cast<size_t>(row) * G * 20;
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
-            const int g = j + (k0 + u) * LPR;
-            if (row_ok && g < G) {
-                const uint8_t* b = rb + static_cast<size_t>(g) * 20;
-                h[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(b));
-                t[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(b + 16));
-            } else {
-                h[u] = u32x4_a4{0u, 0u, 0u, 0u};
-                t[u] = 0u;
-            }
+            const int g = min(j + (k0 + u) * LPR, G - 1);
+            const uint8_t* b = rb + static_cast<size_t>(g) * 20;
+            h[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(b));
+            t[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(b + 16));
         }
     };
-    if (tile < ntiles) load_batch(tile, 0);
-
-    {
-        const int nchunk = K >> 3;
-        for (int base = 0; base < nchunk; base += kThreads) {
-            const int c = base + static_cast<int>(threadIdx.x);
-            const bool active = c < nchunk;
-            if (xq8 != nullptr) load_chunk_q8<32>(xq8, xsc, c, active, s_xq, s_xs, s_xsum);
-            else quantize_chunk_q8<32>(x, c, active, s_xq, s_xs, s_xsum, nullptr, nullptr);
-        }
-    }
+    ActStage<32, kThreads, NCH, Q8> act;
+    act.load(x, xq8, xsc, K);  // activation loads first: they retire first
+    load_batch(tile, 0);  // unconditional: indices are clamped
+    act.process(K, im);
     __syncthreads();
 
     const int nk = (G + LPR - 1) / LPR;
@@ -87,22 +74,23 @@ __global__ __launch_bounds__(kThreads) void preq_gemv_kernel(const uint8_t* __re
                 const int g = j + (k0 + u) * LPR;
                 if (g < G) {
                     const uint4 nib = make_uint4(h[u].y, h[u].z, h[u].w, t[u]);
-                    const int d = unit_dot(nib, s_xq + g * 8);
+                    const int d = unit_dot(nib, im.xq + g * 8);
                     const float s = half_bits_to_float(h[u].x);
                     const float z = half_bits_to_float(h[u].x >> 16);
-                    acc = fmaf(static_cast<float>(d), s * s_xs[g], acc);
-                    acc = fmaf(-(z * s), s_xsum[g], acc);
+                    acc = fmaf(static_cast<float>(d), s * im.scale[g], acc);
+                    acc = fmaf(-(z * s), im.usum[g], acc);
                 }
             }
         }
-#pragma unroll
-        for (int m = 1; m < LPR; m <<= 1) acc += __shfl_xor(acc, m, kWave);
+        const int next = tile + tile_step;
+        if (next < ntiles) load_batch(next, 0);
+        acc = group_sum<(LPR < 16 ? LPR : 16)>(acc);
+        if (LPR >= 32) acc += swz_xor16(acc);
+        if (LPR >= 64) acc += __shfl_xor(acc, 32, kWave);
         if (j == 0) {
             const int row = tile * RPW + rin;
             if (row < M) y[row] = acc;
         }
-        const int next = tile + tile_step;
-        if (next < ntiles) load_batch(next, 0);
     }
 }
 
@@ -112,8 +100,22 @@ void launch_lpr(const uint8_t* blocks, const float* x, const int8_t* xq8, const 
     constexpr int RPW = kWave / LPR;
     const int ntiles = (M + RPW - 1) / RPW;
     const int grid = stream_grid(ntiles, kWavesPerWg, 4, cus);
-    const size_t lds = static_cast<size_t>(K) + static_cast<size_t>(K / 32) * 8;
-    preq_gemv_kernel<LPR, 4><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
+    const size_t lds = x_image_bytes(K, 32);
+    if (xq8 != nullptr) {
+        if (K <= 8 * kThreads * 2)
+            preq_gemv_kernel<LPR, 4, 2, true><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
+        else if (K <= 8 * kThreads * 4)
+            preq_gemv_kernel<LPR, 4, 4, true><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
+        else
+            preq_gemv_kernel<LPR, 4, 10, true><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
+    } else {
+        if (K <= 8 * kThreads * 2)
+            preq_gemv_kernel<LPR, 4, 2, false><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
+        else if (K <= 8 * kThreads * 4)
+            preq_gemv_kernel<LPR, 4, 4, false><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
+        else
+            preq_gemv_kernel<LPR, 4, 10, false><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
+    }
 }
 
 asdsl_status launch_preq(const uint8_t* blocks, const float* x, const int8_t* xq8, const float* xsc, float* y,

@@ -147,3 +147,102 @@ def load_reference(name: str = "_native_gemv"):
     loader.exec_module(mod)
     _ref_modules[name] = mod
     return mod
+
+
+# ----------------------------------------------------------- more restatements
+def gemv_q4_128(blocks, x_q8, x_scales, M: int, K: int) -> np.ndarray:
+    blocks, xq, xs = _u8(blocks), _i8(x_q8), _f32(x_scales)
+    y = np.empty(M, np.float32)
+    lib().oracle_gemv_q4_128(_p(blocks, _c_u8p), _p(xq, _c_i8p), _p(xs, _c_f32p), _p(y, _c_f32p), M, K)
+    return y
+
+
+def gemm_q4_128(blocks, X, M: int, K: int, B: int) -> np.ndarray:
+    blocks, X = _u8(blocks), _f32(X)
+    Y = np.zeros((B, M), np.float32)
+    lib().oracle_gemm_q4_128(_p(blocks, _c_u8p), _p(X, _c_f32p), _p(Y, _c_f32p), M, K, B)
+    return Y
+
+
+def gemv_q4_q8(w_packed, scales, x, M: int, K: int, group_size: int = 32) -> np.ndarray:
+    w, s, x = _u8(w_packed), _f32(scales), _f32(x).reshape(-1)
+    y = np.empty(M, np.float32)
+    sq = np.empty(K, np.int8)
+    ss = np.empty(K // group_size, np.float32)
+    lib().oracle_gemv_q4_q8(_p(w, _c_u8p), _p(s, _c_f32p), _p(x, _c_f32p), _p(y, _c_f32p), M, K, group_size,
+                            _p(sq, _c_i8p), _p(ss, _c_f32p))
+    return y
+
+
+def quantize_activation_q4k(x) -> tuple[np.ndarray, np.ndarray]:
+    x = _f32(x).reshape(-1)
+    K = x.shape[0]
+    xq = np.empty(K, np.int8)
+    xs = np.empty(K // 32, np.float32)
+    lib().oracle_quantize_activation_q4k(_p(x, _c_f32p), _p(xq, _c_i8p), _p(xs, _c_f32p), K)
+    return xq, xs
+
+
+def gemv_q4km(w, x, M: int, K: int) -> np.ndarray:
+    w, x = _u8(w), _f32(x).reshape(-1)
+    y = np.empty(M, np.float32)
+    sq = np.empty(K, np.int8)
+    ss = np.empty(K // 32, np.float32)
+    lib().oracle_gemv_q4km(_p(w, _c_u8p), _p(x, _c_f32p), _p(y, _c_f32p), M, K, _p(sq, _c_i8p), _p(ss, _c_f32p))
+    return y
+
+
+def gemv_affine(w, x, scales, biases, M: int, K: int, group_size: int, packed: bool = True) -> np.ndarray:
+    w, x, s = _u8(w), _f32(x).reshape(-1), _f32(scales)
+    b = None if biases is None else _f32(biases)
+    y = np.empty(M, np.float32)
+    lib().oracle_gemv_affine(_p(w, _c_u8p), int(packed), _p(x, _c_f32p), _p(s, _c_f32p),
+                             None if b is None else _p(b, _c_f32p), _p(y, _c_f32p), M, K, group_size)
+    return y
+
+
+def gemv_q4_gs64(w, x, scales, M: int, K: int) -> np.ndarray:
+    return gemv_affine(w, x, scales, None, M, K, 64, packed=True)
+
+
+def matmul_batch_q4(w, scales, biases, X, M: int, K: int, B: int, group_size: int = 32) -> np.ndarray:
+    w, s, b, X = _u8(w), _f32(scales), _f32(biases), _f32(X)
+    Y = np.zeros((B, M), np.float32)
+    lib().oracle_matmul_batch_q4(_p(w, _c_u8p), _p(s, _c_f32p), _p(b, _c_f32p), _p(X, _c_f32p), _p(Y, _c_f32p),
+                                 M, K, B, group_size)
+    return Y
+
+
+def compute_bitmask(x, threshold: float) -> np.ndarray:
+    x = _f32(x).reshape(-1)
+    K = x.shape[0]
+    m = np.zeros((K + 31) // 32, np.uint32)
+    f = lib().oracle_compute_bitmask
+    f.argtypes = [_c_f32p, ctypes.POINTER(ctypes.c_uint32), ctypes.c_int, ctypes.c_float]
+    f(_p(x, _c_f32p), m.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), K, float(threshold))
+    return m
+
+
+def gemv_sparse_indices(w, x, scales, biases, idx, M: int, K: int, group_size: int) -> np.ndarray:
+    w, x, s, b = _u8(w), _f32(x).reshape(-1), _f32(scales), _f32(biases)
+    idx = np.ascontiguousarray(idx, np.int32).reshape(-1)
+    y = np.empty(M, np.float32)
+    lib().oracle_gemv_sparse_indices(_p(w, _c_u8p), _p(x, _c_f32p), _p(s, _c_f32p), _p(b, _c_f32p),
+                                     idx.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), idx.size,
+                                     _p(y, _c_f32p), M, K, group_size)
+    return y
+
+
+def bitmask_indices(mask, K: int) -> np.ndarray:
+    bits = np.unpackbits(np.ascontiguousarray(mask, np.uint32).view(np.uint8), bitorder="little")[:K]
+    return np.nonzero(bits)[0].astype(np.int32)
+
+
+def sparse_down_proj_T(wT, sT, bT, x, rows, in_dim: int, out_dim: int, group_size: int) -> np.ndarray:
+    wT, sT, bT, x = _u8(wT), _f32(sT), _f32(bT), _f32(x).reshape(-1)
+    rows = np.ascontiguousarray(rows, np.int32).reshape(-1)
+    y = np.empty(out_dim, np.float32)
+    lib().oracle_sparse_down_proj_T(_p(wT, _c_u8p), _p(sT, _c_f32p), _p(bT, _c_f32p), _p(x, _c_f32p),
+                                    rows.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), rows.size,
+                                    _p(y, _c_f32p), in_dim, out_dim, group_size)
+    return y

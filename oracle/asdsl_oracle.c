@@ -191,3 +191,222 @@ EXPORT void oracle_dequant_preq(const uint8_t* blocks, float* w, int M, int K) {
         }
     }
 }
+
+/* ------------------------------------------------------------------ A6
+ * Q4_128 symmetric GEMV on 66-byte blocks (asdsl/kernels/native/gemv_q4_128.cpp:94-257):
+ * x pre-quantized per 128; per group term D*(ws*xs), correction (8*X*xs)*ws
+ * (process_r8 form, gemv_q4_128.cpp:174-217). */
+EXPORT void oracle_gemv_q4_128(const uint8_t* blocks, const int8_t* xq, const float* xs, float* y, int M, int K) {
+    const int G = K / 128;
+    for (int r = 0; r < M; ++r) {
+        double acc = 0.0, corr = 0.0;
+        for (int g = 0; g < G; ++g) {
+            const uint8_t* b = blocks + ((size_t)r * G + g) * 66;
+            const float ws = half_to_float(rd16(b));
+            int32_t d, xsum;
+            nib_dot(b + 2, xq + (size_t)g * 128, 128, &d, &xsum);
+            acc += (double)((float)d * (ws * xs[g]));
+            corr += (double)((8.0f * (float)xsum * xs[g]) * ws);
+        }
+        y[r] = (float)(acc - corr);
+    }
+}
+
+/* Batched Q4_128 with an fp32 activation, no quantization
+ * (gemm_q4_128_q8_avx2, asdsl/kernels/native/gemv_q4_128.cpp:262-306):
+ * w = (q-8)*ws in fp32, Y[b][r] = sum_k w*X[b][k] (b < 64). */
+EXPORT void oracle_gemm_q4_128(const uint8_t* blocks, const float* X, float* Y, int M, int K, int B) {
+    const int G = K / 128;
+    for (int r = 0; r < M; ++r) {
+        for (int bb = 0; bb < B && bb < 64; ++bb) {
+            double acc = 0.0;
+            for (int g = 0; g < G; ++g) {
+                const uint8_t* b = blocks + ((size_t)r * G + g) * 66;
+                const float ws = half_to_float(rd16(b));
+                for (int k = 0; k < 128; ++k) {
+                    const float w = (float)(nib(b + 2, k) - 8) * ws;
+                    acc += (double)w * (double)X[(size_t)bb * K + (size_t)g * 128 + k];
+                }
+            }
+            Y[(size_t)bb * M + r] = (float)acc;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ A9(ii)
+ * gemv_q4_q8_avx2 (asdsl/kernels/native/gemv_q4_avx2.cpp:131-253): symmetric
+ * packed Q4 with fp32 scales; x quantized per group_size with the A1 rule;
+ * y = sum_g ((float)sum (q-8)*xq * ws) * xs. */
+EXPORT void oracle_gemv_q4_q8(const uint8_t* w, const float* scales, const float* x, float* y, int M, int K, int gs,
+                              int8_t* scratch_q, float* scratch_s) {
+    const int G = K / gs;
+    oracle_quantize_activation(x, scratch_q, scratch_s, K, gs);
+    for (int r = 0; r < M; ++r) {
+        double acc = 0.0;
+        const uint8_t* row = w + (size_t)r * (K / 2);
+        for (int g = 0; g < G; ++g) {
+            int32_t d = 0;
+            for (int k = 0; k < gs; ++k) d += (nib(row, g * gs + k) - 8) * (int32_t)scratch_q[(size_t)g * gs + k];
+            acc += (double)(((float)d * scales[(size_t)r * G + g]) * scratch_s[g]);
+        }
+        y[r] = (float)acc;
+    }
+}
+
+/* ------------------------------------------------------------------ A8
+ * Q4_K (ASDSL variant) superblock GEMV (asdsl/kernels/native/gemv_q4_avx2.cpp:78-120,283-420):
+ * 144-byte block per 256 weights: fp16 d, fp16 dmin, 12 bytes of a linear
+ * LSB-first 6-bit bitstream (entries 0-7 scales, 8-15 mins), 8 x 16 bytes of
+ * nibbles.  x quantized per 32: scale = amax/127 (0 if amax < 1e-12),
+ * q = clamp(round_half_away(x*127/amax), -127, 127).
+ * y = sum_sb (d*sc*D - dmin*m*X) * xs. */
+static int get6(const uint8_t* bytes, int idx) {
+    const int bit = idx * 6, byte = bit / 8, off = bit % 8;
+    int v = bytes[byte] >> off;
+    if (off > 2) v |= bytes[byte + 1] << (8 - off);
+    return v & 0x3F;
+}
+
+EXPORT void oracle_quantize_activation_q4k(const float* x, int8_t* xq, float* xs, int K) {
+    const float r127 = 1.0f / 127.0f;
+    for (int g = 0; g < K / 32; ++g) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float a = fabsf(x[g * 32 + i]);
+            if (a > amax) amax = a;
+        }
+        if (amax < 1e-12f) {
+            xs[g] = 0.0f;
+            for (int i = 0; i < 32; ++i) xq[g * 32 + i] = 0;
+            continue;
+        }
+        const float inv = 127.0f / amax;
+        xs[g] = amax * r127;
+        for (int i = 0; i < 32; ++i) {
+            volatile float p = x[g * 32 + i] * inv;
+            int q = (int)roundf(p);
+            q = q > 127 ? 127 : (q < -127 ? -127 : q);
+            xq[g * 32 + i] = (int8_t)q;
+        }
+    }
+}
+
+EXPORT void oracle_gemv_q4km(const uint8_t* w, const float* x, float* y, int M, int K, int8_t* scratch_q,
+                             float* scratch_s) {
+    const int nb = K / 256;
+    oracle_quantize_activation_q4k(x, scratch_q, scratch_s, K);
+    for (int r = 0; r < M; ++r) {
+        double acc = 0.0;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t* blk = w + ((size_t)r * nb + b) * 144;
+            const float d = half_to_float(rd16(blk));
+            const float dmin = half_to_float(rd16(blk + 2));
+            for (int sb = 0; sb < 8; ++sb) {
+                const float sub_scale = d * (float)get6(blk + 4, sb);
+                const float sub_min = dmin * (float)get6(blk + 4, sb + 8);
+                const int8_t* q8 = scratch_q + (size_t)b * 256 + sb * 32;
+                int32_t dot, xsum;
+                nib_dot(blk + 16 + sb * 16, q8, 32, &dot, &xsum);
+                acc += (double)((sub_scale * (float)dot - sub_min * (float)xsum) * scratch_s[b * 8 + sb]);
+            }
+        }
+        y[r] = (float)acc;
+    }
+}
+
+/* ------------------------------------------------------------------ A10
+ * fp32 affine Q4 GEMVs (asdsl/kernels/native/gemv_q4_avx2.cpp:665-806):
+ * y = sum_g (sum_k q*x)*s + b*sum_k x.  `packed` = 2 nibbles per byte (low =
+ * even); unpacked = one raw byte per element (the byte value is used as is). */
+EXPORT void oracle_gemv_affine(const uint8_t* w, int packed, const float* x, const float* s, const float* bias,
+                               float* y, int M, int K, int gs) {
+    const int G = K / gs;
+    for (int r = 0; r < M; ++r) {
+        double acc = 0.0;
+        for (int g = 0; g < G; ++g) {
+            double dot = 0.0, sx = 0.0;
+            for (int k = g * gs; k < (g + 1) * gs; ++k) {
+                const int q = packed ? nib(w + (size_t)r * (K / 2), k) : w[(size_t)r * K + k];
+                dot += (double)q * x[k];
+                sx += x[k];
+            }
+            acc += dot * s[(size_t)r * G + g] + (bias ? (double)bias[(size_t)r * G + g] * sx : 0.0);
+        }
+        y[r] = (float)acc;
+    }
+}
+
+/* gemv_q4_avx2 gs64 (asdsl/kernels/native/gemv_q4_kernel.cpp:96-122): scales only. */
+EXPORT void oracle_gemv_q4_gs64(const uint8_t* w, const float* x, const float* s, float* y, int M, int K) {
+    oracle_gemv_affine(w, 1, x, s, NULL, y, M, K, 64);
+}
+
+/* matmul_batch_q4 (asdsl/kernels/native/gemv_q4_avx2.cpp:950-1021): each weight
+ * dequantized once as fma(q, s, b) in fp32, then dotted with every batch row. */
+EXPORT void oracle_matmul_batch_q4(const uint8_t* w, const float* s, const float* bias, const float* X, float* Y,
+                                   int M, int K, int B, int gs) {
+    const int G = K / gs;
+    for (int r = 0; r < M; ++r) {
+        for (int bb = 0; bb < B; ++bb) {
+            double acc = 0.0;
+            for (int k = 0; k < K; ++k) {
+                const int g = k / gs;
+                const float wf = fmaf((float)nib(w + (size_t)r * (K / 2), k), s[(size_t)r * G + g],
+                                      bias[(size_t)r * G + g]);
+                acc += (double)wf * X[(size_t)bb * K + k];
+            }
+            Y[(size_t)bb * M + r] = (float)acc;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ A12
+ * compute_bitmask (asdsl/kernels/native/gemv_sparse_avx2.cpp:144-179): bit k
+ * set iff |x[k]| >= threshold (ordered compares: NaN is inactive). */
+EXPORT void oracle_compute_bitmask(const float* x, uint32_t* mask, int K, float thr) {
+    for (int w = 0; w < (K + 31) / 32; ++w) mask[w] = 0;
+    for (int k = 0; k < K; ++k)
+        if (x[k] >= thr || x[k] <= -thr) mask[k / 32] |= 1u << (k % 32);
+}
+
+/* gemv_sparse_with_indices / gemv_sparse_unpacked
+ * (asdsl/kernels/native/gemv_sparse_avx2.cpp:66-139): over the listed columns
+ * only, y = sum_g s*sum w*x + b*sum x (raw bytes; repeats count again;
+ * indices outside [0,K) are ignored here, the reference reads them unchecked). */
+EXPORT void oracle_gemv_sparse_indices(const uint8_t* w, const float* x, const float* s, const float* b,
+                                       const int32_t* idx, int n, float* y, int M, int K, int gs) {
+    const int G = K / gs;
+    for (int r = 0; r < M; ++r) {
+        double acc = 0.0;
+        for (int i = 0; i < n; ++i) {
+            const int k = idx[i];
+            if (k < 0 || k >= K) continue;
+            const int g = k / gs;
+            acc += (double)s[(size_t)r * G + g] * w[(size_t)r * K + k] * x[k] + (double)b[(size_t)r * G + g] * x[k];
+        }
+        y[r] = (float)acc;
+    }
+}
+
+/* sparse_down_proj_T (asdsl/kernels/native/gemv_sparse_avx2.cpp:273-382):
+ * K-major packed Q4 w_T[in_dim][out_dim/2]; for every listed row r with
+ * x[r] != 0: y[o] += fma(q, s*x_r, b*x_r) with s, b the fp32 scale/bias of
+ * (r, o/gs).  Out-of-range rows are skipped (as the reference does). */
+EXPORT void oracle_sparse_down_proj_T(const uint8_t* wT, const float* sT, const float* bT, const float* x,
+                                      const int32_t* rows, int n, float* y, int in_dim, int out_dim, int gs) {
+    const int G = out_dim / gs;
+    for (int o = 0; o < out_dim; ++o) {
+        double a = 0.0;
+        for (int i = 0; i < n; ++i) {
+            const int r = rows[i];
+            if (r < 0 || r >= in_dim) continue;
+            const float xv = x[r];
+            if (xv == 0.0f) continue;
+            const int g = o / gs;
+            const float sv = sT[(size_t)r * G + g] * xv;
+            const float bv = bT[(size_t)r * G + g] * xv;
+            a += (double)fmaf((float)nib(wT + (size_t)r * (out_dim / 2), o), sv, bv);
+        }
+        y[o] = (float)a;
+    }
+}

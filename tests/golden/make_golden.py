@@ -68,6 +68,86 @@ def main() -> None:
     ng.gemv_preq2_fused_avx2(meta.reshape(-1), quant.reshape(-1), x, y3, M, K, 32)
     out.update(preq2_meta=meta.reshape(-1), preq2_quant=quant.reshape(-1), preq2_y=y3)
 
+    # A6: Q4_128 (pre-quantized per 128) and its batched fp32 GEMM
+    M, K = 24, 512
+    w = syn.gaussian_weights(M, K, 21)
+    w[3, 128:256] = 0.0                                  # all-zero group -> scale 0, nibbles 0x88
+    b128 = syn.q4_128_blocks(w)
+    x = syn.activation(K, 22)
+    xq = np.zeros(K, np.int8)
+    xs = np.zeros(K // 128, np.float32)
+    ng.quantize_activation_avx2(x, xq, xs, K, 128)
+    y = np.zeros(M, np.float32)
+    ng.gemv_q4_128_preq_avx2(b128, xq, xs, y, M, K, 128)
+    out.update(q128_blocks=b128, q128_x=x, q128_xq=xq, q128_xs=xs, q128_y=y, q128_shape=np.array([M, K]))
+
+    rng = np.random.default_rng(31)
+    # A9(ii): gemv_q4_q8 (symmetric packed + fp32 scales), gs 32
+    M, K = 20, 512
+    wp = rng.integers(0, 256, M * K // 2, dtype=np.uint8)
+    sc = (rng.random(M * K // 32) * 0.01 + 1e-3).astype(np.float32)
+    x = syn.activation(K, 32)
+    y = np.zeros(M, np.float32)
+    ng.gemv_q4_q8_avx2(wp, sc, x, y, M, K, 32)
+    out.update(q4q8_w=wp, q4q8_s=sc, q4q8_x=x, q4q8_y=y, q4q8_shape=np.array([M, K]))
+
+    # A8: Q4_K (ASDSL variant), random superblocks with small fp16 d/dmin
+    M, K = 12, 512
+    wk = rng.integers(0, 256, (M, K // 256, 144), dtype=np.uint8)
+    wk[:, :, 0:2] = np.frombuffer(np.float16(0.0123).tobytes(), np.uint8)
+    wk[:, :, 2:4] = np.frombuffer(np.float16(0.0041).tobytes(), np.uint8)
+    wk = wk.reshape(-1)
+    x = syn.activation(K, 33)
+    x[32:64] = 0.0                                       # amax < 1e-12 -> scale 0
+    y = np.zeros(M, np.float32)
+    ng.gemv_q4km_q8_avx2(wk, x, y, M, K)
+    out.update(q4k_w=wk, q4k_x=x, q4k_y=y, q4k_shape=np.array([M, K]))
+
+    # A10: packed / unpacked affine fp32 GEMV, gs64, matmul_batch_q4
+    M, K = 16, 256
+    wp = rng.integers(0, 256, M * K // 2, dtype=np.uint8)
+    wu = rng.integers(0, 16, M * K, dtype=np.uint8)
+    s32 = (rng.random(M * K // 32) * 0.01).astype(np.float32)
+    b32 = (rng.standard_normal(M * K // 32) * 0.01).astype(np.float32)
+    s64 = (rng.random(M * K // 64) * 0.01).astype(np.float32)
+    x = syn.activation(K, 34)
+    X = rng.standard_normal((3, K)).astype(np.float32)
+    Y = np.zeros((3, M), np.float32)
+    ng.matmul_batch_q4(wp, s32, b32, X, Y, M, K, 3, 32)
+    out.update(aff_wp=wp, aff_wu=wu, aff_s32=s32, aff_b32=b32, aff_s64=s64, aff_x=x, aff_X=X,
+               aff_y_packed=np.asarray(ng.gemv_q4_packed(wp, x, s32, b32, M, K, 32)),
+               aff_y_unpacked=np.asarray(ng.gemv_q4_unpacked(wu, x, s32, b32, M, K, 32)),
+               aff_y_gs64=np.asarray(ng.gemv_q4_avx2_gs64(wp, x, s64, M, K)),
+               aff_Y_batch=Y, aff_shape=np.array([M, K]))
+
+    # A9(i): Q8 weight GEMV (gemv_q8_unpacked / fused_dequant_gemv), gs 128
+    q8 = oracle.load_reference("_native_gemv_q8")
+    M, K = 16, 512
+    w8 = rng.integers(0, 256, M * K, dtype=np.uint8)
+    s8 = (rng.random(M * K // 128) * 0.01).astype(np.float32)
+    b8 = (rng.standard_normal(M * K // 128) * 0.01).astype(np.float32)
+    x = syn.activation(K, 35)
+    out.update(q8_w=w8, q8_s=s8, q8_b=b8, q8_x=x, q8_shape=np.array([M, K]),
+               q8_y=np.asarray(q8.gemv_q8_unpacked(w8, x, s8, b8, M, K, 128, True)))
+
+    # A12: bitmask, sparse GEMVs, sparse_down_proj_T (4 active rows: the
+    # reference runs them as one serial chunk, see tests/test_oracle.py)
+    sp = oracle.load_reference("_native_sparse_gemv")
+    xs_ = np.maximum(0.0, syn.activation(K, 36) - np.float32(0.841621)).astype(np.float32)
+    mask = np.asarray(sp.compute_bitmask(xs_, 0.01))
+    idx = np.nonzero(np.abs(xs_) >= 0.01)[0].astype(np.int32)
+    out.update(sp_x=xs_, sp_mask=mask, sp_idx=idx,
+               sp_y_idx=np.asarray(sp.gemv_sparse_with_indices(w8, xs_, s8, b8, idx, M, K, 128)),
+               sp_y_mask=np.asarray(sp.gemv_sparse_unpacked(w8, xs_, s8, b8, mask, M, K, 128)))
+    IN, OUT = 64, 96
+    wT = rng.integers(0, 256, IN * OUT // 2, dtype=np.uint8)
+    sT = (rng.random(IN * OUT // 32) * 0.01).astype(np.float32)
+    bT = (-8.0 * sT).astype(np.float32)
+    xT = np.maximum(0.0, syn.activation(IN, 37)).astype(np.float32)
+    rows = np.nonzero(xT)[0][:4].astype(np.int32)
+    out.update(dT_w=wT, dT_s=sT, dT_b=bT, dT_x=xT, dT_rows=rows, dT_shape=np.array([IN, OUT]),
+               dT_y=np.asarray(sp.sparse_down_proj_T(wT, sT, bT, xT, rows, IN, OUT, 32)))
+
     np.savez_compressed(HERE / "gemv_q4_reference.npz", **out)
     total = sum(v.nbytes for v in out.values())
     print(f"wrote {HERE / 'gemv_q4_reference.npz'} ({len(out)} arrays, {total} raw bytes)")

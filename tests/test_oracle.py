@@ -170,3 +170,219 @@ def test_preq2_vs_reference():
         y_r = np.zeros(M, np.float32)
         ng.gemv_preq2_fused_avx2(meta.reshape(-1), quant.reshape(-1), x, y_r, M, K, 32)
         assert rel_l2(oracle.gemv_preq2_fused(meta, quant, x, M, K, 32), y_r) < 1e-6
+
+
+# ------------------------------------------------------------------ A6 Q4_128
+def test_q4_128_golden(golden):
+    M, K = map(int, golden["q128_shape"])
+    y = oracle.gemv_q4_128(golden["q128_blocks"], golden["q128_xq"], golden["q128_xs"], M, K)
+    assert rel_l2(y, golden["q128_y"]) < 1e-6
+
+
+def test_q4_128_closed_form_and_zero_group():
+    M, K = 9, 512
+    w = syn.gaussian_weights(M, K, 3)
+    w[2, :128] = 0.0
+    blocks = syn.q4_128_blocks(w).reshape(M, K // 128, 66)
+    assert blocks[2, 0, 0] == 0 and blocks[2, 0, 1] == 0 and np.all(blocks[2, 0, 2:] == 0x88)
+    q = np.stack([blocks[:, :, 2:] & 15, blocks[:, :, 2:] >> 4], -1).reshape(M, K // 128, 128).astype(np.float64)
+    s = blocks[:, :, 0:2].copy().view(np.float16).astype(np.float64)
+    wd = ((q - 8.0) * s).reshape(M, K)
+    x = syn.activation(K, 4)
+    xq, xs = oracle.quantize_activation(x, 128)
+    want = wd @ (xq.astype(np.float64) * np.repeat(xs.astype(np.float64), 128))
+    assert rel_l2(oracle.gemv_q4_128(blocks, xq, xs, M, K), want) < 1e-6
+    # sanity only: symmetric 4-bit g128 quantization noise on N(0, 0.02) weights
+    assert rel_l2(wd @ x.astype(np.float64), w.astype(np.float64) @ x.astype(np.float64)) < 0.3
+
+
+def test_gemm_q4_128_is_column_loop():
+    M, K, B = 7, 256, 3
+    blocks = syn.q4_128_blocks(syn.gaussian_weights(M, K, 5))
+    X = np.random.default_rng(1).standard_normal((B, K)).astype(np.float32)
+    bl = blocks.reshape(M, K // 128, 66)
+    q = np.stack([bl[:, :, 2:] & 15, bl[:, :, 2:] >> 4], -1).reshape(M, K // 128, 128).astype(np.float32)
+    s = bl[:, :, 0:2].copy().view(np.float16).astype(np.float32)
+    wd = ((q - 8.0) * s).reshape(M, K).astype(np.float64)
+    assert rel_l2(oracle.gemm_q4_128(blocks, X, M, K, B), X.astype(np.float64) @ wd.T) < 1e-6
+
+
+# ------------------------------------------------------------------ A9(ii) Q4xQ8
+def test_q4_q8_golden(golden):
+    M, K = map(int, golden["q4q8_shape"])
+    y = oracle.gemv_q4_q8(golden["q4q8_w"], golden["q4q8_s"], golden["q4q8_x"], M, K, 32)
+    assert rel_l2(y, golden["q4q8_y"]) < 1e-6
+
+
+@needs_ref
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_q4_q8_vs_reference(gs):
+    ng = oracle.load_reference("_native_gemv")
+    rng = np.random.default_rng(gs)
+    M, K = 33, 3072
+    w = rng.integers(0, 256, M * K // 2, dtype=np.uint8)
+    s = (rng.random(M * K // gs) * 0.01).astype(np.float32)
+    x = syn.activation(K, 9)
+    y = np.zeros(M, np.float32)
+    ng.gemv_q4_q8_avx2(w, s, x, y, M, K, gs)
+    assert rel_l2(oracle.gemv_q4_q8(w, s, x, M, K, gs), y) < 1e-6
+
+
+# ------------------------------------------------------------------ A8 Q4_K
+def test_q4km_golden(golden):
+    M, K = map(int, golden["q4k_shape"])
+    assert rel_l2(oracle.gemv_q4km(golden["q4k_w"], golden["q4k_x"], M, K), golden["q4k_y"]) < 1e-6
+
+
+def test_q4km_closed_form():
+    """Decode the 6-bit bitstream independently (bit arithmetic on a Python int)."""
+    rng = np.random.default_rng(2)
+    M, K = 3, 512
+    w = rng.integers(0, 256, (M, K // 256, 144), dtype=np.uint8)
+    w[:, :, 0:2] = np.frombuffer(np.float16(0.02).tobytes(), np.uint8)
+    w[:, :, 2:4] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+    x = syn.activation(K, 3)
+    xq, xs = oracle.quantize_activation_q4k(x)
+    want = np.zeros(M)
+    for r in range(M):
+        for b in range(K // 256):
+            blk = w[r, b]
+            bits = int.from_bytes(bytes(blk[4:16]), "little")
+            six = [(bits >> (6 * i)) & 63 for i in range(16)]
+            d, dmin = 0.02, 0.01
+            for sb in range(8):
+                q = np.stack([blk[16 + 16 * sb:32 + 16 * sb] & 15, blk[16 + 16 * sb:32 + 16 * sb] >> 4], -1).reshape(-1)
+                xs8 = xq[b * 256 + sb * 32: b * 256 + sb * 32 + 32].astype(np.float64)
+                want[r] += (float(np.float16(d)) * six[sb] * (q @ xs8)
+                            - float(np.float16(dmin)) * six[sb + 8] * xs8.sum()) * xs[b * 8 + sb]
+    assert rel_l2(oracle.gemv_q4km(w.reshape(-1), x, M, K), want) < 1e-6
+    # quantizer: round half away from zero, clamp 127, zero group -> scale 0
+    xx = np.zeros(64, np.float32)
+    xx[32:] = np.linspace(-1, 1, 32)
+    xx[33] = 0.5 * 2 / 31 * 1  # arbitrary
+    q, s = oracle.quantize_activation_q4k(xx)
+    assert s[0] == 0 and np.all(q[:32] == 0)
+    assert np.array_equal(q[32:], np.clip(np.sign(xx[32:] * np.float32(127) / np.float32(1)) *
+                                          np.floor(np.abs((xx[32:] * (np.float32(127.0) / np.float32(1.0))).astype(np.float32)) + 0.5), -127, 127))
+
+
+@needs_ref
+def test_q4km_vs_reference():
+    ng = oracle.load_reference("_native_gemv")
+    rng = np.random.default_rng(5)
+    M, K = 40, 3072
+    w = rng.integers(0, 256, (M, K // 256, 144), dtype=np.uint8)
+    w[:, :, 0:2] = np.frombuffer(np.float16(0.011).tobytes(), np.uint8)
+    w[:, :, 2:4] = np.frombuffer(np.float16(0.003).tobytes(), np.uint8)
+    w = w.reshape(-1)
+    x = syn.activation(K, 6)
+    y = np.zeros(M, np.float32)
+    ng.gemv_q4km_q8_avx2(w, x, y, M, K)
+    assert rel_l2(oracle.gemv_q4km(w, x, M, K), y) < 1e-6
+
+
+# ------------------------------------------------------------------ A10 fp32 affine
+def test_affine_golden(golden):
+    M, K = map(int, golden["aff_shape"])
+    g = golden
+    assert rel_l2(oracle.gemv_affine(g["aff_wp"], g["aff_x"], g["aff_s32"], g["aff_b32"], M, K, 32),
+                  g["aff_y_packed"]) < 1e-6
+    assert rel_l2(oracle.gemv_affine(g["aff_wu"], g["aff_x"], g["aff_s32"], g["aff_b32"], M, K, 32, packed=False),
+                  g["aff_y_unpacked"]) < 1e-6
+    assert rel_l2(oracle.gemv_q4_gs64(g["aff_wp"], g["aff_x"], g["aff_s64"], M, K), g["aff_y_gs64"]) < 1e-6
+    assert rel_l2(oracle.matmul_batch_q4(g["aff_wp"], g["aff_s32"], g["aff_b32"], g["aff_X"], M, K, 3, 32),
+                  g["aff_Y_batch"]) < 1e-6
+
+
+def test_affine_known_answers():
+    """tests/test_gemv_q4.py:150-163 (all weights 8, x=1, s=.1, b=-.75 -> 1.6) and
+    asdsl/kernels/native/test_kernel.cpp:16,39 (0x77 bytes, s=1, x=1 -> 448 exactly)."""
+    w = np.full(32, 0x88, np.uint8)  # 2 rows x 32 nibbles of 8
+    y = oracle.gemv_affine(w, np.ones(32, np.float32), np.array([0.1, 0.1], np.float32),
+                           np.array([-0.75, -0.75], np.float32), 2, 32, 32)
+    np.testing.assert_allclose(y, [1.6, 1.6], rtol=1e-5)
+    y = oracle.gemv_q4_gs64(np.full(32, 0x77, np.uint8), np.ones(64, np.float32), np.ones(1, np.float32), 1, 64)
+    assert y[0] == 448.0
+
+
+def test_affine_closed_form_and_batch_loop():
+    rng = np.random.default_rng(7)
+    M, K, gs = 11, 192, 64
+    w = rng.integers(0, 256, M * K // 2, dtype=np.uint8)
+    s = rng.random(M * K // gs).astype(np.float32)
+    b = rng.standard_normal(M * K // gs).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    q = np.stack([w & 15, w >> 4], -1).reshape(M, K).astype(np.float64)
+    wd = q * np.repeat(s.reshape(M, -1), gs, 1) + np.repeat(b.reshape(M, -1), gs, 1)
+    assert rel_l2(oracle.gemv_affine(w, x, s, b, M, K, gs), wd @ x) < 1e-6
+    X = rng.standard_normal((4, K)).astype(np.float32)
+    Y = oracle.matmul_batch_q4(w, s, b, X, M, K, 4, gs)
+    for i in range(4):  # batch == loop (tests/test_gemv_q4_batched.py:10-64)
+        assert rel_l2(Y[i], oracle.gemv_affine(w, X[i], s, b, M, K, gs)) < 1e-5
+
+
+def test_q8_weight_golden(golden):
+    M, K = map(int, golden["q8_shape"])
+    g = golden
+    assert rel_l2(oracle.gemv_affine(g["q8_w"], g["q8_x"], g["q8_s"], g["q8_b"], M, K, 128, packed=False),
+                  g["q8_y"]) < 1e-6
+
+
+# ------------------------------------------------------------------ A12 sparse
+def test_sparse_golden(golden):
+    g = golden
+    M, K = map(int, g["q8_shape"])
+    assert np.array_equal(oracle.compute_bitmask(g["sp_x"], 0.01), g["sp_mask"])
+    assert np.array_equal(oracle.bitmask_indices(g["sp_mask"], K), g["sp_idx"])
+    assert rel_l2(oracle.gemv_sparse_indices(g["q8_w"], g["sp_x"], g["q8_s"], g["q8_b"], g["sp_idx"], M, K, 128),
+                  g["sp_y_idx"]) < 1e-6
+    assert rel_l2(oracle.gemv_sparse_indices(g["q8_w"], g["sp_x"], g["q8_s"], g["q8_b"],
+                                             oracle.bitmask_indices(g["sp_mask"], K), M, K, 128), g["sp_y_mask"]) < 1e-6
+    IN, OUT = map(int, g["dT_shape"])
+    assert rel_l2(oracle.sparse_down_proj_T(g["dT_w"], g["dT_s"], g["dT_b"], g["dT_x"], g["dT_rows"], IN, OUT, 32),
+                  g["dT_y"]) < 1e-6
+
+
+def test_sparse_equals_dense_on_zeroed_vector():
+    rng = np.random.default_rng(3)
+    M, K, gs = 13, 512, 128
+    w = rng.integers(0, 256, M * K, dtype=np.uint8)
+    s = rng.random(M * K // gs).astype(np.float32)
+    b = rng.standard_normal(M * K // gs).astype(np.float32)
+    x = np.maximum(0, rng.standard_normal(K) - 0.5).astype(np.float32)
+    idx = np.nonzero(x)[0].astype(np.int32)
+    dense = oracle.gemv_affine(w, x, s, b, M, K, gs, packed=False)
+    assert rel_l2(oracle.gemv_sparse_indices(w, x, s, b, idx, M, K, gs), dense) < 1e-6
+
+
+def test_sparse_down_proj_T_closed_form():
+    rng = np.random.default_rng(4)
+    IN, OUT = 512, 96
+    wT = rng.integers(0, 256, IN * OUT // 2, dtype=np.uint8)
+    sT = (rng.random(IN * OUT // 32) * 0.01).astype(np.float32)
+    bT = (-8 * sT).astype(np.float32)
+    x = np.maximum(0, rng.standard_normal(IN) - 0.84).astype(np.float32)
+    rows = np.nonzero(x)[0].astype(np.int32)
+    q = np.stack([wT & 15, wT >> 4], -1).reshape(IN, OUT).astype(np.float64)
+    wd = q * np.repeat(sT.reshape(IN, -1), 32, 1) + np.repeat(bT.reshape(IN, -1), 32, 1)
+    assert rel_l2(oracle.sparse_down_proj_T(wT, sT, bT, x, rows, IN, OUT, 32), x.astype(np.float64) @ wd) < 1e-6
+
+
+@needs_ref
+def test_sparse_down_proj_T_reference_is_racy_beyond_one_chunk():
+    """Finding: the reference accumulates into per-thread buffers indexed by
+    ai % nthreads inside a pool parallel_for (gemv_sparse_avx2.cpp:297-300), so
+    concurrent chunks race.  With <= 4 active rows (one serial chunk) it agrees
+    with the oracle; the oracle follows the intended, race-free sum."""
+    sp = oracle.load_reference("_native_sparse_gemv")
+    rng = np.random.default_rng(0)
+    IN, OUT = 512, 64
+    wT = rng.integers(0, 256, IN * OUT // 2, dtype=np.uint8)
+    sT = (rng.random(IN * OUT // 32) * 0.01).astype(np.float32)
+    bT = (-8 * sT).astype(np.float32)
+    x = np.maximum(0, rng.standard_normal(IN) - 0.84).astype(np.float32)
+    rows = np.nonzero(x)[0].astype(np.int32)
+    for n in (1, 2, 3, 4):
+        r = rows[:n]
+        assert rel_l2(oracle.sparse_down_proj_T(wT, sT, bT, x, r, IN, OUT, 32),
+                      np.asarray(sp.sparse_down_proj_T(wT, sT, bT, x, r, IN, OUT, 32))) < 1e-6
