@@ -11,6 +11,7 @@ namespace asdsl {
 
 namespace {
 thread_local char g_error[512] = "";
+thread_local LaunchEvents g_events;
 
 struct DeviceShape {
     int cus = -1;
@@ -27,6 +28,12 @@ void set_error(const char* fmt, ...) {
 }
 
 void clear_error() { g_error[0] = '\0'; }
+
+LaunchEvents take_launch_events() {
+    const LaunchEvents ev = g_events;
+    g_events = LaunchEvents{};
+    return ev;
+}
 
 int cu_count_current() {
     int dev = -1;
@@ -71,3 +78,9 @@ extern "C" int asdsl_abi_version(void) { return ASDSL_ABI_VERSION; }
 extern "C" const char* asdsl_last_error(void) { return asdsl::g_error; }
 
 extern "C" int asdsl_device_cu_count(void) { return asdsl::cu_count_current(); }
+
+extern "C" asdsl_status asdsl_profile_next_launch(void* start_event, void* stop_event) {
+    asdsl::g_events.start = static_cast<hipEvent_t>(start_event);
+    asdsl::g_events.stop = static_cast<hipEvent_t>(stop_event);
+    return ASDSL_OK;
+}

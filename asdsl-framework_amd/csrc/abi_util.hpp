@@ -2,7 +2,11 @@
 // launch checks and the cached device shape used to size grids.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
+
+#include <tuple>
+#include <utility>
 
 #include "asdsl_hip.h"
 
@@ -18,6 +22,42 @@ int cu_count_current();
 asdsl_status launch_status(const char* what);
 
 inline hipStream_t as_hip(asdsl_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Events armed by asdsl_profile_next_launch for the calling thread's next
+// kernel launch; returned and cleared.
+struct LaunchEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+LaunchEvents take_launch_events();
+
+// Launches `kernel` on `stream`.  With armed events the launch goes through
+// hipExtLaunchKernel, which records them as part of the kernel's own dispatch
+// (start and end of its execution, no extra packets on the stream).
+// Returns ASDSL_OK or ASDSL_ERR_HIP with the error text set.
+template <typename... P, typename... A>
+asdsl_status launch(const char* what, void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                    A... args) {
+    static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+    const LaunchEvents ev = take_launch_events();
+    if (ev.start == nullptr && ev.stop == nullptr) {
+        kernel<<<grid, block, lds, stream>>>(args...);
+        return launch_status(what);
+    }
+    std::tuple<P...> held{static_cast<P>(args)...};
+    void* ptrs[sizeof...(P)];
+    std::apply([&](auto&... v) {
+        size_t i = 0;
+        ((ptrs[i++] = static_cast<void*>(&v)), ...);
+    }, held);
+    const hipError_t e = hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, lds, stream,
+                                            ev.start, ev.stop, 0);
+    if (e != hipSuccess) {
+        set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+        return ASDSL_ERR_HIP;
+    }
+    return launch_status(what);
+}
 
 // Integer tuning knob from the environment, read once (0 = unset).  Knobs
 // only change launch shapes (and with them the fp32 summation order), never

@@ -95,37 +95,32 @@ __global__ __launch_bounds__(kThreads) void preq_gemv_kernel(const uint8_t* __re
 }
 
 template <int LPR>
-void launch_lpr(const uint8_t* blocks, const float* x, const int8_t* xq8, const float* xsc, float* y, int M,
-                int K, hipStream_t stream, int cus) {
+asdsl_status launch_lpr(const uint8_t* blocks, const float* x, const int8_t* xq8, const float* xsc, float* y, int M,
+                        int K, hipStream_t stream, int cus) {
     constexpr int RPW = kWave / LPR;
     const int ntiles = (M + RPW - 1) / RPW;
-    const int grid = stream_grid(ntiles, kWavesPerWg, 4, cus);
+    const dim3 grid(stream_grid(ntiles, kWavesPerWg, 4, cus));
+    const dim3 block(kThreads);
     const size_t lds = x_image_bytes(K, 32);
     if (xq8 != nullptr) {
-        if (K <= 8 * kThreads * 2)
-            preq_gemv_kernel<LPR, 4, 2, true><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
-        else if (K <= 8 * kThreads * 4)
-            preq_gemv_kernel<LPR, 4, 4, true><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
-        else
-            preq_gemv_kernel<LPR, 4, 10, true><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
-    } else {
-        if (K <= 8 * kThreads * 2)
-            preq_gemv_kernel<LPR, 4, 2, false><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
-        else if (K <= 8 * kThreads * 4)
-            preq_gemv_kernel<LPR, 4, 4, false><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
-        else
-            preq_gemv_kernel<LPR, 4, 10, false><<<grid, kThreads, lds, stream>>>(blocks, x, xq8, xsc, y, M, K);
+        auto* k = K <= 8 * kThreads * 2   ? preq_gemv_kernel<LPR, 4, 2, true>
+                  : K <= 8 * kThreads * 4 ? preq_gemv_kernel<LPR, 4, 4, true>
+                                          : preq_gemv_kernel<LPR, 4, 10, true>;
+        return launch("preq_gemv_kernel", k, grid, block, lds, stream, blocks, x, xq8, xsc, y, M, K);
     }
+    auto* k = K <= 8 * kThreads * 2   ? preq_gemv_kernel<LPR, 4, 2, false>
+              : K <= 8 * kThreads * 4 ? preq_gemv_kernel<LPR, 4, 4, false>
+                                      : preq_gemv_kernel<LPR, 4, 10, false>;
+    return launch("preq_gemv_kernel", k, grid, block, lds, stream, blocks, x, xq8, xsc, y, M, K);
 }
 
 asdsl_status launch_preq(const uint8_t* blocks, const float* x, const int8_t* xq8, const float* xsc, float* y,
                          int M, int K, hipStream_t stream, int cus) {
     const int G = K / 32;
-    if (G % 64 == 0) launch_lpr<64>(blocks, x, xq8, xsc, y, M, K, stream, cus);
-    else if (G % 32 == 0) launch_lpr<32>(blocks, x, xq8, xsc, y, M, K, stream, cus);
-    else if (G % 16 == 0 || G < 32) launch_lpr<16>(blocks, x, xq8, xsc, y, M, K, stream, cus);
-    else launch_lpr<64>(blocks, x, xq8, xsc, y, M, K, stream, cus);
-    return launch_status("preq_gemv_kernel");
+    if (G % 64 == 0) return launch_lpr<64>(blocks, x, xq8, xsc, y, M, K, stream, cus);
+    if (G % 32 == 0) return launch_lpr<32>(blocks, x, xq8, xsc, y, M, K, stream, cus);
+    if (G % 16 == 0 || G < 32) return launch_lpr<16>(blocks, x, xq8, xsc, y, M, K, stream, cus);
+    return launch_lpr<64>(blocks, x, xq8, xsc, y, M, K, stream, cus);
 }
 
 int check_preq_args(const void* blocks, const void* x, const void* y, int M, int K, int gs, const char* fn) {

@@ -4,20 +4,29 @@
 //   (asdsl/kernels/native/gemv_preq2_avx2.cpp:196-337), layout
 //   asdsl/quantization/repack_preq2.py:22-62.
 //
-// Mapping.  A band (4 output rows) is K/8 contiguous 16-byte units.  KS waves
-// of a 4-wave workgroup share one band, wave ks taking the contiguous unit
-// slice [ks*NU*64, (ks+1)*NU*64); lane l reads units slice+l, slice+l+64, ...
-// so every load instruction moves 1 KiB of contiguous HBM and a lane issues
-// all NU of its loads before using any.  64 is a multiple of 4*(GS/32), so a
-// lane always sees the same row slot (and, for g128, the same 32-element
-// quarter of its group); the 4 row sums fall out of a butterfly over the
-// other lane bits (DPP + swizzle + one bpermute), and the KS slices are added
-// in a fixed order through LDS, so results are deterministic.
+// Mapping.  A band (4 output rows) is K/8 contiguous 16-byte units.  A
+// workgroup of WAVES waves works on WAVES/KS bands at a time; the KS waves of
+// one band split its units into contiguous slices of NU*64, lane l of a slice
+// owning units slice+l, slice+l+64, ... so each load instruction moves 1 KiB of
+// contiguous HBM.  A lane's units always sit at the same K positions, whatever
+// band it works on, so the activation units it needs are read from LDS into
+// registers once, after the workgroup has quantized x, and reused for every
+// band.  64 is a multiple of 4*(GS/32), so a lane always sees the same row slot
+// (and, for g128, the same 32-element quarter of its group); row sums fall out
+// of a butterfly over the other lane bits (DPP + swizzle + one bpermute), and
+// the KS slices are added in a fixed order through LDS: results are
+// deterministic.
 //
-// The activation is quantized once per workgroup into LDS (split int8 order,
-// per-group scales, per-unit sums) while the first tile's weight loads are
-// already in flight; the next tile's loads are issued before the current
-// tile's reduction.
+// Launch shape (measured on MI355X, rotated weights): fat workgroups (8 waves,
+// 16 when K > 4096) amortize the per-workgroup activation quantization, which
+// for K=8192 reads more bytes than the workgroup's own weights when
+// workgroups are small; KS grows only while fewer than CUs/2 workgroups would
+// be launched.  o_proj 3072x3072 3.0 us (KS=2), gate_up 16384x3072 6.9 us
+// (KS=1), down 3072x8192 5.4 us (KS=4, 16 waves).
+//
+// The activation loads are issued before the weight loads (vmcnt retires in
+// order) and quantized while the weights are in flight; the next tile's loads
+// are issued right after the current tile's dots.
 //
 // Math per unit (32 elements), fp32 after an exact int32 dot:
 //   acc += D*(s*xs) - (z*s)*(X*xs)
@@ -30,18 +39,17 @@ namespace asdsl {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWavesPerWg = kThreads / kWave;
+constexpr int kThreads = 256;  // helper kernels
 
-template <int GS, int NU, int NCH, bool Q8>
-__global__ __launch_bounds__(kThreads) void preq2_gemv_kernel(const uint32_t* __restrict__ meta,
-                                                             const uint4* __restrict__ quant,
-                                                             const float* __restrict__ x,
-                                                             const int8_t* __restrict__ xq8,
-                                                             const float* __restrict__ xsc,
-                                                             float* __restrict__ y, int M, int K, int KS) {
+template <int GS, int NU, int WAVES, int NCH, bool Q8, bool EXACT, bool XREG>
+__global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_t* __restrict__ meta,
+                                                                  const uint4* __restrict__ quant,
+                                                                  const float* __restrict__ x,
+                                                                  const int8_t* __restrict__ xq8,
+                                                                  const float* __restrict__ xsc,
+                                                                  float* __restrict__ y, int M, int K, int lks) {
     extern __shared__ __align__(16) uint32_t lds[];
-    __shared__ float s_part[2][kWavesPerWg][4];
+    __shared__ float s_part[2][WAVES][4];
     constexpr int UPS = GS / 32;       // units per (row, group)
     constexpr int UPG4 = 4 * UPS;      // units per (band, group)
     constexpr int SB = UPS == 1 ? 0 : 2;
@@ -50,69 +58,104 @@ __global__ __launch_bounds__(kThreads) void preq2_gemv_kernel(const uint32_t* __
 
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int wave = static_cast<int>(threadIdx.x) >> 6;
-    const int ks = wave % KS;
-    const int bpt = kWavesPerWg / KS;  // bands per tile
-    const int bl = wave / KS;
+    const int KS = 1 << lks;
+    const int ks = wave & (KS - 1);
+    const int bl = wave >> lks;
+    const int bpt = WAVES >> lks;      // bands per tile
     const int nbands = (M + 3) >> 2;
     const int ntiles = (nbands + bpt - 1) / bpt;
     const int upb = K >> 3;            // units per band
-    const int slice = (upb + KS - 1) / KS;
-    const int c_begin = ks * slice;
-    const int c_end = min(c_begin + slice, upb);
+    const int c0 = ks * (NU * kWave) + lane;
     const int part = lane % UPS;
     const int slot = (lane / UPS) & 3;
     const bool writer = lane < UPG4 && part == 0;
 
+    // This lane's units.  EXACT (KS*NU*64 == K/8): every unit is in the band
+    // and sits at a constant offset from the first.  Otherwise indices are
+    // clamped in bounds and units past the band are masked.
+    int cu[NU];
+    bool valid[NU];
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+        valid[j] = EXACT || c0 + j * kWave < upb;
+        cu[j] = EXACT ? c0 + j * kWave : min(c0 + j * kWave, upb - 1);
+    }
+
     uint4 w[NU];
     uint32_t mt[NU];
-    // Loads are unconditional at clamped, in-bounds indices (so they issue
-    // back to back); values past the slice or of rows >= M are never used.
-    auto load_pass = [&](int band, int c0) {
-        const int b = min(band, nbands - 1);
-        const uint4* qb = quant + static_cast<size_t>(b) * upb;
-        const int row = min(b * 4 + slot, M - 1);
+    // Loads are unconditional at in-bounds indices; values of rows >= M
+    // (tail band) are never stored.
+    auto load_tile = [&](int tile) {
+        const int band = min(tile * bpt + bl, nbands - 1);
+        const uint4* qb = quant + static_cast<size_t>(band) * upb;
+        const int row = min(band * 4 + slot, M - 1);
         const uint32_t* mrow = meta + static_cast<size_t>(row) * G;
+        if (EXACT) {
+            const uint4* qp = qb + c0;
+            const uint32_t* mp = mrow + c0 / UPG4;
 #pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            const int c = min(c0 + j * kWave + lane, c_end - 1);
-            w[j] = load_stream16(qb + c);
-            mt[j] = mrow[c / UPG4];
+            for (int j = 0; j < NU; ++j) w[j] = load_stream16(qp + j * kWave);
+#pragma unroll
+            for (int j = 0; j < NU; ++j) mt[j] = mp[j * (kWave / UPG4)];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NU; ++j) w[j] = load_stream16(qb + cu[j]);
+#pragma unroll
+            for (int j = 0; j < NU; ++j) mt[j] = mrow[cu[j] / UPG4];
         }
     };
 
     int tile = static_cast<int>(blockIdx.x);
     const int tile_step = static_cast<int>(gridDim.x);
-    ActStage<GS, kThreads, NCH, Q8> act;
+    ActStage<GS, WAVES * kWave, NCH, Q8> act;
     act.load(x, xq8, xsc, K);  // activation loads first: they retire first
-    load_pass(tile * bpt + bl, c_begin);  // unconditional: indices are clamped
+    load_tile(tile);           // grid <= ntiles, so this tile exists
     act.process(K, im);        // quantize while the weights are in flight
     __syncthreads();
 
-    int parity = 0;
-    for (; tile < ntiles; tile += tile_step, parity ^= 1) {  // uniform per workgroup
-        const int band = tile * bpt + bl;
-        float acc = 0.0f;
-        for (int c0 = c_begin; c0 < c_end; c0 += NU * kWave) {
-            if (c0 != c_begin) load_pass(band, c0);
+    // XREG: this lane's activation units are copied from LDS into registers
+    // once and reused for every tile; otherwise they are read per tile.
+    uint32_t xr[XREG ? NU : 1][8];
+    float xs[XREG ? NU : 1], xu[XREG ? NU : 1];
+    auto read_x = [&](int j, uint32_t (&dst)[8], float& sc, float& us) {
+        const int g = cu[j] / UPG4;
+        const int u = g * UPS + part;
+        const uint4 a = reinterpret_cast<const uint4*>(im.xq + u * 8)[0];
+        const uint4 b = reinterpret_cast<const uint4*>(im.xq + u * 8)[1];
+        dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
+        dst[4] = b.x; dst[5] = b.y; dst[6] = b.z; dst[7] = b.w;
+        sc = im.scale[g];
+        us = im.usum[u];
+    };
+    if (XREG) {
 #pragma unroll
-            for (int j = 0; j < NU; ++j) {
-                const int c = c0 + j * kWave + lane;
-                if (c < c_end) {
-                    const int g = c / UPG4;
-                    const int u = g * UPS + part;
-                    const int d = unit_dot(w[j], im.xq + u * 8);
-                    const float s = half_bits_to_float(mt[j]);
-                    const float z = half_bits_to_float(mt[j] >> 16);
-                    acc = fmaf(static_cast<float>(d), s * im.scale[g], acc);
-                    acc = fmaf(-(z * s), im.usum[u], acc);
-                }
+        for (int j = 0; j < NU; ++j) read_x(j, xr[XREG ? j : 0], xs[XREG ? j : 0], xu[XREG ? j : 0]);
+    }
+
+    int parity = 0;
+    for (; tile < ntiles; tile += tile_step) {  // uniform per workgroup
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            if (valid[j]) {
+                uint32_t xt[8];
+                float sc, us;
+                if (!XREG) read_x(j, xt, sc, us);
+                const int jj = XREG ? j : 0;
+                const int d = unit_dot(w[j], XREG ? xr[jj] : xt);
+                const float s = half_bits_to_float(mt[j]);
+                const float z = half_bits_to_float(mt[j] >> 16);
+                acc = fmaf(static_cast<float>(d), s * (XREG ? xs[jj] : sc), acc);
+                acc = fmaf(-(z * s), XREG ? xu[jj] : us, acc);
             }
         }
-        const int next = tile + tile_step;
-        if (next < ntiles) load_pass(next * bpt + bl, c_begin);
+        const int band = tile * bpt + bl;
         acc = slot_sum<SB>(acc);
+        // next tile's loads after the reduction: issuing them before it keeps
+        // ~20 more VGPRs live (measured), costing a workgroup per CU at NU=6
+        if (tile + tile_step < ntiles) load_tile(tile + tile_step);
         const int row = band * 4 + slot;
-        if (KS == 1) {
+        if (lks == 0) {
             if (writer && band < nbands && row < M) y[row] = acc;
         } else {
             if (writer) s_part[parity][wave][slot] = acc;
@@ -122,6 +165,7 @@ __global__ __launch_bounds__(kThreads) void preq2_gemv_kernel(const uint32_t* __
                 for (int k = 1; k < KS; ++k) sum += s_part[parity][wave + k][slot];
                 y[row] = sum;
             }
+            parity ^= 1;
         }
     }
 }
@@ -223,70 +267,80 @@ int check_preq2_args(const void* meta, const void* quant, const void* x, const v
     return 0;
 }
 
-// Launch plan: the smallest K split KS in {1,2,4} that leaves each lane at
-// most 4 units (loads) per band slice.  Measured on MI355X with rotated weight
-// copies: K=3072 -> KS=2 (gate_up 16384x3072 8.3 us vs 8.7-9.0 us at KS=1,
-// lm_head g128 52.7 us vs 54.1 us), K=8192 -> KS=4 (down 3072x8192 7.2 us vs
-// 8.2 us).  Shapes with no exact split fall back to looped passes of 8 units.
+// Launch plan.  waves: 8 per workgroup, 16 when K > 4096 (the activation is
+// then 32+ KB of fp32 per workgroup).  KS: the smallest power of two that
+// leaves each lane at most 6 units (loads) per band; then doubled, while it
+// splits the band evenly, as long as fewer than CUs/2 workgroups would run.
+// ASDSL_HIP_KSPLIT forces KS (a power of two <= 8); it changes the fp32
+// summation order, not the formula.
 struct Plan {
-    int ks, nu;
+    int lks, nu, waves, grid;
+    bool exact;
 };
 
-Plan plan_preq2(int K) {
+Plan plan_preq2(int M, int K, int cus) {
     const int upb = K / 8;
+    const int nbands = (M + 3) / 4;
+    Plan p{0, 0, K > 4096 ? 16 : 8, 0, false};
+    auto nu_of = [&](int lks) { return (upb + (kWave << lks) - 1) / (kWave << lks); };
+    auto tiles_of = [&](int lks) {
+        const int bpt = p.waves >> lks;
+        return (nbands + bpt - 1) / bpt;
+    };
     static const int forced = env_knob("ASDSL_HIP_KSPLIT");
-    Plan best{0, 0};
-    for (int ks : {1, 2, 4}) {
-        if (upb % (64 * ks) != 0) continue;
-        if (forced > 0 && ks != forced) continue;
-        const int nu = upb / (64 * ks);
-        if (nu > 8) continue;
-        best = Plan{ks, nu};
-        if (nu <= 4) break;
+    if (forced == 1 || forced == 2 || forced == 4 || forced == 8) {
+        p.lks = forced == 1 ? 0 : forced == 2 ? 1 : forced == 4 ? 2 : 3;
+    } else {
+        while (p.lks < 3 && nu_of(p.lks) > 6) ++p.lks;
+        while (p.lks < 3 && tiles_of(p.lks) < cus / 2 && upb % (kWave << (p.lks + 1)) == 0) ++p.lks;
     }
-    if (best.ks == 0) best = Plan{1, 8};  // generic: looped passes of 8 units
-    return best;
+    p.nu = nu_of(p.lks);
+    p.exact = p.nu * (kWave << p.lks) == upb;
+    const int cap = cus * (32 / p.waves);  // at most 32 waves per compute unit
+    const int tiles = tiles_of(p.lks);
+    p.grid = tiles < cap ? tiles : cap;
+    return p;
 }
 
-template <int GS, int NCH, bool Q8>
-void launch_nu(Plan p, const uint8_t* meta, const uint8_t* quant, const float* x, const int8_t* xq8,
-               const float* xsc, float* y, int M, int K, hipStream_t stream, int cus) {
-    const int nbands = (M + 3) / 4;
-    const int bpt = kWavesPerWg / p.ks;
-    const int ntiles = (nbands + bpt - 1) / bpt;
-    const int grid = stream_grid(ntiles, 1, 4, cus);
+template <int GS, int WAVES, int NCH, bool Q8, bool EXACT>
+asdsl_status launch_exact(const Plan& p, const uint32_t* m, const uint4* q, const float* x, const int8_t* xq8,
+                          const float* xsc, float* y, int M, int K, hipStream_t stream) {
+    constexpr bool XREG = true;
     const size_t lds = x_image_bytes(K, GS);
-    const auto* m = reinterpret_cast<const uint32_t*>(meta);
-    const auto* q = reinterpret_cast<const uint4*>(quant);
-#define ASDSL_PREQ2_NU(N) \
-    case N: preq2_gemv_kernel<GS, N, NCH, Q8><<<grid, kThreads, lds, stream>>>(m, q, x, xq8, xsc, y, M, K, p.ks); break;
+    const dim3 block(WAVES * kWave);
+#define ASDSL_PREQ2_NU(N)                                                                                      \
+    case N:                                                                                                    \
+        return launch("preq2_gemv_kernel", preq2_gemv_kernel<GS, N, WAVES, NCH, Q8, EXACT, XREG>, dim3(p.grid), \
+                      block, lds, stream, m, q, x, xq8, xsc, y, M, K, p.lks);
     switch (p.nu) {
         ASDSL_PREQ2_NU(1)
         ASDSL_PREQ2_NU(2)
         ASDSL_PREQ2_NU(3)
         ASDSL_PREQ2_NU(4)
         ASDSL_PREQ2_NU(5)
-        ASDSL_PREQ2_NU(6)
-        ASDSL_PREQ2_NU(7)
-        default: preq2_gemv_kernel<GS, 8, NCH, Q8><<<grid, kThreads, lds, stream>>>(m, q, x, xq8, xsc, y, M, K, p.ks);
+        default: ASDSL_PREQ2_NU(6)
     }
 #undef ASDSL_PREQ2_NU
 }
 
-template <int GS>
+template <int GS, int WAVES, int NCH, bool Q8>
+asdsl_status launch_waves(const Plan& p, const uint32_t* m, const uint4* q, const float* x, const int8_t* xq8,
+                          const float* xsc, float* y, int M, int K, hipStream_t stream) {
+    if (p.exact) return launch_exact<GS, WAVES, NCH, Q8, true>(p, m, q, x, xq8, xsc, y, M, K, stream);
+    return launch_exact<GS, WAVES, NCH, Q8, false>(p, m, q, x, xq8, xsc, y, M, K, stream);
+}
+
+template <int GS, bool Q8>
 asdsl_status launch_preq2(const uint8_t* meta, const uint8_t* quant, const float* x, const int8_t* xq8,
                           const float* xsc, float* y, int M, int K, hipStream_t stream, int cus) {
-    const Plan p = plan_preq2(K);
-    if (xq8 != nullptr) {
-        if (K <= 8 * kThreads * 2) launch_nu<GS, 2, true>(p, meta, quant, x, xq8, xsc, y, M, K, stream, cus);
-        else if (K <= 8 * kThreads * 4) launch_nu<GS, 4, true>(p, meta, quant, x, xq8, xsc, y, M, K, stream, cus);
-        else launch_nu<GS, 10, true>(p, meta, quant, x, xq8, xsc, y, M, K, stream, cus);
-    } else {
-        if (K <= 8 * kThreads * 2) launch_nu<GS, 2, false>(p, meta, quant, x, xq8, xsc, y, M, K, stream, cus);
-        else if (K <= 8 * kThreads * 4) launch_nu<GS, 4, false>(p, meta, quant, x, xq8, xsc, y, M, K, stream, cus);
-        else launch_nu<GS, 10, false>(p, meta, quant, x, xq8, xsc, y, M, K, stream, cus);
-    }
-    return launch_status("preq2_gemv_kernel");
+    const Plan p = plan_preq2(M, K, cus);
+    const auto* m = reinterpret_cast<const uint32_t*>(meta);
+    const auto* q = reinterpret_cast<const uint4*>(quant);
+    // one 8-element activation chunk per thread and pass: NCH = ceil(K / (8 * threads))
+    if (p.waves == 8) return launch_waves<GS, 8, 1, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);
+    if (K <= 8192) return launch_waves<GS, 16, 1, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);
+    if (K <= 16384) return launch_waves<GS, 16, 2, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);
+    return launch_waves<GS, 16, 3, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);
 }
 
 }  // namespace
@@ -302,8 +356,8 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused(const uint8_t* meta, const uint8_
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CU_COUNT(cus);
     if (group_size == 32)
-        return launch_preq2<32>(meta, quant, x, nullptr, nullptr, y, out_features, in_features, as_hip(stream), cus);
-    return launch_preq2<128>(meta, quant, x, nullptr, nullptr, y, out_features, in_features, as_hip(stream), cus);
+        return launch_preq2<32, false>(meta, quant, x, nullptr, nullptr, y, out_features, in_features, as_hip(stream), cus);
+    return launch_preq2<128, false>(meta, quant, x, nullptr, nullptr, y, out_features, in_features, as_hip(stream), cus);
 }
 
 extern "C" asdsl_status asdsl_gemv_preq2(const uint8_t* meta, const uint8_t* quant, const int8_t* x_q8,
@@ -314,8 +368,8 @@ extern "C" asdsl_status asdsl_gemv_preq2(const uint8_t* meta, const uint8_t* qua
     ASDSL_CHECK_ARG(x_scales != nullptr, "gemv_preq2: null pointer");
     ASDSL_CU_COUNT(cus);
     if (group_size == 32)
-        return launch_preq2<32>(meta, quant, nullptr, x_q8, x_scales, y, out_features, in_features, as_hip(stream), cus);
-    return launch_preq2<128>(meta, quant, nullptr, x_q8, x_scales, y, out_features, in_features, as_hip(stream), cus);
+        return launch_preq2<32, true>(meta, quant, nullptr, x_q8, x_scales, y, out_features, in_features, as_hip(stream), cus);
+    return launch_preq2<128, true>(meta, quant, nullptr, x_q8, x_scales, y, out_features, in_features, as_hip(stream), cus);
 }
 
 extern "C" asdsl_status asdsl_dequant_preq2(const uint8_t* meta, const uint8_t* quant, float* w, int out_features,
@@ -325,14 +379,10 @@ extern "C" asdsl_status asdsl_dequant_preq2(const uint8_t* meta, const uint8_t* 
     ASDSL_CU_COUNT(cus);
     const long long units = static_cast<long long>(out_features) * (in_features / 32);
     const int grid = stream_grid(units, kThreads, 16, cus);
-    if (group_size == 32) {
-        preq2_dequant_kernel<32><<<grid, kThreads, 0, as_hip(stream)>>>(
-            reinterpret_cast<const uint32_t*>(meta), reinterpret_cast<const uint4*>(quant), w, out_features, in_features);
-    } else {
-        preq2_dequant_kernel<128><<<grid, kThreads, 0, as_hip(stream)>>>(
-            reinterpret_cast<const uint32_t*>(meta), reinterpret_cast<const uint4*>(quant), w, out_features, in_features);
-    }
-    return launch_status("preq2_dequant_kernel");
+    const auto* m = reinterpret_cast<const uint32_t*>(meta);
+    const auto* q = reinterpret_cast<const uint4*>(quant);
+    return launch("preq2_dequant_kernel", group_size == 32 ? preq2_dequant_kernel<32> : preq2_dequant_kernel<128>,
+                  dim3(grid), dim3(kThreads), 0, as_hip(stream), m, q, w, out_features, in_features);
 }
 
 extern "C" asdsl_status asdsl_quantize_activation(const float* x, int8_t* x_q8, float* x_scales, int in_features,
@@ -345,9 +395,9 @@ extern "C" asdsl_status asdsl_quantize_activation(const float* x, int8_t* x_q8, 
     ASDSL_CU_COUNT(cus);
     const int nchunk = in_features / 8;
     const int grid = stream_grid(nchunk, kThreads, 1, cus);
-    hipStream_t s = as_hip(stream);
-    if (group_size == 32) quantize_activation_kernel<32><<<grid, kThreads, 0, s>>>(x, x_q8, x_scales, in_features);
-    else if (group_size == 64) quantize_activation_kernel<64><<<grid, kThreads, 0, s>>>(x, x_q8, x_scales, in_features);
-    else quantize_activation_kernel<128><<<grid, kThreads, 0, s>>>(x, x_q8, x_scales, in_features);
-    return launch_status("quantize_activation_kernel");
+    auto* kernel = group_size == 32   ? quantize_activation_kernel<32>
+                   : group_size == 64 ? quantize_activation_kernel<64>
+                                      : quantize_activation_kernel<128>;
+    return launch("quantize_activation_kernel", kernel, dim3(grid), dim3(kThreads), 0, as_hip(stream), x, x_q8,
+                  x_scales, in_features);
 }

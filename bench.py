@@ -9,11 +9,20 @@ Steps rotate over --layers distinct weight sets (default 16, ~1 GB) so that the
 256 MB Infinity Cache cannot serve the weights: every step streams its
 62.9 MB from HBM.  Inputs are resident in HBM before the timed region.
 
-value = algorithmic bytes per step (packed weights + fp32 x + fp32 y) / step time.
-roofline = the gate_up kernel (the largest GEMV), timed with HIP events on its
-stream inside the timed region.  cpu_baseline = the reference's own
-gemv_preq2_fused_avx2 (compiled from its sources into oracle/_ref) on one
-layer's four GEMVs, on the host cores, for ~10 s.
+value    = algorithmic bytes per step (packed weights + fp16 meta + fp32 x + fp32 y)
+           / wall time per step (HIP events around the K timed steps).
+           The K steps run as replays of HIP graphs (one graph = one rotation
+           cycle of 16 steps = 64 GEMV launches), as a decode engine launches.
+roofline = the gate_up GEMV kernel: its algorithmic bytes / its average
+           launch duration, from HIP events around replays of a graph of 64
+           back-to-back gate_up launches over the rotated weights (the dispatch
+           gaps between graph nodes are included, so this bounds the kernel
+           duration from above).
+cpu_baseline = the reference's own gemv_preq2_fused_avx2 (compiled from its
+           sources into oracle/_ref) on one layer's four GEMVs on the host
+           cores for ~10 s (OpenMP, OMP_NUM_THREADS threads).
+extra    = lm_head 200064x3072 preq2-g128 GEMV (untimed phase, same graph
+           method, two alternating copies of 327 MB).
 
 Prints one JSON line.
 """
@@ -37,6 +46,13 @@ HBM_PEAK_GBS = 8000.0
 # (name, out_features M, in_features K)
 LAYER = [("qkv", 5120, 3072), ("o_proj", 3072, 3072), ("gate_up", 16384, 3072), ("down", 3072, 8192)]
 GS = 32
+LM_HEAD = (200064, 3072, 128)
+# HBM bytes per gate_up launch measured by rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE on `bench.py --pmc-probe`, each scaled by the same counter on a
+# 64 MiB device copy (fetch x1.9993, write x1.0); see
+# profiles/preq2_gemv_phi4_layer_g32.md.  A property of the kernel's access
+# pattern: re-measure when the kernel's loads change.
+GATE_UP_TRAFFIC_BYTES = 31_681_704
 
 
 def gemv_bytes(M: int, K: int, gs: int = GS) -> int:
@@ -105,9 +121,43 @@ def cpu_baseline(layer0, xs, ys_gpu, seconds: float):
         "unit": "GB/s",
         "cores": threads,
         "kind": kind,
-        "sample": f"{steps} steps of one layer's 4 preq2 GEMVs (gemv_preq2_fused_avx2) in {el:.1f} s, "
-                  f"ms_per_step={1e3 * el / steps:.2f}",
+        "sample": f"{steps} steps of one layer's 4 preq2 g32 GEMVs (gemv_preq2_fused_avx2, OpenMP) "
+                  f"in {el:.1f} s, ms_per_step={1e3 * el / steps:.3f}",
     }, parity
+
+
+def lm_head_kernel(lib, capture, timed_replays):
+    """lm_head preq2-g128 GEMV: a graph of 8 back-to-back launches alternating
+    between two 327 MB weight copies, replayed; time per launch."""
+    import torch
+
+    from asdsl import _hip
+    from asdsl.quantization.synthetic import preq2_from_weights_torch
+
+    M, K, gs = LM_HEAD
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    copies = []
+    for _ in range(2):
+        w = torch.randn((M, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+        copies.append(preq2_from_weights_torch(w, gs))
+        del w
+    x = torch.randn(K, generator=gen, device="cuda", dtype=torch.float32)
+    y = torch.empty(M, device="cuda", dtype=torch.float32)
+    ptrs = [(_hip.ptr(m), _hip.ptr(q)) for m, q in copies]
+
+    def calls(h):
+        for i in range(8):
+            if lib.asdsl_gemv_preq2_fused(ptrs[i % 2][0], ptrs[i % 2][1], _hip.ptr(x), _hip.ptr(y), M, K, gs, h):
+                raise RuntimeError(_hip.last_error())
+    g = capture(calls)
+    reps = 12
+    us = 1e3 * timed_replays(g, reps) / (reps * 8)
+    nbytes = gemv_bytes(M, K, gs)
+    del g, copies
+    torch.cuda.empty_cache()
+    return {"shape": [M, K], "group_size": gs, "kernel_us": round(us, 2), "bytes": nbytes,
+            "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac_of_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def main() -> int:
@@ -118,10 +168,14 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-lm-head", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: 50 gate_up GEMVs over rotated weights, then 50 plain "
+                         "64 MiB device copies (the counter scale reference); prints nothing else")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the GEMV path has no "
-              "multi-GPU mode.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this GEMV path runs on a "
+              "single MI355X and has no multi-GPU mode.", file=sys.stderr)
         return 2
 
     import torch
@@ -135,57 +189,103 @@ def main() -> int:
     ptrs = [{n: (_hip.ptr(m), _hip.ptr(q)) for n, (m, q) in L.items()} for L in layers]
     xp = {n: _hip.ptr(x) for n, x in xs.items()}
     yp = {n: _hip.ptr(y) for n, y in ys.items()}
+    if args.pmc_probe:
+        n, M, K = LAYER[2]
+        for i in range(50):
+            p = ptrs[i % len(ptrs)]
+            lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], xp[n], yp[n], M, K, GS, sh)
+        src = torch.ones(16 << 20, device="cuda", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(50):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": "gate_up preq2 g32 x50 then copy 64 MiB x50",
+                          "gemv_bytes": gemv_bytes(M, K), "copy_bytes": src.numel() * 4}), flush=True)
+        return 0
+    L = len(layers)
 
-    def step(i, ev=None):
-        p = ptrs[i % len(ptrs)]
+    def step(i, stream_handle):
+        p = ptrs[i % L]
         for n, M, K in LAYER:
-            if ev is not None and n == "gate_up":
-                ev[0].record(stream)
-            st = lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], xp[n], yp[n], M, K, GS, sh)
-            if ev is not None and n == "gate_up":
-                ev[1].record(stream)
+            st = lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], xp[n], yp[n], M, K, GS, stream_handle)
             if st:
                 raise RuntimeError(_hip.last_error())
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    def capture(calls):
+        """HIP graph of `calls(stream_handle)` (torch's capture stream)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up on the side stream before capture
+            calls(int(side.cuda_stream))
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            calls(int(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        return g
+
+    def timed_replays(g, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    # One rotation cycle (L steps) per graph, plus the remainder, so that
+    # exactly --steps steps run back to back with no host launch gaps.
+    cycle = capture(lambda h: [step(i, h) for i in range(L)])
+    rem = args.steps % L
+    tail = capture(lambda h: [step(i, h) for i in range(rem)]) if rem else None
+    for _ in range(max(1, args.warmup // L)):
+        cycle.replay()
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t_start.record(stream)
-    for i in range(args.steps):
-        step(i, evs[i])
-    t_end.record(stream)
+    t_start.record()
+    for _ in range(args.steps // L):
+        cycle.replay()
+    if tail is not None:
+        tail.replay()
+    t_end.record()
     torch.cuda.synchronize()
-    ms_total = t_start.elapsed_time(t_end)
-    ms_step = ms_total / args.steps
-    gu_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    ms_step = t_start.elapsed_time(t_end) / args.steps
 
     step_bytes = sum(gemv_bytes(M, K) for _, M, K in LAYER)
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    gu_bytes = gemv_bytes(16384, 3072)
-    gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
 
-    # per-GEMV event timing (separate, untimed pass) for the report
+    # Per-GEMV kernel time: a graph of 4*L back-to-back launches of one GEMV
+    # over the rotated weights, replayed; time / launches.  Includes the
+    # (small) dispatch gaps between graph nodes, so it bounds the kernel
+    # duration from above.
     per = {}
     for n, M, K in LAYER:
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 200
-        e0.record(stream)
-        for i in range(reps):
-            p = ptrs[i % len(ptrs)]
-            lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], xp[n], yp[n], M, K, GS, sh)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
-        per[n] = {"us": round(us, 2), "GB/s": round(gemv_bytes(M, K) / (us * 1e-6) / 1e9, 1)}
+        def calls(h, n=n, M=M, K=K):
+            for i in range(4 * L):
+                p = ptrs[i % L]
+                if lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], xp[n], yp[n], M, K, GS, h):
+                    raise RuntimeError(_hip.last_error())
+        g = capture(calls)
+        reps = 25
+        us = 1e3 * timed_replays(g, reps) / (reps * 4 * L)
+        per[n] = {"kernel_us": round(us, 3), "GB/s": round(gemv_bytes(M, K) / (us * 1e-6) / 1e9, 1)}
+        del g
+    gu_us = per["gate_up"]["kernel_us"]
+    gu_bytes = gemv_bytes(16384, 3072)
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
 
     # outputs of layer 0 for the parity spot check
-    step(0)
+    step(0, int(torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     ys_host = {n: y.cpu().numpy() for n, y in ys.items()}
+    del cycle, tail
+
+    extra = {}
+    if not args.no_lm_head:
+        extra["lm_head_preq2_g128"] = lm_head_kernel(lib, capture, timed_replays)
 
     cpu, parity = (None, None)
     if not args.no_cpu:
@@ -215,16 +315,19 @@ def main() -> int:
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "preq2_gemv_kernel (gate_up 16384x3072)",
+            "kernel": "preq2_gemv_kernel (gate_up 16384x3072, gs=32)",
             "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "avg_us": round(gu_ms * 1e3, 3),
+            "traffic": GATE_UP_TRAFFIC_BYTES,
+            "avg_us": round(gu_us, 3),
+            "timing": "HIP events around replays of a HIP graph of 64 back-to-back gate_up launches "
+                      "over 16 rotated weight sets; per-launch average",
             "bytes_per_launch": gu_bytes,
         },
         "per_gemv": per,
+        "extra": extra,
         "cpu_baseline": cpu,
         "parity_rel_l2_vs_cpu": parity,
     }

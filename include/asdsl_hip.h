@@ -52,6 +52,14 @@ const char* asdsl_last_error(void);
  * get_num_threads/has_openmp (asdsl/kernels/native/gemv_q4_avx2.cpp:1490-1505). */
 int asdsl_device_cu_count(void);
 
+/* Instrumentation, no reference counterpart: arms two HIP events (hipEvent_t,
+ * created by the caller; either may be NULL) for the calling thread's next
+ * kernel launch by this library.  The launch records them as part of the
+ * kernel's own dispatch (hipExtLaunchKernel), at the start and end of its
+ * execution, so hipEventElapsedTime(start, stop) is that kernel's duration
+ * alone, with no extra commands on the stream. */
+asdsl_status asdsl_profile_next_launch(void* start_event, void* stop_event);
+
 /* ------------------------------------------------------------------ A1 ---
  * Per-group int8 activation quantizer.
  * Replaces quantize_activation_avx2
