@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
     "asdsl_gemv_preq2_fused": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_preq2": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_dequant_preq2": [_P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_q4_128_preq": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_q4_128_fused": [_P, _P, _P, _I, _I, _I, _P],
 }
 _RESTYPE = {"asdsl_last_error": ctypes.c_char_p}
 

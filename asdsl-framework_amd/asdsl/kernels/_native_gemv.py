@@ -123,6 +123,37 @@ def gemv_preq2_avx2(meta, quant, x_q8, x_scales, y, out_features: int, in_featur
     c.run("asdsl_gemv_preq2", pm, pq, pxq, pxs, py, out_features, in_features, group_size)
 
 
+# ------------------------------------------------------------ Q4_128
+def gemv_q4_128_preq_avx2(blocks, x_q8, x_scales, y, out_features: int, in_features: int,
+                          group_size: int = 128) -> None:
+    """Reference: gemv_q4_128_preq_avx2 (gemv_q4_128.cpp:94-257), symmetric
+    66-byte g128 blocks, activation pre-quantized per 128."""
+    fn = "gemv_q4_128_preq_avx2"
+    _check_gs(group_size, (128,), fn)
+    _check_dims(out_features, in_features, group_size, fn)
+    G = in_features // 128
+    c = DeviceCall(fn)
+    pb = c.input(blocks, np.uint8, out_features * G * 66, "blocks")
+    pq = c.input(x_q8, np.int8, in_features, "x_q8")
+    ps = c.input(x_scales, np.float32, G, "x_scales")
+    py = c.output(y, np.float32, out_features, "y")
+    c.run("asdsl_gemv_q4_128_preq", pb, pq, ps, py, out_features, in_features, group_size)
+
+
+def gemv_q4_128_fused(blocks, x_fp32, y, out_features: int, in_features: int, group_size: int = 128) -> None:
+    """Q4_128 GEMV that quantizes the fp32 activation per 128 inside the call
+    (the engine's quantize + gemv_q4_128_preq_avx2 pair, unified_engine.cpp:1646-1653)."""
+    fn = "gemv_q4_128_fused"
+    _check_gs(group_size, (128,), fn)
+    _check_dims(out_features, in_features, group_size, fn)
+    G = in_features // 128
+    c = DeviceCall(fn)
+    pb = c.input(blocks, np.uint8, out_features * G * 66, "blocks")
+    px = c.input(x_fp32, np.float32, in_features, "x_fp32")
+    py = c.output(y, np.float32, out_features, "y")
+    c.run("asdsl_gemv_q4_128_fused", pb, px, py, out_features, in_features, group_size)
+
+
 def dequant_preq2(meta, quant, out_features: int, in_features: int, group_size: int = 32):
     """Dequantized fp32 W[M, K] = (q - z) * s of a preq2 matrix (debug/validation)."""
     fn = "dequant_preq2"

@@ -80,3 +80,27 @@ def preq2_from_weights_torch(w, group_size: int = 32):
     padded[:rows] = nib
     quant = padded.reshape(n_bands, 4, G, group_size // 2).permute(0, 2, 1, 3).contiguous().reshape(-1)
     return meta, quant
+
+
+def q4_128_from_weights_torch(w):
+    """torch fp32 W (rows, cols) on any device -> flat Q4_128 66-byte blocks
+    (uint8), the torch restatement of repack.q4_128_groups: scale =
+    f16(amax/7), q = clip(rne(w * f32(7/amax)) + 8, 0, 15), all-zero group ->
+    scale 0 and q = 8."""
+    import torch
+
+    rows, cols = w.shape
+    G = cols // 128
+    g = w.reshape(rows * G, 128).float()
+    amax = g.abs().amax(dim=1)
+    tiny = amax < 1e-12
+    safe = torch.where(tiny, torch.ones_like(amax), amax).double()
+    inv32 = (7.0 / safe).float()
+    q = torch.clamp(torch.round(g * inv32[:, None]) + 8.0, 0, 15).to(torch.uint8)
+    q[tiny] = 8
+    scale = torch.where(tiny, torch.zeros_like(safe), safe / 7.0).half()
+    nib = (q[:, 0::2] | (q[:, 1::2] << 4))
+    blocks = torch.empty((rows * G, 66), dtype=torch.uint8, device=w.device)
+    blocks[:, 0:2] = scale.view(torch.int16).reshape(-1, 1).view(torch.uint8)
+    blocks[:, 2:] = nib
+    return blocks.reshape(-1)

@@ -1,0 +1,253 @@
+// Row-major block-quantized Q4 GEMV for gfx950, shared by two layouts:
+//
+//   preq    20-byte block per (row, 32-group): fp16 s | fp16 z | 16 B nibbles
+//           (asdsl/quantization/repack_q4_32.py:1-7); activation groups of 32.
+//   Q4_128  66-byte block per (row, 128-group): fp16 s | 64 B nibbles, zero 8
+//           (asdsl/quantization/repack_q4_128.py:1-6); activation groups of 128.
+//
+// In both, a row is a sequence of 16-byte "units" (32 nibbles = 32 consecutive
+// K elements), unit t covering K elements [32t, 32t+32): preq has one unit per
+// block, Q4_128 four.  Lane j of the LPR lanes serving a row owns units
+// j, j+LPR, ..., j+(NU-1)*LPR, so the lanes of a row read LPR consecutive units
+// (LPR*20 contiguous bytes for preq, 4-block runs with 2-byte header gaps for
+// Q4_128) and a lane's K positions are the same for every row: its activation
+// units are read from LDS into registers once per workgroup.  A 66-byte block
+// is 2-byte aligned only; gfx950 global loads are unaligned-capable, so a unit
+// is one dwordx4 either way.
+//
+// Math per unit, fp32 after an exact int32 dot (D = sum q*xq, X = sum xq):
+//   acc += D*(s*xs) - (z*s)*(X*xs)
+// with z the block's zero-point (preq) or 8 (Q4_128): the reference's
+// per-group terms (gemv_q4_preq_restored.cpp:318-336; gemv_q4_128.cpp:174-217)
+// split per 32-element unit.  y is overwritten.
+//
+// Launch: workgroups of WAVES waves, each wave serving 64/LPR rows at a time;
+// LPR in {16, 32, 64} is the smallest with NU <= 6 units per lane, doubled
+// while fewer than CUs/2 workgroups would run.  Rows of more than 6*64 units
+// (K > 12288) are walked in passes of 4 units per lane.
+#pragma once
+
+#include "abi_util.hpp"
+#include "device_common.hpp"
+
+namespace asdsl {
+
+enum class RowLayout { kPreq, kQ4_128 };
+
+template <RowLayout L>
+struct RowFmt;
+
+template <>
+struct RowFmt<RowLayout::kPreq> {
+    static constexpr int kBlockBytes = 20;
+    static constexpr int kUnitsPerBlock = 1;
+    static constexpr int kHeaderBytes = 4;
+    static constexpr int kActGroup = 32;
+};
+
+template <>
+struct RowFmt<RowLayout::kQ4_128> {
+    static constexpr int kBlockBytes = 66;
+    static constexpr int kUnitsPerBlock = 4;
+    static constexpr int kHeaderBytes = 2;
+    static constexpr int kActGroup = 128;
+};
+
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+
+template <RowLayout L, int NU, int WAVES, int NCH, bool Q8, bool EXACT, bool MULTI>
+__global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_t* __restrict__ blocks,
+                                                                   const float* __restrict__ x,
+                                                                   const int8_t* __restrict__ xq8,
+                                                                   const float* __restrict__ xsc,
+                                                                   float* __restrict__ y, int M, int K,
+                                                                   int llpr) {
+    using F = RowFmt<L>;
+    constexpr int GSX = F::kActGroup;
+    constexpr int UPG = GSX / 32;  // units per activation group
+    extern __shared__ __align__(16) uint32_t lds[];
+    const XImage im = x_image(lds, K, GSX);
+
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const int lpr = 1 << llpr;
+    const int j = lane & (lpr - 1);
+    const int rin = lane >> llpr;
+    const int rpw = kWave >> llpr;         // rows per wave pass
+    const int rpt = rpw * WAVES;           // rows per tile
+    const int U = K >> 5;                  // units per row
+    const size_t row_bytes = static_cast<size_t>(U / F::kUnitsPerBlock) * F::kBlockBytes;
+    const int ntiles = (M + rpt - 1) / rpt;
+    // MULTI: rows longer than NU*LPR units are walked in passes, with the
+    // activation read from LDS per unit; otherwise one pass, activation in
+    // registers.
+    const int per_pass = NU << llpr;
+    const int npass = MULTI ? (U + per_pass - 1) / per_pass : 1;
+
+    int tu[NU];
+    bool valid[NU];
+    auto set_units = [&](int pass) {
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int t = pass * per_pass + j + i * lpr;
+            valid[i] = EXACT || t < U;
+            tu[i] = EXACT ? t : min(t, U - 1);
+        }
+    };
+    set_units(0);
+
+    uint4 w[NU];
+    uint32_t hd[NU];
+    // Unconditional loads at clamped, in-bounds rows; rows >= M are never stored.
+    auto load_units = [&](int tile) {
+        const int row = min(tile * rpt + wave * rpw + rin, M - 1);
+        const uint8_t* rb = blocks + static_cast<size_t>(row) * row_bytes;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int t = tu[i];
+            const uint8_t* bp = rb + static_cast<size_t>(t / F::kUnitsPerBlock) * F::kBlockBytes;
+            const u32x4_a2 v = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4_a2*>(bp + F::kHeaderBytes + 16 * (t % F::kUnitsPerBlock)));
+            w[i] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int t = tu[i];
+            const uint8_t* bp = rb + static_cast<size_t>(t / F::kUnitsPerBlock) * F::kBlockBytes;
+            if (L == RowLayout::kPreq) hd[i] = *reinterpret_cast<const uint32_t*>(bp);
+            else hd[i] = *reinterpret_cast<const uint16_t*>(bp);
+        }
+    };
+
+    int tile = static_cast<int>(blockIdx.x);
+    const int tile_step = static_cast<int>(gridDim.x);
+    ActStage<GSX, WAVES * kWave, NCH, Q8> act;
+    act.load(x, xq8, xsc, K);  // activation loads first: they retire first
+    load_units(tile);          // grid <= ntiles, so this tile exists
+    act.process(K, im);
+    __syncthreads();
+
+    auto read_x = [&](int t, uint32_t (&dst)[8], float& sc, float& us) {
+        const uint4 a = reinterpret_cast<const uint4*>(im.xq + t * 8)[0];
+        const uint4 b = reinterpret_cast<const uint4*>(im.xq + t * 8)[1];
+        dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
+        dst[4] = b.x; dst[5] = b.y; dst[6] = b.z; dst[7] = b.w;
+        sc = im.scale[t / UPG];
+        us = im.usum[t];
+    };
+    uint32_t xr[MULTI ? 1 : NU][8];
+    float xs[MULTI ? 1 : NU], xu[MULTI ? 1 : NU];
+    if (!MULTI) {
+#pragma unroll
+        for (int i = 0; i < NU; ++i) read_x(tu[i], xr[MULTI ? 0 : i], xs[MULTI ? 0 : i], xu[MULTI ? 0 : i]);
+    }
+    auto dots = [&](float acc) {
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            if (valid[i]) {
+                uint32_t xt[8];
+                float sc, us;
+                if (MULTI) read_x(tu[i], xt, sc, us);
+                const int ii = MULTI ? 0 : i;
+                const int d = unit_dot(w[i], MULTI ? xt : xr[ii]);
+                const float s = half_bits_to_float(hd[i]);
+                const float z = L == RowLayout::kPreq ? half_bits_to_float(hd[i] >> 16) : 8.0f;
+                acc = fmaf(static_cast<float>(d), s * (MULTI ? sc : xs[ii]), acc);
+                acc = fmaf(-(z * s), MULTI ? us : xu[ii], acc);
+            }
+        }
+        return acc;
+    };
+
+    for (; tile < ntiles; tile += tile_step) {  // uniform per workgroup
+        float acc = dots(0.0f);
+        for (int pass = 1; pass < npass; ++pass) {  // MULTI only
+            set_units(pass);
+            load_units(tile);
+            acc = dots(acc);
+        }
+        acc = group_sum<16>(acc);
+        if (lpr >= 32) acc += swz_xor16(acc);
+        if (lpr >= 64) acc += __shfl_xor(acc, 32, kWave);
+        const int row = tile * rpt + wave * rpw + rin;
+        if (tile + tile_step < ntiles) {
+            if (MULTI) set_units(0);
+            load_units(tile + tile_step);
+        }
+        if (j == 0 && row < M) y[row] = acc;
+    }
+}
+
+struct RowPlan {
+    int llpr, nu, waves, grid;
+    bool exact, multi;
+};
+
+inline RowPlan plan_rowblk(int M, int K, int cus) {
+    const int U = K / 32;
+    RowPlan p{4, 0, K > 4096 ? 16 : 8, 0, false, false};
+    auto nu_of = [&](int llpr) { return (U + (1 << llpr) - 1) >> llpr; };
+    auto tiles_of = [&](int llpr) {
+        const int rpt = (kWave >> llpr) * p.waves;
+        return (M + rpt - 1) / rpt;
+    };
+    while (p.llpr < 6 && nu_of(p.llpr) > 6) ++p.llpr;
+    while (p.llpr < 6 && tiles_of(p.llpr) < cus / 2 && U % (1 << (p.llpr + 1)) == 0) ++p.llpr;
+    p.nu = nu_of(p.llpr);
+    if (p.nu > 6) {  // rows longer than 6*64 units: passes of 4 units per lane
+        p.multi = true;
+        p.nu = 4;
+    }
+    p.exact = !p.multi && (p.nu << p.llpr) == U;
+    const int cap = cus * (32 / p.waves);  // at most 32 waves per compute unit
+    const int tiles = tiles_of(p.llpr);
+    p.grid = tiles < cap ? tiles : cap;
+    return p;
+}
+
+template <RowLayout L, int WAVES, int NCH, bool Q8, bool EXACT, bool MULTI>
+asdsl_status launch_rowblk_exact(const RowPlan& p, const uint8_t* blocks, const float* x, const int8_t* xq8,
+                                 const float* xsc, float* y, int M, int K, hipStream_t stream) {
+    const size_t lds = x_image_bytes(K, RowFmt<L>::kActGroup);
+    const dim3 block(WAVES * kWave);
+#define ASDSL_ROWBLK_NU(N)                                                                                 \
+    case N:                                                                                                \
+        return launch("rowblk_gemv_kernel", rowblk_gemv_kernel<L, N, WAVES, NCH, Q8, EXACT, MULTI>, dim3(p.grid), \
+                      block, lds, stream, blocks, x, xq8, xsc, y, M, K, p.llpr);
+    switch (p.nu) {
+        ASDSL_ROWBLK_NU(1)
+        ASDSL_ROWBLK_NU(2)
+        ASDSL_ROWBLK_NU(3)
+        ASDSL_ROWBLK_NU(4)
+        ASDSL_ROWBLK_NU(5)
+        default: ASDSL_ROWBLK_NU(6)
+    }
+#undef ASDSL_ROWBLK_NU
+}
+
+template <RowLayout L, int WAVES, int NCH, bool Q8>
+asdsl_status launch_rowblk_waves(const RowPlan& p, const uint8_t* blocks, const float* x, const int8_t* xq8,
+                                 const float* xsc, float* y, int M, int K, hipStream_t stream) {
+    if (p.multi) return launch_rowblk_exact<L, WAVES, NCH, Q8, false, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
+    if (p.exact) return launch_rowblk_exact<L, WAVES, NCH, Q8, true, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
+    return launch_rowblk_exact<L, WAVES, NCH, Q8, false, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
+}
+
+// x (fp32, quantized inside) or xq8/xsc (pre-quantized) — exactly one non-null.
+template <RowLayout L>
+asdsl_status launch_rowblk(const uint8_t* blocks, const float* x, const int8_t* xq8, const float* xsc, float* y,
+                           int M, int K, hipStream_t stream, int cus) {
+    const RowPlan p = plan_rowblk(M, K, cus);
+    if (xq8 != nullptr) {
+        if (p.waves == 8) return launch_rowblk_waves<L, 8, 1, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
+        if (K <= 8192) return launch_rowblk_waves<L, 16, 1, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
+        if (K <= 16384) return launch_rowblk_waves<L, 16, 2, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
+        return launch_rowblk_waves<L, 16, 3, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
+    }
+    if (p.waves == 8) return launch_rowblk_waves<L, 8, 1, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
+    if (K <= 8192) return launch_rowblk_waves<L, 16, 1, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
+    if (K <= 16384) return launch_rowblk_waves<L, 16, 2, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
+    return launch_rowblk_waves<L, 16, 3, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
+}
+
+}  // namespace asdsl

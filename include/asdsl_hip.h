@@ -109,6 +109,24 @@ asdsl_status asdsl_gemv_preq2(const uint8_t* meta, const uint8_t* quant,
                               int out_features, int in_features, int group_size,
                               asdsl_stream_t stream);
 
+/* ------------------------------------------------------------------ A6 ---
+ * Q4_128 symmetric GEMV: 66-byte blocks per (row, 128-group), fp16 scale,
+ * implicit zero 8; activation pre-quantized per 128 (x_scales has
+ * in_features/128 entries).  blocks must be 2-byte aligned.
+ * Replaces gemv_q4_128_preq_avx2 (asdsl/kernels/native/gemv_q4_128.cpp:94-257;
+ *   pybind asdsl/kernels/native/gemv_q4_avx2.cpp:1461-1477).
+ * y[r] = sum_g D_g*(ws*xs) - 8*X_g*xs*ws.  group_size must be 128, y overwritten. */
+asdsl_status asdsl_gemv_q4_128_preq(const uint8_t* blocks, const int8_t* x_q8, const float* x_scales, float* y,
+                                    int out_features, int in_features, int group_size,
+                                    asdsl_stream_t stream);
+
+/* Same, quantizing the fp32 activation per 128 inside the call (the A1 rule).
+ * Replaces the engine's quantize-then-GEMV pair for the g128 lm_head
+ * (asdsl/kernels/native/unified_engine.cpp:1646-1653). */
+asdsl_status asdsl_gemv_q4_128_fused(const uint8_t* blocks, const float* x, float* y,
+                                     int out_features, int in_features, int group_size,
+                                     asdsl_stream_t stream);
+
 /* Debug dequantization of a preq2 matrix to fp32 W[M][K]: w = (q - z) * s,
  * bit-exact with the reference's dequant (experiments/phi4_cpu_run.py:3450-3467). */
 asdsl_status asdsl_dequant_preq2(const uint8_t* meta, const uint8_t* quant, float* w,
