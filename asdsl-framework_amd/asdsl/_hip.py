@@ -43,6 +43,13 @@ SIGNATURES: dict[str, list] = {
     "asdsl_dequant_preq2": [_P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_128_preq": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_128_fused": [_P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_q4_packed": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "asdsl_gemv_q4_unpacked": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_q4_gs64": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_q8_unpacked": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "asdsl_compute_bitmask": [_P, _P, _I, _F, _P],
+    "asdsl_gemv_sparse_unpacked": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_sparse_with_indices": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P],
 }
 _RESTYPE = {"asdsl_last_error": ctypes.c_char_p}
 

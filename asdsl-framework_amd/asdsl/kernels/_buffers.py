@@ -21,11 +21,36 @@ def _numel(a) -> int:
     return int(np.asarray(a).size)
 
 
+def shape_of(a) -> tuple:
+    if type(a).__module__.startswith("torch"):
+        return tuple(a.shape)
+    return tuple(np.shape(a))
+
+
+def on_device(*arrays) -> bool:
+    return any(_hip.is_device_tensor(a) for a in arrays if a is not None)
+
+
+def new_output(shape, dtype, *like):
+    """Output array for a returning wrapper: a device tensor when any input is
+    one (the call stays asynchronous on the current stream), else numpy."""
+    if on_device(*like):
+        return _hip.empty_device(shape, dtype)
+    return np.empty(shape, dtype)
+
+
 class _Slot:
     __slots__ = ("array", "dtype", "n", "name", "is_output")
 
     def __init__(self, array, dtype, n, name, is_output):
         self.array, self.dtype, self.n, self.name, self.is_output = array, np.dtype(dtype), n, name, is_output
+
+
+class _Scratch:
+    __slots__ = ("n", "dtype")
+
+    def __init__(self, n, dtype):
+        self.n, self.dtype = n, np.dtype(dtype)
 
 
 class DeviceCall:
@@ -57,9 +82,18 @@ class DeviceCall:
     def output(self, a, dtype, n: int, name: str) -> _Slot:
         return self._check(a, dtype, n, name, True)
 
+    def scratch(self, n: int, dtype) -> "_Scratch":
+        """Device-only temporary of n elements (never copied back)."""
+        return _Scratch(n, dtype)
+
     def run(self, entry: str, *args) -> None:
         keep, copyback, cargs = [], [], []
         for a in args:
+            if isinstance(a, _Scratch):
+                t = _hip.empty_device((max(a.n, 1),), a.dtype)
+                keep.append(t)
+                cargs.append(_hip.ptr(t))
+                continue
             if not isinstance(a, _Slot):
                 cargs.append(a)
                 continue

@@ -14,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 
 from asdsl import _hip
-from asdsl.kernels._buffers import DeviceCall
+from asdsl.kernels._buffers import DeviceCall, new_output, shape_of
 
 has_q4km_gemv = False  # set True once the Q4_K kernel is linked (see bottom)
 
@@ -168,6 +168,110 @@ def dequant_preq2(meta, quant, out_features: int, in_features: int, group_size: 
     pw = c.output(w, np.float32, out_features * in_features, "w")
     c.run("asdsl_dequant_preq2", pm, pq, pw, out_features, in_features, group_size)
     return w
+
+
+# ------------------------------------------------------------ fp32 affine
+def _numel(a) -> int:
+    n = 1
+    for d in shape_of(a):
+        n *= d
+    return n
+
+
+def _validate_gemv_args(w, x, scales, biases, M: int, K: int, group_size: int, expected_w: int) -> int:
+    """validate_gemv_args (gemv_q4_avx2.cpp:901-929) + assert_x_gemv_layout
+    (1065-1082): same checks, same messages; returns the batch size."""
+    if M <= 0 or K <= 0 or group_size <= 0:
+        raise ValueError("M, K, group_size must be positive")
+    xs = shape_of(x)
+    if len(xs) == 1:
+        batch = 1
+        if xs[0] != K:
+            raise ValueError("x length must equal K")
+    elif len(xs) == 2:
+        batch = xs[0]
+        if xs[1] != K:
+            raise ValueError("x shape must be (batch, K) matching arguments")
+    else:
+        raise ValueError("x must be 1-D (K,) or 2-D (batch, K)")
+    if batch < 1:
+        raise ValueError("batch must be >= 1")
+    if K % 2 != 0:
+        raise ValueError("K must be even for 4-bit packing")
+    if K % group_size != 0:
+        raise ValueError("K must be divisible by group_size")
+    if group_size % 8 != 0:
+        raise ValueError("group_size must be a multiple of 8 for AVX2 vectorization")
+    if _numel(w) != expected_w:
+        raise ValueError("weight buffer size mismatch")
+    groups = M * (K // group_size)
+    if _numel(scales) != groups:
+        raise ValueError("scales size mismatch")
+    if biases is not None and _numel(biases) != groups:
+        raise ValueError("biases size mismatch")
+    return batch
+
+
+def gemv_q4_packed(w_packed, x, scales, biases, M: int, K: int, group_size: int):
+    """Reference: gemv_q4_packed (gemv_q4_avx2.cpp:665-749, pybind 1084-1126).
+    x (K,) -> y (M,); x (B, K) -> y (B, M)."""
+    batch = _validate_gemv_args(w_packed, x, scales, biases, M, K, group_size, M * K // 2)
+    if group_size % 16 != 0:
+        raise ValueError("group_size must be a multiple of 16 for packed weights")
+    y = new_output((M,) if len(shape_of(x)) == 1 else (batch, M), np.float32, w_packed, x)
+    c = DeviceCall("gemv_q4_packed")
+    c.run("asdsl_gemv_q4_packed", c.input(w_packed, np.uint8, M * K // 2, "w_packed"),
+          c.input(x, np.float32, batch * K, "x"), c.input(scales, np.float32, M * (K // group_size), "scales"),
+          c.input(biases, np.float32, M * (K // group_size), "biases"), c.output(y, np.float32, batch * M, "y"),
+          M, K, group_size, batch)
+    return y
+
+
+def gemv_q4_unpacked(w, x, scales, biases, M: int, K: int, group_size: int):
+    """Reference: gemv_q4_unpacked (gemv_q4_avx2.cpp:755-806, pybind 1128-1160);
+    one byte per value, used as is."""
+    _validate_gemv_args(w, x, scales, biases, M, K, group_size, M * K)
+    if len(shape_of(x)) != 1:
+        raise ValueError("x size must equal batch * K")
+    y = new_output((M,), np.float32, w, x)
+    c = DeviceCall("gemv_q4_unpacked")
+    c.run("asdsl_gemv_q4_unpacked", c.input(w, np.uint8, M * K, "w"), c.input(x, np.float32, K, "x"),
+          c.input(scales, np.float32, M * (K // group_size), "scales"),
+          c.input(biases, np.float32, M * (K // group_size), "biases"), c.output(y, np.float32, M, "y"),
+          M, K, group_size)
+    return y
+
+
+def gemv_q4_avx2_gs64(w_packed, x, scales, rows: int, cols: int):
+    """Reference: gemv_q4_avx2_gs64 (gemv_q4_avx2.cpp:1211-1268 -> gemv_q4_kernel.cpp:96-122)."""
+    if cols <= 0 or rows <= 0 or cols % 64 != 0 or cols % 2 != 0:
+        raise ValueError("cols must be positive, even, and divisible by 64")
+    if _numel(w_packed) != rows * (cols // 2):
+        raise ValueError("w_packed size must be rows * (cols/2)")
+    if _numel(scales) != rows * (cols // 64):
+        raise ValueError("scales length must be rows * (cols/64)")
+    xs = shape_of(x)
+    batch = 1 if len(xs) == 1 else xs[0]
+    if len(xs) not in (1, 2) or xs[-1] != cols or _numel(x) != batch * cols:
+        raise ValueError("x size must equal batch * cols")
+    y = new_output((rows,) if len(xs) == 1 else (batch, rows), np.float32, w_packed, x)
+    c = DeviceCall("gemv_q4_avx2_gs64")
+    c.run("asdsl_gemv_q4_gs64", c.input(w_packed, np.uint8, rows * cols // 2, "w_packed"),
+          c.input(x, np.float32, batch * cols, "x"), c.input(scales, np.float32, rows * (cols // 64), "scales"),
+          c.output(y, np.float32, batch * rows, "y"), rows, cols, batch)
+    return y
+
+
+has_openmp = False
+
+
+def get_num_threads() -> int:
+    """The reference reports its CPU thread count; here the GPU's compute units."""
+    return _hip.cu_count()
+
+
+def set_num_threads(n: int) -> None:
+    """No-op, as in the reference's own binding (gemv_q4_avx2.cpp:1496-1497)."""
 
 
 def check_avx2() -> bool:

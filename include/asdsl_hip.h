@@ -127,6 +127,64 @@ asdsl_status asdsl_gemv_q4_128_fused(const uint8_t* blocks, const float* x, floa
                                      int out_features, int in_features, int group_size,
                                      asdsl_stream_t stream);
 
+/* ------------------------------------------------------------- A10 / A9(i) ---
+ * fp32-affine GEMVs, activation not quantized:
+ *   y[r] = sum_g scales[r,g] * (sum_{k in g} q[r,k] * x[k]) + biases[r,g] * (sum_{k in g} x[k])
+ * Weights row-major; x and weights 16-byte aligned; K <= 32768.
+ * Argument rules and messages follow validate_gemv_args
+ *   (asdsl/kernels/native/gemv_q4_avx2.cpp:901-929). */
+
+/* 4-bit, 2 nibbles per byte (low = even column); x is [batch][K], y [batch][M].
+ * Replaces gemv_q4_packed (gemv_q4_avx2.cpp:665-749, pybind 1084-1126).
+ * group_size must be a multiple of 16. */
+asdsl_status asdsl_gemv_q4_packed(const uint8_t* w_packed, const float* x, const float* scales,
+                                  const float* biases, float* y, int M, int K, int group_size, int batch,
+                                  asdsl_stream_t stream);
+
+/* One byte per value, used as is.  Replaces gemv_q4_unpacked
+ * (gemv_q4_avx2.cpp:755-806, pybind 1128-1160). */
+asdsl_status asdsl_gemv_q4_unpacked(const uint8_t* w, const float* x, const float* scales,
+                                    const float* biases, float* y, int M, int K, int group_size,
+                                    asdsl_stream_t stream);
+
+/* 4-bit packed, scales only, group 64; x [batch][cols], y [batch][rows].
+ * Replaces gemv_q4_avx2 / gemv_q4_avx2_gs64 (asdsl/kernels/native/gemv_q4_kernel.cpp:96-122;
+ * pybind gemv_q4_avx2.cpp:1211-1268). */
+asdsl_status asdsl_gemv_q4_gs64(const uint8_t* w_packed, const float* x, const float* scales, float* y,
+                                int rows, int cols, int batch, asdsl_stream_t stream);
+
+/* uint8 weights (one per byte), fp32 scale and bias per group.
+ * Replaces fused_dequant_gemv / gemv_q8_unpacked
+ * (asdsl/kernels/native/gemv_q8_avx2.cpp:67-144, pybind 159-215); the
+ * reference's cache_tiling flag changes loop blocking only and has no
+ * counterpart here. */
+asdsl_status asdsl_gemv_q8_unpacked(const uint8_t* w, const float* x, const float* scales,
+                                    const float* biases, float* y, int M, int K, int group_size,
+                                    asdsl_stream_t stream);
+
+/* --------------------------------------------------------------- A12(ii) ---
+ * Bit k of bitmask[(K+31)/32] set iff |x[k]| >= threshold (NaN: clear).
+ * Replaces compute_bitmask (asdsl/kernels/native/gemv_sparse_avx2.cpp:144-179). */
+asdsl_status asdsl_compute_bitmask(const float* x, uint32_t* bitmask, int K, float threshold,
+                                   asdsl_stream_t stream);
+
+/* Activation-sparse GEMV over uint8 weights: only columns whose bit is set
+ * count (in both sums).  32-column runs with a zero mask word skip their
+ * weight loads.  Replaces gemv_sparse_unpacked
+ * (asdsl/kernels/native/gemv_sparse_avx2.cpp:66-139, bitmask path). */
+asdsl_status asdsl_gemv_sparse_unpacked(const uint8_t* w, const float* x, const float* scales,
+                                        const float* biases, const uint32_t* bitmask, float* y, int M, int K,
+                                        int group_size, asdsl_stream_t stream);
+
+/* Same over an explicit list of active columns (a column listed c times counts
+ * c times; indices outside [0, K) are ignored).  work_mask[(K+31)/32] and
+ * work_x[K] (16-byte aligned) are caller-provided device scratch, overwritten.
+ * Replaces gemv_sparse_with_indices (gemv_sparse_avx2.cpp:66-110, index path). */
+asdsl_status asdsl_gemv_sparse_with_indices(const uint8_t* w, const float* x, const float* scales,
+                                            const float* biases, const int32_t* active_indices, int n_active,
+                                            float* y, int M, int K, int group_size, uint32_t* work_mask,
+                                            float* work_x, asdsl_stream_t stream);
+
 /* Debug dequantization of a preq2 matrix to fp32 W[M][K]: w = (q - z) * s,
  * bit-exact with the reference's dequant (experiments/phi4_cpu_run.py:3450-3467). */
 asdsl_status asdsl_dequant_preq2(const uint8_t* meta, const uint8_t* quant, float* w,
