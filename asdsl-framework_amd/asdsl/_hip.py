@@ -43,6 +43,8 @@ SIGNATURES: dict[str, list] = {
     "asdsl_dequant_preq2": [_P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_128_preq": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_128_fused": [_P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_q4_q8": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_q4km_q8": [_P, _P, _P, _I, _I, _P],
     "asdsl_gemv_q4_packed": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "asdsl_gemv_q4_unpacked": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_gs64": [_P, _P, _P, _P, _I, _I, _I, _P],

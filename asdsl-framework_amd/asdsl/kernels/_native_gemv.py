@@ -16,7 +16,7 @@ import numpy as np
 from asdsl import _hip
 from asdsl.kernels._buffers import DeviceCall, new_output, shape_of
 
-has_q4km_gemv = False  # set True once the Q4_K kernel is linked (see bottom)
+has_q4km_gemv = True
 
 
 def _preq2_quant_bytes(M: int, K: int, gs: int) -> int:
@@ -260,6 +260,36 @@ def gemv_q4_avx2_gs64(w_packed, x, scales, rows: int, cols: int):
           c.input(x, np.float32, batch * cols, "x"), c.input(scales, np.float32, rows * (cols // 64), "scales"),
           c.output(y, np.float32, batch * rows, "y"), rows, cols, batch)
     return y
+
+
+def gemv_q4_q8_avx2(weights_packed, scales, x, y, out_features: int, in_features: int,
+                    group_size: int = 32) -> None:
+    """Reference: gemv_q4_q8_avx2 (gemv_q4_avx2.cpp:131-253): symmetric packed Q4
+    with fp32 scales, x quantized per group inside; y is an out-parameter."""
+    fn = "gemv_q4_q8_avx2"
+    _check_gs(group_size, (32, 64, 128), fn)
+    _check_dims(out_features, in_features, group_size, fn)
+    G = in_features // group_size
+    c = DeviceCall(fn)
+    c.run("asdsl_gemv_q4_q8", c.input(weights_packed, np.uint8, out_features * in_features // 2, "weights_packed"),
+          c.input(scales, np.float32, out_features * G, "scales"), c.input(x, np.float32, in_features, "x"),
+          c.output(y, np.float32, out_features, "y"), out_features, in_features, group_size)
+
+
+def gemv_q4km_q8_avx2(weights_q4km, x, y, out_features: int, in_features: int) -> None:
+    """Reference: gemv_q4km_q8_avx2 (gemv_q4_avx2.cpp:283-420, pybind 1318-1348)."""
+    fn = "gemv_q4km_q8_avx2"
+    if in_features <= 0 or out_features <= 0 or in_features % 256:
+        raise ValueError("in_features must be divisible by 256 for Q4_K_M")
+    expected = out_features * (in_features // 256) * 144
+    if _numel(weights_q4km) != expected:
+        raise ValueError("Q4_K_M weight size mismatch")
+    if _numel(x) != in_features or _numel(y) != out_features:
+        raise ValueError("x/y size mismatch for out_features/in_features")
+    c = DeviceCall(fn)
+    c.run("asdsl_gemv_q4km_q8", c.input(weights_q4km, np.uint8, expected, "weights_q4km"),
+          c.input(x, np.float32, in_features, "x"), c.output(y, np.float32, out_features, "y"),
+          out_features, in_features)
 
 
 has_openmp = False

@@ -154,13 +154,19 @@ inline size_t x_image_bytes(int K, int gs) {
     return static_cast<size_t>(K) + static_cast<size_t>(K / gs) * 4 + static_cast<size_t>(K / 32) * 4;
 }
 
-// Activation quantizer of the reference (quantize_activation_avx2,
-// asdsl/kernels/native/gemv_q4_preq_restored.cpp:505-549) as built with
-// -O3 -ffast-math (setup.py:56-65): the compiler turns amax/127.0f into
-// amax*(1/127.0f); 127.0f/amax stays a true division; cvtps_epi32 rounds
-// half to even; packs saturate.  One thread owns one 8-element chunk; the GS/8
-// threads of a group are consecutive, aligned lanes of one wave.
-template <int GS>
+// Activation quantization rules of the reference.
+//  kRne: quantize_activation_avx2 (asdsl/kernels/native/gemv_q4_preq_restored.cpp:505-549)
+//    as built with -O3 -ffast-math (setup.py:56-65): amax/127.0f becomes
+//    amax*(1/127.0f); 127.0f/amax stays a true division; cvtps_epi32 rounds half
+//    to even; packs saturate to [-128, 127]; amax < 1e-9 -> q = 0, scale 1.
+//  kRoundAway: the Q4_K path (asdsl/kernels/native/gemv_q4_avx2.cpp:377-400):
+//    std::round (half away from zero), clamp to [-127, 127]; amax < 1e-12 ->
+//    q = 0, scale 0.
+enum class QRule { kRne, kRoundAway };
+
+// One thread owns one 8-element chunk; the GS/8 threads of a group are
+// consecutive, aligned lanes of one wave.
+template <int GS, QRule R = QRule::kRne>
 __device__ __forceinline__ void quantize_chunk(const float (&v)[8], int chunk, bool active, XImage im,
                                                int8_t* __restrict__ xq_nat, float* __restrict__ xscale_out) {
     constexpr int kLanes = GS / 8;
@@ -170,15 +176,22 @@ __device__ __forceinline__ void quantize_chunk(const float (&v)[8], int chunk, b
     const float amax = group_max<kLanes>(m);
     int q[8];
     float scale;
-    if (amax < 1e-9f) {
+    if (amax < (R == QRule::kRne ? 1e-9f : 1e-12f)) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) q[i] = 0;
-        scale = 1.0f;
+        scale = R == QRule::kRne ? 1.0f : 0.0f;
     } else {
         scale = amax * (1.0f / 127.0f);
         const float inv = 127.0f / amax;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = sat_rne_i8(v[i] * inv);
+        for (int i = 0; i < 8; ++i) {
+            if (R == QRule::kRne) {
+                q[i] = sat_rne_i8(v[i] * inv);
+            } else {
+                int r = static_cast<int>(__builtin_roundf(v[i] * inv));
+                q[i] = r > 127 ? 127 : (r < -127 ? -127 : r);
+            }
+        }
     }
     const uint32_t even = pack4_i8(q[0], q[2], q[4], q[6]);
     const uint32_t odd = pack4_i8(q[1], q[3], q[5], q[7]);
@@ -219,7 +232,7 @@ __device__ __forceinline__ void load_q8_chunk(uint2 n, float scale, int chunk, b
 //   ActStage::process() quantizes them into the LDS image (no global loads)
 // One workgroup of NT threads covers K <= 8*NT*NCH; lanes past the end form
 // whole groups of their own and never store.
-template <int GS, int NT, int NCH, bool Q8>
+template <int GS, int NT, int NCH, bool Q8, QRule R = QRule::kRne>
 struct ActStage {
     float v[Q8 ? 1 : NCH][8];
     uint2 n[Q8 ? NCH : 1];
@@ -251,7 +264,7 @@ struct ActStage {
         for (int i = 0; i < NCH; ++i) {
             const int c = i * NT + tid;
             if constexpr (Q8) load_q8_chunk<GS>(n[i], s[i], c, c < nchunk, im);
-            else quantize_chunk<GS>(v[i], c, c < nchunk, im, nullptr, nullptr);
+            else quantize_chunk<GS, R>(v[i], c, c < nchunk, im, nullptr, nullptr);
         }
     }
 };

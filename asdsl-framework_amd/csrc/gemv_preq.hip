@@ -49,7 +49,7 @@ extern "C" asdsl_status asdsl_gemv_q4_32_preq(const uint8_t* blocks, const int8_
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CHECK_ARG(x_scales != nullptr, "gemv_q4_32_preq: null input pointer");
     ASDSL_CU_COUNT(cus);
-    return launch_rowblk<RowLayout::kPreq>(blocks, nullptr, x_q8, x_scales, y, out_features, in_features,
+    return launch_rowblk<RowLayout::kPreq, 32, true>(blocks, nullptr, nullptr, x_q8, x_scales, y, out_features, in_features,
                                            as_hip(stream), cus);
 }
 
@@ -59,6 +59,6 @@ extern "C" asdsl_status asdsl_gemv_q4_32_preq_fused(const uint8_t* blocks, const
     if (check_preq_args(blocks, x, y, out_features, in_features, group_size, "gemv_q4_32_preq_fused"))
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CU_COUNT(cus);
-    return launch_rowblk<RowLayout::kPreq>(blocks, x, nullptr, nullptr, y, out_features, in_features,
+    return launch_rowblk<RowLayout::kPreq, 32, false>(blocks, nullptr, x, nullptr, nullptr, y, out_features, in_features,
                                            as_hip(stream), cus);
 }

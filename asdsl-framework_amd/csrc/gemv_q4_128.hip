@@ -49,7 +49,7 @@ extern "C" asdsl_status asdsl_gemv_q4_128_preq(const uint8_t* blocks, const int8
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CHECK_ARG(x_scales != nullptr, "gemv_q4_128_preq_avx2: null pointer");
     ASDSL_CU_COUNT(cus);
-    return launch_rowblk<RowLayout::kQ4_128>(blocks, nullptr, x_q8, x_scales, y, out_features, in_features,
+    return launch_rowblk<RowLayout::kQ4_128, 128, true>(blocks, nullptr, nullptr, x_q8, x_scales, y, out_features, in_features,
                                              as_hip(stream), cus);
 }
 
@@ -58,6 +58,6 @@ extern "C" asdsl_status asdsl_gemv_q4_128_fused(const uint8_t* blocks, const flo
     if (check_q4_128_args(blocks, x, y, out_features, in_features, group_size, "gemv_q4_128_fused"))
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CU_COUNT(cus);
-    return launch_rowblk<RowLayout::kQ4_128>(blocks, x, nullptr, nullptr, y, out_features, in_features,
+    return launch_rowblk<RowLayout::kQ4_128, 128, false>(blocks, nullptr, x, nullptr, nullptr, y, out_features, in_features,
                                              as_hip(stream), cus);
 }

@@ -1,13 +1,20 @@
-// Row-major block-quantized Q4 GEMV for gfx950, shared by two layouts:
+// Row-major block-quantized Q4 GEMV for gfx950, shared by four layouts:
 //
 //   preq    20-byte block per (row, 32-group): fp16 s | fp16 z | 16 B nibbles
 //           (asdsl/quantization/repack_q4_32.py:1-7); activation groups of 32.
 //   Q4_128  66-byte block per (row, 128-group): fp16 s | 64 B nibbles, zero 8
 //           (asdsl/quantization/repack_q4_128.py:1-6); activation groups of 128.
+//   packed  K/2 nibble bytes per row, fp32 scale per (row, group) in a side
+//           array, zero 8 (gemv_q4_q8_avx2, asdsl/kernels/native/gemv_q4_avx2.cpp:131-253);
+//           activation groups of group_size (32, 64 or 128).
+//   Q4_K    144-byte superblock per (row, 256): fp16 d | fp16 dmin | 12 B of
+//           6-bit scales (0-7) and mins (8-15), LSB-first | 8 x 16 B nibbles
+//           (gemv_q4km_q8_avx2, gemv_q4_avx2.cpp:110-120,283-420); activation
+//           groups of 32 under the round-half-away rule.
 //
-// In both, a row is a sequence of 16-byte "units" (32 nibbles = 32 consecutive
-// K elements), unit t covering K elements [32t, 32t+32): preq has one unit per
-// block, Q4_128 four.  Lane j of the LPR lanes serving a row owns units
+// In all, a row is a sequence of 16-byte "units" (32 nibbles = 32 consecutive
+// K elements), unit t covering K elements [32t, 32t+32): preq and packed have
+// one unit per block, Q4_128 four, Q4_K eight.  Lane j of the LPR lanes serving a row owns units
 // j, j+LPR, ..., j+(NU-1)*LPR, so the lanes of a row read LPR consecutive units
 // (LPR*20 contiguous bytes for preq, 4-block runs with 2-byte header gaps for
 // Q4_128) and a lane's K positions are the same for every row: its activation
@@ -17,9 +24,11 @@
 //
 // Math per unit, fp32 after an exact int32 dot (D = sum q*xq, X = sum xq):
 //   acc += D*(s*xs) - (z*s)*(X*xs)
-// with z the block's zero-point (preq) or 8 (Q4_128): the reference's
-// per-group terms (gemv_q4_preq_restored.cpp:318-336; gemv_q4_128.cpp:174-217)
-// split per 32-element unit.  y is overwritten.
+// with z the block's zero-point (preq) or 8 (Q4_128, packed): the reference's
+// per-group terms (gemv_q4_preq_restored.cpp:318-336; gemv_q4_128.cpp:174-217;
+// gemv_q4_avx2.cpp:225-248) split per 32-element unit; for Q4_K
+//   acc += (d*sc*D - dmin*m*X) * xs          (gemv_q4_avx2.cpp:316)
+// y is overwritten.
 //
 // Launch: workgroups of WAVES waves, each wave serving 64/LPR rows at a time;
 // LPR in {16, 32, 64} is the smallest with NU <= 6 units per lane, doubled
@@ -27,44 +36,65 @@
 // (K > 12288) are walked in passes of 4 units per lane.
 #pragma once
 
+#include <type_traits>
+
 #include "abi_util.hpp"
 #include "device_common.hpp"
 
 namespace asdsl {
 
-enum class RowLayout { kPreq, kQ4_128 };
+enum class RowLayout { kPreq, kQ4_128, kPacked, kQ4K };
 
+// kBlockBytes: bytes per block; kUnitsPerBlock: 16-byte units per block;
+// kDataOffset: offset of the first unit in a block.
 template <RowLayout L>
 struct RowFmt;
 
 template <>
 struct RowFmt<RowLayout::kPreq> {
-    static constexpr int kBlockBytes = 20;
-    static constexpr int kUnitsPerBlock = 1;
-    static constexpr int kHeaderBytes = 4;
-    static constexpr int kActGroup = 32;
+    static constexpr int kBlockBytes = 20, kUnitsPerBlock = 1, kDataOffset = 4;
 };
 
 template <>
 struct RowFmt<RowLayout::kQ4_128> {
-    static constexpr int kBlockBytes = 66;
-    static constexpr int kUnitsPerBlock = 4;
-    static constexpr int kHeaderBytes = 2;
-    static constexpr int kActGroup = 128;
+    static constexpr int kBlockBytes = 66, kUnitsPerBlock = 4, kDataOffset = 2;
 };
+
+template <>
+struct RowFmt<RowLayout::kPacked> {
+    static constexpr int kBlockBytes = 16, kUnitsPerBlock = 1, kDataOffset = 0;
+};
+
+template <>
+struct RowFmt<RowLayout::kQ4K> {
+    static constexpr int kBlockBytes = 144, kUnitsPerBlock = 8, kDataOffset = 16;
+};
+
+// 6-bit field idx of the Q4_K scale bitstream held in 3 dwords (12 bytes,
+// LSB-first), as get_6bit_packed reads it (gemv_q4_avx2.cpp:110-120).
+__device__ __forceinline__ uint32_t q4k_field(uint32_t b0, uint32_t b1, uint32_t b2, int idx) {
+    const uint64_t lo = static_cast<uint64_t>(b0) | (static_cast<uint64_t>(b1) << 32);
+    const int bit = idx * 6;
+    if (bit + 6 <= 64) return static_cast<uint32_t>(lo >> bit) & 0x3Fu;
+    if (bit >= 64) return (b2 >> (bit - 64)) & 0x3Fu;
+    return static_cast<uint32_t>((lo >> bit) | (static_cast<uint64_t>(b2) << (64 - bit))) & 0x3Fu;
+}
 
 typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
 
-template <RowLayout L, int NU, int WAVES, int NCH, bool Q8, bool EXACT, bool MULTI>
+// side: per-(row, group) fp32 scales for kPacked, unused otherwise.
+template <RowLayout L, int GSX, int NU, int WAVES, int NCH, bool Q8, bool EXACT, bool MULTI>
 __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_t* __restrict__ blocks,
+                                                                   const float* __restrict__ side,
                                                                    const float* __restrict__ x,
                                                                    const int8_t* __restrict__ xq8,
                                                                    const float* __restrict__ xsc,
                                                                    float* __restrict__ y, int M, int K,
                                                                    int llpr) {
     using F = RowFmt<L>;
-    constexpr int GSX = F::kActGroup;
+    using Hd = typename std::conditional<L == RowLayout::kQ4K, uint4, uint32_t>::type;
     constexpr int UPG = GSX / 32;  // units per activation group
+    constexpr QRule kRule = L == RowLayout::kQ4K ? QRule::kRoundAway : QRule::kRne;
     extern __shared__ __align__(16) uint32_t lds[];
     const XImage im = x_image(lds, K, GSX);
 
@@ -76,6 +106,7 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
     const int rpw = kWave >> llpr;         // rows per wave pass
     const int rpt = rpw * WAVES;           // rows per tile
     const int U = K >> 5;                  // units per row
+    const int G = K / GSX;                 // activation (and kPacked scale) groups per row
     const size_t row_bytes = static_cast<size_t>(U / F::kUnitsPerBlock) * F::kBlockBytes;
     const int ntiles = (M + rpt - 1) / rpt;
     // MULTI: rows longer than NU*LPR units are walked in passes, with the
@@ -97,7 +128,7 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
     set_units(0);
 
     uint4 w[NU];
-    uint32_t hd[NU];
+    Hd hd[NU];
     // Unconditional loads at clamped, in-bounds rows; rows >= M are never stored.
     auto load_units = [&](int tile) {
         const int row = min(tile * rpt + wave * rpw + rin, M - 1);
@@ -107,21 +138,24 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
             const int t = tu[i];
             const uint8_t* bp = rb + static_cast<size_t>(t / F::kUnitsPerBlock) * F::kBlockBytes;
             const u32x4_a2 v = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4_a2*>(bp + F::kHeaderBytes + 16 * (t % F::kUnitsPerBlock)));
+                reinterpret_cast<const u32x4_a2*>(bp + F::kDataOffset + 16 * (t % F::kUnitsPerBlock)));
             w[i] = make_uint4(v.x, v.y, v.z, v.w);
         }
 #pragma unroll
         for (int i = 0; i < NU; ++i) {
             const int t = tu[i];
             const uint8_t* bp = rb + static_cast<size_t>(t / F::kUnitsPerBlock) * F::kBlockBytes;
-            if (L == RowLayout::kPreq) hd[i] = *reinterpret_cast<const uint32_t*>(bp);
-            else hd[i] = *reinterpret_cast<const uint16_t*>(bp);
+            if constexpr (L == RowLayout::kPreq) hd[i] = *reinterpret_cast<const uint32_t*>(bp);
+            else if constexpr (L == RowLayout::kQ4_128) hd[i] = *reinterpret_cast<const uint16_t*>(bp);
+            else if constexpr (L == RowLayout::kPacked)
+                hd[i] = __float_as_uint(side[static_cast<size_t>(row) * G + t / UPG]);
+            else hd[i] = *reinterpret_cast<const uint4*>(bp);
         }
     };
 
     int tile = static_cast<int>(blockIdx.x);
     const int tile_step = static_cast<int>(gridDim.x);
-    ActStage<GSX, WAVES * kWave, NCH, Q8> act;
+    ActStage<GSX, WAVES * kWave, NCH, Q8, kRule> act;
     act.load(x, xq8, xsc, K);  // activation loads first: they retire first
     load_units(tile);          // grid <= ntiles, so this tile exists
     act.process(K, im);
@@ -149,11 +183,24 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
                 float sc, us;
                 if (MULTI) read_x(tu[i], xt, sc, us);
                 const int ii = MULTI ? 0 : i;
-                const int d = unit_dot(w[i], MULTI ? xt : xr[ii]);
-                const float s = half_bits_to_float(hd[i]);
-                const float z = L == RowLayout::kPreq ? half_bits_to_float(hd[i] >> 16) : 8.0f;
-                acc = fmaf(static_cast<float>(d), s * (MULTI ? sc : xs[ii]), acc);
-                acc = fmaf(-(z * s), MULTI ? us : xu[ii], acc);
+                const uint32_t(&xv)[8] = MULTI ? xt : xr[ii];
+                const float xsv = MULTI ? sc : xs[ii];
+                const int d = unit_dot(w[i], xv);
+                if constexpr (L == RowLayout::kQ4K) {
+                    const uint4 h = hd[i];
+                    const int sb = tu[i] % 8;
+                    const float sub_scale = half_bits_to_float(h.x) * static_cast<float>(q4k_field(h.y, h.z, h.w, sb));
+                    const float sub_min = half_bits_to_float(h.x >> 16) * static_cast<float>(q4k_field(h.y, h.z, h.w, sb + 8));
+                    int xsum = 0;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) xsum = __builtin_amdgcn_sdot4(static_cast<int>(xv[k]), 0x01010101, xsum, false);
+                    acc = fmaf(sub_scale * static_cast<float>(d) - sub_min * static_cast<float>(xsum), xsv, acc);
+                } else {
+                    const float s = L == RowLayout::kPacked ? __uint_as_float(hd[i]) : half_bits_to_float(hd[i]);
+                    const float z = L == RowLayout::kPreq ? half_bits_to_float(hd[i] >> 16) : 8.0f;
+                    acc = fmaf(static_cast<float>(d), s * xsv, acc);
+                    acc = fmaf(-(z * s), MULTI ? us : xu[ii], acc);
+                }
             }
         }
         return acc;
@@ -205,15 +252,15 @@ inline RowPlan plan_rowblk(int M, int K, int cus) {
     return p;
 }
 
-template <RowLayout L, int WAVES, int NCH, bool Q8, bool EXACT, bool MULTI>
-asdsl_status launch_rowblk_exact(const RowPlan& p, const uint8_t* blocks, const float* x, const int8_t* xq8,
-                                 const float* xsc, float* y, int M, int K, hipStream_t stream) {
-    const size_t lds = x_image_bytes(K, RowFmt<L>::kActGroup);
+template <RowLayout L, int GSX, int WAVES, int NCH, bool Q8, bool EXACT, bool MULTI>
+asdsl_status launch_rowblk_exact(const RowPlan& p, const uint8_t* blocks, const float* side, const float* x,
+                                 const int8_t* xq8, const float* xsc, float* y, int M, int K, hipStream_t stream) {
+    const size_t lds = x_image_bytes(K, GSX);
     const dim3 block(WAVES * kWave);
-#define ASDSL_ROWBLK_NU(N)                                                                                 \
-    case N:                                                                                                \
-        return launch("rowblk_gemv_kernel", rowblk_gemv_kernel<L, N, WAVES, NCH, Q8, EXACT, MULTI>, dim3(p.grid), \
-                      block, lds, stream, blocks, x, xq8, xsc, y, M, K, p.llpr);
+#define ASDSL_ROWBLK_NU(N)                                                                                  \
+    case N:                                                                                                 \
+        return launch("rowblk_gemv_kernel", rowblk_gemv_kernel<L, GSX, N, WAVES, NCH, Q8, EXACT, MULTI>,    \
+                      dim3(p.grid), block, lds, stream, blocks, side, x, xq8, xsc, y, M, K, p.llpr);
     switch (p.nu) {
         ASDSL_ROWBLK_NU(1)
         ASDSL_ROWBLK_NU(2)
@@ -225,29 +272,25 @@ asdsl_status launch_rowblk_exact(const RowPlan& p, const uint8_t* blocks, const 
 #undef ASDSL_ROWBLK_NU
 }
 
-template <RowLayout L, int WAVES, int NCH, bool Q8>
-asdsl_status launch_rowblk_waves(const RowPlan& p, const uint8_t* blocks, const float* x, const int8_t* xq8,
-                                 const float* xsc, float* y, int M, int K, hipStream_t stream) {
-    if (p.multi) return launch_rowblk_exact<L, WAVES, NCH, Q8, false, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
-    if (p.exact) return launch_rowblk_exact<L, WAVES, NCH, Q8, true, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
-    return launch_rowblk_exact<L, WAVES, NCH, Q8, false, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
+template <RowLayout L, int GSX, int WAVES, int NCH, bool Q8>
+asdsl_status launch_rowblk_waves(const RowPlan& p, const uint8_t* blocks, const float* side, const float* x,
+                                 const int8_t* xq8, const float* xsc, float* y, int M, int K, hipStream_t stream) {
+    if (p.multi)
+        return launch_rowblk_exact<L, GSX, WAVES, NCH, Q8, false, true>(p, blocks, side, x, xq8, xsc, y, M, K, stream);
+    if (p.exact)
+        return launch_rowblk_exact<L, GSX, WAVES, NCH, Q8, true, false>(p, blocks, side, x, xq8, xsc, y, M, K, stream);
+    return launch_rowblk_exact<L, GSX, WAVES, NCH, Q8, false, false>(p, blocks, side, x, xq8, xsc, y, M, K, stream);
 }
 
-// x (fp32, quantized inside) or xq8/xsc (pre-quantized) — exactly one non-null.
-template <RowLayout L>
-asdsl_status launch_rowblk(const uint8_t* blocks, const float* x, const int8_t* xq8, const float* xsc, float* y,
-                           int M, int K, hipStream_t stream, int cus) {
+// x (fp32, quantized inside) or xq8/xsc (pre-quantized, when Q8) — one of them.
+template <RowLayout L, int GSX, bool Q8>
+asdsl_status launch_rowblk(const uint8_t* blocks, const float* side, const float* x, const int8_t* xq8,
+                           const float* xsc, float* y, int M, int K, hipStream_t stream, int cus) {
     const RowPlan p = plan_rowblk(M, K, cus);
-    if (xq8 != nullptr) {
-        if (p.waves == 8) return launch_rowblk_waves<L, 8, 1, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
-        if (K <= 8192) return launch_rowblk_waves<L, 16, 1, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
-        if (K <= 16384) return launch_rowblk_waves<L, 16, 2, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
-        return launch_rowblk_waves<L, 16, 3, true>(p, blocks, x, xq8, xsc, y, M, K, stream);
-    }
-    if (p.waves == 8) return launch_rowblk_waves<L, 8, 1, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
-    if (K <= 8192) return launch_rowblk_waves<L, 16, 1, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
-    if (K <= 16384) return launch_rowblk_waves<L, 16, 2, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
-    return launch_rowblk_waves<L, 16, 3, false>(p, blocks, x, xq8, xsc, y, M, K, stream);
+    if (p.waves == 8) return launch_rowblk_waves<L, GSX, 8, 1, Q8>(p, blocks, side, x, xq8, xsc, y, M, K, stream);
+    if (K <= 8192) return launch_rowblk_waves<L, GSX, 16, 1, Q8>(p, blocks, side, x, xq8, xsc, y, M, K, stream);
+    if (K <= 16384) return launch_rowblk_waves<L, GSX, 16, 2, Q8>(p, blocks, side, x, xq8, xsc, y, M, K, stream);
+    return launch_rowblk_waves<L, GSX, 16, 3, Q8>(p, blocks, side, x, xq8, xsc, y, M, K, stream);
 }
 
 }  // namespace asdsl

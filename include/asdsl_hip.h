@@ -127,6 +127,27 @@ asdsl_status asdsl_gemv_q4_128_fused(const uint8_t* blocks, const float* x, floa
                                      int out_features, int in_features, int group_size,
                                      asdsl_stream_t stream);
 
+/* ---------------------------------------------------------------- A9(ii) ---
+ * Symmetric packed Q4 (nibbles row-major, K/2 bytes per row, low = even
+ * column, zero 8) with fp32 scales[M][K/group_size]; x quantized per
+ * group_size inside the call (the A1 rule).  y[r] = sum_g D'(q-8, xq)*ws*xs.
+ * group_size in {32, 64, 128}; weights 16-byte aligned.
+ * Replaces gemv_q4_q8_avx2 (asdsl/kernels/native/gemv_q4_avx2.cpp:131-253;
+ * pybind 1301-1316; reached from gemv_q4_packed(use_q8=True), asdsl/kernels/gemv_q4.py:269-273). */
+asdsl_status asdsl_gemv_q4_q8(const uint8_t* weights_packed, const float* scales, const float* x, float* y,
+                              int out_features, int in_features, int group_size, asdsl_stream_t stream);
+
+/* ------------------------------------------------------------------- A8 ---
+ * Q4_K (ASDSL variant) GEMV: 144-byte superblock per (row, 256): fp16 d |
+ * fp16 dmin | 12 bytes of 6-bit fields (0-7 scales, 8-15 mins; LSB-first
+ * bitstream) | 8 x 16 bytes of nibbles.  x quantized per 32 inside the call
+ * with round-half-away, clamp +-127, amax < 1e-12 -> scale 0.
+ * y[r] = sum_sb (d*sc*D - dmin*m*X) * xs.  in_features % 256 == 0.
+ * Replaces gemv_q4km_q8_avx2 (asdsl/kernels/native/gemv_q4_avx2.cpp:283-420;
+ * pybind 1318-1348). */
+asdsl_status asdsl_gemv_q4km_q8(const uint8_t* weights_q4km, const float* x, float* y, int out_features,
+                                int in_features, asdsl_stream_t stream);
+
 /* ------------------------------------------------------------- A10 / A9(i) ---
  * fp32-affine GEMVs, activation not quantized:
  *   y[r] = sum_g scales[r,g] * (sum_{k in g} q[r,k] * x[k]) + biases[r,g] * (sum_{k in g} x[k])
