@@ -39,6 +39,7 @@ SIGNATURES: dict[str, list] = {
     "asdsl_gemv_q4_32_preq": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_32_preq_fused": [_P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_preq2_fused": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_preq2_fused_batch": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "asdsl_gemv_preq2": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_dequant_preq2": [_P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_128_preq": [_P, _P, _P, _P, _I, _I, _I, _P],

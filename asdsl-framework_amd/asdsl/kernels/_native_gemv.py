@@ -94,17 +94,27 @@ def gemv_q4_32_preq_8row_avx2(blocks, x_fp32, y, out_features: int, in_features:
 def gemv_preq2_fused_avx2(meta, quant, x_fp32, y, out_features: int, in_features: int,
                           group_size: int = 32) -> None:
     """Reference: gemv_preq2_fused_avx2 (gemv_preq2_avx2.cpp:301-319).
-    group_size=128 selects the asymmetric preq2-g128 layout (no reference counterpart)."""
+    group_size=128 selects the asymmetric preq2-g128 layout (no reference counterpart).
+    A 2-D x_fp32 of shape (N, K) with y of shape (N, M) runs the batched
+    verification kernel: every row of x is quantized on its own, so y[n]
+    equals the 1-D call on x[n]."""
     fn = "gemv_preq2_fused_avx2"
     _check_gs(group_size, (32, 128), fn)
     _check_dims(out_features, in_features, group_size, fn)
     G = in_features // group_size
+    xs = shape_of(x_fp32)
+    n_cols = xs[0] if len(xs) == 2 else 1
+    if len(xs) == 2 and xs[1] != in_features:
+        raise ValueError(f"{fn}: x_fp32 must be (N, in_features)")
     c = DeviceCall(fn)
     pm = c.input(meta, np.uint8, out_features * G * 4, "meta")
     pq = c.input(quant, np.uint8, _preq2_quant_bytes(out_features, in_features, group_size), "quant")
-    px = c.input(x_fp32, np.float32, in_features, "x_fp32")
-    py = c.output(y, np.float32, out_features, "y")
-    c.run("asdsl_gemv_preq2_fused", pm, pq, px, py, out_features, in_features, group_size)
+    px = c.input(x_fp32, np.float32, n_cols * in_features, "x_fp32")
+    py = c.output(y, np.float32, n_cols * out_features, "y")
+    if len(xs) == 2:
+        c.run("asdsl_gemv_preq2_fused_batch", pm, pq, px, py, out_features, in_features, group_size, n_cols)
+    else:
+        c.run("asdsl_gemv_preq2_fused", pm, pq, px, py, out_features, in_features, group_size)
 
 
 def gemv_preq2_avx2(meta, quant, x_q8, x_scales, y, out_features: int, in_features: int,

@@ -150,7 +150,7 @@ __device__ __forceinline__ XImage x_image(uint32_t* lds, int K, int gs) {
     return im;
 }
 
-inline size_t x_image_bytes(int K, int gs) {
+__host__ __device__ inline size_t x_image_bytes(int K, int gs) {
     return static_cast<size_t>(K) + static_cast<size_t>(K / gs) * 4 + static_cast<size_t>(K / 32) * 4;
 }
 

@@ -101,6 +101,18 @@ asdsl_status asdsl_gemv_preq2_fused(const uint8_t* meta, const uint8_t* quant,
                                     int out_features, int in_features, int group_size,
                                     asdsl_stream_t stream);
 
+/* Batched preq2 GEMV for speculative verification: X[n_cols][in_features]
+ * (16-byte aligned) -> Y[n_cols][out_features]; every column quantized
+ * independently, so Y[n] equals asdsl_gemv_preq2_fused on X[n] up to fp32
+ * summation order.  Each weight byte is read once per launch of up to 16
+ * columns (8 when in_features > 4096).  n_cols in [1, 64].
+ * No reference counterpart: the reference engine verifies preq2 drafts with
+ * serial forward_token calls (asdsl/kernels/native/unified_engine.cpp:1768-1789);
+ * this is the batched kernel its forward_verify_batch would call. */
+asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X, float* Y,
+                                          int out_features, int in_features, int group_size, int n_cols,
+                                          asdsl_stream_t stream);
+
 /* preq2 GEMV on a pre-quantized activation.
  * Replaces gemv_preq2_avx2 (asdsl/kernels/native/gemv_preq2_avx2.cpp:321-337).
  * group_size as for asdsl_gemv_preq2_fused; x_scales has in_features/group_size entries. */

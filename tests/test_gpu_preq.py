@@ -165,3 +165,29 @@ def test_lm_head_preq2_g128_full_size(gpu):
     torch.cuda.synchronize()
     want = oracle.gemv_preq2_fused(meta.cpu().numpy(), quant.cpu().numpy(), x, M, K, 128)
     assert rel_l2(y.cpu().numpy(), want) < TOL
+
+
+@pytest.mark.parametrize("gs", [32, 128])
+@pytest.mark.parametrize("M,K,N", [(16384, 3072, 2), (16384, 3072, 16), (3072, 8192, 4), (3072, 8192, 16),
+                                   (70, 512, 3), (129, 3072, 8), (257, 5120, 17), (33, 640, 5)])
+def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
+    """Batched verification GEMV: column n == gemv_preq2_fused(x_n) (each column
+    quantized on its own), against the oracle per column."""
+    if K % gs:
+        pytest.skip("K not a multiple of the group size")
+    import torch
+    from asdsl.kernels import _native_gemv as ng
+
+    g = torch.Generator(device="cuda").manual_seed(M + K + N)
+    w = torch.randn((M, K), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    meta, quant = syn.preq2_from_weights_torch(w, gs)
+    del w
+    X = syn.activation(K, N, batch=N)
+    X[0, :gs] = 0.0  # an all-zero group in one column only
+    Y = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    ng.gemv_preq2_fused_avx2(meta, quant, torch.from_numpy(X).cuda(), Y, M, K, gs)
+    torch.cuda.synchronize()
+    Yh = Y.cpu().numpy()
+    mh, qh = meta.cpu().numpy(), quant.cpu().numpy()
+    for n in range(N):
+        assert rel_l2(Yh[n], oracle.gemv_preq2_fused(mh, qh, X[n], M, K, gs)) < TOL, f"column {n}"
