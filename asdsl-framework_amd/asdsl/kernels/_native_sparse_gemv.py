@@ -10,7 +10,10 @@ from __future__ import annotations
 
 import numpy as np
 
+from asdsl import _hip
 from asdsl.kernels._buffers import DeviceCall, new_output, shape_of
+
+has_openmp = False
 
 
 def _numel(a) -> int:
@@ -72,4 +75,30 @@ def gemv_sparse_with_indices(w, x, scales, biases, active_indices, M: int, K: in
           c.input(active_indices if n else np.zeros(1, np.int32), np.int32, max(n, 1), "active_indices"), n,
           c.output(y, np.float32, M, "y"), M, K, group_size,
           c.scratch((K + 31) // 32, np.uint32), c.scratch(K, np.float32))
+    return y
+
+
+def sparse_down_proj_T(w_T_packed, scales_T, biases_T, sparse_x, active_rows, in_dim: int, out_dim: int,
+                       group_size: int):
+    """gemv_sparse_avx2.cpp:273-418: y[out_dim] = sum over listed rows r with
+    x[r] != 0 of x[r] * dequant(w_T[r, :]), per element fma(q, s*x, b*x)."""
+    if in_dim <= 0 or out_dim <= 0 or group_size <= 0:
+        raise ValueError("in_dim, out_dim, group_size must be positive")
+    if out_dim % group_size != 0:
+        raise ValueError("out_dim must be divisible by group_size")
+    G = out_dim // group_size
+    for a, n, name in ((w_T_packed, in_dim * out_dim // 2, "w_T_packed"), (scales_T, in_dim * G, "scales_T"),
+                       (biases_T, in_dim * G, "biases_T"), (sparse_x, in_dim, "sparse_x")):
+        if _numel(a) < n:
+            raise ValueError(f"sparse_down_proj_T: {name} is too small for in_dim={in_dim}, out_dim={out_dim}")
+    n = _numel(active_rows)
+    y = new_output((out_dim,), np.float32, w_T_packed, sparse_x)
+    work_bytes = int(_hip.LIB.asdsl_sparse_down_proj_T_workspace_bytes(n, out_dim))
+    c = DeviceCall("sparse_down_proj_T")
+    c.run("asdsl_sparse_down_proj_T", c.input(w_T_packed, np.uint8, in_dim * out_dim // 2, "w_T_packed"),
+          c.input(scales_T, np.float32, in_dim * G, "scales_T"), c.input(biases_T, np.float32, in_dim * G, "biases_T"),
+          c.input(sparse_x, np.float32, in_dim, "sparse_x"),
+          c.input(active_rows if n else np.zeros(1, np.int32), np.int32, max(n, 1), "active_rows"), n,
+          c.output(y, np.float32, out_dim, "y"), in_dim, out_dim, group_size,
+          c.scratch(work_bytes // 4, np.float32), work_bytes)
     return y

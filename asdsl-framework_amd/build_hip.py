@@ -51,15 +51,28 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile all HIP sources and link lib/libasdsl_hip.so; returns its path."""
+def _stale(src: Path, headers: list[Path]) -> bool:
+    obj = BUILD / (src.stem + ".o")
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    return src.stat().st_mtime > t or any(h.stat().st_mtime > t for h in headers)
+
+
+def build(verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile all HIP sources and link lib/libasdsl_hip.so; returns its path.
+    incremental=True recompiles only sources newer than their objects (or any
+    header); the default rebuilds everything."""
     BUILD.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), sources))
+    headers = sorted(CSRC.glob("*.hpp")) + sorted((REPO_ROOT / "include").glob("*.h"))
+    todo = [s for s in sources if not incremental or _stale(s, headers)]
+    with cf.ThreadPoolExecutor(max_workers=min(8, max(1, len(todo)))) as ex:
+        list(ex.map(lambda s: _compile(s, verbose), todo))
+    objs = [BUILD / (s.stem + ".o") for s in sources]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
@@ -72,4 +85,4 @@ def build(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, incremental="-i" in sys.argv))

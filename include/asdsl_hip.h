@@ -23,6 +23,7 @@
 #ifndef ASDSL_HIP_H
 #define ASDSL_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -217,6 +218,24 @@ asdsl_status asdsl_gemv_sparse_with_indices(const uint8_t* w, const float* x, co
                                             const float* biases, const int32_t* active_indices, int n_active,
                                             float* y, int M, int K, int group_size, uint32_t* work_mask,
                                             float* work_x, asdsl_stream_t stream);
+
+/* ---------------------------------------------------------------- A12(i) ---
+ * FATReLU-sparse down-projection over K-major packed Q4:
+ * w_T[in_dim][out_dim/2] (low nibble = even output), scales_T/biases_T
+ * [in_dim][out_dim/group_size] fp32.  For every listed row r with
+ * 0 <= r < in_dim and sparse_x[r] != 0:
+ *     y[o] += fma(q[r][o], scales_T[r][o/gs]*x[r], biases_T[r][o/gs]*x[r])
+ * y[out_dim] is overwritten (starts from zero).  A row listed twice adds twice.
+ * out_dim % 32 == 0, group_size % 8 == 0, w_T 16-byte aligned.
+ * work: caller-provided device scratch of at least
+ * asdsl_sparse_down_proj_T_workspace_bytes(n_active, out_dim) bytes.
+ * Replaces sparse_down_proj_T (asdsl/kernels/native/gemv_sparse_avx2.cpp:273-418),
+ * called from experiments/phi4_cpu_run.py:3949-3967. */
+size_t asdsl_sparse_down_proj_T_workspace_bytes(int n_active, int out_dim);
+asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, const float* scales_T, const float* biases_T,
+                                      const float* sparse_x, const int32_t* active_rows, int n_active, float* y,
+                                      int in_dim, int out_dim, int group_size, float* work, size_t work_bytes,
+                                      asdsl_stream_t stream);
 
 /* Debug dequantization of a preq2 matrix to fp32 W[M][K]: w = (q - z) * s,
  * bit-exact with the reference's dequant (experiments/phi4_cpu_run.py:3450-3467). */
