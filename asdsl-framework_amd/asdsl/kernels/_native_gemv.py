@@ -302,6 +302,47 @@ def gemv_q4km_q8_avx2(weights_q4km, x, y, out_features: int, in_features: int) -
           out_features, in_features)
 
 
+def matmul_batch_q4(w_packed, scales, biases, X_batch, Y_batch, M: int, K: int, B: int, group_size: int = 32) -> None:
+    """Reference: matmul_batch_q4 (gemv_q4_avx2.cpp:950-1059): Y_batch (B, M) out-parameter,
+    overwritten.  B <= 64 (beyond it the reference overruns its accumulators)."""
+    xs, ys = shape_of(X_batch), shape_of(Y_batch)
+    if len(xs) != 2 or xs[0] != B or xs[1] != K:
+        raise ValueError("X_batch must be shape (B, K)")
+    if len(ys) != 2 or ys[0] != B or ys[1] != M:
+        raise ValueError("Y_batch must be shape (B, M), caller zero-init")
+    if _numel(w_packed) != M * (K // 2):
+        raise ValueError("w_packed size must equal M * K/2")
+    if group_size <= 0 or K % group_size or _numel(scales) != M * (K // group_size):
+        raise ValueError("scales size must equal M * n_groups")
+    if _numel(biases) != M * (K // group_size):
+        raise ValueError("biases size must equal M * n_groups")
+    if B < 1 or B > 64:
+        raise ValueError("B must be in [1, 64]")
+    G = K // group_size
+    c = DeviceCall("matmul_batch_q4")
+    c.run("asdsl_matmul_batch_q4", c.input(w_packed, np.uint8, M * K // 2, "w_packed"),
+          c.input(scales, np.float32, M * G, "scales"), c.input(biases, np.float32, M * G, "biases"),
+          c.input(X_batch, np.float32, B * K, "X_batch"), c.output(Y_batch, np.float32, B * M, "Y_batch"),
+          M, K, B, group_size)
+
+
+def gemm_q4_128_q8_avx2(blocks, x_batch, y_batch, out_features: int, in_features: int, group_size: int,
+                        batch_size: int) -> None:
+    """Reference: gemm_q4_128_q8_avx2 (gemv_q4_128.cpp:262-306), the engine's
+    batched g128 GEMM: fp32 x (not quantized), y_batch (B, M) overwritten."""
+    fn = "gemm_q4_128_q8_avx2"
+    _check_gs(group_size, (128,), fn)
+    _check_dims(out_features, in_features, group_size, fn)
+    if batch_size < 1 or batch_size > 64:
+        raise ValueError(f"{fn}: batch_size must be in [1, 64]")
+    G = in_features // 128
+    c = DeviceCall(fn)
+    c.run("asdsl_gemm_q4_128", c.input(blocks, np.uint8, out_features * G * 66, "blocks"),
+          c.input(x_batch, np.float32, batch_size * in_features, "x_batch"),
+          c.output(y_batch, np.float32, batch_size * out_features, "y_batch"),
+          out_features, in_features, group_size, batch_size)
+
+
 has_openmp = False
 
 

@@ -93,7 +93,12 @@ __device__ __forceinline__ float unit_dot_f32(const uint4 (&w)[BITS / 4], const 
     return d;
 }
 
-template <int BITS, bool BIAS, bool MASKED, int NU, int WAVES>
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+
+// Q128: weights are Q4_128 66-byte blocks (fp16 scale | 64 B nibbles, zero 8)
+// instead of packed nibbles with side scale/bias arrays: per unit
+// acc += ws * (dot - 8 * sum_x) (gemm_q4_128_q8_avx2's w = (q - 8) * ws).
+template <int BITS, bool BIAS, bool MASKED, int NU, int WAVES, bool Q128 = false>
 __global__ __launch_bounds__(WAVES * kWave) void affine_gemv_kernel(const uint8_t* __restrict__ w,
                                                                    const float* __restrict__ x,
                                                                    const float* __restrict__ scales,
@@ -116,7 +121,7 @@ __global__ __launch_bounds__(WAVES * kWave) void affine_gemv_kernel(const uint8_
     const int U = K >> 5;
     const int G = K / gs;
     const int upg = gs >> 5;  // units per group
-    const size_t row_bytes = static_cast<size_t>(U) * UB;
+    const size_t row_bytes = Q128 ? static_cast<size_t>(U / 4) * 66 : static_cast<size_t>(U) * UB;
     const int ntiles = (M + rpt - 1) / rpt;
     const int per_pass = NU << llpr;
     const int npass = (U + per_pass - 1) / per_pass;
@@ -127,7 +132,7 @@ __global__ __launch_bounds__(WAVES * kWave) void affine_gemv_kernel(const uint8_
     for (int tile = static_cast<int>(blockIdx.x); tile < ntiles; tile += static_cast<int>(gridDim.x)) {
         const int row = min(tile * rpt + wave * rpw + rin, M - 1);
         const uint8_t* rb = w + static_cast<size_t>(row) * row_bytes;
-        const float* srow = scales + static_cast<size_t>(row) * G;
+        const float* srow = Q128 ? nullptr : scales + static_cast<size_t>(row) * G;
         const float* brow = BIAS ? biases + static_cast<size_t>(row) * G : nullptr;
         float acc = 0.0f;
         for (int pass = 0; pass < npass; ++pass) {
@@ -138,19 +143,31 @@ __global__ __launch_bounds__(WAVES * kWave) void affine_gemv_kernel(const uint8_
                 const int t = pass * per_pass + j + i * lpr;
                 live[i] = t < U && (!MASKED || mask[t] != 0u);
                 if (live[i]) {
+                    if (Q128) {
+                        const u32x4_a2 v = __builtin_nontemporal_load(
+                            reinterpret_cast<const u32x4_a2*>(rb + static_cast<size_t>(t / 4) * 66 + 2 + 16 * (t % 4)));
+                        wu[i][0] = make_uint4(v.x, v.y, v.z, v.w);
+                    } else {
 #pragma unroll
-                    for (int h = 0; h < BITS / 4; ++h)
-                        wu[i][h] = load_stream16(reinterpret_cast<const uint4*>(rb + static_cast<size_t>(t) * UB) + h);
+                        for (int h = 0; h < BITS / 4; ++h)
+                            wu[i][h] = load_stream16(reinterpret_cast<const uint4*>(rb + static_cast<size_t>(t) * UB) + h);
+                    }
                 }
             }
 #pragma unroll
             for (int i = 0; i < NU; ++i) {
                 const int t = pass * per_pass + j + i * lpr;
                 if (live[i]) {
-                    const int g = t / upg;
                     const float d = unit_dot_f32<BITS>(wu[i], xs + t * 32);
-                    acc = fmaf(srow[g], d, acc);
-                    if (BIAS) acc = fmaf(brow[g], usum[t], acc);
+                    if (Q128) {
+                        const float ws = half_bits_to_float(*reinterpret_cast<const uint16_t*>(rb + static_cast<size_t>(t / 4) * 66));
+                        acc = fmaf(ws, d, acc);
+                        acc = fmaf(-8.0f * ws, usum[t], acc);
+                    } else {
+                        const int g = t / upg;
+                        acc = fmaf(srow[g], d, acc);
+                        if (BIAS) acc = fmaf(brow[g], usum[t], acc);
+                    }
                 }
             }
         }
@@ -266,10 +283,10 @@ AffinePlan plan_affine(int M, int K, int cus) {
     return p;
 }
 
-template <int BITS, bool BIAS, bool MASKED>
+template <int BITS, bool BIAS, bool MASKED, bool Q128 = false>
 asdsl_status launch_affine(const uint8_t* w, const float* x, const float* s, const float* b, const uint32_t* mask,
                            float* y, int M, int K, int gs, hipStream_t stream, int cus) {
-    if (gs % 32 != 0 || K % 32 != 0) {
+    if (!Q128 && (gs % 32 != 0 || K % 32 != 0)) {
         const int grid = stream_grid(M, kThreads / kWave, 8, cus);
         return launch("affine_gemv_generic", affine_gemv_generic<BITS, BIAS, MASKED>, dim3(grid), dim3(kThreads), 0,
                       stream, w, x, s, b, mask, y, M, K, gs);
@@ -280,7 +297,7 @@ asdsl_status launch_affine(const uint8_t* w, const float* x, const float* s, con
     switch (p.nu) {
 #define ASDSL_AFFINE_NU(N)                                                                                    \
     case N:                                                                                                   \
-        return launch("affine_gemv_kernel", affine_gemv_kernel<BITS, BIAS, MASKED, N, W>, dim3(p.grid),       \
+        return launch("affine_gemv_kernel", affine_gemv_kernel<BITS, BIAS, MASKED, N, W, Q128>, dim3(p.grid), \
                       dim3(W * kWave), lds, stream, w, x, s, b, mask, y, M, K, gs, p.llpr);
         ASDSL_AFFINE_NU(1)
         ASDSL_AFFINE_NU(2)
@@ -429,4 +446,41 @@ extern "C" asdsl_status asdsl_gemv_sparse_with_indices(const uint8_t* w, const f
     }
     // work_x holds c_k*x_k on listed columns and 0 elsewhere; work_mask marks them
     return launch_affine<8, true, true>(w, work_x, scales, biases, work_mask, y, M, K, group_size, s, cus);
+}
+
+extern "C" asdsl_status asdsl_matmul_batch_q4(const uint8_t* w_packed, const float* scales, const float* biases,
+                                              const float* X, float* Y, int M, int K, int B, int group_size,
+                                              asdsl_stream_t stream) {
+    if (check_affine(w_packed, X, scales, Y, M, K, group_size, B, "matmul_batch_q4")) return ASDSL_ERR_INVALID_ARGUMENT;
+    ASDSL_CHECK_ARG(biases != nullptr, "matmul_batch_q4: null pointer");
+    ASDSL_CHECK_ARG(B <= 64, "matmul_batch_q4: B must be <= 64 (the reference's accumulator limit)");
+    ASDSL_CHECK_ARG(group_size % 16 == 0, "matmul_batch_q4: group_size must be a multiple of 16");
+    ASDSL_CU_COUNT(cus);
+    for (int bi = 0; bi < B; ++bi) {
+        const asdsl_status st = launch_affine<4, true, false>(w_packed, X + static_cast<size_t>(bi) * K, scales, biases,
+                                                              nullptr, Y + static_cast<size_t>(bi) * M, M, K,
+                                                              group_size, as_hip(stream), cus);
+        if (st != ASDSL_OK) return st;
+    }
+    return ASDSL_OK;
+}
+
+extern "C" asdsl_status asdsl_gemm_q4_128(const uint8_t* blocks, const float* X, float* Y, int out_features,
+                                          int in_features, int group_size, int batch_size, asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(blocks && X && Y, "gemm_q4_128_q8_avx2: null pointer");
+    ASDSL_CHECK_ARG(group_size == 128, "gemm_q4_128_q8_avx2: group_size must be 128");
+    ASDSL_CHECK_ARG(out_features > 0 && in_features > 0 && in_features % 128 == 0,
+                    "gemm_q4_128_q8_avx2: in_features must be a positive multiple of 128");
+    ASDSL_CHECK_ARG(in_features <= kMaxAffineK, "gemm_q4_128_q8_avx2: in_features too large");
+    ASDSL_CHECK_ARG(batch_size >= 1 && batch_size <= 64, "gemm_q4_128_q8_avx2: batch_size must be in [1, 64]");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(blocks) % 2 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0,
+                    "gemm_q4_128_q8_avx2: blocks must be 2-byte and X 16-byte aligned");
+    ASDSL_CU_COUNT(cus);
+    for (int bi = 0; bi < batch_size; ++bi) {
+        const asdsl_status st = launch_affine<4, false, false, true>(
+            blocks, X + static_cast<size_t>(bi) * in_features, nullptr, nullptr, nullptr,
+            Y + static_cast<size_t>(bi) * out_features, out_features, in_features, 128, as_hip(stream), cus);
+        if (st != ASDSL_OK) return st;
+    }
+    return ASDSL_OK;
 }

@@ -187,6 +187,21 @@ asdsl_status asdsl_gemv_q4_unpacked(const uint8_t* w, const float* x, const floa
 asdsl_status asdsl_gemv_q4_gs64(const uint8_t* w_packed, const float* x, const float* scales, float* y,
                                 int rows, int cols, int batch, asdsl_stream_t stream);
 
+/* ------------------------------------------------------------------ A11 ---
+ * Batched fp32 Q4 GEMM over packed weights: Y[b][r] = sum_k dequant(W[r,k]) X[b][k]
+ * with dequant = q*s + b per group; X [B][K], Y [B][M] overwritten, B <= 64.
+ * Replaces matmul_batch_q4 (asdsl/kernels/native/gemv_q4_avx2.cpp:950-1059). */
+asdsl_status asdsl_matmul_batch_q4(const uint8_t* w_packed, const float* scales, const float* biases,
+                                   const float* X, float* Y, int M, int K, int B, int group_size,
+                                   asdsl_stream_t stream);
+
+/* Batched Q4_128 GEMM with an fp32 activation, not quantized:
+ * Y[b][r] = sum_g ws * sum_k (q-8) X[b][k]; X [B][K], Y [B][M], B <= 64.
+ * Replaces gemm_q4_128_q8_avx2 (asdsl/kernels/native/gemv_q4_128.cpp:262-306),
+ * the engine's forward_batch GEMM under g128 (unified_engine.cpp:1153-1158). */
+asdsl_status asdsl_gemm_q4_128(const uint8_t* blocks, const float* X, float* Y, int out_features,
+                               int in_features, int group_size, int batch_size, asdsl_stream_t stream);
+
 /* uint8 weights (one per byte), fp32 scale and bias per group.
  * Replaces fused_dequant_gemv / gemv_q8_unpacked
  * (asdsl/kernels/native/gemv_q8_avx2.cpp:67-144, pybind 159-215); the

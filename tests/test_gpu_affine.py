@@ -184,3 +184,44 @@ def test_device_tensors_stay_on_device(gpu):
     y = ng.gemv_q4_packed(*dev, M, K, gs)
     assert isinstance(y, torch.Tensor) and y.is_cuda
     assert rel_l2(y.cpu().numpy(), oracle.gemv_affine(w, x, s, b, M, K, gs)) < TOL
+
+
+def test_golden_matmul_batch(gpu, golden):
+    from asdsl.kernels import _native_gemv as ng
+
+    g = golden
+    M, K = map(int, g["aff_shape"])
+    Y = np.zeros((3, M), np.float32)
+    ng.matmul_batch_q4(g["aff_wp"], g["aff_s32"], g["aff_b32"], g["aff_X"], Y, M, K, 3, 32)
+    assert rel_l2(Y, g["aff_Y_batch"]) < TOL
+
+
+@pytest.mark.parametrize("M,K,B,gs", [(16384, 3072, 4, 32), (3072, 8192, 16, 32), (33, 1024, 64, 64), (5, 96, 2, 16)])
+def test_matmul_batch_vs_oracle(gpu, M, K, B, gs):
+    from asdsl.kernels import _native_gemv as ng
+
+    w, s, b, _ = _rand(M, K, gs, M + B)
+    X = np.random.default_rng(B).standard_normal((B, K)).astype(np.float32)
+    Y = np.full((B, M), np.nan, np.float32)
+    ng.matmul_batch_q4(w, s, b, X, Y, M, K, B, gs)
+    if M * K <= 1 << 22:
+        assert rel_l2(Y, oracle.matmul_batch_q4(w, s, b, X, M, K, B, gs)) < TOL
+    else:  # batch == loop of single GEMVs against the oracle, two rows checked
+        for i in (0, B - 1):
+            assert rel_l2(Y[i], oracle.gemv_affine(w, X[i], s, b, M, K, gs)) < TOL
+    with pytest.raises(ValueError, match="B must be"):
+        ng.matmul_batch_q4(w, s, b, np.zeros((65, K), np.float32), np.zeros((65, M), np.float32), M, K, 65, gs)
+
+
+@pytest.mark.parametrize("M,K,B", [(7, 256, 3), (200, 3072, 8), (64, 8192, 2)])
+def test_gemm_q4_128_vs_oracle(gpu, M, K, B):
+    from asdsl.kernels import _native_gemv as ng
+    from asdsl.quantization import synthetic as syn
+
+    w = syn.gaussian_weights(M, K, 5 + B)
+    w[1, :128] = 0.0
+    blocks = syn.q4_128_blocks(w)
+    X = np.random.default_rng(M).standard_normal((B, K)).astype(np.float32)
+    Y = np.full((B, M), np.nan, np.float32)
+    ng.gemm_q4_128_q8_avx2(blocks, X, Y, M, K, 128, B)
+    assert rel_l2(Y, oracle.gemm_q4_128(blocks, X, M, K, B)) < TOL
