@@ -54,11 +54,10 @@ SIGNATURES: dict[str, list] = {
     "asdsl_gemv_q8_unpacked": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_compute_bitmask": [_P, _P, _I, _F, _P],
     "asdsl_gemv_sparse_unpacked": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
-    "asdsl_sparse_down_proj_T_workspace_bytes": [_I, _I],
-    "asdsl_sparse_down_proj_T": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "asdsl_sparse_down_proj_T": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P],
     "asdsl_gemv_sparse_with_indices": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P],
 }
-_RESTYPE = {"asdsl_last_error": ctypes.c_char_p, "asdsl_sparse_down_proj_T_workspace_bytes": ctypes.c_size_t}
+_RESTYPE = {"asdsl_last_error": ctypes.c_char_p}
 
 
 class HipLibraryMissing(ImportError):

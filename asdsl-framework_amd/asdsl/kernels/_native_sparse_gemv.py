@@ -93,12 +93,10 @@ def sparse_down_proj_T(w_T_packed, scales_T, biases_T, sparse_x, active_rows, in
             raise ValueError(f"sparse_down_proj_T: {name} is too small for in_dim={in_dim}, out_dim={out_dim}")
     n = _numel(active_rows)
     y = new_output((out_dim,), np.float32, w_T_packed, sparse_x)
-    work_bytes = int(_hip.LIB.asdsl_sparse_down_proj_T_workspace_bytes(n, out_dim))
     c = DeviceCall("sparse_down_proj_T")
     c.run("asdsl_sparse_down_proj_T", c.input(w_T_packed, np.uint8, in_dim * out_dim // 2, "w_T_packed"),
           c.input(scales_T, np.float32, in_dim * G, "scales_T"), c.input(biases_T, np.float32, in_dim * G, "biases_T"),
           c.input(sparse_x, np.float32, in_dim, "sparse_x"),
           c.input(active_rows if n else np.zeros(1, np.int32), np.int32, max(n, 1), "active_rows"), n,
-          c.output(y, np.float32, out_dim, "y"), in_dim, out_dim, group_size,
-          c.scratch(work_bytes // 4, np.float32), work_bytes)
+          c.output(y, np.float32, out_dim, "y"), in_dim, out_dim, group_size)
     return y

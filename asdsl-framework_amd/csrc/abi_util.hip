@@ -18,6 +18,13 @@ struct DeviceShape {
 };
 std::mutex g_shape_mu;
 DeviceShape g_shape[64];
+
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+Workspace g_ws[64];
 }  // namespace
 
 void set_error(const char* fmt, ...) {
@@ -53,6 +60,43 @@ int cu_count_current() {
         g_shape[dev].cus = cus;
     }
     return g_shape[dev].cus;
+}
+
+asdsl_status device_workspace(hipStream_t stream, size_t bytes, void** out, const char* what) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("%s: no usable HIP device: %s", what, hipGetErrorString(e));
+        return ASDSL_ERR_HIP;
+    }
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace& ws = g_ws[dev];
+    if (ws.bytes < bytes) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cap);
+        if (e != hipSuccess) {
+            set_error("%s: hipStreamIsCapturing failed: %s", what, hipGetErrorString(e));
+            return ASDSL_ERR_HIP;
+        }
+        if (cap != hipStreamCaptureStatusNone) {
+            set_error("%s: needs a %zu-byte work buffer, which cannot be allocated under graph capture; "
+                      "make one call of this size before capturing", what, bytes);
+            return ASDSL_ERR_UNSUPPORTED;
+        }
+        // A smaller buffer is kept, not freed: queued work or a graph captured
+        // earlier may still use it.
+        const size_t grown = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
+        void* fresh = nullptr;
+        e = hipMalloc(&fresh, grown);
+        if (e != hipSuccess) {
+            set_error("%s: hipMalloc(%zu) for the work buffer failed: %s", what, grown, hipGetErrorString(e));
+            return ASDSL_ERR_HIP;
+        }
+        ws.ptr = fresh;
+        ws.bytes = grown;
+    }
+    *out = ws.ptr;
+    return ASDSL_OK;
 }
 
 int env_knob(const char* name) {

@@ -59,6 +59,15 @@ asdsl_status launch(const char* what, void (*kernel)(P...), dim3 grid, dim3 bloc
     return launch_status(what);
 }
 
+// Device buffer private to the library, one per device, grown on demand;
+// every buffer it hands out stays allocated until the process ends.  Calls
+// that use it and overlap on one device (different streams, no ordering
+// between them) race on it; calls ordered by a stream or by events do not.
+// Growing calls hipMalloc, which a stream under graph capture does not allow:
+// an earlier call of at least the same size sizes it first
+// (ASDSL_ERR_UNSUPPORTED otherwise).
+asdsl_status device_workspace(hipStream_t stream, size_t bytes, void** out, const char* what);
+
 // Integer tuning knob from the environment, read once (0 = unset).  Knobs
 // only change launch shapes (and with them the fp32 summation order), never
 // the formula: ASDSL_HIP_WG_PER_CU caps workgroups per compute unit,

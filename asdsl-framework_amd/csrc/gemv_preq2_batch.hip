@@ -80,41 +80,49 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_batch_kernel(const u
 
     int parity = 0;
     for (; tile < ntiles; tile += tile_step) {  // uniform per workgroup
-        float acc[NB];
-#pragma unroll
-        for (int n = 0; n < NB; ++n) acc[n] = 0.0f;
+        // Nibbles split once per unit (lo: even elements, hi: odd, the LDS
+        // split order); then column by column, units inner, with a scheduling
+        // barrier per column so the LDS reads of all columns are not hoisted
+        // at once (that spilled at 16 columns).
+        uint32_t lo[NU][4], hi[NU][4];
+        float s_[NU], zs_[NU];
 #pragma unroll
         for (int j = 0; j < NU; ++j) {
-            const int g = (c0 + j * kWave) / UPG4;
-            const int u = g * UPS + part;
-            const float s = half_bits_to_float(mt[j]);
-            const float zs = -(half_bits_to_float(mt[j] >> 16) * s);
-            uint32_t lo[4], hi[4];
             const uint32_t wv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                lo[i] = wv[i] & 0x0F0F0F0Fu;
-                hi[i] = (wv[i] >> 4) & 0x0F0F0F0Fu;
+                lo[j][i] = wv[i] & 0x0F0F0F0Fu;
+                hi[j][i] = (wv[i] >> 4) & 0x0F0F0F0Fu;
             }
+            s_[j] = half_bits_to_float(mt[j]);
+            zs_[j] = -(half_bits_to_float(mt[j] >> 16) * s_[j]);
+        }
+        float acc[NB];
 #pragma unroll
-            for (int n = 0; n < NB; ++n) {
-                if (n < ncols) {
-                    const XImage im = x_image(lds + n * img_words, K, GS);
+        for (int n = 0; n < NB; ++n) {
+            acc[n] = 0.0f;
+            if (n < ncols) {
+                const XImage im = x_image(lds + n * img_words, K, GS);
+#pragma unroll
+                for (int j = 0; j < NU; ++j) {
+                    const int g = (c0 + j * kWave) / UPG4;
+                    const int u = g * UPS + part;
                     const uint4 a = reinterpret_cast<const uint4*>(im.xq + u * 8)[0];
                     const uint4 b = reinterpret_cast<const uint4*>(im.xq + u * 8)[1];
                     int d = 0;
-                    d = __builtin_amdgcn_sdot4(static_cast<int>(lo[0]), static_cast<int>(a.x), d, false);
-                    d = __builtin_amdgcn_sdot4(static_cast<int>(hi[0]), static_cast<int>(a.y), d, false);
-                    d = __builtin_amdgcn_sdot4(static_cast<int>(lo[1]), static_cast<int>(a.z), d, false);
-                    d = __builtin_amdgcn_sdot4(static_cast<int>(hi[1]), static_cast<int>(a.w), d, false);
-                    d = __builtin_amdgcn_sdot4(static_cast<int>(lo[2]), static_cast<int>(b.x), d, false);
-                    d = __builtin_amdgcn_sdot4(static_cast<int>(hi[2]), static_cast<int>(b.y), d, false);
-                    d = __builtin_amdgcn_sdot4(static_cast<int>(lo[3]), static_cast<int>(b.z), d, false);
-                    d = __builtin_amdgcn_sdot4(static_cast<int>(hi[3]), static_cast<int>(b.w), d, false);
-                    acc[n] = fmaf(static_cast<float>(d), s * im.scale[g], acc[n]);
-                    acc[n] = fmaf(zs, im.usum[u], acc[n]);
+                    d = __builtin_amdgcn_sdot4(static_cast<int>(lo[j][0]), static_cast<int>(a.x), d, false);
+                    d = __builtin_amdgcn_sdot4(static_cast<int>(hi[j][0]), static_cast<int>(a.y), d, false);
+                    d = __builtin_amdgcn_sdot4(static_cast<int>(lo[j][1]), static_cast<int>(a.z), d, false);
+                    d = __builtin_amdgcn_sdot4(static_cast<int>(hi[j][1]), static_cast<int>(a.w), d, false);
+                    d = __builtin_amdgcn_sdot4(static_cast<int>(lo[j][2]), static_cast<int>(b.x), d, false);
+                    d = __builtin_amdgcn_sdot4(static_cast<int>(hi[j][2]), static_cast<int>(b.y), d, false);
+                    d = __builtin_amdgcn_sdot4(static_cast<int>(lo[j][3]), static_cast<int>(b.z), d, false);
+                    d = __builtin_amdgcn_sdot4(static_cast<int>(hi[j][3]), static_cast<int>(b.w), d, false);
+                    acc[n] = fmaf(static_cast<float>(d), s_[j] * im.scale[g], acc[n]);
+                    acc[n] = fmaf(zs_[j], im.usum[u], acc[n]);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
         const int band = tile * bpt + bl;
 #pragma unroll
@@ -153,24 +161,35 @@ struct BatchPlan {
     bool exact;
 };
 
-// Same tiling rule as the single-column preq2 plan; columns per launch: up to
-// 16 within ~96 KB of LDS images.
+// Tiling: the largest K split (KS <= 8) that divides the band exactly, i.e.
+// the fewest units per lane, since every unit's nibbles stay in registers
+// while all columns are dotted; then columns per launch capped so no
+// instantiation spills (measured VGPRs: 8 waves, NU <= 4: 16 columns within
+// 208 VGPRs; 16 waves: 128-VGPR budget, 8 columns at NU <= 4) and the column
+// images stay within ~96 KB of LDS.
 BatchPlan plan_batch(int M, int K, int gs, int cus) {
     const int upb = K / 8;
     const int nbands = (M + 3) / 4;
     BatchPlan p{0, 0, K > 4096 ? 16 : 8, 0, 16, false};
-    auto nu_of = [&](int l) { return (upb + (kWave << l) - 1) / (kWave << l); };
     auto tiles_of = [&](int l) {
         const int bpt = p.waves >> l;
         return (nbands + bpt - 1) / bpt;
     };
-    while (p.lks < 3 && nu_of(p.lks) > 6) ++p.lks;
-    while (p.lks < 3 && tiles_of(p.lks) < cus / 2 && upb % (kWave << (p.lks + 1)) == 0) ++p.lks;
-    p.nu = nu_of(p.lks);
-    p.exact = p.nu * (kWave << p.lks) == upb;
+    int best = -1;
+    for (int l = 0; l <= 3; ++l)
+        if (upb % (kWave << l) == 0 && (p.waves >> l) >= 1) best = l;
+    if (best < 0) {  // no exact split: the caller falls back to per-column GEMVs
+        p.exact = false;
+        return p;
+    }
+    p.lks = best;
+    p.nu = upb / (kWave << p.lks);
+    p.exact = p.nu <= 6;
     const int cap = cus * (32 / p.waves);
     const int tiles = tiles_of(p.lks);
     p.grid = tiles < cap ? tiles : cap;
+    if (p.waves == 8) p.nb = p.nu <= 4 ? 16 : 8;
+    else p.nb = p.nu <= 4 ? 8 : 4;
     const size_t img = batch_image_bytes(K, gs);
     while (p.nb > 2 && static_cast<size_t>(p.nb) * img > 96 * 1024) p.nb >>= 1;
     return p;

@@ -9,106 +9,159 @@
 //   A row listed twice adds twice.  Only listed rows are read: at 80 % zeros
 //   the kernel streams a fifth of the matrix.
 //
-// Pass 1: P workgroups each take a contiguous chunk of the active list; a
-//   wave walks rows of the chunk (two rows' loads in flight), its lanes owning
-//   fixed 32-output units (lane l: units l, l+64, ...), so the per-lane
-//   accumulators stay in registers.  Waves add their partial y in LDS in a
-//   fixed order and the workgroup writes work[p][:].
-// Pass 2: y[o] = sum_p work[p][o] in order p = 0..P-1.
-// No atomics: results are reproducible run to run (the reference's own
-// per-thread buffers race across pool chunks, gemv_sparse_avx2.cpp:297-300).
+// The active list is cut into P contiguous parts and the outputs into slices
+// of 256; workgroup (slice, part) walks its part's rows for its slice.  Per
+// listed row a workgroup touches one 128-byte nibble line and one scale and
+// one bias segment, so the cost is set by rows per workgroup (scattered line
+// lookups in the compute unit's cache), and splitting the list is what spreads
+// it over the chip.  Eight lanes serve a row (16 bytes = 32 outputs each), a
+// wave load covers 8 rows and every lane requests its 4 rows before using any.
+// Each lane keeps its 32 sums in registers; the 8 rows of a wave fold with DPP
+// and lane swizzles, the 4 waves through LDS in fixed order.
+//   P == 1: the workgroup writes y.
+//   P > 1:  it writes part[p][slice], and a second launch adds the P parts of
+//           each output in order p = 0..P-1.
+// A last-arriving-workgroup reduction in one launch was measured 2-5x slower:
+// its device-scope fences cost more than the second launch.  No atomics, so
+// results are reproducible run to run on a device (P follows n and the CU
+// count).  The reference's own per-thread buffers race across pool chunks
+// (gemv_sparse_avx2.cpp:297-300).
 #include "abi_util.hpp"
 #include "device_common.hpp"
 
 namespace asdsl {
 namespace {
 
-constexpr int kWaves = 8;
-constexpr int kMaxSlice = 4096;   // outputs per launch: 64 lanes x 2 units x 32
-constexpr int kUnitsPerLane = kMaxSlice / (32 * kWave);
+constexpr int kWaves = 4;
+constexpr int kLanesPerRow = 8;                    // 8 x 16 bytes = 256 outputs
+constexpr int kSliceOut = kLanesPerRow * 32;
+constexpr int kRowsPerWave = kWave / kLanesPerRow;
+constexpr int kDepth = 4;                          // rows per lane in flight
+constexpr int kXcds = 8;                           // MI355X: workgroup i runs on XCD i % 8
+constexpr int kMaxParts = 32;
+constexpr int kMinRowsPerPart = 32;
 
-__global__ __launch_bounds__(kWaves * kWave) void sparse_down_pass1(
+// WIDE: group_size % 32 == 0, so a lane's 32 outputs share one (scale, bias)
+// and a row costs the lane one load of each; otherwise one per 8 outputs.
+template <bool WIDE>
+__global__ __launch_bounds__(kWaves * kWave) void sparse_down_kernel(
     const uint8_t* __restrict__ wT, const float* __restrict__ sT, const float* __restrict__ bT,
-    const float* __restrict__ x, const int32_t* __restrict__ rows, int n, float* __restrict__ work,
-    int in_dim, int out_dim, int gs, int o_off, int o_len, int per_wg) {
-    extern __shared__ __align__(16) float part[];  // [kWaves][o_len]
+    const float* __restrict__ x, const int32_t* __restrict__ rows, int n, float* __restrict__ out, int in_dim,
+    int out_dim, int gs, int nslices, int nparts, int per_part) {
+    __shared__ __align__(16) float red[kWaves][kSliceOut];
+    // Consecutive tiles t run on one XCD, so neighbouring slices (which share
+    // scale lines) of one part meet in one L2.  The grid is a multiple of 8.
+    const int bid = static_cast<int>(blockIdx.x);
+    const int per_xcd = static_cast<int>(gridDim.x) / kXcds;
+    const int t = (bid % kXcds) * per_xcd + bid / kXcds;
+    if (t >= nslices * nparts) return;  // padding workgroup: the whole workgroup leaves
+    const int slice = t % nslices;
+    const int p = t / nslices;
+
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const int sub = lane / kLanesPerRow;  // row within the wave load
+    const int j = lane % kLanesPerRow;
+    const int o0 = slice * kSliceOut + j * 32;  // this lane's first output
+    const bool live_out = o0 < out_dim;
     const int G = out_dim / gs;
-    const int units = o_len >> 5;
-    const int a0 = static_cast<int>(blockIdx.x) * per_wg;
-    const int a1 = min(a0 + per_wg, n);
+    const size_t row_bytes = static_cast<size_t>(out_dim / 2);
+    const int a_begin = p * per_part;
+    const int a_end = min(a_begin + per_part, n);
 
-    float acc[kUnitsPerLane][32];
+    float acc[32];
 #pragma unroll
-    for (int i = 0; i < kUnitsPerLane; ++i)
-#pragma unroll
-        for (int e = 0; e < 32; ++e) acc[i][e] = 0.0f;
+    for (int e = 0; e < 32; ++e) acc[e] = 0.0f;
 
-    for (int a = a0 + wave; a < a1; a += kWaves) {
-        const int r = rows[a];
-        if (r < 0 || r >= in_dim) continue;  // skipped, as the reference does
-        const float xv = x[r];
-        if (xv == 0.0f) continue;
-        const uint8_t* rp = wT + static_cast<size_t>(r) * (out_dim / 2) + o_off / 2;
-        const float* sp = sT + static_cast<size_t>(r) * G;
-        const float* bp = bT + static_cast<size_t>(r) * G;
+    constexpr int stride = kWaves * kRowsPerWave;
+    for (int a0 = a_begin + wave * kRowsPerWave + sub; a0 < a_end; a0 += kDepth * stride) {
+        int r[kDepth];
+        float xv[kDepth];
+        uint4 w[kDepth];
+        float s[kDepth][4], b[kDepth][4];
+        bool ok[kDepth];
 #pragma unroll
-        for (int i = 0; i < kUnitsPerLane; ++i) {
-            const int u = lane + i * kWave;
-            if (u < units) {
-                const uint4 w = load_stream16(reinterpret_cast<const uint4*>(rp) + u);
-                const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+        for (int d = 0; d < kDepth; ++d) {
+            const int a = a0 + d * stride;
+            r[d] = a < a_end ? rows[a] : -1;
+        }
 #pragma unroll
-                for (int dw = 0; dw < 4; ++dw) {  // 8 outputs per dword, one group (8 | gs)
-                    const int g = (o_off + u * 32 + dw * 8) / gs;
-                    const float s = sp[g] * xv;
-                    const float b = bp[g] * xv;
+        for (int d = 0; d < kDepth; ++d) {
+            ok[d] = live_out && r[d] >= 0 && r[d] < in_dim;
+            const int rr = ok[d] ? r[d] : 0;  // in-bounds row for the loads below
+            const int oo = live_out ? o0 : 0;
+            xv[d] = x[rr];
+            w[d] = load_stream16(reinterpret_cast<const uint4*>(wT + static_cast<size_t>(rr) * row_bytes + oo / 2));
+            if (WIDE) {
+                const size_t at = static_cast<size_t>(rr) * G + oo / gs;
+                s[d][0] = sT[at];
+                b[d][0] = bT[at];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float q = static_cast<float>((wv[dw] >> (4 * e)) & 0xFu);
-                        acc[i][dw * 8 + e] += fmaf(q, s, b);
-                    }
+                for (int dw = 1; dw < 4; ++dw) {
+                    s[d][dw] = s[d][0];
+                    b[d][dw] = b[d][0];
+                }
+            } else {
+#pragma unroll
+                for (int dw = 0; dw < 4; ++dw) {  // 8 outputs per dword lie in one group (8 | gs)
+                    const size_t at = static_cast<size_t>(rr) * G + (oo + dw * 8) / gs;
+                    s[d][dw] = sT[at];
+                    b[d][dw] = bT[at];
+                }
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            if (ok[d] && xv[d] != 0.0f) {
+                const uint32_t wv[4] = {w[d].x, w[d].y, w[d].z, w[d].w};
+#pragma unroll
+                for (int dw = 0; dw < 4; ++dw) {
+                    const float sx = s[d][dw] * xv[d];
+                    const float bx = b[d][dw] * xv[d];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        acc[dw * 8 + e] += fmaf(static_cast<float>((wv[dw] >> (4 * e)) & 0xFu), sx, bx);
                 }
             }
         }
     }
-    // fixed-order combine of the waves' partials
+
+    // fold the 8 rows of a wave load: lanes that agree in bits 0-2 (the unit j)
 #pragma unroll
-    for (int i = 0; i < kUnitsPerLane; ++i) {
-        const int u = lane + i * kWave;
-        if (u < units) {
-            float* dst = part + wave * o_len + u * 32;
+    for (int e = 0; e < 32; ++e) {
+        float v = acc[e];
+        v += dpp<kDppRowRor8>(v);       // lane bit 3
+        v += swz_xor16(v);              // bit 4
+        v += __shfl_xor(v, 32, kWave);  // bit 5
+        acc[e] = v;
+    }
+    if (sub == 0) {
+        float* dst = &red[wave][j * 32];
 #pragma unroll
-            for (int e = 0; e < 32; e += 4)
-                *reinterpret_cast<float4*>(dst + e) = make_float4(acc[i][e], acc[i][e + 1], acc[i][e + 2], acc[i][e + 3]);
-        }
+        for (int e = 0; e < 32; e += 4)
+            *reinterpret_cast<float4*>(dst + e) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
     }
     __syncthreads();
-    float* out = work + static_cast<size_t>(blockIdx.x) * o_len;
-    for (int o = static_cast<int>(threadIdx.x); o < o_len; o += kWaves * kWave) {
-        float sum = part[o];
-        for (int v = 1; v < kWaves; ++v) sum += part[v * o_len + o];
-        out[o] = sum;
+    for (int o = static_cast<int>(threadIdx.x); o < kSliceOut; o += kWaves * kWave) {
+        const int og = slice * kSliceOut + o;
+        if (og < out_dim) {
+            float sum = red[0][o];
+#pragma unroll
+            for (int v = 1; v < kWaves; ++v) sum += red[v][o];
+            out[static_cast<size_t>(p) * out_dim + og] = sum;
+        }
     }
 }
 
-__global__ __launch_bounds__(256) void sparse_down_pass2(const float* __restrict__ work, int P, float* __restrict__ y,
-                                                        int o_off, int o_len) {
+// y[o] = part[0][o] + part[1][o] + ... + part[P-1][o], in that order.
+__global__ __launch_bounds__(256) void sparse_down_sum_parts(const float* __restrict__ part, float* __restrict__ y,
+                                                             int out_dim, int nparts) {
     const int o = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
-    if (o >= o_len) return;
-    float sum = 0.0f;
-    for (int p = 0; p < P; ++p) sum += work[static_cast<size_t>(p) * o_len + o];
-    y[o_off + o] = sum;
-}
-
-// Workgroups for n listed rows: enough to keep ~8 rows per wave in flight
-// territory without multiplying the partial traffic (P * o_len * 4 bytes).
-int sparse_down_wgs(int n, int cus) {
-    int p = (n + kWaves * 4 - 1) / (kWaves * 4);  // ~4 rows per wave
-    const int cap = cus / 2 > 0 ? cus / 2 : 1;
-    if (p > cap) p = cap;
-    return p < 1 ? 1 : p;
+    if (o >= out_dim) return;
+    float sum = part[o];
+#pragma unroll 8
+    for (int p = 1; p < nparts; ++p) sum += part[static_cast<size_t>(p) * out_dim + o];
+    y[o] = sum;
 }
 
 }  // namespace
@@ -116,18 +169,10 @@ int sparse_down_wgs(int n, int cus) {
 
 using namespace asdsl;
 
-extern "C" size_t asdsl_sparse_down_proj_T_workspace_bytes(int n_active, int out_dim) {
-    const int cus = cu_count_current();
-    const int P = sparse_down_wgs(n_active > 0 ? n_active : 1, cus > 0 ? cus : 256);
-    const int slice = out_dim < kMaxSlice ? out_dim : kMaxSlice;
-    return static_cast<size_t>(P) * static_cast<size_t>(slice > 0 ? slice : 1) * sizeof(float);
-}
-
 extern "C" asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, const float* scales_T,
                                                  const float* biases_T, const float* sparse_x,
                                                  const int32_t* active_rows, int n_active, float* y, int in_dim,
-                                                 int out_dim, int group_size, float* work, size_t work_bytes,
-                                                 asdsl_stream_t stream) {
+                                                 int out_dim, int group_size, asdsl_stream_t stream) {
     ASDSL_CHECK_ARG(in_dim > 0 && out_dim > 0 && group_size > 0, "in_dim, out_dim, group_size must be positive");
     ASDSL_CHECK_ARG(out_dim % group_size == 0, "out_dim must be divisible by group_size");
     ASDSL_CHECK_ARG(w_T_packed && scales_T && biases_T && sparse_x && y, "sparse_down_proj_T: null pointer");
@@ -135,24 +180,32 @@ extern "C" asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, cons
                     "sparse_down_proj_T: invalid active row list");
     ASDSL_CHECK_ARG(out_dim % 32 == 0 && group_size % 8 == 0,
                     "sparse_down_proj_T: out_dim must be a multiple of 32 and group_size of 8");
-    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(w_T_packed) % 16 == 0 && (out_dim / 2) % 16 == 0,
-                    "sparse_down_proj_T: weight rows must be 16-byte aligned");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(w_T_packed) % 16 == 0,
+                    "sparse_down_proj_T: w_T_packed must be 16-byte aligned");
     ASDSL_CU_COUNT(cus);
+    const int nslices = (out_dim + kSliceOut - 1) / kSliceOut;
+    // about 3 workgroups per 4 compute units, at least 32 rows per part
+    int nparts = (3 * cus / 4) / nslices;
+    nparts = min(nparts, (n_active + kMinRowsPerPart - 1) / kMinRowsPerPart);
+    nparts = max(1, min(nparts, kMaxParts));
+    const int per_part = max(1, (n_active + nparts - 1) / nparts);
+    const int tiles = nslices * nparts;
+    const int grid = (tiles + kXcds - 1) / kXcds * kXcds;
     hipStream_t s = as_hip(stream);
-    const int P = sparse_down_wgs(n_active > 0 ? n_active : 1, cus);
-    const int per_wg = (n_active + P - 1) / P > 0 ? (n_active + P - 1) / P : 1;
-    for (int o_off = 0; o_off < out_dim; o_off += kMaxSlice) {
-        const int o_len = out_dim - o_off < kMaxSlice ? out_dim - o_off : kMaxSlice;
-        ASDSL_CHECK_ARG(work != nullptr && work_bytes >= static_cast<size_t>(P) * o_len * sizeof(float),
-                        "sparse_down_proj_T: workspace too small (asdsl_sparse_down_proj_T_workspace_bytes)");
-        const size_t lds = static_cast<size_t>(kWaves) * o_len * sizeof(float);
-        asdsl_status st = launch("sparse_down_pass1", sparse_down_pass1, dim3(P), dim3(kWaves * kWave), lds, s,
-                                 w_T_packed, scales_T, biases_T, sparse_x, active_rows, n_active, work, in_dim,
-                                 out_dim, group_size, o_off, o_len, per_wg);
-        if (st != ASDSL_OK) return st;
-        st = launch("sparse_down_pass2", sparse_down_pass2, dim3((o_len + 255) / 256), dim3(256), 0, s,
-                    static_cast<const float*>(work), P, y, o_off, o_len);
-        if (st != ASDSL_OK) return st;
-    }
-    return ASDSL_OK;
+    auto kernel = group_size % 32 == 0 ? sparse_down_kernel<true> : sparse_down_kernel<false>;
+    if (nparts == 1)
+        return launch("sparse_down_kernel", kernel, dim3(grid), dim3(kWaves * kWave), 0, s, w_T_packed, scales_T,
+                      biases_T, sparse_x, active_rows, n_active, y, in_dim, out_dim, group_size, nslices, nparts,
+                      per_part);
+    void* part = nullptr;
+    const asdsl_status st = device_workspace(s, static_cast<size_t>(nparts) * out_dim * sizeof(float), &part,
+                                             "sparse_down_proj_T");
+    if (st != ASDSL_OK) return st;
+    float* pf = static_cast<float*>(part);
+    const asdsl_status st1 = launch("sparse_down_kernel", kernel, dim3(grid), dim3(kWaves * kWave), 0, s, w_T_packed,
+                                    scales_T, biases_T, sparse_x, active_rows, n_active, pf, in_dim, out_dim,
+                                    group_size, nslices, nparts, per_part);
+    if (st1 != ASDSL_OK) return st1;
+    return launch("sparse_down_sum_parts", sparse_down_sum_parts, dim3((out_dim + 255) / 256), dim3(256), 0, s,
+                  static_cast<const float*>(pf), y, out_dim, nparts);
 }

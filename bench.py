@@ -30,6 +30,7 @@ Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -58,6 +59,37 @@ GATE_UP_TRAFFIC_BYTES = 31_681_704
 def gemv_bytes(M: int, K: int, gs: int = GS) -> int:
     G = K // gs
     return M * G * 4 + ((M + 3) // 4) * G * 4 * (gs // 2) + 4 * K + 4 * M
+
+
+def capture(calls):
+    """HIP graph of `calls(stream_handle)` on torch's capture stream (warmed up
+    once on a side stream first, as torch requires)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls(int(side.cuda_stream))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        calls(int(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return g
+
+
+def timed_replays(g, n):
+    import torch
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(n):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
 
 
 def build_layers(n_layers: int, seed: int):
@@ -160,6 +192,308 @@ def lm_head_kernel(lib, capture, timed_replays):
             "frac_of_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+# --------------------------------------------------------------------------- suite
+def _dev_bytes(n, gen, valid_f16_pairs=False):
+    """n random device bytes; with valid_f16_pairs every 16-bit half is a
+    small finite fp16 (exponent bits masked)."""
+    import torch
+
+    words = torch.randint(0, 2**31 - 1, ((n + 3) // 4,), generator=gen, device="cuda", dtype=torch.int32)
+    if valid_f16_pairs:
+        words &= 0x3BFF3BFF
+    return words.view(torch.uint8)[:n].contiguous()
+
+
+def _dev_f32(n, gen, scale=0.01, offset=0.0):
+    import torch
+
+    return torch.rand(n, generator=gen, device="cuda", dtype=torch.float32) * scale + offset
+
+
+def run_suite(args) -> int:
+    """One JSON line per hot-path row of the reference: kernel time at the row's
+    workload (graph replay over rotated weight copies, so HBM serves the
+    weights), algorithmic bytes, fraction of the 8 TB/s roofline, and the
+    reference's own compiled CPU kernel (oracle/_ref) timed on the same inputs
+    of copy 0, with the GPU/CPU relative L2 difference."""
+    import torch
+
+    from asdsl import _hip
+    from asdsl.quantization.synthetic import preq2_from_weights_torch, q4_128_from_weights_torch
+
+    sys.path.insert(0, str(REPO))
+    import oracle
+
+    lib = _hip.LIB
+    P = _hip.ptr
+    ref = {m: oracle.load_reference(m) if oracle.reference_available(m) else None
+           for m in ("_native_gemv", "_native_gemv_q8", "_native_sparse_gemv")}
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    results = []
+
+    def ncopies(nbytes):
+        return int(min(32, max(2, -(-640_000_000 // max(nbytes, 1)))))
+
+    def measure(name, workload, nbytes, make_copy, launch, out_shape, cpu=None, reps=None, note=None, exact=False):
+        """make_copy() -> dict of device tensors; launch(copy, y, h) issues the
+        GPU call; cpu(host_copy) -> numpy output or None."""
+        n = ncopies(nbytes)
+        copies = [make_copy() for _ in range(n)]
+        y = torch.empty(out_shape, device="cuda", dtype=torch.float32)
+        per_graph = max(n, 8)
+
+        def calls(h):
+            for i in range(per_graph):
+                st = launch(copies[i % n], y, h)
+                if st:
+                    raise RuntimeError(f"{name}: {_hip.last_error()}")
+        g = capture(calls)
+        r = reps or max(3, int(2e8 // max(nbytes * per_graph, 1)))
+        r = min(r, 200)
+        timed_replays(g, 2)
+        us = 1e3 * timed_replays(g, r) / (r * per_graph)
+        del g
+        # output of copy 0 for the parity spot check
+        launch(copies[0], y, int(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        got = y.cpu().numpy().reshape(-1)
+        row = {"row": name, "workload": workload, "gpu_us": round(us, 3), "bytes": int(nbytes),
+               "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+               "frac_of_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "rotated_copies": n}
+        if note:
+            row["note"] = note
+        if cpu is not None and not args.no_cpu:
+            host = {k: (v.cpu().numpy() if isinstance(v, torch.Tensor) else v) for k, v in copies[0].items()}
+            want = np.asarray(cpu(host))
+            want = (want.view(np.float32) if exact else want.astype(np.float32)).reshape(-1)
+            calls_n, t0 = 0, time.perf_counter()
+            while True:
+                cpu(host)
+                calls_n += 1
+                el = time.perf_counter() - t0
+                if el >= args.cpu_seconds_per_row or calls_n >= 2000:
+                    break
+            cus = 1e6 * el / calls_n
+            row["cpu_reference"] = {"us": round(cus, 1), "GB/s": round(nbytes / (cus * 1e-6) / 1e9, 2),
+                                    "threads": threads, "calls": calls_n}
+            row["gpu_speedup"] = round(cus / us, 1)
+            if exact:
+                row["bit_exact_vs_reference"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+            else:
+                den = float(np.linalg.norm(want)) or 1.0
+                row["rel_l2_vs_reference"] = float(np.linalg.norm(got - want) / den)
+        del copies, y
+        torch.cuda.empty_cache()
+        results.append(row)
+        print(json.dumps(row), flush=True)
+
+    ng, q8m, spm = ref["_native_gemv"], ref["_native_gemv_q8"], ref["_native_sparse_gemv"]
+
+    # A1 activation quantizer
+    K = 3072
+    x = torch.randn(K, generator=gen, device="cuda")
+    xq = torch.empty(K, dtype=torch.int8, device="cuda")
+
+    def q_launch(c, y, h):
+        return lib.asdsl_quantize_activation(P(c["x"]), P(xq), P(y), K, 32, h)
+
+    def q_cpu(hc):
+        a, b = np.zeros(K, np.int8), np.zeros(K // 32, np.float32)
+        ng.quantize_activation_avx2(hc["x"], a, b, K, 32)
+        return b
+    measure("A1 quantize_activation", "K=3072 gs=32", 4 * K + K + 4 * (K // 32), lambda: {"x": x.clone()},
+            q_launch, (K // 32,), q_cpu if ng else None)
+
+    # A3 preq g32 (20-byte blocks), built from preq2 bytes on the device
+    def preq_copy(M, K):
+        m, q = preq2_from_weights_torch(torch.randn((M, K), generator=gen, device="cuda") * 0.02, 32)
+        G = K // 32
+        meta = m.view(M, G, 4)
+        quant = q.view((M + 3) // 4, G, 4, 16).permute(0, 2, 1, 3).reshape(-1, G, 16)[:M]
+        blocks = torch.cat([meta, quant], dim=2).contiguous().view(-1)
+        return {"blocks": blocks, "x": torch.randn(K, generator=gen, device="cuda")}
+
+    for (M, K, wl) in [(3072, 3072, "3072x3072 (the reference's single-GEMV case)"), (16384, 3072, "gate_up 16384x3072")]:
+        def launch(c, y, h, M=M, K=K):
+            return lib.asdsl_gemv_q4_32_preq_fused(P(c["blocks"]), P(c["x"]), P(y), M, K, 32, h)
+
+        def cpu(hc, M=M, K=K):
+            y = np.zeros(M, np.float32)
+            ng.gemv_q4_32_preq_fused_avx2(hc["blocks"], hc["x"], y, M, K, 32)
+            return y
+        measure("A3 preq g32 fused GEMV", wl, M * (K // 32) * 20 + 4 * K + 4 * M,
+                lambda M=M, K=K: preq_copy(M, K), launch, (M,), cpu if ng else None)
+
+    # A5 / A7 preq2 (g32 reference layout; g128 asymmetric extension)
+    def preq2_copy(M, K, gs):
+        m, q = preq2_from_weights_torch(torch.randn((M, K), generator=gen, device="cuda") * 0.02, gs)
+        return {"meta": m, "quant": q, "x": torch.randn(K, generator=gen, device="cuda")}
+
+    for (M, K, gs, wl) in [(16384, 3072, 32, "gate_up 16384x3072"), (3072, 8192, 32, "down 3072x8192"),
+                           (200064, 3072, 32, "lm_head 200064x3072"), (200064, 3072, 128, "lm_head 200064x3072")]:
+        def launch(c, y, h, M=M, K=K, gs=gs):
+            return lib.asdsl_gemv_preq2_fused(P(c["meta"]), P(c["quant"]), P(c["x"]), P(y), M, K, gs, h)
+
+        def cpu(hc, M=M, K=K):
+            y = np.zeros(M, np.float32)
+            ng.gemv_preq2_fused_avx2(hc["meta"], hc["quant"], hc["x"], y, M, K, 32)
+            return y
+        measure("A5 preq2 g32 fused GEMV" if gs == 32 else "A7 preq2-g128 fused GEMV", wl, gemv_bytes(M, K, gs),
+                lambda M=M, K=K, gs=gs: preq2_copy(M, K, gs), launch, (M,), cpu if (ng and gs == 32) else None,
+                note=None if gs == 32 else "no reference kernel for this layout")
+
+    # A6 Q4_128 (x pre-quantized per 128, as the reference's engine calls it)
+    for (M, K, wl) in [(200064, 3072, "lm_head 200064x3072"), (16384, 3072, "gate_up 16384x3072")]:
+        def q128_copy(M=M, K=K):
+            b = q4_128_from_weights_torch(torch.randn((M, K), generator=gen, device="cuda") * 0.02)
+            x = torch.randn(K, generator=gen, device="cuda")
+            xq8 = torch.empty(K, dtype=torch.int8, device="cuda")
+            xs = torch.empty(K // 128, device="cuda")
+            lib.asdsl_quantize_activation(P(x), P(xq8), P(xs), K, 128, int(torch.cuda.current_stream().cuda_stream))
+            return {"blocks": b, "xq": xq8, "xs": xs}
+
+        def launch(c, y, h, M=M, K=K):
+            return lib.asdsl_gemv_q4_128_preq(P(c["blocks"]), P(c["xq"]), P(c["xs"]), P(y), M, K, 128, h)
+
+        def cpu(hc, M=M, K=K):
+            y = np.zeros(M, np.float32)
+            ng.gemv_q4_128_preq_avx2(hc["blocks"], hc["xq"], hc["xs"], y, M, K, 128)
+            return y
+        measure("A6 Q4_128 GEMV (pre-quantized x)", wl, M * (K // 128) * 66 + K + 4 * (K // 128) + 4 * M,
+                q128_copy, launch, (M,), cpu if ng else None)
+
+    # A8 Q4_K superblocks
+    M, K = 16384, 3072
+
+    def q4k_copy():
+        w = _dev_bytes(M * (K // 256) * 144, gen).view(M, K // 256, 144)
+        w[:, :, 0:4] = _dev_bytes(M * (K // 256) * 4, gen, valid_f16_pairs=True).view(M, K // 256, 4)
+        return {"w": w.contiguous().view(-1), "x": torch.randn(K, generator=gen, device="cuda")}
+
+    def q4k_cpu(hc):
+        y = np.zeros(M, np.float32)
+        ng.gemv_q4km_q8_avx2(hc["w"], hc["x"], y, M, K)
+        return y
+    measure("A8 Q4_K GEMV", "gate_up 16384x3072", M * (K // 256) * 144 + 4 * K + 4 * M, q4k_copy,
+            lambda c, y, h: lib.asdsl_gemv_q4km_q8(P(c["w"]), P(c["x"]), P(y), M, K, h), (M,), q4k_cpu if ng else None)
+
+    # A9(ii) symmetric packed Q4 x Q8
+    def pk_copy(M, K, gs, bias=False, bytes_per=0.5):
+        c = {"w": _dev_bytes(int(M * K * bytes_per), gen), "s": _dev_f32(M * (K // gs), gen, 0.01, 1e-3),
+             "x": torch.randn(K, generator=gen, device="cuda")}
+        if bias:
+            c["b"] = _dev_f32(M * (K // gs), gen, 0.02, -0.01)
+        return c
+
+    def q4q8_cpu(hc):
+        y = np.zeros(M, np.float32)
+        ng.gemv_q4_q8_avx2(hc["w"], hc["s"], hc["x"], y, M, K, 32)
+        return y
+    measure("A9(ii) Q4xQ8 symmetric GEMV", "gate_up 16384x3072 gs=32", M * K // 2 + M * (K // 32) * 4 + 4 * K + 4 * M,
+            lambda: pk_copy(M, K, 32), lambda c, y, h: lib.asdsl_gemv_q4_q8(P(c["w"]), P(c["s"]), P(c["x"]), P(y), M, K, 32, h),
+            (M,), q4q8_cpu if ng else None)
+
+    # A9(i) Q8 weights, A10 packed / unpacked / gs64
+    M8, K8 = 3072, 3072
+
+    def q8_cpu(hc):
+        return q8m.gemv_q8_unpacked(hc["w"], hc["x"], hc["s"], hc["b"], M8, K8, 128, True)
+    measure("A9(i) Q8-weight fp32 GEMV", "3072x3072 gs=128", M8 * K8 + 2 * M8 * (K8 // 128) * 4 + 4 * K8 + 4 * M8,
+            lambda: pk_copy(M8, K8, 128, True, 1.0),
+            lambda c, y, h: lib.asdsl_gemv_q8_unpacked(P(c["w"]), P(c["x"]), P(c["s"]), P(c["b"]), P(y), M8, K8, 128, h),
+            (M8,), q8_cpu if q8m else None)
+    measure("A10 packed Q4 fp32 GEMV", "gate_up 16384x3072 gs=32", M * K // 2 + 2 * M * (K // 32) * 4 + 4 * K + 4 * M,
+            lambda: pk_copy(M, K, 32, True),
+            lambda c, y, h: lib.asdsl_gemv_q4_packed(P(c["w"]), P(c["x"]), P(c["s"]), P(c["b"]), P(y), M, K, 32, 1, h),
+            (M,), (lambda hc: ng.gemv_q4_packed(hc["w"], hc["x"], hc["s"], hc["b"], M, K, 32)) if ng else None)
+    measure("A10 unpacked Q4 fp32 GEMV", "3072x3072 gs=32", M8 * K8 + 2 * M8 * (K8 // 32) * 4 + 4 * K8 + 4 * M8,
+            lambda: pk_copy(M8, K8, 32, True, 1.0),
+            lambda c, y, h: lib.asdsl_gemv_q4_unpacked(P(c["w"]), P(c["x"]), P(c["s"]), P(c["b"]), P(y), M8, K8, 32, h),
+            (M8,), (lambda hc: ng.gemv_q4_unpacked(hc["w"], hc["x"], hc["s"], hc["b"], M8, K8, 32)) if ng else None)
+    measure("A10 gs64 packed Q4 GEMV", "gate_up 16384x3072", M * K // 2 + M * (K // 64) * 4 + 4 * K + 4 * M,
+            lambda: pk_copy(M, K, 64),
+            lambda c, y, h: lib.asdsl_gemv_q4_gs64(P(c["w"]), P(c["x"]), P(c["s"]), P(y), M, K, 1, h),
+            (M,), (lambda hc: ng.gemv_q4_avx2_gs64(hc["w"], hc["x"], hc["s"], M, K)) if ng else None)
+
+    # A11 batched verification (preq2, each column quantized) and the fp32 batched GEMMs
+    for (Mb, Kb, wl) in [(16384, 3072, "gate_up 16384x3072"), (3072, 8192, "down 3072x8192")]:
+        for N in (2, 4, 8, 16):
+            def bcopy(Mb=Mb, Kb=Kb, N=N):
+                c = preq2_copy(Mb, Kb, 32)
+                c["X"] = torch.randn((N, Kb), generator=gen, device="cuda")
+                return c
+
+            def blaunch(c, y, h, Mb=Mb, Kb=Kb, N=N):
+                return lib.asdsl_gemv_preq2_fused_batch(P(c["meta"]), P(c["quant"]), P(c["X"]), P(y), Mb, Kb, 32, N, h)
+
+            def bcpu(hc, Mb=Mb, Kb=Kb, N=N):  # the reference verifies preq2 drafts one column at a time
+                Y = np.zeros((N, Mb), np.float32)
+                for n in range(N):
+                    ng.gemv_preq2_fused_avx2(hc["meta"], hc["quant"], hc["X"][n], Y[n], Mb, Kb, 32)
+                return Y
+            wbytes = gemv_bytes(Mb, Kb, 32) - 4 * Kb - 4 * Mb
+            measure("A11 batched preq2 g32 verify GEMV", f"{wl} N={N}", wbytes + N * (4 * Kb + 4 * Mb), bcopy, blaunch,
+                    (N, Mb), bcpu if ng else None, note="cpu_reference = N serial gemv_preq2_fused_avx2 calls")
+
+    B = 4
+
+    def mb_copy():
+        c = pk_copy(M, K, 32, True)
+        c["X"] = torch.randn((B, K), generator=gen, device="cuda")
+        return c
+
+    def mb_cpu(hc):
+        Y = np.zeros((B, M), np.float32)
+        ng.matmul_batch_q4(hc["w"], hc["s"], hc["b"], hc["X"], Y, M, K, B, 32)
+        return Y
+    measure("A11 matmul_batch_q4", "gate_up 16384x3072 B=4", M * K // 2 + 2 * M * (K // 32) * 4 + B * (4 * K + 4 * M),
+            mb_copy, lambda c, y, h: lib.asdsl_matmul_batch_q4(P(c["w"]), P(c["s"]), P(c["b"]), P(c["X"]), P(y), M, K, B, 32, h),
+            (B, M), mb_cpu if ng else None)
+
+    def g128_copy():
+        c = {"blocks": q4_128_from_weights_torch(torch.randn((M, K), generator=gen, device="cuda") * 0.02)}
+        c["X"] = torch.randn((B, K), generator=gen, device="cuda")
+        return c
+    measure("A11 gemm_q4_128 (fp32 x)", "gate_up 16384x3072 B=4", M * (K // 128) * 66 + B * (4 * K + 4 * M), g128_copy,
+            lambda c, y, h: lib.asdsl_gemm_q4_128(P(c["blocks"]), P(c["X"]), P(y), M, K, 128, B, h), (B, M), None,
+            note="reference kernel not exposed to Python (engine-internal)")
+
+    # A12 FATReLU sparse down-projection (K-major), bitmask, row-major sparse GEMV
+    IN, OUT = 8192, 3072
+    for zero_frac, t in ((0.5, 0.0), (0.8, 0.841621)):
+        xs_ = torch.clamp(torch.randn(IN, generator=gen, device="cuda") - t, min=0.0)
+        rows = torch.nonzero(xs_).to(torch.int32).view(-1).contiguous()
+        na = int(rows.numel())
+
+        def sd_copy(xs_=xs_, rows=rows):
+            return {"w": _dev_bytes(IN * OUT // 2, gen), "s": _dev_f32(IN * OUT // 32, gen, 0.01, 1e-3),
+                    "b": _dev_f32(IN * OUT // 32, gen, -0.08, 0.0), "x": xs_, "rows": rows}
+
+        def sd_launch(c, y, h, na=na):
+            return lib.asdsl_sparse_down_proj_T(P(c["w"]), P(c["s"]), P(c["b"]), P(c["x"]), P(c["rows"]), na, P(y),
+                                                IN, OUT, 32, h)
+
+        def sd_cpu(hc):
+            return spm.sparse_down_proj_T(hc["w"], hc["s"], hc["b"], hc["x"], hc["rows"], IN, OUT, 32)
+        measure("A12 FATReLU sparse_down_proj_T", f"down 8192x3072 K-major, {int(zero_frac * 100)}% zeros",
+                na * (OUT // 2 + 2 * (OUT // 32) * 4 + 8) + 4 * OUT, sd_copy, sd_launch, (OUT,),
+                sd_cpu if spm else None,
+                note="reference result races beyond one pool chunk; rel_l2 compares against it as is")
+
+    xb = torch.randn(8192, generator=gen, device="cuda")
+    mask = torch.empty(256, dtype=torch.int32, device="cuda")
+
+    def bm_cpu(hc):
+        return np.asarray(spm.compute_bitmask(hc["x"], 0.5), np.uint32)
+    measure("A12 compute_bitmask", "K=8192", 4 * 8192 + 1024, lambda: {"x": xb.clone()},
+            lambda c, y, h: lib.asdsl_compute_bitmask(P(c["x"]), P(y), 8192, ctypes.c_float(0.5), h), (256,),
+            bm_cpu if spm else None, exact=True)
+
+    print(json.dumps({"suite": "done", "rows": len(results)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,6 +503,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true")
+    ap.add_argument("--suite", action="store_true",
+                    help="one JSON line per hot-path row: kernel at its workload vs the HBM roofline, "
+                         "with the reference's compiled CPU kernel timed on the same inputs")
+    ap.add_argument("--cpu-seconds-per-row", type=float, default=1.0)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: 50 gate_up GEMVs over rotated weights, then 50 plain "
                          "64 MiB device copies (the counter scale reference); prints nothing else")
@@ -177,6 +515,9 @@ def main() -> int:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this GEMV path runs on a "
               "single MI355X and has no multi-GPU mode.", file=sys.stderr)
         return 2
+
+    if args.suite:
+        return run_suite(args)
 
     import torch
 
@@ -210,30 +551,6 @@ def main() -> int:
             st = lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], xp[n], yp[n], M, K, GS, stream_handle)
             if st:
                 raise RuntimeError(_hip.last_error())
-
-    def capture(calls):
-        """HIP graph of `calls(stream_handle)` (torch's capture stream)."""
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):  # warm-up on the side stream before capture
-            calls(int(side.cuda_stream))
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            calls(int(torch.cuda.current_stream().cuda_stream))
-        torch.cuda.synchronize()
-        return g
-
-    def timed_replays(g, n):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(n):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1)
 
     # One rotation cycle (L steps) per graph, plus the remainder, so that
     # exactly --steps steps run back to back with no host launch gaps.

@@ -2,8 +2,9 @@
  * asdsl_hip.h — C ABI of the MI355X (gfx950) Q4 GEMV family.
  *
  * Every entry point is stream-ordered and asynchronous: pointers are DEVICE
- * pointers, nothing is allocated, and the call returns as soon as the kernel
- * is queued on `stream` (0 = the null stream).  Buffers are owned by the
+ * pointers, nothing is allocated (apart from the one work buffer per device
+ * of asdsl_sparse_down_proj_T, sized on first use), and the call returns as
+ * soon as the kernel is queued on `stream` (0 = the null stream).  Buffers are owned by the
  * caller, exactly as in the reference kernels, which take caller-owned
  * host buffers (asdsl/kernels/native/gemv_q4_kernel.h:25-121).
  *
@@ -242,15 +243,16 @@ asdsl_status asdsl_gemv_sparse_with_indices(const uint8_t* w, const float* x, co
  *     y[o] += fma(q[r][o], scales_T[r][o/gs]*x[r], biases_T[r][o/gs]*x[r])
  * y[out_dim] is overwritten (starts from zero).  A row listed twice adds twice.
  * out_dim % 32 == 0, group_size % 8 == 0, w_T 16-byte aligned.
- * work: caller-provided device scratch of at least
- * asdsl_sparse_down_proj_T_workspace_bytes(n_active, out_dim) bytes.
+ * Long lists are summed in parts through a device buffer the library keeps
+ * per device: calls that overlap on one device (unordered streams) race on
+ * it.  Sizing it allocates, so under graph capture a call with at least the
+ * same n_active and out_dim must have run on the device before (else
+ * ASDSL_ERR_UNSUPPORTED).  Repeat calls are bitwise equal.
  * Replaces sparse_down_proj_T (asdsl/kernels/native/gemv_sparse_avx2.cpp:273-418),
  * called from experiments/phi4_cpu_run.py:3949-3967. */
-size_t asdsl_sparse_down_proj_T_workspace_bytes(int n_active, int out_dim);
 asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, const float* scales_T, const float* biases_T,
                                       const float* sparse_x, const int32_t* active_rows, int n_active, float* y,
-                                      int in_dim, int out_dim, int group_size, float* work, size_t work_bytes,
-                                      asdsl_stream_t stream);
+                                      int in_dim, int out_dim, int group_size, asdsl_stream_t stream);
 
 /* Debug dequantization of a preq2 matrix to fp32 W[M][K]: w = (q - z) * s,
  * bit-exact with the reference's dequant (experiments/phi4_cpu_run.py:3450-3467). */

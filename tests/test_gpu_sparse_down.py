@@ -80,3 +80,65 @@ def test_deterministic_and_on_device(gpu):
     a, b = y1.cpu().numpy(), y2.cpu().numpy()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert rel_l2(a, oracle.sparse_down_proj_T(wT, sT, bT, x, rows, IN, OUT, gs)) < TOL
+
+
+def test_workspace_reused_across_shapes(gpu):
+    """Calls of different out_dim back to back."""
+    from asdsl.kernels import _native_sparse_gemv as sp
+
+    for IN, OUT, gs in [(256, 3072, 32), (64, 96, 32), (256, 3072, 32), (128, 1024, 16), (64, 96, 32)]:
+        wT, sT, bT = _weights(IN, OUT, gs, IN * 3 + OUT)
+        x = np.maximum(0, np.random.default_rng(OUT).standard_normal(IN) - 0.3).astype(np.float32)
+        rows = np.nonzero(x)[0].astype(np.int32)
+        y = sp.sparse_down_proj_T(wT, sT, bT, x, rows, IN, OUT, gs)
+        assert rel_l2(y, oracle.sparse_down_proj_T(wT, sT, bT, x, rows, IN, OUT, gs)) < TOL, (IN, OUT)
+
+
+def test_unsorted_list_with_repeats_many_parts(gpu):
+    """A long shuffled list with every active row twice: the list is cut in
+    parts, and the sum must not depend on where the cuts fall."""
+    from asdsl.kernels import _native_sparse_gemv as sp
+
+    IN, OUT, gs = 8192, 3072, 32
+    wT, sT, bT = _weights(IN, OUT, gs, 21)
+    x = np.maximum(0.0, syn.activation(IN, 13) - np.float32(0.3)).astype(np.float32)
+    act = np.nonzero(x)[0].astype(np.int32)
+    rows = np.concatenate([act, act])
+    np.random.default_rng(3).shuffle(rows)
+    y = sp.sparse_down_proj_T(wT, sT, bT, x, rows, IN, OUT, gs)
+    want = oracle.sparse_down_proj_T(wT, sT, bT, x, rows, IN, OUT, gs)
+    assert rel_l2(y, want) < TOL
+    once = oracle.sparse_down_proj_T(wT, sT, bT, x, act, IN, OUT, gs)
+    assert rel_l2(y, 2.0 * once) < TOL
+
+
+def test_graph_replays_match_eager(gpu):
+    """Captured after one eager call (which sizes the work buffer); replays
+    with eager work in between each equal the eager result bitwise."""
+    import torch
+    from asdsl import _hip
+
+    IN, OUT, gs = 8192, 3072, 32
+    wT, sT, bT = _weights(IN, OUT, gs, 8)
+    x = np.maximum(0.0, syn.activation(IN, 14) - np.float32(0.841621)).astype(np.float32)
+    rows = np.nonzero(x)[0].astype(np.int32)
+    d = [torch.from_numpy(a).cuda() for a in (wT, sT, bT, x, rows)]
+    y_eager = torch.empty(OUT, device="cuda")
+    y_graph = torch.full((OUT,), float("nan"), device="cuda")
+    def call(y, stream):
+        _hip.call("asdsl_sparse_down_proj_T", d[0].data_ptr(), d[1].data_ptr(), d[2].data_ptr(), d[3].data_ptr(),
+                  d[4].data_ptr(), rows.size, y.data_ptr(), IN, OUT, gs, stream)
+
+    call(y_eager, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(y_graph, torch.cuda.current_stream().cuda_stream)
+    want = y_eager.cpu().numpy().view(np.uint32)
+    for i in range(4):
+        y_graph.fill_(float("nan"))
+        call(y_eager, torch.cuda.current_stream().cuda_stream)  # eager use of the same work buffer
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y_graph.cpu().numpy().view(np.uint32), want), i
