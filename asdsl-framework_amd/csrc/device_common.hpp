@@ -164,49 +164,64 @@ __host__ __device__ inline size_t x_image_bytes(int K, int gs) {
 //    q = 0, scale 0.
 enum class QRule { kRne, kRoundAway };
 
+// One 8-element chunk quantized: split-order int8 (even = elements 0,2,4,6;
+// odd = 1,3,5,7), the group scale, and the integer sum of its 32-element unit.
+struct QChunk {
+    uint32_t even, odd;
+    float scale;
+    int usum;
+    int q[8];
+};
+
 // One thread owns one 8-element chunk; the GS/8 threads of a group are
-// consecutive, aligned lanes of one wave.
+// consecutive, aligned lanes of one wave (all of them must call this).
 template <int GS, QRule R = QRule::kRne>
-__device__ __forceinline__ void quantize_chunk(const float (&v)[8], int chunk, bool active, XImage im,
-                                               int8_t* __restrict__ xq_nat, float* __restrict__ xscale_out) {
+__device__ __forceinline__ QChunk quantize8(const float (&v)[8]) {
     constexpr int kLanes = GS / 8;
+    QChunk c;
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
     const float amax = group_max<kLanes>(m);
-    int q[8];
-    float scale;
     if (amax < (R == QRule::kRne ? 1e-9f : 1e-12f)) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = 0;
-        scale = R == QRule::kRne ? 1.0f : 0.0f;
+        for (int i = 0; i < 8; ++i) c.q[i] = 0;
+        c.scale = R == QRule::kRne ? 1.0f : 0.0f;
     } else {
-        scale = amax * (1.0f / 127.0f);
+        c.scale = amax * (1.0f / 127.0f);
         const float inv = 127.0f / amax;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             if (R == QRule::kRne) {
-                q[i] = sat_rne_i8(v[i] * inv);
+                c.q[i] = sat_rne_i8(v[i] * inv);
             } else {
                 int r = static_cast<int>(__builtin_roundf(v[i] * inv));
-                q[i] = r > 127 ? 127 : (r < -127 ? -127 : r);
+                c.q[i] = r > 127 ? 127 : (r < -127 ? -127 : r);
             }
         }
     }
-    const uint32_t even = pack4_i8(q[0], q[2], q[4], q[6]);
-    const uint32_t odd = pack4_i8(q[1], q[3], q[5], q[7]);
-    const int usum = group_sum<4>(sum4_i8(even) + sum4_i8(odd));  // 4 chunks = 1 unit
+    c.even = pack4_i8(c.q[0], c.q[2], c.q[4], c.q[6]);
+    c.odd = pack4_i8(c.q[1], c.q[3], c.q[5], c.q[7]);
+    c.usum = group_sum<4>(sum4_i8(c.even) + sum4_i8(c.odd));  // 4 chunks = 1 unit
+    return c;
+}
+
+template <int GS, QRule R = QRule::kRne>
+__device__ __forceinline__ void quantize_chunk(const float (&v)[8], int chunk, bool active, XImage im,
+                                               int8_t* __restrict__ xq_nat, float* __restrict__ xscale_out) {
+    constexpr int kLanes = GS / 8;
+    const QChunk c = quantize8<GS, R>(v);
     if (active) {
-        reinterpret_cast<uint2*>(im.xq)[chunk] = make_uint2(even, odd);
+        reinterpret_cast<uint2*>(im.xq)[chunk] = make_uint2(c.even, c.odd);
         if (xq_nat) {
             reinterpret_cast<uint2*>(xq_nat)[chunk] =
-                make_uint2(pack4_i8(q[0], q[1], q[2], q[3]), pack4_i8(q[4], q[5], q[6], q[7]));
+                make_uint2(pack4_i8(c.q[0], c.q[1], c.q[2], c.q[3]), pack4_i8(c.q[4], c.q[5], c.q[6], c.q[7]));
         }
         if ((chunk & (kLanes - 1)) == 0) {
-            im.scale[chunk / kLanes] = scale;
-            if (xscale_out) xscale_out[chunk / kLanes] = scale;
+            im.scale[chunk / kLanes] = c.scale;
+            if (xscale_out) xscale_out[chunk / kLanes] = c.scale;
         }
-        if ((chunk & 3) == 0) im.usum[chunk >> 2] = static_cast<float>(usum) * scale;
+        if ((chunk & 3) == 0) im.usum[chunk >> 2] = static_cast<float>(c.usum) * c.scale;
     }
 }
 

@@ -153,14 +153,19 @@ __global__ __launch_bounds__(kWaves * kWave) void sparse_down_kernel(
     }
 }
 
-// y[o] = part[0][o] + part[1][o] + ... + part[P-1][o], in that order.
-__global__ __launch_bounds__(256) void sparse_down_sum_parts(const float* __restrict__ part, float* __restrict__ y,
-                                                             int out_dim, int nparts) {
-    const int o = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+// y[o] = part[0][o] + part[1][o] + ... + part[P-1][o], in that order.  All P
+// loads are issued before the first add, so the kernel waits on memory once.
+__global__ __launch_bounds__(64) void sparse_down_sum_parts(const float* __restrict__ part, float* __restrict__ y,
+                                                            int out_dim, int nparts) {
+    const int o = static_cast<int>(blockIdx.x) * 64 + static_cast<int>(threadIdx.x);
     if (o >= out_dim) return;
-    float sum = part[o];
-#pragma unroll 8
-    for (int p = 1; p < nparts; ++p) sum += part[static_cast<size_t>(p) * out_dim + o];
+    float v[kMaxParts];
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) v[p] = p < nparts ? part[static_cast<size_t>(p) * out_dim + o] : 0.0f;
+    float sum = v[0];
+#pragma unroll
+    for (int p = 1; p < kMaxParts; ++p)
+        if (p < nparts) sum += v[p];
     y[o] = sum;
 }
 
@@ -206,6 +211,6 @@ extern "C" asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, cons
                                     scales_T, biases_T, sparse_x, active_rows, n_active, pf, in_dim, out_dim,
                                     group_size, nslices, nparts, per_part);
     if (st1 != ASDSL_OK) return st1;
-    return launch("sparse_down_sum_parts", sparse_down_sum_parts, dim3((out_dim + 255) / 256), dim3(256), 0, s,
+    return launch("sparse_down_sum_parts", sparse_down_sum_parts, dim3((out_dim + 63) / 64), dim3(64), 0, s,
                   static_cast<const float*>(pf), y, out_dim, nparts);
 }

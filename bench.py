@@ -238,6 +238,8 @@ def run_suite(args) -> int:
     def measure(name, workload, nbytes, make_copy, launch, out_shape, cpu=None, reps=None, note=None, exact=False):
         """make_copy() -> dict of device tensors; launch(copy, y, h) issues the
         GPU call; cpu(host_copy) -> numpy output or None."""
+        if args.rows and not any(f in name for f in args.rows.split(",")):
+            return
         n = ncopies(nbytes)
         copies = [make_copy() for _ in range(n)]
         y = torch.empty(out_shape, device="cuda", dtype=torch.float32)
@@ -507,6 +509,8 @@ def main() -> int:
                     help="one JSON line per hot-path row: kernel at its workload vs the HBM roofline, "
                          "with the reference's compiled CPU kernel timed on the same inputs")
     ap.add_argument("--cpu-seconds-per-row", type=float, default=1.0)
+    ap.add_argument("--rows", default="", help="--suite: only rows whose name contains one of these "
+                                                "comma-separated strings")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: 50 gate_up GEMVs over rotated weights, then 50 plain "
                          "64 MiB device copies (the counter scale reference); prints nothing else")
