@@ -19,8 +19,9 @@ roofline = the gate_up GEMV kernel: its algorithmic bytes / its average
            gaps between graph nodes are included, so this bounds the kernel
            duration from above).
 cpu_baseline = the reference's own gemv_preq2_fused_avx2 (compiled from its
-           sources into oracle/_ref) on one layer's four GEMVs on the host
-           cores for ~10 s (OpenMP, OMP_NUM_THREADS threads).
+           sources into oracle/_ref) on the layer's four GEMVs, rotating over the
+           same weight sets, on the host cores for ~10 s (OpenMP,
+           OMP_NUM_THREADS threads).
 extra    = lm_head 200064x3072 preq2-g128 GEMV (untimed phase, same graph
            method, two alternating copies of 327 MB).
 
@@ -112,27 +113,29 @@ def build_layers(n_layers: int, seed: int):
     return layers, xs, ys
 
 
-def cpu_baseline(layer0, xs, ys_gpu, seconds: float):
-    """Reference CPU path (oracle/_ref) on one layer; also a parity spot check."""
+def cpu_baseline(layers, xs, ys_gpu, seconds: float):
+    """Reference CPU path (oracle/_ref) over the same rotated layers as the GPU
+    (so the host's last-level cache cannot hold the weights); layer 0's
+    outputs double as a parity spot check."""
     sys.path.insert(0, str(REPO))
     import oracle
 
-    host = {n: (m.cpu().numpy(), q.cpu().numpy()) for n, (m, q) in layer0.items()}
+    host = [{n: (m.cpu().numpy(), q.cpu().numpy()) for n, (m, q) in layer.items()} for layer in layers]
     xh = {n: x.cpu().numpy() for n, x in xs.items()}
     if oracle.reference_available("_native_gemv"):
         ng = oracle.load_reference("_native_gemv")
         kind = "reference"
 
-        def run(n, M, K, y):
-            ng.gemv_preq2_fused_avx2(host[n][0], host[n][1], xh[n], y, M, K, GS)
+        def run(li, n, M, K, y):
+            ng.gemv_preq2_fused_avx2(host[li][n][0], host[li][n][1], xh[n], y, M, K, GS)
     else:
         kind = "port"
 
-        def run(n, M, K, y):
-            y[:] = oracle.gemv_preq2_fused(host[n][0], host[n][1], xh[n], M, K, GS)
+        def run(li, n, M, K, y):
+            y[:] = oracle.gemv_preq2_fused(host[li][n][0], host[li][n][1], xh[n], M, K, GS)
     ys = {n: np.zeros(M, np.float32) for n, M, K in LAYER}
     for n, M, K in LAYER:  # warm-up + parity
-        run(n, M, K, ys[n])
+        run(0, n, M, K, ys[n])
     parity = {}
     for n, M, K in LAYER:
         g = ys_gpu[n]
@@ -140,8 +143,9 @@ def cpu_baseline(layer0, xs, ys_gpu, seconds: float):
     t0 = time.perf_counter()
     steps = 0
     while True:
+        li = steps % len(host)
         for n, M, K in LAYER:
-            run(n, M, K, ys[n])
+            run(li, n, M, K, ys[n])
         steps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
@@ -154,6 +158,7 @@ def cpu_baseline(layer0, xs, ys_gpu, seconds: float):
         "cores": threads,
         "kind": kind,
         "sample": f"{steps} steps of one layer's 4 preq2 g32 GEMVs (gemv_preq2_fused_avx2, OpenMP) "
+                  f"rotating over {len(host)} layers ({len(host) * step_bytes / 1e9:.2f} GB) "
                   f"in {el:.1f} s, ms_per_step={1e3 * el / steps:.3f}",
     }, parity
 
@@ -610,7 +615,7 @@ def main() -> int:
 
     cpu, parity = (None, None)
     if not args.no_cpu:
-        cpu, parity = cpu_baseline(layers[0], xs, ys_host, args.cpu_seconds)
+        cpu, parity = cpu_baseline(layers, xs, ys_host, args.cpu_seconds)
 
     out = {
         "metric": METRIC,
