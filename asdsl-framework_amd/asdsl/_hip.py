@@ -56,8 +56,15 @@ SIGNATURES: dict[str, list] = {
     "asdsl_gemv_sparse_unpacked": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_sparse_down_proj_T": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P],
     "asdsl_gemv_sparse_with_indices": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P],
+    "asdsl_gemv_preq2_rmsnorm": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P],
+    "asdsl_gemv_preq2_swiglu": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
+    "asdsl_attention_work_floats": [_I, _I],
+    "asdsl_attention_f16kv": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "asdsl_decode_work_bytes": [_P],
+    "asdsl_decode_token": [_P, _P, _P, _P, _P, _P],
 }
-_RESTYPE = {"asdsl_last_error": ctypes.c_char_p}
+_RESTYPE = {"asdsl_last_error": ctypes.c_char_p, "asdsl_attention_work_floats": ctypes.c_size_t,
+            "asdsl_decode_work_bytes": ctypes.c_size_t}
 
 
 class HipLibraryMissing(ImportError):

@@ -1,0 +1,239 @@
+"""Greedy batch-1 decode of a Phi-4-shaped model on the GPU.
+
+Mirrors the reference's UnifiedEngine::forward_token
+(asdsl/kernels/native/unified_engine.cpp:1339-1688, driven from Python by
+asdsl/inference/unified_bridge.py): one call embeds a token, runs every
+decoder layer at a position and produces the logits and the greedy next
+token.  The whole step is one C-ABI call (asdsl_decode_token) that queues
+6 kernels per layer; the token id and position live in device memory, so a
+HIP graph of one step replays token after token.
+
+Weights are preq2 Q4 (attention projections at group size 32, the MLP and
+lm_head at 128 by default), norms fp32, embeddings and the KV cache fp16.
+``DecodeEngine.synthetic`` builds a model with random weights of the given
+shape (W ~ N(0, 0.02) quantized, embeddings ~ N(0, 1), norm weights 1 + N(0, 0.1)).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from asdsl import _hip
+
+
+@dataclass
+class DecodeConfig:
+    """Model shape (Phi-4 defaults, experiments/phi4_cpu_run.py:316-334)."""
+
+    hidden: int = 3072
+    ffn: int = 8192
+    vocab: int = 200064
+    n_layers: int = 32
+    n_heads: int = 24
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    rotary_dim: int = 96
+    max_seq: int = 4352
+    gs_attn: int = 32
+    gs_ffn: int = 128
+    gs_lm: int = 128
+    rms_eps: float = 1e-5
+    rope_theta: float = 10000.0
+
+    @property
+    def qkv_dim(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "qkv_meta", "qkv_quant", "o_meta", "o_quant", "gu_meta", "gu_quant", "down_meta", "down_quant",
+        "rms_att", "rms_ffn", "k_cache", "v_cache")] + [("fatrelu_threshold", ctypes.c_float)]
+
+
+class _Model(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "hidden", "ffn", "vocab", "n_layers", "n_heads", "n_kv_heads", "head_dim", "rotary_dim", "max_seq",
+        "gs_attn", "gs_ffn", "gs_lm")] + [("rms_eps", ctypes.c_float), ("layers", ctypes.POINTER(_Layer))] + [
+        (n, ctypes.c_void_p) for n in ("embed", "rms_out", "lm_meta", "lm_quant", "rope_cos", "rope_sin")]
+
+
+def rope_tables(max_seq: int, rotary_dim: int, theta: float = 10000.0) -> tuple[np.ndarray, np.ndarray]:
+    """cos/sin[pos][i] = cos/sin(pos * theta^(-2i/rotary_dim)) computed in float64,
+    stored fp32 (the reference's _build_rope_native_tables,
+    experiments/phi4_cpu_run.py:3318-3344)."""
+    half = rotary_dim // 2
+    i = np.arange(half, dtype=np.float64)
+    freq = 1.0 / (theta ** (2.0 * i / rotary_dim))
+    ang = np.arange(max_seq, dtype=np.float64)[:, None] * freq[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+# names of the per-layer matrices: (rows, cols, group size attribute)
+def _layer_mats(cfg: DecodeConfig):
+    return {"qkv": (cfg.qkv_dim, cfg.hidden, cfg.gs_attn), "o": (cfg.hidden, cfg.n_heads * cfg.head_dim, cfg.gs_attn),
+            "gu": (2 * cfg.ffn, cfg.hidden, cfg.gs_ffn), "down": (cfg.hidden, cfg.ffn, cfg.gs_ffn)}
+
+
+class DecodeEngine:
+    """Holds the device weights, KV caches and step buffers of one model."""
+
+    def __init__(self, cfg: DecodeConfig, layers: list[dict], embed, rms_out, lm_meta, lm_quant,
+                 fatrelu_threshold: float = 0.0):
+        import torch
+
+        self.cfg = cfg
+        dev = _hip.device()
+        self.layers = layers
+        self.embed, self.rms_out, self.lm_meta, self.lm_quant = embed, rms_out, lm_meta, lm_quant
+        cos, sin = rope_tables(cfg.max_seq, cfg.rotary_dim, cfg.rope_theta)
+        self.rope_cos = torch.from_numpy(cos).to(dev)
+        self.rope_sin = torch.from_numpy(sin).to(dev)
+        for L in layers:
+            if "k_cache" not in L:
+                L["k_cache"] = torch.zeros((cfg.n_kv_heads, cfg.max_seq, cfg.head_dim), dtype=torch.float16, device=dev)
+                L["v_cache"] = torch.zeros_like(L["k_cache"])
+        self._c_layers = (_Layer * cfg.n_layers)()
+        for i, L in enumerate(layers):
+            c = self._c_layers[i]
+            for n in ("qkv", "o", "gu", "down"):
+                setattr(c, f"{n}_meta", _hip.ptr(L[n][0]))
+                setattr(c, f"{n}_quant", _hip.ptr(L[n][1]))
+            c.rms_att, c.rms_ffn = _hip.ptr(L["rms_att"]), _hip.ptr(L["rms_ffn"])
+            c.k_cache, c.v_cache = _hip.ptr(L["k_cache"]), _hip.ptr(L["v_cache"])
+            c.fatrelu_threshold = float(fatrelu_threshold)
+        m = _Model()
+        for n in ("hidden", "ffn", "vocab", "n_layers", "n_heads", "n_kv_heads", "head_dim", "rotary_dim",
+                  "max_seq", "gs_attn", "gs_ffn", "gs_lm"):
+            setattr(m, n, int(getattr(cfg, n)))
+        m.rms_eps = float(cfg.rms_eps)
+        m.layers = ctypes.cast(self._c_layers, ctypes.POINTER(_Layer))
+        m.embed, m.rms_out = _hip.ptr(embed), _hip.ptr(rms_out)
+        m.lm_meta, m.lm_quant = _hip.ptr(lm_meta), _hip.ptr(lm_quant)
+        m.rope_cos, m.rope_sin = _hip.ptr(self.rope_cos), _hip.ptr(self.rope_sin)
+        self._model = m
+        nbytes = _hip.LIB.asdsl_decode_work_bytes(ctypes.byref(m))
+        if nbytes == 0:
+            raise ValueError(f"invalid decode model: {_hip.last_error()}")
+        self.work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.logits = torch.empty(cfg.vocab, dtype=torch.float32, device=dev)
+        self._graph = None
+
+    # ------------------------------------------------------------ building
+    @classmethod
+    def synthetic(cls, cfg: DecodeConfig, seed: int = 0, fatrelu_threshold: float = 0.0) -> "DecodeEngine":
+        import torch
+
+        from asdsl.quantization.synthetic import preq2_from_weights_torch
+
+        dev = _hip.device()
+        gen = torch.Generator(device=dev).manual_seed(seed)
+
+        def packed(rows, cols, gs):
+            w = torch.randn((rows, cols), generator=gen, device=dev, dtype=torch.float32) * 0.02
+            out = preq2_from_weights_torch(w, gs)
+            del w
+            return out
+
+        def norm_w():
+            return 1.0 + 0.1 * torch.randn(cfg.hidden, generator=gen, device=dev, dtype=torch.float32)
+
+        layers = []
+        for _ in range(cfg.n_layers):
+            L = {n: packed(r, c, g) for n, (r, c, g) in _layer_mats(cfg).items()}
+            L["rms_att"], L["rms_ffn"] = norm_w(), norm_w()
+            layers.append(L)
+        embed = torch.randn((cfg.vocab, cfg.hidden), generator=gen, device=dev, dtype=torch.float32).half()
+        lm_meta, lm_quant = packed(cfg.vocab, cfg.hidden, cfg.gs_lm)
+        return cls(cfg, layers, embed, norm_w(), lm_meta, lm_quant, fatrelu_threshold)
+
+    def prefill_kv_random(self, ctx: int, seed: int = 1) -> None:
+        """Positions [0, ctx) of every layer's cache ~ N(0, 1) in fp16; the
+        next step decodes at position ctx."""
+        import torch
+
+        if not 0 <= ctx < self.cfg.max_seq:
+            raise ValueError(f"ctx must be in [0, {self.cfg.max_seq})")
+        gen = torch.Generator(device=_hip.device()).manual_seed(seed)
+        for L in self.layers:
+            for n in ("k_cache", "v_cache"):
+                L[n].zero_()
+                if ctx:
+                    L[n][:, :ctx] = torch.randn((self.cfg.n_kv_heads, ctx, self.cfg.head_dim), generator=gen,
+                                                device=L[n].device, dtype=torch.float32).half()
+        self.pos.fill_(ctx)
+
+    # ------------------------------------------------------------ stepping
+    def _queue_step(self, stream: int) -> None:
+        _hip.check(_hip.LIB.asdsl_decode_token(ctypes.byref(self._model), _hip.ptr(self.token), _hip.ptr(self.pos),
+                                               _hip.ptr(self.logits), _hip.ptr(self.work), stream),
+                   "asdsl_decode_token")
+
+    def forward_token(self, token_id: int, pos: int):
+        """Reference: UnifiedEngine::forward_token(token_id, pos, logits).
+        Returns the logits (device tensor); ``next_token()`` is their argmax."""
+        if not 0 <= token_id < self.cfg.vocab:
+            raise ValueError("forward_token: token_id out of vocab range")
+        if not 0 <= pos < self.cfg.max_seq:
+            raise ValueError("forward_token: pos out of kv-cache range")
+        self.token.fill_(token_id)
+        self.pos.fill_(pos)
+        self._queue_step(_hip.stream_handle())
+        return self.logits
+
+    def next_token(self) -> int:
+        return int(self.token.item())
+
+    def capture(self) -> None:
+        """HIP graph of one step (token and position advance on the device)."""
+        import torch
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        tok, pos = self.token.clone(), self.pos.clone()
+        with torch.cuda.stream(side):
+            self._queue_step(int(side.cuda_stream))  # warm-up (also the library's one-time set-up)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.token.copy_(tok)
+        self.pos.copy_(pos)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._queue_step(int(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        self.token.copy_(tok)
+        self.pos.copy_(pos)
+        self._graph = g
+
+    def step(self) -> None:
+        """One captured step: consumes self.token at self.pos, leaves the next
+        greedy token and pos + 1."""
+        if self._graph is None:
+            self.capture()
+        self._graph.replay()
+
+    # ------------------------------------------------------------ accounting
+    def weight_bytes(self) -> int:
+        n = 0
+        for L in self.layers:
+            for k in ("qkv", "o", "gu", "down"):
+                n += L[k][0].numel() + L[k][1].numel()
+            n += 2 * 4 * self.cfg.hidden
+        return n + self.lm_meta.numel() + self.lm_quant.numel() + 4 * self.cfg.hidden
+
+    def bytes_per_token(self, pos: int) -> int:
+        """HBM bytes one step must move at position pos: every weight once,
+        the K and V cache rows of positions 0..pos (fp16), one embedding row;
+        activations and logits are included for completeness."""
+        c = self.cfg
+        kv = c.n_layers * 2 * c.n_kv_heads * (pos + 1) * c.head_dim * 2
+        return self.weight_bytes() + kv + 2 * c.hidden + 4 * c.vocab
+
+
+def ideal_tokens_per_s(bytes_per_token: int, peak_gbs: float = 8000.0) -> float:
+    return peak_gbs * 1e9 / bytes_per_token

@@ -41,13 +41,83 @@ namespace {
 
 constexpr int kThreads = 256;  // helper kernels
 
-template <int GS, int NU, int WAVES, int NCH, bool Q8, bool EXACT, bool XREG>
+// Decode-step work fused into the GEMV's activation prologue / epilogue.
+//   kNorm:   h = x (+ delta); workgroup 0 writes h to h_out (the new residual
+//            stream); the GEMV input is rmsnorm(h) = (h * inv_rms) * nw with
+//            inv_rms = 1/sqrt(sum(h^2)/K + eps)
+//            (residual_add_rmsnorm_f32 / rmsnorm_f32, unified_engine.cpp:499-524,651-688).
+//   kSwiglu: the GEMV input is silu(x) * up, zeroed where |value| < thr when
+//            thr > 0 (swiglu_inplace with fast_exp_avx2, unified_engine.cpp:803-857).
+//   ARGMAX:  the largest output and its row (first on ties, as argmax_f32_avx2,
+//            unified_engine.cpp:207-233) are folded into *amax with a 64-bit
+//            atomicMax: key = order-preserving float bits << 32 | ~row, so the
+//            result does not depend on workgroup order.  *amax must be zero
+//            before the launch.
+enum class Pro { kPlain, kNorm, kSwiglu };
+
+struct ProArgs {
+    const float* delta = nullptr;
+    const float* nw = nullptr;
+    float* h_out = nullptr;
+    const float* up = nullptr;
+    unsigned long long* amax = nullptr;
+    float eps = 0.0f;
+    float thr = 0.0f;
+};
+
+// The reference's exp polynomial (fast_exp_avx2, unified_engine.cpp:781-801):
+// clamp to [-87.3, 87.3], x*log2(e) split into round-to-nearest integer i and
+// fraction f, 2^f by a degree-5 polynomial, 2^i by exponent bits.
+__device__ __forceinline__ float fast_exp_ref(float x) {
+    x = fmaxf(x, -87.3f);
+    x = fminf(x, 87.3f);
+    x = x * 1.4426950408889634f;
+    const float fi = __builtin_rintf(x);
+    const int i = static_cast<int>(fi);
+    const float f = x - fi;
+    float p = fmaf(0.001333838100523091f, f, 0.009618129107628477f);
+    p = fmaf(p, f, 0.05550410866482158f);
+    p = fmaf(p, f, 0.2402265069591007f);
+    p = fmaf(p, f, 0.6931471805599453f);
+    p = fmaf(p, f, 1.0f);
+    return p * __builtin_bit_cast(float, (i + 127) << 23);
+}
+
+__device__ __forceinline__ float swiglu_ref(float g, float u, float thr) {
+    const float sigmoid = 1.0f / (1.0f + fast_exp_ref(0.0f - g));
+    float v = (g * sigmoid) * u;
+    if (thr > 0.0f && !(fabsf(v) >= thr)) v = 0.0f;
+    return v;
+}
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (static_cast<unsigned long long>(k) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(row));
+}
+
+template <int WAVES>
+__device__ __forceinline__ float block_sum_fixed(float v, float* s_red) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    if ((threadIdx.x & (kWave - 1)) == 0) s_red[wave] = v;
+    __syncthreads();
+    float t = s_red[0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) t += s_red[w];
+    return t;
+}
+
+template <int GS, int NU, int WAVES, int NCH, bool Q8, bool EXACT, bool XREG, Pro PRO = Pro::kPlain,
+          bool ARGMAX = false>
 __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_t* __restrict__ meta,
                                                                   const uint4* __restrict__ quant,
                                                                   const float* __restrict__ x,
                                                                   const int8_t* __restrict__ xq8,
                                                                   const float* __restrict__ xsc,
-                                                                  float* __restrict__ y, int M, int K, int lks) {
+                                                                  float* __restrict__ y, int M, int K, int lks,
+                                                                  ProArgs pa) {
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ float s_part[2][WAVES][4];
     constexpr int UPS = GS / 32;       // units per (row, group)
@@ -109,7 +179,63 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     const int tile_step = static_cast<int>(gridDim.x);
     ActStage<GS, WAVES * kWave, NCH, Q8> act;
     act.load(x, xq8, xsc, K);  // activation loads first: they retire first
+    constexpr int NX = PRO == Pro::kPlain ? 1 : NCH;
+    float ex[NX][8], ew[NX][8];  // kNorm: delta, norm weight; kSwiglu: up
+    const int nchunk = K >> 3;
+    const int tid = static_cast<int>(threadIdx.x);
+    if constexpr (PRO != Pro::kPlain) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = min(i * WAVES * kWave + tid, nchunk - 1);
+            const float* src0 = PRO == Pro::kNorm ? pa.delta : pa.up;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ex[i][e] = 0.0f;
+            if (src0) {
+                const float4 a = reinterpret_cast<const float4*>(src0)[2 * c];
+                const float4 b = reinterpret_cast<const float4*>(src0)[2 * c + 1];
+                ex[i][0] = a.x; ex[i][1] = a.y; ex[i][2] = a.z; ex[i][3] = a.w;
+                ex[i][4] = b.x; ex[i][5] = b.y; ex[i][6] = b.z; ex[i][7] = b.w;
+            }
+            if constexpr (PRO == Pro::kNorm) {
+                const float4 a = reinterpret_cast<const float4*>(pa.nw)[2 * c];
+                const float4 b = reinterpret_cast<const float4*>(pa.nw)[2 * c + 1];
+                ew[i][0] = a.x; ew[i][1] = a.y; ew[i][2] = a.z; ew[i][3] = a.w;
+                ew[i][4] = b.x; ew[i][5] = b.y; ew[i][6] = b.z; ew[i][7] = b.w;
+            }
+        }
+    }
     load_tile(tile);           // grid <= ntiles, so this tile exists
+    if constexpr (PRO == Pro::kNorm) {
+        __shared__ float s_red[WAVES];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = i * WAVES * kWave + tid;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) act.v[i][e] += ex[i][e];
+            if (c < nchunk) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss = fmaf(act.v[i][e], act.v[i][e], ss);
+                if (pa.h_out && blockIdx.x == 0) {
+                    reinterpret_cast<float4*>(pa.h_out)[2 * c] =
+                        make_float4(act.v[i][0], act.v[i][1], act.v[i][2], act.v[i][3]);
+                    reinterpret_cast<float4*>(pa.h_out)[2 * c + 1] =
+                        make_float4(act.v[i][4], act.v[i][5], act.v[i][6], act.v[i][7]);
+                }
+            }
+        }
+        ss = block_sum_fixed<WAVES>(ss, s_red);
+        const float inv_rms = 1.0f / sqrtf(ss / static_cast<float>(K) + pa.eps);
+#pragma unroll
+        for (int i = 0; i < NCH; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) act.v[i][e] = (act.v[i][e] * inv_rms) * ew[i][e];
+    } else if constexpr (PRO == Pro::kSwiglu) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) act.v[i][e] = swiglu_ref(act.v[i][e], ex[i][e], pa.thr);
+    }
     act.process(K, im);        // quantize while the weights are in flight
     __syncthreads();
 
@@ -133,6 +259,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     }
 
     int parity = 0;
+    unsigned long long best = 0;  // ARGMAX: this thread's largest key
     for (; tile < ntiles; tile += tile_step) {  // uniform per workgroup
         float acc = 0.0f;
 #pragma unroll
@@ -156,7 +283,10 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
         if (tile + tile_step < ntiles) load_tile(tile + tile_step);
         const int row = band * 4 + slot;
         if (lks == 0) {
-            if (writer && band < nbands && row < M) y[row] = acc;
+            if (writer && band < nbands && row < M) {
+                y[row] = acc;
+                if constexpr (ARGMAX) best = max(best, argmax_key(acc, row));
+            }
         } else {
             if (writer) s_part[parity][wave][slot] = acc;
             __syncthreads();
@@ -164,8 +294,29 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
                 float sum = s_part[parity][wave][slot];
                 for (int k = 1; k < KS; ++k) sum += s_part[parity][wave + k][slot];
                 y[row] = sum;
+                if constexpr (ARGMAX) best = max(best, argmax_key(sum, row));
             }
             parity ^= 1;
+        }
+    }
+    if constexpr (ARGMAX) {
+        // max is order-free: any reduction order gives the same key.  One
+        // atomic per workgroup (one per wave serialized on the single address:
+        // measured 2x the whole lm_head).
+        __shared__ unsigned long long s_best[WAVES];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const uint32_t lo = __shfl_xor(static_cast<uint32_t>(best), o, kWave);
+            const uint32_t hi = __shfl_xor(static_cast<uint32_t>(best >> 32), o, kWave);
+            best = max(best, (static_cast<unsigned long long>(hi) << 32) | lo);
+        }
+        if (lane == 0) s_best[wave] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long b = s_best[0];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) b = max(b, s_best[w]);
+            if (b != 0) atomicMax(pa.amax, b);
         }
     }
 }
@@ -302,16 +453,16 @@ Plan plan_preq2(int M, int K, int cus) {
     return p;
 }
 
-template <int GS, int WAVES, int NCH, bool Q8, bool EXACT>
+template <int GS, int WAVES, int NCH, bool Q8, bool EXACT, Pro PRO = Pro::kPlain, bool ARGMAX = false>
 asdsl_status launch_exact(const Plan& p, const uint32_t* m, const uint4* q, const float* x, const int8_t* xq8,
-                          const float* xsc, float* y, int M, int K, hipStream_t stream) {
+                          const float* xsc, float* y, int M, int K, hipStream_t stream, const ProArgs& pa = ProArgs{}) {
     constexpr bool XREG = true;
     const size_t lds = x_image_bytes(K, GS);
     const dim3 block(WAVES * kWave);
-#define ASDSL_PREQ2_NU(N)                                                                                      \
-    case N:                                                                                                    \
-        return launch("preq2_gemv_kernel", preq2_gemv_kernel<GS, N, WAVES, NCH, Q8, EXACT, XREG>, dim3(p.grid), \
-                      block, lds, stream, m, q, x, xq8, xsc, y, M, K, p.lks);
+#define ASDSL_PREQ2_NU(N)                                                                                       \
+    case N:                                                                                                     \
+        return launch("preq2_gemv_kernel", preq2_gemv_kernel<GS, N, WAVES, NCH, Q8, EXACT, XREG, PRO, ARGMAX>,   \
+                      dim3(p.grid), block, lds, stream, m, q, x, xq8, xsc, y, M, K, p.lks, pa);
     switch (p.nu) {
         ASDSL_PREQ2_NU(1)
         ASDSL_PREQ2_NU(2)
@@ -323,11 +474,22 @@ asdsl_status launch_exact(const Plan& p, const uint32_t* m, const uint4* q, cons
 #undef ASDSL_PREQ2_NU
 }
 
-template <int GS, int WAVES, int NCH, bool Q8>
+template <int GS, int WAVES, int NCH, bool Q8, Pro PRO = Pro::kPlain, bool ARGMAX = false>
 asdsl_status launch_waves(const Plan& p, const uint32_t* m, const uint4* q, const float* x, const int8_t* xq8,
-                          const float* xsc, float* y, int M, int K, hipStream_t stream) {
-    if (p.exact) return launch_exact<GS, WAVES, NCH, Q8, true>(p, m, q, x, xq8, xsc, y, M, K, stream);
-    return launch_exact<GS, WAVES, NCH, Q8, false>(p, m, q, x, xq8, xsc, y, M, K, stream);
+                          const float* xsc, float* y, int M, int K, hipStream_t stream, const ProArgs& pa = ProArgs{}) {
+    if (p.exact) return launch_exact<GS, WAVES, NCH, Q8, true, PRO, ARGMAX>(p, m, q, x, xq8, xsc, y, M, K, stream, pa);
+    return launch_exact<GS, WAVES, NCH, Q8, false, PRO, ARGMAX>(p, m, q, x, xq8, xsc, y, M, K, stream, pa);
+}
+
+// Decode-step variants (fp32 activation, one chunk per thread: K <= 8192).
+template <int GS, Pro PRO, bool ARGMAX>
+asdsl_status launch_preq2_fused(const uint8_t* meta, const uint8_t* quant, const float* x, float* y, int M, int K,
+                                const ProArgs& pa, hipStream_t stream, int cus) {
+    const Plan p = plan_preq2(M, K, cus);
+    const auto* m = reinterpret_cast<const uint32_t*>(meta);
+    const auto* q = reinterpret_cast<const uint4*>(quant);
+    if (p.waves == 8) return launch_waves<GS, 8, 1, false, PRO, ARGMAX>(p, m, q, x, nullptr, nullptr, y, M, K, stream, pa);
+    return launch_waves<GS, 16, 1, false, PRO, ARGMAX>(p, m, q, x, nullptr, nullptr, y, M, K, stream, pa);
 }
 
 template <int GS, bool Q8>
@@ -358,6 +520,48 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused(const uint8_t* meta, const uint8_
     if (group_size == 32)
         return launch_preq2<32, false>(meta, quant, x, nullptr, nullptr, y, out_features, in_features, as_hip(stream), cus);
     return launch_preq2<128, false>(meta, quant, x, nullptr, nullptr, y, out_features, in_features, as_hip(stream), cus);
+}
+
+extern "C" asdsl_status asdsl_gemv_preq2_rmsnorm(const uint8_t* meta, const uint8_t* quant, const float* h_in,
+                                                 const float* delta, const float* norm_w, float* h_out, float* y,
+                                                 int out_features, int in_features, int group_size, float eps,
+                                                 unsigned long long* argmax_key, asdsl_stream_t stream) {
+    if (check_preq2_args(meta, quant, h_in, y, out_features, in_features, group_size, "gemv_preq2_rmsnorm"))
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    ASDSL_CHECK_ARG(norm_w != nullptr, "gemv_preq2_rmsnorm: null norm weight");
+    ASDSL_CHECK_ARG(in_features <= 8192, "gemv_preq2_rmsnorm: in_features must be <= 8192");
+    ASDSL_CHECK_ARG(h_out == nullptr || (h_out != h_in && h_out != delta),
+                    "gemv_preq2_rmsnorm: h_out must not alias h_in or delta (other workgroups still read them)");
+    ASDSL_CU_COUNT(cus);
+    ProArgs pa;
+    pa.delta = delta;
+    pa.nw = norm_w;
+    pa.h_out = h_out;
+    pa.eps = eps;
+    pa.amax = argmax_key;
+    hipStream_t s = as_hip(stream);
+    const int M = out_features, K = in_features;
+    if (group_size == 32)
+        return argmax_key ? launch_preq2_fused<32, Pro::kNorm, true>(meta, quant, h_in, y, M, K, pa, s, cus)
+                          : launch_preq2_fused<32, Pro::kNorm, false>(meta, quant, h_in, y, M, K, pa, s, cus);
+    return argmax_key ? launch_preq2_fused<128, Pro::kNorm, true>(meta, quant, h_in, y, M, K, pa, s, cus)
+                      : launch_preq2_fused<128, Pro::kNorm, false>(meta, quant, h_in, y, M, K, pa, s, cus);
+}
+
+extern "C" asdsl_status asdsl_gemv_preq2_swiglu(const uint8_t* meta, const uint8_t* quant, const float* gate_up,
+                                                float* y, int out_features, int in_features, int group_size,
+                                                float threshold, asdsl_stream_t stream) {
+    if (check_preq2_args(meta, quant, gate_up, y, out_features, in_features, group_size, "gemv_preq2_swiglu"))
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    ASDSL_CHECK_ARG(in_features <= 8192, "gemv_preq2_swiglu: in_features must be <= 8192");
+    ASDSL_CU_COUNT(cus);
+    ProArgs pa;
+    pa.up = gate_up + in_features;
+    pa.thr = threshold;
+    hipStream_t s = as_hip(stream);
+    if (group_size == 32)
+        return launch_preq2_fused<32, Pro::kSwiglu, false>(meta, quant, gate_up, y, out_features, in_features, pa, s, cus);
+    return launch_preq2_fused<128, Pro::kSwiglu, false>(meta, quant, gate_up, y, out_features, in_features, pa, s, cus);
 }
 
 extern "C" asdsl_status asdsl_gemv_preq2(const uint8_t* meta, const uint8_t* quant, const int8_t* x_q8,

@@ -197,6 +197,53 @@ def lm_head_kernel(lib, capture, timed_replays):
             "frac_of_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+# --------------------------------------------------------------------------- decode
+def decode_tokens_per_s(contexts=(128, 1024, 4096), steps: int = 64, n_layers: int = 32, seed: int = 11):
+    """Greedy batch-1 decode of a Phi-4-shaped model (32 layers, hidden 3072,
+    FFN 8192, vocab 200064, 24/8 heads, head_dim 128; qkv/o preq2 g32,
+    gate_up/down/lm_head preq2 g128; random weights) at each context length:
+    the KV cache holds `ctx` random fp16 positions, then `steps` captured
+    steps replay back to back (each consumes the previous step's argmax and
+    advances the position).  bytes/token = every weight once + the K/V rows
+    read (fp16) + one embedding row + the logits."""
+    import torch
+
+    from asdsl.engine import DecodeConfig, DecodeEngine
+
+    cfg = DecodeConfig(n_layers=n_layers, max_seq=max(contexts) + steps + 8)
+    eng = DecodeEngine.synthetic(cfg, seed=seed)
+    out = {"model": "phi4-shaped 32L h3072 ffn8192 v200064 24/8 heads, preq2 g32 attn / g128 mlp+lm_head, fp16 KV",
+           "weight_bytes": eng.weight_bytes(), "steps_per_ctx": steps, "per_ctx": {}}
+    for ctx in contexts:
+        eng.prefill_kv_random(ctx, seed=ctx)
+        eng.token.fill_(1)
+        eng.capture()
+        eng.step()  # warm
+        torch.cuda.synchronize()
+        eng.prefill_kv_random(ctx, seed=ctx)
+        eng.token.fill_(1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            eng.step()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1e3 * e0.elapsed_time(e1) / steps
+        mid = ctx + steps // 2
+        bpt = eng.bytes_per_token(mid)
+        tps = 1e6 / us
+        ideal = HBM_PEAK_GBS * 1e9 / bpt
+        out["per_ctx"][str(ctx)] = {"us_per_token": round(us, 2), "tokens_per_s": round(tps, 1),
+                                    "bytes_per_token": bpt, "GB/s": round(bpt / (us * 1e-6) / 1e9, 1),
+                                    "roofline_tokens_per_s": round(ideal, 1), "frac_of_roofline": round(tps / ideal, 4),
+                                    "final_pos": int(eng.pos.item())}
+        eng._graph = None
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
 # --------------------------------------------------------------------------- suite
 def _dev_bytes(n, gen, valid_f16_pairs=False):
     """n random device bytes; with valid_f16_pairs every 16-bit half is a
@@ -510,6 +557,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the 32-layer decode tokens/s measurement")
+    ap.add_argument("--decode", action="store_true", help="only the decode tokens/s measurement (one JSON line)")
     ap.add_argument("--suite", action="store_true",
                     help="one JSON line per hot-path row: kernel at its workload vs the HBM roofline, "
                          "with the reference's compiled CPU kernel timed on the same inputs")
@@ -527,6 +576,11 @@ def main() -> int:
 
     if args.suite:
         return run_suite(args)
+    if args.decode:
+        import torch  # noqa: F401
+
+        print(json.dumps({"decode": decode_tokens_per_s()}), flush=True)
+        return 0
 
     import torch
 
@@ -616,6 +670,10 @@ def main() -> int:
     cpu, parity = (None, None)
     if not args.no_cpu:
         cpu, parity = cpu_baseline(layers, xs, ys_host, args.cpu_seconds)
+    if not args.no_decode:
+        del layers
+        torch.cuda.empty_cache()
+        extra["decode"] = decode_tokens_per_s()
 
     out = {
         "metric": METRIC,

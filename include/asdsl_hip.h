@@ -260,6 +260,86 @@ asdsl_status asdsl_dequant_preq2(const uint8_t* meta, const uint8_t* quant, floa
                                  int out_features, int in_features, int group_size,
                                  asdsl_stream_t stream);
 
+/* ------------------------------------------------------------------ A13 ---
+ * Batch-1 decode step (the glue around the GEMVs).
+ *
+ * preq2 GEMV whose fp32 input is rmsnorm(h) with h = h_in + delta (delta may
+ * be NULL): inv_rms = 1/sqrt(sum(h^2)/K + eps), x = (h*inv_rms)*norm_w, then
+ * quantized inside as asdsl_gemv_preq2_fused.  If h_out is not NULL, h is
+ * stored there (the new residual stream; must not alias h_in or delta).  If
+ * argmax_key is not NULL (zeroed before the call), the largest y and its row
+ * (first on ties) are folded into it: key = order-preserving float bits << 32
+ * | (0xFFFFFFFF - row).  in_features <= 8192.
+ * Replaces residual_add_rmsnorm_f32 / rmsnorm_f32 + the fused preq GEMV and
+ * argmax_f32_avx2 (asdsl/kernels/native/unified_engine.cpp:499-524,651-688,207-233,
+ * call sites 1377-1421,1521-1528,1634-1648). */
+asdsl_status asdsl_gemv_preq2_rmsnorm(const uint8_t* meta, const uint8_t* quant, const float* h_in,
+                                      const float* delta, const float* norm_w, float* h_out, float* y,
+                                      int out_features, int in_features, int group_size, float eps,
+                                      unsigned long long* argmax_key, asdsl_stream_t stream);
+
+/* preq2 GEMV whose fp32 input is swiglu(gate_up[0:K], gate_up[K:2K]):
+ * v = (g * 1/(1 + exp(-g))) * u with the reference's polynomial exp, zeroed
+ * where |v| < threshold if threshold > 0 (FATReLU).  in_features <= 8192.
+ * Replaces swiglu_inplace + the down GEMV (unified_engine.cpp:781-857, call
+ * sites 1581-1628). */
+asdsl_status asdsl_gemv_preq2_swiglu(const uint8_t* meta, const uint8_t* quant, const float* gate_up,
+                                     float* y, int out_features, int in_features, int group_size,
+                                     float threshold, asdsl_stream_t stream);
+
+/* Floats of device work buffer asdsl_attention_f16kv needs. */
+size_t asdsl_attention_work_floats(int n_heads, int max_seq);
+
+/* RoPE + KV write + attention for one token at position *pos (device int):
+ * qkv = [q n_heads*128 | k n_kv_heads*128 | v n_kv_heads*128] fp32.  RoPE
+ * rotates the first rotary_dim dims of every q and k head, half split
+ * (x[i], x[i+rotary_dim/2]) with rope_cos/rope_sin[pos][rotary_dim/2].  The new
+ * k, v are rounded to fp16 and stored at [kv_head][pos] of the caches
+ * (fp16 [n_kv_heads][max_seq][128]); att_out[h] = softmax(q_h.K/sqrt(128)) V
+ * over positions 0..pos of kv head h / (n_heads/n_kv_heads).  head_dim = 128.
+ * Replaces rope_apply_inplace + set_kv_cache + compute_attention_flash_q8
+ * (unified_engine.cpp:768-801,859-1027), with an fp16 instead of int8 cache. */
+asdsl_status asdsl_attention_f16kv(const float* qkv, uint16_t* k_cache, uint16_t* v_cache,
+                                   const float* rope_cos, const float* rope_sin, const int* pos,
+                                   float* att_out, float* work, int n_heads, int n_kv_heads,
+                                   int head_dim, int rotary_dim, int max_seq, asdsl_stream_t stream);
+
+/* Weights of one decoder layer (device pointers). */
+typedef struct asdsl_decode_layer {
+    const uint8_t* qkv_meta;  const uint8_t* qkv_quant;   /* preq2, [(h + 2 kv) * 128] x hidden, gs_attn */
+    const uint8_t* o_meta;    const uint8_t* o_quant;     /* preq2, hidden x hidden, gs_attn */
+    const uint8_t* gu_meta;   const uint8_t* gu_quant;    /* preq2, [gate ffn | up ffn] x hidden, gs_ffn */
+    const uint8_t* down_meta; const uint8_t* down_quant;  /* preq2, hidden x ffn, gs_ffn */
+    const float* rms_att;     const float* rms_ffn;       /* [hidden] */
+    uint16_t* k_cache;        uint16_t* v_cache;          /* fp16 [n_kv_heads][max_seq][128] */
+    float fatrelu_threshold;                              /* 0: plain SwiGLU */
+} asdsl_decode_layer;
+
+/* A Phi-4-shaped decoder (layers is a HOST array of n_layers entries). */
+typedef struct asdsl_decode_model {
+    int hidden, ffn, vocab, n_layers, n_heads, n_kv_heads, head_dim, rotary_dim, max_seq;
+    int gs_attn, gs_ffn, gs_lm;                           /* preq2 group sizes: 32 or 128 */
+    float rms_eps;
+    const asdsl_decode_layer* layers;
+    const uint16_t* embed;                                /* fp16 [vocab][hidden] */
+    const float* rms_out;                                 /* [hidden] */
+    const uint8_t* lm_meta;   const uint8_t* lm_quant;    /* preq2, vocab x hidden, gs_lm */
+    const float* rope_cos;    const float* rope_sin;      /* fp32 [max_seq][rotary_dim/2] */
+} asdsl_decode_model;
+
+/* Bytes of device work buffer asdsl_decode_token needs (0 for an invalid model). */
+size_t asdsl_decode_work_bytes(const asdsl_decode_model* model);
+
+/* Queues one greedy decode step on `stream`: embeds *token (device int),
+ * runs every layer at position *pos (device int), writes logits[vocab], then
+ * sets *token to the argmax and increments *pos.  Nothing else changes on
+ * the host side between steps, so a HIP graph of one call replays step after
+ * step.  work: asdsl_decode_work_bytes() bytes, 256-byte aligned.
+ * Replaces UnifiedEngine::forward_token + greedy argmax
+ * (asdsl/kernels/native/unified_engine.cpp:1339-1688,207-233). */
+asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int* pos, float* logits,
+                                void* work, asdsl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
