@@ -490,20 +490,22 @@ def run_suite(args) -> int:
             measure("A11 batched preq2 g32 verify GEMV", f"{wl} N={N}", wbytes + N * (4 * Kb + 4 * Mb), bcopy, blaunch,
                     (N, Mb), bcpu if ng else None, note="cpu_reference = N serial gemv_preq2_fused_avx2 calls")
 
+    for B in (4, 2, 8, 16):
+        def mb_copy(B=B):
+            c = pk_copy(M, K, 32, True)
+            c["X"] = torch.randn((B, K), generator=gen, device="cuda")
+            return c
+
+        def mb_cpu(hc, B=B):
+            Y = np.zeros((B, M), np.float32)
+            ng.matmul_batch_q4(hc["w"], hc["s"], hc["b"], hc["X"], Y, M, K, B, 32)
+            return Y
+        measure("A11 matmul_batch_q4", f"gate_up 16384x3072 B={B}",
+                M * K // 2 + 2 * M * (K // 32) * 4 + B * (4 * K + 4 * M), mb_copy,
+                lambda c, y, h, B=B: lib.asdsl_matmul_batch_q4(P(c["w"]), P(c["s"]), P(c["b"]), P(c["X"]), P(y), M, K,
+                                                               B, 32, h),
+                (B, M), mb_cpu if ng else None)
     B = 4
-
-    def mb_copy():
-        c = pk_copy(M, K, 32, True)
-        c["X"] = torch.randn((B, K), generator=gen, device="cuda")
-        return c
-
-    def mb_cpu(hc):
-        Y = np.zeros((B, M), np.float32)
-        ng.matmul_batch_q4(hc["w"], hc["s"], hc["b"], hc["X"], Y, M, K, B, 32)
-        return Y
-    measure("A11 matmul_batch_q4", "gate_up 16384x3072 B=4", M * K // 2 + 2 * M * (K // 32) * 4 + B * (4 * K + 4 * M),
-            mb_copy, lambda c, y, h: lib.asdsl_matmul_batch_q4(P(c["w"]), P(c["s"]), P(c["b"]), P(c["X"]), P(y), M, K, B, 32, h),
-            (B, M), mb_cpu if ng else None)
 
     def g128_copy():
         c = {"blocks": q4_128_from_weights_torch(torch.randn((M, K), generator=gen, device="cuda") * 0.02)}

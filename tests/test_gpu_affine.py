@@ -62,7 +62,8 @@ def test_known_answers(gpu):
 
 
 @pytest.mark.parametrize("M,K,gs", [(1, 32, 32), (17, 256, 32), (70, 3072, 64), (129, 3072, 128),
-                                    (33, 8192, 32), (9, 20480, 128), (40, 96, 16), (31, 240, 48)])
+                                    (33, 8192, 32), (9, 20480, 128), (3, 32768, 128), (40, 96, 16),
+                                    (31, 240, 48)])
 def test_packed_and_unpacked_vs_oracle(gpu, M, K, gs):
     from asdsl.kernels import _native_gemv as ng
 
@@ -211,6 +212,50 @@ def test_matmul_batch_vs_oracle(gpu, M, K, B, gs):
             assert rel_l2(Y[i], oracle.gemv_affine(w, X[i], s, b, M, K, gs)) < TOL
     with pytest.raises(ValueError, match="B must be"):
         ng.matmul_batch_q4(w, s, b, np.zeros((65, K), np.float32), np.zeros((65, M), np.float32), M, K, 65, gs)
+
+
+@pytest.mark.parametrize("M,K,B,gs", [(64, 3072, 2, 32), (200, 4096, 17, 128), (300, 8192, 5, 64)])
+def test_matmul_batch_each_column(gpu, M, K, B, gs):
+    """Each column on its own against the oracle, at 1e-5 (the batched kernel
+    carries x in two fp16 digits per power-of-two-scaled group: a lost low
+    digit shows as ~2e-4): column magnitudes spread over 1e-30..1e30, one
+    all-zero column (exact zeros out), one zero group; 17 columns take two
+    16-column passes, K=4096/8192 two and four K-slabs."""
+    from asdsl.kernels import _native_gemv as ng
+
+    w, s, b, _ = _rand(M, K, gs, 11 + B)
+    rng = np.random.default_rng(B + K)
+    X = rng.standard_normal((B, K)).astype(np.float32) * np.logspace(-30, 30, B).astype(np.float32)[:, None]
+    X[1] = 0.0
+    X[0, gs:2 * gs] = 0.0
+    Y = np.full((B, M), np.nan, np.float32)
+    ng.matmul_batch_q4(w, s, b, X, Y, M, K, B, gs)
+    want = oracle.matmul_batch_q4(w, s, b, X, M, K, B, gs)
+    assert np.array_equal(Y[1], np.zeros(M, np.float32))
+    for n in [0] + list(range(2, B)):
+        assert rel_l2(Y[n], want[n]) < 1e-5, n
+
+
+@pytest.mark.parametrize("M,K,B", [(100, 3072, 17), (40, 8192, 3)])
+def test_gemm_q4_128_each_column(gpu, M, K, B):
+    """The batched Q4_128 path, each column on its own against the oracle at
+    1e-5: magnitudes 1e-20..1e20 per column, an all-zero column, an all-zero
+    weight block (scale 0)."""
+    from asdsl.kernels import _native_gemv as ng
+    from asdsl.quantization import synthetic as syn
+
+    w = syn.gaussian_weights(M, K, 9 + B)
+    w[3, 128:256] = 0.0
+    blocks = syn.q4_128_blocks(w)
+    X = np.random.default_rng(K + B).standard_normal((B, K)).astype(np.float32)
+    X *= np.logspace(-20, 20, B).astype(np.float32)[:, None]
+    X[1] = 0.0
+    Y = np.full((B, M), np.nan, np.float32)
+    ng.gemm_q4_128_q8_avx2(blocks, X, Y, M, K, 128, B)
+    want = oracle.gemm_q4_128(blocks, X, M, K, B)
+    assert np.array_equal(Y[1], np.zeros(M, np.float32))
+    for n in [0] + list(range(2, B)):
+        assert rel_l2(Y[n], want[n]) < 1e-5, n
 
 
 @pytest.mark.parametrize("M,K,B", [(7, 256, 3), (200, 3072, 8), (64, 8192, 2)])
