@@ -2,9 +2,14 @@
  * asdsl_hip.h — C ABI of the MI355X (gfx950) Q4 GEMV family.
  *
  * Every entry point is stream-ordered and asynchronous: pointers are DEVICE
- * pointers, nothing is allocated (apart from the one work buffer per device
- * of asdsl_sparse_down_proj_T, sized on first use), and the call returns as
- * soon as the kernel is queued on `stream` (0 = the null stream).  Buffers are owned by the
+ * pointers, nothing is allocated (apart from one work buffer per device,
+ * grown on first use and kept, which asdsl_sparse_down_proj_T and the batched
+ * calls share: asdsl_gemv_preq2_fused_batch with n_cols >= 5, and with
+ * K % 128 == 0 asdsl_matmul_batch_q4, asdsl_gemm_q4_128 and
+ * asdsl_gemv_q4_packed / asdsl_gemv_q4_gs64 with batch > 1; calls that
+ * overlap on one device on unordered streams race on it), and the call
+ * returns as soon as the kernel is queued on `stream` (0 = the null stream).
+ * Buffers are owned by the
  * caller, exactly as in the reference kernels, which take caller-owned
  * host buffers (asdsl/kernels/native/gemv_q4_kernel.h:25-121).
  *
@@ -191,6 +196,9 @@ asdsl_status asdsl_gemv_q4_gs64(const uint8_t* w_packed, const float* x, const f
 /* ------------------------------------------------------------------ A11 ---
  * Batched fp32 Q4 GEMM over packed weights: Y[b][r] = sum_k dequant(W[r,k]) X[b][k]
  * with dequant = q*s + b per group; X [B][K], Y [B][M] overwritten, B <= 64.
+ * For B >= 2, group_size 32/64/128 and K % 128 == 0 one weight pass serves 16
+ * columns (MFMA on fp16 hi/lo digits of each column, within 1e-5 of fp32);
+ * other shapes run one GEMV per column.
  * Replaces matmul_batch_q4 (asdsl/kernels/native/gemv_q4_avx2.cpp:950-1059). */
 asdsl_status asdsl_matmul_batch_q4(const uint8_t* w_packed, const float* scales, const float* biases,
                                    const float* X, float* Y, int M, int K, int B, int group_size,
