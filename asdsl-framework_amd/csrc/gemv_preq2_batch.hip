@@ -11,6 +11,8 @@
 // the fp32 epilogue acc_n += D*(s*xs_n) - (z*s)*(X_n*xs_n).  Column chunks of
 // up to 16 (8 when K > 4096, LDS-bound) run as separate launches over the
 // same weights.  Deterministic: no atomics, fixed-order K-split combine.
+#include <type_traits>
+
 #include "abi_util.hpp"
 #include "device_common.hpp"
 
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(W * kWave) void preq2_batch_mfma_kernel(const uint3
 
     const v4i32 zero = {0, 0, 0, 0};
     const int rd = (r16 >> 2) * kBand + (r16 & 3) * 16 + q * 4;  // row r16, chunk q
-    auto run_tile = [&](uint4 (&wc)[kLoads], uint32_t (&mc)[GPW], auto& wn, auto& mn, int parity) {
+    auto run_tile = [&](auto prefetch, uint4 (&wc)[kLoads], uint32_t (&mc)[GPW], auto& wn, auto& mn, int parity) {
         // stage this tile's weights (the wave reads back only what it wrote;
         // LDS operations of a wave complete in order), then request the next
         // tile's before computing
@@ -312,10 +314,9 @@ __global__ __launch_bounds__(W * kWave) void preq2_batch_mfma_kernel(const uint3
             zsf[j] = -(half_bits_to_float(mc[j] >> 16) * sf[j]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        // unconditional, clamped to the last tile (which every workgroup
-        // reads last, so the extra request is a cache hit): a branch here
-        // would make every later use wait for the prefetch
-        if constexpr (PF) load_tile(wn, mn, min(tile + step, ntiles - 1));
+        // (a workgroup's last tile requests nothing: a wave ends only once its
+        // loads have landed)
+        if constexpr (decltype(prefetch)::value) load_tile(wn, mn, tile + step);
         __builtin_amdgcn_sched_barrier(0);
 
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -352,18 +353,29 @@ __global__ __launch_bounds__(W * kWave) void preq2_batch_mfma_kernel(const uint3
             if (n < ncols && row < M) Y[static_cast<size_t>(n) * M + row] = sum;
         }
     };
+    const std::true_type pf_on;
+    const std::false_type pf_off;
     if constexpr (PF) {
-        while (tile < ntiles) {  // uniform per workgroup
-            run_tile(w0, m0, w1, m1, 0);
+        // every path has a fixed number of requests in flight at each wait (a
+        // conditional request would make every wait drain all of them)
+        while (true) {  // uniform per workgroup
+            if (tile + step >= ntiles) {
+                run_tile(pf_off, w0, m0, w0, m0, 0);
+                break;
+            }
+            run_tile(pf_on, w0, m0, w1, m1, 0);
             tile += step;
-            if (tile >= ntiles) break;
-            run_tile(w1, m1, w0, m0, 1);
+            if (tile + step >= ntiles) {
+                run_tile(pf_off, w1, m1, w1, m1, 1);
+                break;
+            }
+            run_tile(pf_on, w1, m1, w0, m0, 1);
             tile += step;
         }
     } else {
         int parity = 0;
         while (true) {  // uniform per workgroup
-            run_tile(w0, m0, w0, m0, parity);
+            run_tile(pf_off, w0, m0, w0, m0, parity);
             tile += step;
             if (tile >= ntiles) break;
             load_tile(w0, m0, tile);
@@ -526,10 +538,12 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const 
     const BatchPlan p = plan_batch(out_features, in_features, group_size, cus);
     const int M = out_features, K = in_features;
     const auto* m = reinterpret_cast<const uint32_t*>(meta);
-    // gs = 32 with at least ASDSL_HIP_BATCH_MFMA_MIN_N columns (default 5,
-    // where the MFMA path overtakes the dot4 kernel): 16 columns per pass.
+    // gs = 32 with at least ASDSL_HIP_BATCH_MFMA_MIN_N columns: 16 columns per
+    // pass.  Default where the MFMA path was measured to overtake the dot4
+    // kernel: N >= 4 (gate_up 16384x3072: 13.0 vs 13.9 us; N = 3: 12.9 vs
+    // 12.1), N >= 3 once K >= 4096 (down 3072x8192, N = 3: 10.9 vs 12.2 us).
     static const int mfma_knob = env_knob("ASDSL_HIP_BATCH_MFMA_MIN_N");
-    const int mfma_min = mfma_knob > 0 ? mfma_knob : 5;
+    const int mfma_min = mfma_knob > 0 ? mfma_knob : (in_features >= 4096 ? 3 : 4);
     const MfmaPlan mp = plan_mfma(M, K, cus);
     if (group_size == 32 && n_cols >= mfma_min && mp.ok && reinterpret_cast<uintptr_t>(meta) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(quant) % 4 == 0) {

@@ -472,7 +472,7 @@ def run_suite(args) -> int:
 
     # A11 batched verification (preq2, each column quantized) and the fp32 batched GEMMs
     for (Mb, Kb, wl) in [(16384, 3072, "gate_up 16384x3072"), (3072, 8192, "down 3072x8192")]:
-        for N in (2, 4, 8, 16):
+        for N in (2, 3, 4, 8, 16):
             def bcopy(Mb=Mb, Kb=Kb, N=N):
                 c = preq2_copy(Mb, Kb, 32)
                 c["X"] = torch.randn((N, Kb), generator=gen, device="cuda")

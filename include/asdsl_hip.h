@@ -4,7 +4,8 @@
  * Every entry point is stream-ordered and asynchronous: pointers are DEVICE
  * pointers, nothing is allocated (apart from one work buffer per device,
  * grown on first use and kept, which asdsl_sparse_down_proj_T and the batched
- * calls share: asdsl_gemv_preq2_fused_batch with n_cols >= 5, and with
+ * calls share: asdsl_gemv_preq2_fused_batch with n_cols >= 4 (>= 3 when
+ * in_features >= 4096), and with
  * K % 128 == 0 asdsl_matmul_batch_q4, asdsl_gemm_q4_128 and
  * asdsl_gemv_q4_packed / asdsl_gemv_q4_gs64 with batch > 1; calls that
  * overlap on one device on unordered streams race on it), and the call

@@ -169,7 +169,7 @@ def test_lm_head_preq2_g128_full_size(gpu):
 
 @pytest.mark.parametrize("gs", [32, 128])
 @pytest.mark.parametrize("M,K,N", [(16384, 3072, 2), (16384, 3072, 16), (3072, 8192, 4), (3072, 8192, 16),
-                                   (70, 512, 3), (129, 3072, 8), (257, 5120, 17), (33, 640, 5)])
+                                   (70, 512, 3), (40, 4096, 3), (129, 3072, 8), (257, 5120, 17), (33, 640, 5)])
 def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
     """Batched verification GEMV: column n == gemv_preq2_fused(x_n) (each column
     quantized on its own), against the oracle per column."""
