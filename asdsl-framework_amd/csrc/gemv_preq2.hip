@@ -422,7 +422,8 @@ int check_preq2_args(const void* meta, const void* quant, const void* x, const v
 // then 32+ KB of fp32 per workgroup).  KS: the smallest power of two that
 // leaves each lane at most 6 units (loads) per band; then doubled, while it
 // splits the band evenly, as long as fewer than CUs/2 workgroups would run.
-// ASDSL_HIP_KSPLIT forces KS (a power of two <= 8); it changes the fp32
+// ASDSL_HIP_KSPLIT forces KS (a power of two <= 8; raised where the forced
+// value would leave more than 6 units per lane); it changes the fp32
 // summation order, not the formula.
 struct Plan {
     int lks, nu, waves, grid;
@@ -438,9 +439,12 @@ Plan plan_preq2(int M, int K, int cus) {
         const int bpt = p.waves >> lks;
         return (nbands + bpt - 1) / bpt;
     };
-    static const int forced = env_knob("ASDSL_HIP_KSPLIT");
+    const int forced = env_knob("ASDSL_HIP_KSPLIT");  // read per call (a test sets it in-process)
     if (forced == 1 || forced == 2 || forced == 4 || forced == 8) {
         p.lks = forced == 1 ? 0 : forced == 2 ? 1 : forced == 4 ? 2 : 3;
+        // never more than 6 units per lane (the kernel's largest NU); K/32 <=
+        // 640 keeps KS = 8 within it
+        while (p.lks < 3 && nu_of(p.lks) > 6) ++p.lks;
     } else {
         while (p.lks < 3 && nu_of(p.lks) > 6) ++p.lks;
         while (p.lks < 3 && tiles_of(p.lks) < cus / 2 && upb % (kWave << (p.lks + 1)) == 0) ++p.lks;

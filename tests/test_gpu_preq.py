@@ -191,3 +191,19 @@ def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
     mh, qh = meta.cpu().numpy(), quant.cpu().numpy()
     for n in range(N):
         assert rel_l2(Yh[n], oracle.gemv_preq2_fused(mh, qh, X[n], M, K, gs)) < TOL, f"column {n}"
+
+
+def test_forced_ksplit_still_covers_every_unit(gpu, monkeypatch):
+    """ASDSL_HIP_KSPLIT=2 on K=8192 would leave 8 units per lane (the kernel
+    takes at most 6): the plan raises the split, and the GEMV still matches
+    the oracle (the knob is read on every call)."""
+    from asdsl.kernels import _native_gemv as ng
+
+    M, K = 3072, 8192
+    meta, quant = syn.preq2(syn.gaussian_weights(M, K, 5), 32)
+    x = syn.activation(K, 6)
+    monkeypatch.setenv("ASDSL_HIP_KSPLIT", "2")
+    y = np.full(M, np.nan, np.float32)
+    ng.gemv_preq2_fused_avx2(meta, quant, x, y, M, K, 32)
+    monkeypatch.delenv("ASDSL_HIP_KSPLIT")
+    assert rel_l2(y, oracle.gemv_preq2_fused(meta, quant, x, M, K, 32)) < TOL
