@@ -35,6 +35,7 @@ SIGNATURES: dict[str, list] = {
     "asdsl_last_error": [],
     "asdsl_device_cu_count": [],
     "asdsl_profile_next_launch": [_P, _P],
+    "asdsl_stream_read": [_P, ctypes.c_size_t, _P, _I, _P],
     "asdsl_quantize_activation": [_P, _P, _P, _I, _I, _P],
     "asdsl_gemv_q4_32_preq": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_32_preq_fused": [_P, _P, _P, _I, _I, _I, _P],

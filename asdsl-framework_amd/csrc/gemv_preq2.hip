@@ -204,6 +204,14 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
             }
         }
     }
+    // 16-wave workgroups (K > 4096): every wave's activation requests go
+    // out before any wave's weight requests.  A CU returns vector-memory data
+    // in request order, so activation loads queued behind other waves' weight
+    // misses wait for HBM, and the staging barrier below waits for the
+    // slowest wave (down 3072x8192: 5.55 -> 5.24 us; at 8 waves it measured
+    // ~1 % slower, so it is not done there).  The barrier waits on nothing
+    // outstanding.
+    if constexpr (WAVES == 16) __syncthreads();
     load_tile(tile);           // grid <= ntiles, so this tile exists
     if constexpr (PRO == Pro::kNorm) {
         __shared__ float s_red[WAVES];

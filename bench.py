@@ -24,6 +24,10 @@ cpu_baseline = the reference's own gemv_preq2_fused_avx2 (compiled from its
            OMP_NUM_THREADS threads).
 extra    = lm_head 200064x3072 preq2-g128 GEMV (untimed phase, same graph
            method, two alternating copies of 327 MB).
+stream floor = per GEMV (and in `roofline`), the time of the library's
+           calibration read kernel (asdsl_stream_read) streaming the same
+           byte count, timed the same way: what one launch of that size can
+           reach at best; frac_of_floor = floor / kernel time.
 
 Prints one JSON line.
 """
@@ -195,6 +199,36 @@ def lm_head_kernel(lib, capture, timed_replays):
     return {"shape": [M, K], "group_size": gs, "kernel_us": round(us, 2), "bytes": nbytes,
             "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
             "frac_of_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def stream_floor_us(lib, nbytes: int, launches: int = 64) -> dict:
+    """The practical ceiling for one launch that streams `nbytes`: the library's
+    calibration read kernel (asdsl_stream_read), a graph of back-to-back
+    launches over rotated buffers (~1 GB in all, at least two), timed exactly
+    like the GEMVs; the faster of 256 and 1024 workgroups."""
+    import torch
+
+    from asdsl import _hip
+
+    nbytes = (nbytes + 15) // 16 * 16
+    ncopies = max(2, min(16, (1 << 30) // nbytes))
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device="cuda") for _ in range(ncopies)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    best = None
+    for grid in (256, 1024):
+        def calls(h, grid=grid):
+            for i in range(launches):
+                if lib.asdsl_stream_read(_hip.ptr(bufs[i % ncopies]), nbytes, _hip.ptr(sink), grid, h):
+                    raise RuntimeError(_hip.last_error())
+        g = capture(calls)
+        reps = 10
+        us = 1e3 * timed_replays(g, reps) / (reps * launches)
+        del g
+        if best is None or us < best[0]:
+            best = (us, grid)
+    del bufs
+    torch.cuda.empty_cache()
+    return {"us": round(best[0], 3), "GB/s": round(nbytes / (best[0] * 1e-6) / 1e9, 1), "grid": best[1]}
 
 
 # --------------------------------------------------------------------------- decode
@@ -668,6 +702,16 @@ def main() -> int:
     extra = {}
     if not args.no_lm_head:
         extra["lm_head_preq2_g128"] = lm_head_kernel(lib, capture, timed_replays)
+    # practical streaming ceiling per launch at each GEMV's byte count
+    floors = {n: stream_floor_us(lib, gemv_bytes(M, K)) for n, M, K in LAYER}
+    for n in per:
+        per[n]["stream_floor_us"] = floors[n]["us"]
+        per[n]["frac_of_floor"] = round(floors[n]["us"] / per[n]["kernel_us"], 4)
+    if "lm_head_preq2_g128" in extra:
+        lm = extra["lm_head_preq2_g128"]
+        lf = stream_floor_us(lib, lm["bytes"], launches=8)
+        lm["stream_floor_us"] = lf["us"]
+        lm["frac_of_floor"] = round(lf["us"] / lm["kernel_us"], 4)
 
     cpu, parity = (None, None)
     if not args.no_cpu:
@@ -711,6 +755,11 @@ def main() -> int:
             "timing": "HIP events around replays of a HIP graph of 64 back-to-back gate_up launches "
                       "over 16 rotated weight sets; per-launch average",
             "bytes_per_launch": gu_bytes,
+            "stream_floor_us": floors["gate_up"]["us"],
+            "stream_floor_GB/s": floors["gate_up"]["GB/s"],
+            "frac_of_stream_floor": round(floors["gate_up"]["us"] / gu_us, 4),
+            "stream_floor": "asdsl_stream_read over the same byte count, same graph timing: the practical "
+                            "ceiling for one launch of this size",
         },
         "per_gemv": per,
         "extra": extra,

@@ -68,6 +68,14 @@ int asdsl_device_cu_count(void);
  * alone, with no extra commands on the stream. */
 asdsl_status asdsl_profile_next_launch(void* start_event, void* stop_event);
 
+/* Calibration, no reference counterpart: reads `bytes` (a multiple of 16)
+ * from the 16-byte-aligned device buffer `data` with 16-byte non-temporal
+ * loads over `grid` workgroups of 512 threads (<= 0: one per compute unit)
+ * and writes nothing in practice (`sink`, one device word, is written only
+ * if the loaded words fold to a fixed sentinel).  Timed like a GEMV it gives
+ * the practical ceiling for streaming that many bytes in one launch. */
+asdsl_status asdsl_stream_read(const void* data, size_t bytes, uint32_t* sink, int grid, asdsl_stream_t stream);
+
 /* ------------------------------------------------------------------ A1 ---
  * Per-group int8 activation quantizer.
  * Replaces quantize_activation_avx2
