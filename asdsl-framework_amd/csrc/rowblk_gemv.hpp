@@ -129,8 +129,67 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
 
     uint4 w[NU];
     Hd hd[NU];
+    // STAGE (blocks whose header serves several units: Q4_128, Q4_K; one
+    // pass): a wave's rpw rows are one contiguous byte range, requested with
+    // aligned 16-byte loads into registers, written to the wave's LDS area at
+    // the start of the tile and read back per unit (Q4_128's units are 2-byte
+    // aligned, which gfx950 LDS serves) and per header.  Measured: Q4_128
+    // lm_head 80.3 -> 61.7 us, Q4_K gate_up 10.4 -> 10.2 us; for preq (one
+    // unit per block) it was slower (gate_up 8.1 -> 10.0 us), so preq keeps
+    // per-unit loads.
+    constexpr bool STAGE = (L == RowLayout::kQ4_128 || L == RowLayout::kQ4K) && !MULTI;
+    constexpr int kStageLoads = STAGE ? (NU * kWave * F::kBlockBytes / F::kUnitsPerBlock + 32 + 16 * kWave - 1) /
+                                            (16 * kWave) : 1;
+    uint4 cw[kStageLoads];
+    const size_t stage_bytes = static_cast<size_t>(rpw) * row_bytes;  // one tile's rows of this wave
+    const size_t total_bytes = static_cast<size_t>(M) * row_bytes;
+    uint8_t* wstage = reinterpret_cast<uint8_t*>(lds) + ((x_image_bytes(K, GSX) + 15) & ~static_cast<size_t>(15)) +
+                      static_cast<size_t>(wave) * ((stage_bytes + 47) & ~static_cast<size_t>(15));
+    size_t st_a0 = 0, st_lead = 0;  // aligned start of the staged range, and the range's offset in it
+    int st_count = 0;                // 16-byte chunks of the staged range
+    auto load_stage = [&](int tile) {
+        const int r0 = min(tile * rpt + wave * rpw, M - 1);
+        const size_t a = static_cast<size_t>(r0) * row_bytes;
+        const size_t end = min(a + stage_bytes, total_bytes);  // rows past M: not loaded, never stored
+        st_a0 = a & ~static_cast<size_t>(15);
+        st_lead = a - st_a0;
+        st_count = static_cast<int>((end - st_a0 + 15) / 16);
+#pragma unroll
+        for (int k = 0; k < kStageLoads; ++k) {
+            const int c = min(k * kWave + lane, st_count - 1);
+            // the last chunk may run past the buffer's end: it is read ending there
+            const size_t at = min(st_a0 + static_cast<size_t>(c) * 16, total_bytes - 16);
+            const u32x4_a2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a2*>(blocks + at));
+            cw[k] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    };
+    auto unstage = [&]() {
+#pragma unroll
+        for (int k = 0; k < kStageLoads; ++k) {
+            const int c = k * kWave + lane;
+            if (c < st_count) {
+                const size_t at = min(st_a0 + static_cast<size_t>(c) * 16, total_bytes - 16);
+                *reinterpret_cast<u32x4_a2*>(wstage + (at - st_a0)) = u32x4_a2{cw[k].x, cw[k].y, cw[k].z, cw[k].w};
+            }
+        }
+        const uint8_t* rb = wstage + st_lead + static_cast<size_t>(rin) * row_bytes;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int t = tu[i];
+            const uint8_t* bp = rb + static_cast<size_t>(t / F::kUnitsPerBlock) * F::kBlockBytes;
+            const u32x4_a2 v = *reinterpret_cast<const u32x4_a2*>(bp + F::kDataOffset + 16 * (t % F::kUnitsPerBlock));
+            w[i] = make_uint4(v.x, v.y, v.z, v.w);
+            if constexpr (L == RowLayout::kPreq) hd[i] = *reinterpret_cast<const uint32_t*>(bp);
+            else if constexpr (L == RowLayout::kQ4_128) hd[i] = *reinterpret_cast<const uint16_t*>(bp);
+            else if constexpr (L == RowLayout::kQ4K) hd[i] = *reinterpret_cast<const uint4*>(bp);
+        }
+    };
     // Unconditional loads at clamped, in-bounds rows; rows >= M are never stored.
     auto load_units = [&](int tile) {
+        if constexpr (STAGE) {
+            load_stage(tile);
+            return;
+        }
         const int row = min(tile * rpt + wave * rpw + rin, M - 1);
         const uint8_t* rb = blocks + static_cast<size_t>(row) * row_bytes;
 #pragma unroll
@@ -176,6 +235,7 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
         for (int i = 0; i < NU; ++i) read_x(tu[i], xr[MULTI ? 0 : i], xs[MULTI ? 0 : i], xu[MULTI ? 0 : i]);
     }
     auto dots = [&](float acc) {
+        if constexpr (STAGE) unstage();
 #pragma unroll
         for (int i = 0; i < NU; ++i) {
             if (valid[i]) {
@@ -255,7 +315,12 @@ inline RowPlan plan_rowblk(int M, int K, int cus) {
 template <RowLayout L, int GSX, int WAVES, int NCH, bool Q8, bool EXACT, bool MULTI>
 asdsl_status launch_rowblk_exact(const RowPlan& p, const uint8_t* blocks, const float* side, const float* x,
                                  const int8_t* xq8, const float* xsc, float* y, int M, int K, hipStream_t stream) {
-    const size_t lds = x_image_bytes(K, GSX);
+    using F = RowFmt<L>;
+    constexpr bool STAGE = (L == RowLayout::kQ4_128 || L == RowLayout::kQ4K) && !MULTI;
+    const size_t row_bytes = static_cast<size_t>(K / 32 / F::kUnitsPerBlock) * F::kBlockBytes;
+    const size_t stage = STAGE ? WAVES * (((static_cast<size_t>(kWave >> p.llpr) * row_bytes) + 47) & ~static_cast<size_t>(15))
+                               : 0;
+    const size_t lds = ((x_image_bytes(K, GSX) + 15) & ~static_cast<size_t>(15)) + stage;
     const dim3 block(WAVES * kWave);
 #define ASDSL_ROWBLK_NU(N)                                                                                  \
     case N:                                                                                                 \
