@@ -60,6 +60,10 @@ __global__ void finalize_kernel(const unsigned long long* __restrict__ amax, int
 // consecutive positions.  Writes per query head (m, l, acc[128]) with
 // acc = sum_p exp(s_p - m) v_p.  The split holding `pos` also applies RoPE to
 // the new K, rounds K and V to fp16 and stores them in the cache.
+// Each wave keeps its 32 positions' scores in registers and forms its own
+// (max, sum, P.V); the four waves are merged in LDS behind one barrier (a
+// block-wide softmax through LDS took two more barriers and ~2 us longer).
+
 template <int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const float* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
@@ -67,8 +71,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     float* __restrict__ part, int n_heads, int n_kv, int max_seq, int rot_half, int nsplit) {
     __shared__ float q_s[G][kHeadDim];
     __shared__ float kv_new[2][kHeadDim];
-    __shared__ float sc[G][kSplit];
-    __shared__ float ml[G][2];
+    __shared__ float wml[kAttnThreads / kWave][G][2];
     __shared__ float wacc[kAttnThreads / kWave][G][kHeadDim];
     const int s = static_cast<int>(blockIdx.x);
     const int kvh = static_cast<int>(blockIdx.y);
@@ -177,7 +180,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         }
     };
 
-    // scores
+    // scores of this lane's positions (the 16 lanes of a position all hold
+    // it after the DPP sum); positions past the split are -inf
+    float sr[kIt][G];
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
         const int p = p0 + wave * 4 + pg + 16 * it;
@@ -192,79 +197,96 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
             d += dpp<kDppQuadXor2>(d);
             d += dpp<kDppRowRor4>(d);
             d += dpp<kDppRowRor8>(d);
-            if (dc == 0 && p < p1) sc[hh][p - p0] = d * inv_sqrt_d;
+            sr[it][hh] = p < p1 ? d * inv_sqrt_d : -INFINITY;
         }
     }
-    __syncthreads();
-
-    // softmax within the split: wave hh owns query head hh (2 scores per lane)
-    if (wave < G) {
-        const int n = p1 - p0;
-        const float v0 = lane < n ? sc[wave][lane] : -INFINITY;
-        const float v1 = lane + kWave < n ? sc[wave][lane + kWave] : -INFINITY;
-        float m = fmaxf(v0, v1);
+    // the wave's max and exp-sum per head (over its iterations, then over the
+    // four position groups: lanes 16 apart); a wave with no position keeps
+    // m = -inf and l = 0
+    float m[G], l[G];
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-        const float w0 = lane < n ? expf(v0 - m) : 0.0f;
-        const float w1 = lane + kWave < n ? expf(v1 - m) : 0.0f;
-        if (lane < n) sc[wave][lane] = w0;
-        if (lane + kWave < n) sc[wave][lane + kWave] = w1;
-        float l = w0 + w1;
+    for (int hh = 0; hh < G; ++hh) {
+        float v = sr[0][hh];
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, kWave);
-        if (lane == 0) {
-            ml[wave][0] = m;
-            ml[wave][1] = l;
-        }
+        for (int it = 1; it < kIt; ++it) v = fmaxf(v, sr[it][hh]);
+        v = fmaxf(v, swz_xor16(v));
+        v = fmaxf(v, __shfl_xor(v, 32, kWave));
+        m[hh] = v;
     }
-    __syncthreads();
-
-    // acc = sum_p w_p v_p
     float acc[G][8];
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh)
+    for (int hh = 0; hh < G; ++hh) {
+        l[hh] = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[hh][e] = 0.0f;
+    }
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
         const int p = p0 + wave * 4 + pg + 16 * it;
-        if (p < p1) {
-            float v8[8];
-            row_of(vraw[it], 1, p, v8);
+        float v8[8];
+        row_of(vraw[it], 1, p, v8);
 #pragma unroll
-            for (int hh = 0; hh < G; ++hh) {
-                const float w = sc[hh][p - p0];
+        for (int hh = 0; hh < G; ++hh) {
+            const float w = p < p1 ? expf(sr[it][hh] - m[hh]) : 0.0f;
+            l[hh] += w;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[hh][e] = fmaf(w, v8[e], acc[hh][e]);
-            }
+            for (int e = 0; e < 8; ++e) acc[hh][e] = fmaf(w, v8[e], acc[hh][e]);
         }
     }
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh)
+    for (int hh = 0; hh < G; ++hh) {
+        l[hh] += swz_xor16(l[hh]);
+        l[hh] += __shfl_xor(l[hh], 32, kWave);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            acc[hh][e] += __shfl_xor(acc[hh][e], 16, kWave);
+            acc[hh][e] += swz_xor16(acc[hh][e]);
             acc[hh][e] += __shfl_xor(acc[hh][e], 32, kWave);
         }
+    }
     if (pg == 0) {
 #pragma unroll
         for (int hh = 0; hh < G; ++hh)
 #pragma unroll
             for (int e = 0; e < 8; ++e) wacc[wave][hh][8 * dc + e] = acc[hh][e];
     }
+    if (lane == 0) {  // m and l are uniform across the wave
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh) {
+            wml[wave][hh][0] = m[hh];
+            wml[wave][hh][1] = l[hh];
+        }
+    }
     __syncthreads();
+
+    // merge the waves: M = max m_w, acc = sum_w exp(m_w - M) acc_w, L likewise
+    constexpr int kWaves = kAttnThreads / kWave;
     for (int e = tid; e < G * kHeadDim; e += kAttnThreads) {
         const int hh = e / kHeadDim;
         const int d = e % kHeadDim;
-        float sum = wacc[0][hh][d];
+        float M = wml[0][hh][0];
 #pragma unroll
-        for (int w = 1; w < kAttnThreads / kWave; ++w) sum += wacc[w][hh][d];
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][hh][0]);
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = wml[w][hh][0];
+            sum = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wacc[w][hh][d], sum);
+        }
         part[(static_cast<size_t>(kvh * G + hh) * nsplit + s) * kPartStride + 2 + d] = sum;
     }
     if (tid < G) {
+        float M = wml[0][tid][0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][tid][0]);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = wml[w][tid][0];
+            L = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wml[w][tid][1], L);
+        }
         float* pp = part + (static_cast<size_t>(kvh * G + tid) * nsplit + s) * kPartStride;
-        pp[0] = ml[tid][0];
-        pp[1] = ml[tid][1];
+        pp[0] = M;
+        pp[1] = L;
     }
 }
 
