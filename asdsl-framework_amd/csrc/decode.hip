@@ -290,28 +290,41 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     }
 }
 
-// out[h][d] = sum_s e_s acc_s[d] / sum_s e_s l_s, e_s = exp(m_s - max m), in split order.
-__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __restrict__ part,
-                                                               const int* __restrict__ pos_ptr,
-                                                               float* __restrict__ out, int nsplit, int max_seq) {
+// out[h][d] = sum_s e_s acc_s[d] / sum_s e_s l_s, e_s = exp(m_s - max m).
+// Up to kCombineGroups groups of 128 threads each fold a contiguous run of
+// splits (chunks of kChunk loads issued together, a running (max, sum,
+// output) rescaled between chunks); with more than one group the runs are
+// merged in LDS in split order.  One group when the splits fit one chunk.
+constexpr int kCombineGroups = 4;
+constexpr int kCombineThreads = kCombineGroups * kHeadDim;
+
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const float* __restrict__ part,
+                                                                      const int* __restrict__ pos_ptr,
+                                                                      float* __restrict__ out, int nsplit,
+                                                                      int max_seq) {
+    constexpr int kChunk = 16;
+    __shared__ float gml[kCombineGroups][2];
+    __shared__ float go[kCombineGroups][kHeadDim];
     const int h = static_cast<int>(blockIdx.x);
-    const int d = static_cast<int>(threadIdx.x);
+    const int d = static_cast<int>(threadIdx.x) % kHeadDim;
+    const int g = static_cast<int>(threadIdx.x) / kHeadDim;
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) {  // outside the cache: no partials were written
-        out[static_cast<size_t>(h) * kHeadDim + d] = 0.0f;
+        if (g == 0) out[static_cast<size_t>(h) * kHeadDim + d] = 0.0f;
         return;
     }
     const int ns = pos / kSplit + 1;
+    const int ng = min(kCombineGroups, (ns + kChunk - 1) / kChunk);  // groups with splits
+    const int per = (ns + ng - 1) / ng;
+    const int s_begin = min(ns, g * per);
+    const int s_end = min(ns, s_begin + per);
     const float* ph = part + static_cast<size_t>(h) * nsplit * kPartStride;
-    // chunks of kChunk splits, each chunk's loads issued together; a running
-    // (max, sum, output) is rescaled between chunks, in split order
-    constexpr int kChunk = 16;
     float M = -INFINITY, L = 0.0f, o = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += kChunk) {  // uniform
+    for (int s0 = s_begin; s0 < s_end; s0 += kChunk) {  // uniform per group
         float mv[kChunk], lv[kChunk], av[kChunk];
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
-            const bool live = s0 + j < ns;
+            const bool live = s0 + j < s_end;
             const float* pp = ph + static_cast<size_t>(live ? s0 + j : 0) * kPartStride;
             mv[j] = live ? pp[0] : -INFINITY;
             lv[j] = live ? pp[1] : 0.0f;
@@ -325,7 +338,7 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __r
         o *= r;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
-            if (s0 + j < ns) {
+            if (s0 + j < s_end) {
                 const float e = expf(mv[j] - cm);
                 L = fmaf(e, lv[j], L);
                 o = fmaf(e, av[j], o);
@@ -333,7 +346,28 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __r
         }
         M = cm;
     }
-    out[static_cast<size_t>(h) * kHeadDim + d] = o * (1.0f / L);
+    if (ng == 1) {  // uniform: group 0 holds every split
+        if (g == 0) out[static_cast<size_t>(h) * kHeadDim + d] = o * (1.0f / L);
+        return;
+    }
+    go[g][d] = o;
+    if (d == 0) {
+        gml[g][0] = M;
+        gml[g][1] = L;
+    }
+    __syncthreads();
+    if (g == 0) {
+        float Mx = gml[0][0];
+        for (int q = 1; q < ng; ++q) Mx = fmaxf(Mx, gml[q][0]);
+        float sum = 0.0f, Ls = 0.0f;
+        for (int q = 0; q < ng; ++q) {
+            const float mq = gml[q][0];
+            const float e = mq == -INFINITY ? 0.0f : expf(mq - Mx);
+            sum = fmaf(e, go[q][d], sum);
+            Ls = fmaf(e, gml[q][1], Ls);
+        }
+        out[static_cast<size_t>(h) * kHeadDim + d] = sum * (1.0f / Ls);
+    }
 }
 
 int attn_splits(int max_seq) { return (max_seq + kSplit - 1) / kSplit; }
@@ -355,7 +389,7 @@ asdsl_status launch_attention(const float* qkv, uint16_t* kc, uint16_t* vc, cons
             return ASDSL_ERR_UNSUPPORTED;
     }
     if (st != ASDSL_OK) return st;
-    return launch("attn_combine_kernel", attn_combine_kernel, dim3(n_heads), dim3(kHeadDim), 0, s,
+    return launch("attn_combine_kernel", attn_combine_kernel, dim3(n_heads), dim3(kCombineThreads), 0, s,
                   static_cast<const float*>(part), pos, att, nsplit, max_seq);
 }
 

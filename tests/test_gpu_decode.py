@@ -101,13 +101,16 @@ def test_swiglu_gemv_matches_oracle(gpu, gs, thr):
     assert rel_l2(_host(y), want) < TOL
 
 
-@pytest.mark.parametrize("pos", [0, 1, 127, 128, 129, 383, 1500])
-def test_attention_rope_kv_matches_oracle(gpu, pos):
+@pytest.mark.parametrize("pos,max_seq", [(0, 1600), (1, 1600), (127, 1600), (128, 1600), (129, 1600), (383, 1600),
+                                         (1500, 1600), (4100, 4224), (9000, 9100)])
+def test_attention_rope_kv_matches_oracle(gpu, pos, max_seq):
+    """RoPE, the KV write and attention at 1 to 71 splits of 128 positions
+    (past 16 splits the combine folds runs of splits in parallel groups)."""
     import torch
     from asdsl import _hip
     from asdsl.engine import rope_tables
 
-    nh, nkv, hd, rot, max_seq = 24, 8, 128, 96, 1600
+    nh, nkv, hd, rot = 24, 8, 128, 96
     rng = np.random.default_rng(pos)
     qkv = rng.standard_normal((nh + 2 * nkv) * hd).astype(np.float32)
     kc = rng.standard_normal((nkv, max_seq, hd)).astype(np.float16)
@@ -179,6 +182,31 @@ def test_decode_steps_match_oracle(gpu):
         assert rel_l2(got, want_logits) < 1e-3, step
         assert eng.next_token() == want_next, step
         assert int(eng.pos.item()) == pos + 1
+        tok = want_next
+
+
+@pytest.mark.parametrize("ctx", [127, 129, 2100, 4100])
+def test_decode_long_context_matches_oracle(gpu, ctx):
+    """One layer at contexts whose attention spans 1, 2, 17 and 33 splits of
+    128 positions (the combine then merges one, one, two and three chunks of
+    16 splits), two steps each: logits within 1e-3 and the same tokens."""
+    import torch
+
+    eng = _small_engine(n_layers=1, vocab=4096, max_seq=4224, seed=ctx)
+    eng.prefill_kv_random(ctx, seed=5)
+    model = _oracle_model(eng)
+    kc = [_host(L["k_cache"]) for L in eng.layers]
+    vc = [_host(L["v_cache"]) for L in eng.layers]
+    tok = 321
+    eng.token.fill_(tok)
+    eng.pos.fill_(ctx)
+    for step in range(2):
+        pos = ctx + step
+        want_logits, want_next = od.decode_step(model, tok, pos, kc, vc)
+        eng._queue_step(int(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert rel_l2(_host(eng.logits), want_logits) < 1e-3, (ctx, step)
+        assert eng.next_token() == want_next, (ctx, step)
         tok = want_next
 
 
