@@ -11,7 +11,9 @@ HIP graph of one step replays token after token.
 Weights are preq2 Q4 (attention projections at group size 32, the MLP and
 lm_head at 128 by default), norms fp32, embeddings and the KV cache fp16.
 ``DecodeEngine.synthetic`` builds a model with random weights of the given
-shape (W ~ N(0, 0.02) quantized, embeddings ~ N(0, 1), norm weights 1 + N(0, 0.1)).
+shape (W ~ N(0, 0.02) quantized, embeddings ~ N(0, 1), norm weights 1 + N(0, 0.1));
+``layers_from_preq_blocks`` builds the layer operands on the device from the
+preq blocks of the reference's preq cache (asdsl.quantization.preq_cache).
 """
 
 from __future__ import annotations
@@ -76,6 +78,37 @@ def rope_tables(max_seq: int, rotary_dim: int, theta: float = 10000.0) -> tuple[
 def _layer_mats(cfg: DecodeConfig):
     return {"qkv": (cfg.qkv_dim, cfg.hidden, cfg.gs_attn), "o": (cfg.hidden, cfg.n_heads * cfg.head_dim, cfg.gs_attn),
             "gu": (2 * cfg.ffn, cfg.hidden, cfg.gs_ffn), "down": (cfg.hidden, cfg.ffn, cfg.gs_ffn)}
+
+
+# the reference's projection names (experiments/phi4_cpu_run.py:628)
+PROJ_NAMES = {"qkv": "qkv_proj", "o": "o_proj", "gu": "gate_up_proj", "down": "down_proj"}
+
+
+def layers_from_preq_blocks(cfg: "DecodeConfig", blocks: dict, norms: list) -> list[dict]:
+    """Layer operands for DecodeEngine from preq blocks on the device.
+
+    blocks: {(layer, projection name): device uint8 tensor} as
+    ``preq_cache.try_restore_preq_cache(store, path, device=...)`` leaves in
+    ``store._preq_blocks_dev`` -- 20-byte Q4_32 blocks for projections at
+    group size 32, 66-byte Q4_128 blocks at 128 (cfg.gs_attn for qkv/o,
+    cfg.gs_ffn for gate_up/down).  norms: per layer (rms_att, rms_ffn) fp32
+    device tensors.  The preq2 operands are built by the repack kernels on
+    the current stream; nothing passes through host memory."""
+    from asdsl.quantization.preq_cache import preq2_from_preq_blocks
+
+    if len(norms) != cfg.n_layers:
+        raise ValueError(f"layers_from_preq_blocks: {len(norms)} norm pairs for {cfg.n_layers} layers")
+    layers = []
+    for li in range(cfg.n_layers):
+        L = {}
+        for n, (rows, cols, gs) in _layer_mats(cfg).items():
+            key = (li, PROJ_NAMES[n])
+            if key not in blocks:
+                raise ValueError(f"layers_from_preq_blocks: no preq blocks for layer {li} {PROJ_NAMES[n]}")
+            L[n] = preq2_from_preq_blocks(blocks[key], rows, cols, gs)
+        L["rms_att"], L["rms_ffn"] = norms[li]
+        layers.append(L)
+    return layers
 
 
 class DecodeEngine:

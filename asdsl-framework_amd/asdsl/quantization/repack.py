@@ -1,6 +1,10 @@
 """Repackers into the byte layouts the GEMV kernels read.
 
-Vectorized restatements of the reference's per-row Python loops:
+Given device tensors, every function here runs its HIP kernel on the current
+stream and returns device tensors (``asdsl.quantization._device_repack``);
+given numpy arrays it runs the host restatement below.  Both produce the
+reference's bytes.  Vectorized restatements of the reference's per-row
+Python loops:
   * preq   20-byte blocks  — asdsl/quantization/repack_q4_32.py:63-108
   * preq2  meta + bands    — asdsl/quantization/repack_preq2.py:22-62
   * Q4_128 66-byte blocks  — asdsl/quantization/repack_q4_128.py:22-97
@@ -22,7 +26,26 @@ Q4_128_BLOCK_SIZE = 66
 
 
 def _f16_bits(a) -> np.ndarray:
-    return np.asarray(a, dtype=np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):  # out-of-range zero points become inf, as numpy casts them
+        return np.asarray(a, dtype=np.float16).view(np.uint16)
+
+
+def _on_device(*arrays) -> bool:
+    return any(type(a).__module__.startswith("torch") and getattr(a, "is_cuda", False) for a in arrays)
+
+
+def _dev():
+    from asdsl.quantization import _device_repack
+
+    return _device_repack
+
+
+def _floor_scale(scales) -> np.ndarray:
+    """float(max(s, 1e-8)) per float32 scale s, as the reference forms it
+    (repack_q4_32.py:87): Python's max keeps s unless 1e-8 > s, which numpy
+    compares in float32; the result is the float64 1e-8 or s."""
+    s = np.asarray(scales, np.float32)
+    return np.where(np.float32(1e-8) > s, 1e-8, s.astype(np.float64))
 
 
 def _nibbles(q: np.ndarray) -> np.ndarray:
@@ -39,9 +62,11 @@ def repack_asymmetric_to_q4_32_blocks(packed, scales, biases, rows: int, cols: i
     the reference does with Python floats (repack_q4_32.py:84-97)."""
     if group_size != 32:
         raise ValueError("repack_asymmetric_to_q4_32_blocks requires group_size=32")
+    if _on_device(packed, scales, biases):
+        return _dev().asym_to_q4_32(packed, scales, biases, rows, cols)
     G = cols // group_size
     q = _unpack_bits(np.asarray(packed, np.uint8).reshape(rows, cols // 2), bits).reshape(rows, G, 32)
-    sc = np.maximum(np.asarray(scales, np.float32).reshape(rows, G).astype(np.float64), 1e-8)
+    sc = _floor_scale(np.asarray(scales, np.float32).reshape(rows, G))
     bi = np.asarray(biases, np.float32).reshape(rows, G).astype(np.float64)
     zero = -bi / sc
     blocks = np.empty((rows, G, PREQ_BLOCK_SIZE), np.uint8)
@@ -51,8 +76,10 @@ def repack_asymmetric_to_q4_32_blocks(packed, scales, biases, rows: int, cols: i
     return np.ascontiguousarray(blocks)
 
 
-def blocks_to_flat(blocks: np.ndarray) -> np.ndarray:
+def blocks_to_flat(blocks):
     rows, n_groups, bs = blocks.shape
+    if _on_device(blocks):
+        return blocks.reshape(rows, n_groups * bs).contiguous()
     return np.ascontiguousarray(blocks.reshape(rows, n_groups * bs))
 
 
@@ -61,6 +88,8 @@ def repack_preq_blocks_to_preq2(flat_preq, rows: int, cols: int, group_size: int
     """20-byte preq rows -> (meta (rows, G*4), quant (n_bands, G, 64))."""
     if group_size != 32:
         raise ValueError("preq2 repack requires group_size=32")
+    if _on_device(flat_preq):
+        return _dev().preq_to_preq2(flat_preq, rows, cols)
     G = cols // group_size
     flat = np.ravel(np.asarray(flat_preq, np.uint8))
     if flat.size < rows * G * PREQ_BLOCK_SIZE:
@@ -85,12 +114,49 @@ def preq2_flat_sizes(rows: int, cols: int, group_size: int = 32) -> tuple[int, i
     return rows * G * PREQ2_META_BYTES, n_bands * G * 4 * (group_size // 2)
 
 
-def meta_to_flat(meta: np.ndarray) -> np.ndarray:
+def meta_to_flat(meta):
+    if _on_device(meta):
+        return meta.reshape(-1).contiguous()
     return np.ascontiguousarray(meta.reshape(-1))
 
 
-def quant_to_flat(quant: np.ndarray) -> np.ndarray:
+def quant_to_flat(quant):
+    if _on_device(quant):
+        return quant.reshape(-1).contiguous()
     return np.ascontiguousarray(quant.reshape(-1))
+
+
+def repack_asymmetric_to_preq2(packed, scales, biases, rows: int, cols: int, group_size: int = 32):
+    """Packed Q4 + fp32 (scale, bias) -> flat preq2 (meta, quant) at group
+    size 32 (byte for byte repack_asymmetric_to_q4_32_blocks then
+    repack_preq_blocks_to_preq2) or 128 (the same fp16 pair per group, 4-row
+    bands of 64-byte row slots)."""
+    if group_size not in (32, 128):
+        raise ValueError("repack_asymmetric_to_preq2: group_size must be 32 or 128")
+    if _on_device(packed, scales, biases):
+        return _dev().asym_to_preq2(packed, scales, biases, rows, cols, group_size)
+    G = cols // group_size
+    sc = _floor_scale(np.asarray(scales, np.float32).reshape(rows, G))
+    zero = -np.asarray(biases, np.float32).reshape(rows, G).astype(np.float64) / sc
+    meta = np.empty((rows, G, 2), np.uint16)
+    meta[:, :, 0] = _f16_bits(sc)
+    meta[:, :, 1] = _f16_bits(zero)
+    nib = np.asarray(packed, np.uint8).reshape(rows, G, group_size // 2)
+    return meta.view(np.uint8).reshape(-1), _bands(nib, rows, G, group_size // 2).reshape(-1)
+
+
+def repack_q4_128_blocks_to_preq2(blocks, rows: int, cols: int) -> tuple:
+    """Q4_128 blocks (rows, cols/128, 66) -> flat preq2-g128 (meta, quant):
+    the symmetric group as scale s, zero 8 (no reference counterpart; lets
+    g128 preq caches feed the preq2-g128 GEMVs)."""
+    if _on_device(blocks):
+        return _dev().q4_128_to_preq2(blocks, rows, cols)
+    G = cols // 128
+    b = np.asarray(blocks, np.uint8).reshape(rows, G, Q4_128_BLOCK_SIZE)
+    meta = np.empty((rows, G, 2), np.uint16)
+    meta[:, :, 0] = b[:, :, 0:2].copy().view(np.uint16)[:, :, 0]
+    meta[:, :, 1] = _f16_bits(8.0)
+    return meta.view(np.uint8).reshape(-1), _bands(b[:, :, 2:], rows, G, 64).reshape(-1)
 
 
 def pack_preq2(q: np.ndarray, scale_f16: np.ndarray, zero_f16: np.ndarray, rows: int, cols: int,
@@ -118,7 +184,7 @@ def quantize_preq2(weights: np.ndarray, group_size: int = 32) -> tuple[np.ndarra
     q, s16, z16 = quantize_groups(w, 4, group_size, symmetric=False)
     sc = s16.astype(np.float32)
     bi = (-z16.astype(np.float32) * sc).astype(np.float32)
-    sc64 = np.maximum(sc.astype(np.float64), 1e-8)
+    sc64 = _floor_scale(sc)
     zero = -bi.astype(np.float64) / sc64
     return pack_preq2(q.reshape(rows, cols), sc64.astype(np.float16), zero.astype(np.float16),
                       rows, cols, group_size)
@@ -143,6 +209,8 @@ def q4_128_groups(wg: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
 def repack_fp32_to_q4_128_blocks(weights, rows: int, cols: int, group_size: int = 128) -> np.ndarray:
     if group_size != 128:
         raise ValueError("repack_fp32_to_q4_128_blocks requires group_size=128")
+    if _on_device(weights):
+        return _dev().fp32_to_q4_128(weights, rows, cols)
     G = cols // 128
     q, s16 = q4_128_groups(np.asarray(weights, np.float32).reshape(rows * G, 128))
     blocks = np.empty((rows, G, Q4_128_BLOCK_SIZE), np.uint8)
@@ -158,9 +226,11 @@ def repack_asymmetric_to_q4_128_blocks(packed, scales, biases, rows: int, cols: 
     requantize symmetric per group."""
     if group_size != 128:
         raise ValueError("repack_asymmetric_to_q4_128_blocks requires group_size=128")
+    if _on_device(packed, scales, biases):
+        return _dev().asym_to_q4_128(packed, scales, biases, rows, cols)
     G = cols // 128
     q = _unpack_bits(np.asarray(packed, np.uint8).reshape(rows, cols // 2), bits).reshape(rows * G, 128)
-    sc = np.maximum(np.asarray(scales, np.float32).reshape(-1).astype(np.float64), 1e-8)
+    sc = _floor_scale(np.asarray(scales, np.float32).reshape(-1))
     zero = -np.asarray(biases, np.float32).reshape(-1).astype(np.float64) / sc
     # (q - zero) * scale with q float32 and Python-float operands -> float32 result
     w_f = ((q.astype(np.float32) - zero.astype(np.float32)[:, None]) * sc.astype(np.float32)[:, None])

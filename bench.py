@@ -580,8 +580,122 @@ def run_suite(args) -> int:
             lambda c, y, h: lib.asdsl_compute_bitmask(P(c["x"]), P(y), 8192, ctypes.c_float(0.5), h), (256,),
             bm_cpu if spm else None, exact=True)
 
+    results.extend(repack_rows(args, oracle))
     print(json.dumps({"suite": "done", "rows": len(results)}), flush=True)
     return 0
+
+
+def repack_rows(args, oracle) -> list:
+    """Load-time weight repackers (the reference's per-group Python loops,
+    ~80 s for a Phi-4 model's 128 projection tensors): kernel time at the
+    lm_head and gate_up shapes (graph replay over rotated input copies),
+    algorithmic bytes = bytes read + bytes written, and the scalar C oracle
+    timed on a bounded slice of the same rows (kind "port"), scaled to the
+    whole tensor."""
+    import torch
+
+    from asdsl import _hip
+
+    lib, P = _hip.LIB, _hip.ptr
+    gen = torch.Generator(device="cuda").manual_seed(77)
+    out = []
+
+    def asym(M, K, gs):
+        packed = _dev_bytes(M * K // 2, gen)
+        return {"packed": packed, "sc": _dev_f32(M * (K // gs), gen, 0.49, 0.01),
+                "bi": _dev_f32(M * (K // gs), gen, 0.2, -0.1)}
+
+    def row(name, workload, M, K, nbytes, make_copy, outputs, launch, cpu, cpu_rows):
+        if args.rows and not any(f in name for f in args.rows.split(",")):
+            return
+        n = int(min(8, max(2, -(-640_000_000 // nbytes))))
+        copies = [make_copy() for _ in range(n)]
+        outs = {k: torch.empty(v, dtype=torch.uint8, device="cuda") for k, v in outputs.items()}
+        per_graph = max(n, 8)
+
+        def calls(h):
+            for i in range(per_graph):
+                if launch(copies[i % n], outs, h):
+                    raise RuntimeError(f"{name}: {_hip.last_error()}")
+        g = capture(calls)
+        timed_replays(g, 2)
+        r = max(3, min(50, int(4e9 // (nbytes * per_graph))))
+        us = 1e3 * timed_replays(g, r) / (r * per_graph)
+        del g
+        rec = {"row": name, "workload": workload, "gpu_us": round(us, 2), "bytes": int(nbytes),
+               "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+               "frac_of_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "rotated_copies": n}
+        if not args.no_cpu:
+            host = {k: v.cpu().numpy() for k, v in copies[0].items()}
+            calls_n, t0 = 0, time.perf_counter()
+            while True:
+                cpu(host, cpu_rows)
+                calls_n += 1
+                el = time.perf_counter() - t0
+                if el >= args.cpu_seconds_per_row:
+                    break
+            cus = 1e6 * el / calls_n * (M / cpu_rows)
+            rec["cpu_port"] = {"us": round(cus, 1), "GB/s": round(nbytes / (cus * 1e-6) / 1e9, 2), "threads": 1,
+                               "sample": f"oracle C on rows [0, {cpu_rows}) of {M}, scaled"}
+            rec["gpu_speedup"] = round(cus / us, 1)
+        del copies, outs
+        torch.cuda.empty_cache()
+        out.append(rec)
+        print(json.dumps(rec), flush=True)
+
+    M, K = LM_HEAD[0], LM_HEAD[1]
+    G32, G128 = K // 32, K // 128
+    bands = (M + 3) // 4
+    CR = 4096  # oracle rows per CPU sample
+
+    def preq_copy():
+        a = asym(M, K, 32)
+        blocks = torch.empty(M * G32 * 20, dtype=torch.uint8, device="cuda")
+        st = lib.asdsl_repack_asym_to_q4_32(P(a["packed"]), P(a["sc"]), P(a["bi"]), P(blocks), M, K, 32,
+                                            int(torch.cuda.current_stream().cuda_stream))
+        if st:
+            raise RuntimeError(_hip.last_error())
+        return {"preq": blocks}
+    row("F2 repack preq->preq2", "lm_head 200064x3072 g32", M, K, 2 * M * G32 * 20, preq_copy,
+        {"meta": M * G32 * 4, "quant": bands * G32 * 64},
+        lambda c, o, h: lib.asdsl_repack_preq_to_preq2(P(c["preq"]), P(o["meta"]), P(o["quant"]), M, K, 32, h),
+        lambda hc, n: oracle.repack_preq_to_preq2(hc["preq"][: n * G32 * 20], n, K), CR)
+
+    in_b = M * K // 2 + 8 * M * G128
+    row("F2 repack asym->preq2 g128", "lm_head 200064x3072", M, K, in_b + M * G128 * 4 + bands * G128 * 256,
+        lambda: asym(M, K, 128), {"meta": M * G128 * 4, "quant": bands * G128 * 256},
+        lambda c, o, h: lib.asdsl_repack_asym_to_preq2(P(c["packed"]), P(c["sc"]), P(c["bi"]), P(o["meta"]),
+                                                       P(o["quant"]), M, K, 128, h),
+        lambda hc, n: oracle.repack_asym_to_preq2(hc["packed"][: n * K // 2], hc["sc"][: n * G128],
+                                                  hc["bi"][: n * G128], n, K, 128), CR)
+
+    row("F2 repack asym->Q4_128", "lm_head 200064x3072", M, K, in_b + M * G128 * 66,
+        lambda: asym(M, K, 128), {"blocks": M * G128 * 66},
+        lambda c, o, h: lib.asdsl_repack_asym_to_q4_128(P(c["packed"]), P(c["sc"]), P(c["bi"]), P(o["blocks"]),
+                                                        M, K, 128, h),
+        lambda hc, n: oracle.repack_asym_to_q4_128(hc["packed"][: n * K // 2], hc["sc"][: n * G128],
+                                                   hc["bi"][: n * G128], n, K), CR)
+
+    def q128_copy():
+        a = asym(M, K, 128)
+        blocks = torch.empty(M * G128 * 66, dtype=torch.uint8, device="cuda")
+        st = lib.asdsl_repack_asym_to_q4_128(P(a["packed"]), P(a["sc"]), P(a["bi"]), P(blocks), M, K, 128,
+                                             int(torch.cuda.current_stream().cuda_stream))
+        if st:
+            raise RuntimeError(_hip.last_error())
+        return {"blocks": blocks}
+    row("F2 repack Q4_128->preq2-g128", "lm_head 200064x3072", M, K,
+        M * G128 * 66 + M * G128 * 4 + bands * G128 * 256, q128_copy,
+        {"meta": M * G128 * 4, "quant": bands * G128 * 256},
+        lambda c, o, h: lib.asdsl_repack_q4_128_to_preq2(P(c["blocks"]), P(o["meta"]), P(o["quant"]), M, K, h),
+        lambda hc, n: oracle.repack_q4_128_to_preq2(hc["blocks"][: n * G128 * 66], n, K), CR)
+
+    Mg = 16384
+    row("F2 repack fp32->Q4_128", "gate_up 16384x3072", Mg, K, 4 * Mg * K + Mg * G128 * 66,
+        lambda: {"w": torch.randn(Mg * K, generator=gen, device="cuda") * 0.02}, {"blocks": Mg * G128 * 66},
+        lambda c, o, h: lib.asdsl_repack_fp32_to_q4_128(P(c["w"]), P(o["blocks"]), Mg, K, 128, h),
+        lambda hc, n: oracle.repack_fp32_to_q4_128(hc["w"][: n * K], n, K), 1024)
+    return out
 
 
 def main() -> int:

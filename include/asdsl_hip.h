@@ -357,6 +357,64 @@ size_t asdsl_decode_work_bytes(const asdsl_decode_model* model);
 asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int* pos, float* logits,
                                 void* work, asdsl_stream_t stream);
 
+/* ------------------------------------------------------------- repackers
+ * Load-time conversions of the quantized store's weights into the layouts
+ * above, on the GPU; every output byte equals the reference's.  Inputs are
+ * the asymmetric packed Q4 of the store (row-major, two nibbles per byte,
+ * low nibble = even column) with fp32 scale and bias per (row, group), or
+ * preq blocks.  All pointers are device memory; rows >= 1, cols a multiple
+ * of the group size. */
+
+/* preq (20-byte blocks) -> preq2 meta[rows][cols/32][4] +
+ * quant[ceil(rows/4)][cols/32][64]; group_size must be 32.  preq and meta
+ * 4-byte, quant 16-byte aligned.
+ * Replaces repack_preq_blocks_to_preq2 (asdsl/quantization/repack_preq2.py:22-49). */
+asdsl_status asdsl_repack_preq_to_preq2(const uint8_t* preq, uint8_t* meta, uint8_t* quant, int rows, int cols,
+                                        int group_size, asdsl_stream_t stream);
+
+/* packed + scales + biases (gs 32) -> 20-byte preq blocks[rows][cols/32]:
+ * fp16(max(s, 1e-8)), fp16(-b / max(s, 1e-8)) (float64 division), the 16
+ * packed bytes.  packed 16-byte, the rest 4-byte aligned.
+ * Replaces repack_asymmetric_to_q4_32_blocks (asdsl/quantization/repack_q4_32.py:63-102). */
+asdsl_status asdsl_repack_asym_to_q4_32(const uint8_t* packed, const float* scales, const float* biases,
+                                        uint8_t* blocks, int rows, int cols, int group_size,
+                                        asdsl_stream_t stream);
+
+/* packed + scales + biases -> preq2 (meta, quant) at group_size 32 (the
+ * composition repack_q4_32 -> repack_preq2, byte for byte) or 128 (the same
+ * fp16 pair per group; 4-row bands of 64-byte row slots per group).  packed
+ * and quant 16-byte, the rest 4-byte aligned.
+ * Replaces repack_asymmetric_to_q4_32_blocks + repack_preq_blocks_to_preq2
+ * (asdsl/quantization/repack_q4_32.py:63-102; repack_preq2.py:22-49) in the
+ * preq cache build (experiments/phi4_cpu_run.py:627-787). */
+asdsl_status asdsl_repack_asym_to_preq2(const uint8_t* packed, const float* scales, const float* biases,
+                                        uint8_t* meta, uint8_t* quant, int rows, int cols, int group_size,
+                                        asdsl_stream_t stream);
+
+/* fp32 weights[rows][cols] -> 66-byte Q4_128 blocks: fp16(amax/7), levels
+ * clip(round_half_even(w * f32(7/amax)) + 8, 0, 15); amax < 1e-12: scale 0,
+ * nibbles 0x88.  group_size must be 128; weights 16-byte aligned.
+ * Replaces repack_fp32_to_q4_128_blocks (asdsl/quantization/repack_q4_128.py:72-92). */
+asdsl_status asdsl_repack_fp32_to_q4_128(const float* weights, uint8_t* blocks, int rows, int cols, int group_size,
+                                         asdsl_stream_t stream);
+
+/* packed + scales + biases (gs 128) -> Q4_128 blocks: each group decoded in
+ * float32 as (q - f32(zero)) * f32(max(s, 1e-8)), then requantized as above.
+ * Replaces repack_asymmetric_to_q4_128_blocks (asdsl/quantization/repack_q4_128.py:34-69). */
+asdsl_status asdsl_repack_asym_to_q4_128(const uint8_t* packed, const float* scales, const float* biases,
+                                         uint8_t* blocks, int rows, int cols, int group_size,
+                                         asdsl_stream_t stream);
+
+/* Q4_128 blocks[rows][cols/128][66] -> preq2-g128 (meta, quant): meta =
+ * fp16 block scale | fp16 8.0 (the symmetric group as scale s, zero 8, so
+ * every weight decodes to the same (q - 8) * s); the 64 nibble bytes move
+ * into 4-row bands of 64-byte slots.  blocks 2-byte, meta 4-byte, quant
+ * 16-byte aligned.  No counterpart in the reference (its g128 tensors stay
+ * Q4_128 blocks, experiments/phi4_cpu_run.py:637-646); it lets the preq
+ * cache at group size 128 feed the preq2-g128 GEMVs and decode step. */
+asdsl_status asdsl_repack_q4_128_to_preq2(const uint8_t* blocks, uint8_t* meta, uint8_t* quant, int rows, int cols,
+                                          asdsl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

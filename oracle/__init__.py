@@ -246,3 +246,74 @@ def sparse_down_proj_T(wT, sT, bT, x, rows, in_dim: int, out_dim: int, group_siz
                                     rows.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), rows.size,
                                     _p(y, _c_f32p), in_dim, out_dim, group_size)
     return y
+
+
+# -------------------------------------------------------------------- repack
+_c_u16p = ctypes.POINTER(ctypes.c_uint16)
+_c_f64p = ctypes.POINTER(ctypes.c_double)
+
+
+def double_to_half(d) -> np.ndarray:
+    """float64 -> fp16 bits (uint16), round to nearest even."""
+    d = np.ascontiguousarray(d, dtype=np.float64).reshape(-1)
+    out = np.empty(d.size, np.uint16)
+    lib().oracle_double_to_half(_p(d, _c_f64p), _p(out, _c_u16p), d.size)
+    return out
+
+
+def repack_asym_to_q4_32(packed, scales, biases, rows: int, cols: int) -> np.ndarray:
+    """repack_q4_32.py:63-102 -> flat 20-byte preq blocks (rows * cols/32 * 20)."""
+    pk, sc, bi = _u8(packed), _f32(scales).reshape(-1), _f32(biases).reshape(-1)
+    out = np.empty(rows * (cols // 32) * 20, np.uint8)
+    lib().oracle_repack_asym_to_q4_32(_p(pk, _c_u8p), _p(sc, _c_f32p), _p(bi, _c_f32p), _p(out, _c_u8p), rows, cols)
+    return out
+
+
+def _preq2_sizes(rows: int, cols: int, gs: int) -> tuple[int, int]:
+    G = cols // gs
+    return rows * G * 4, (rows + 3) // 4 * G * 2 * gs
+
+
+def repack_preq_to_preq2(preq, rows: int, cols: int) -> tuple[np.ndarray, np.ndarray]:
+    """repack_preq2.py:22-49 -> flat (meta, quant)."""
+    pq = _u8(preq)
+    mb, qb = _preq2_sizes(rows, cols, 32)
+    meta, quant = np.empty(mb, np.uint8), np.empty(qb, np.uint8)
+    lib().oracle_repack_preq_to_preq2(_p(pq, _c_u8p), _p(meta, _c_u8p), _p(quant, _c_u8p), rows, cols)
+    return meta, quant
+
+
+def repack_asym_to_preq2(packed, scales, biases, rows: int, cols: int, group_size: int = 32):
+    """Asymmetric packed Q4 -> flat preq2 (meta, quant) at group size 32 or 128."""
+    pk, sc, bi = _u8(packed), _f32(scales).reshape(-1), _f32(biases).reshape(-1)
+    mb, qb = _preq2_sizes(rows, cols, group_size)
+    meta, quant = np.empty(mb, np.uint8), np.empty(qb, np.uint8)
+    lib().oracle_repack_asym_to_preq2(_p(pk, _c_u8p), _p(sc, _c_f32p), _p(bi, _c_f32p), _p(meta, _c_u8p),
+                                      _p(quant, _c_u8p), rows, cols, group_size)
+    return meta, quant
+
+
+def repack_fp32_to_q4_128(w, rows: int, cols: int) -> np.ndarray:
+    """repack_q4_128.py:72-92 -> flat 66-byte Q4_128 blocks."""
+    wf = _f32(w).reshape(-1)
+    out = np.empty(rows * (cols // 128) * 66, np.uint8)
+    lib().oracle_repack_fp32_to_q4_128(_p(wf, _c_f32p), _p(out, _c_u8p), rows, cols)
+    return out
+
+
+def repack_asym_to_q4_128(packed, scales, biases, rows: int, cols: int) -> np.ndarray:
+    """repack_q4_128.py:34-69 -> flat 66-byte Q4_128 blocks."""
+    pk, sc, bi = _u8(packed), _f32(scales).reshape(-1), _f32(biases).reshape(-1)
+    out = np.empty(rows * (cols // 128) * 66, np.uint8)
+    lib().oracle_repack_asym_to_q4_128(_p(pk, _c_u8p), _p(sc, _c_f32p), _p(bi, _c_f32p), _p(out, _c_u8p), rows,
+                                       cols)
+    return out
+
+
+def repack_q4_128_to_preq2(blocks, rows: int, cols: int) -> tuple[np.ndarray, np.ndarray]:
+    """Q4_128 blocks -> flat preq2-g128 (meta, quant) with zero 8."""
+    b = _u8(blocks)
+    mb, qb = _preq2_sizes(rows, cols, 128)
+    meta, quant = np.empty(mb, np.uint8), np.empty(qb, np.uint8)
+    lib().oracle_repack_q4_128_to_preq2(_p(b, _c_u8p), _p(meta, _c_u8p), _p(quant, _c_u8p), rows, cols)
+    return meta, quant

@@ -410,3 +410,168 @@ EXPORT void oracle_sparse_down_proj_T(const uint8_t* wT, const float* sT, const 
         y[o] = (float)a;
     }
 }
+
+/* ------------------------------------------------------------------ repack */
+
+/* float64 -> IEEE binary16 bits, round to nearest even: subnormals, overflow
+ * to inf at |d| >= 65520 (the tie above 65504 goes to the even 65536).  This
+ * is numpy's float16 cast of a Python float, which the reference's repackers
+ * apply to fp32 scales and to float64 zero points
+ * (asdsl/quantization/repack_q4_32.py:19-20; repack_q4_128.py:18-19). */
+static uint16_t double_to_half(double d) {
+    const uint16_t sign = signbit(d) ? 0x8000u : 0u;
+    if (isnan(d)) return (uint16_t)(sign | 0x7E00u);
+    const double a = fabs(d);
+    if (a >= 65520.0) return (uint16_t)(sign | 0x7C00u);
+    if (a < ldexp(1.0, -14)) {                          /* subnormal: units of 2^-24 */
+        const double m = nearbyint(ldexp(a, 24));       /* exact scaling, ties to even */
+        return (uint16_t)(sign | (uint16_t)m);          /* m == 1024 is the smallest normal */
+    }
+    int ex;
+    frexp(a, &ex);                                      /* a = f * 2^ex, f in [0.5, 1) */
+    int e = ex - 1;                                     /* a in [2^e, 2^(e+1)) */
+    double m = nearbyint((ldexp(a, -e) - 1.0) * 1024.0);  /* every step exact in double */
+    if (m == 1024.0) {
+        m = 0.0;
+        ++e;
+    }
+    return (uint16_t)(sign | (uint16_t)((e + 15) << 10) | (uint16_t)m);
+}
+
+EXPORT void oracle_double_to_half(const double* d, uint16_t* out, int n) {
+    for (int i = 0; i < n; ++i) out[i] = double_to_half(d[i]);
+}
+
+static void wr16(uint8_t* p, uint16_t v) {
+    p[0] = (uint8_t)(v & 0xFF);
+    p[1] = (uint8_t)(v >> 8);
+}
+
+/* float(max(s, 1e-8)) with s a numpy float32 (repack_q4_32.py:87): Python's
+ * max keeps s unless 1e-8 > s, a comparison numpy makes in float32; the
+ * result is the float64 1e-8 or s. */
+static double floor_scale(float s) { return (float)1e-8 > s ? 1e-8 : (double)s; }
+
+/* repack_asymmetric_to_q4_32_blocks (asdsl/quantization/repack_q4_32.py:63-102):
+ * per (row, group of 32) a 20-byte block: fp16(max(s, 1e-8)), fp16(-b / max(s, 1e-8))
+ * with the division in float64, then the group's 16 packed bytes unchanged
+ * (unpack low-nibble-first, repack (q[1::2] << 4) | q[0::2]: the same bytes). */
+EXPORT void oracle_repack_asym_to_q4_32(const uint8_t* packed, const float* scales, const float* biases,
+                                        uint8_t* blocks, int rows, int cols) {
+    const int G = cols / 32;
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < G; ++g) {
+            const size_t gi = (size_t)r * G + g;
+            const double sc = floor_scale(scales[gi]);
+            const double zero = -(double)biases[gi] / sc;
+            uint8_t* blk = blocks + gi * 20;
+            wr16(blk, double_to_half(sc));
+            wr16(blk + 2, double_to_half(zero));
+            memcpy(blk + 4, packed + (size_t)r * (cols / 2) + (size_t)g * 16, 16);
+        }
+}
+
+/* repack_preq_blocks_to_preq2 (asdsl/quantization/repack_preq2.py:22-49):
+ * meta[row][g] = block bytes 0..3; quant[row/4][g][16*(row%4) ..+16] = block
+ * bytes 4..19; the slots of rows past `rows` in the last band are zero. */
+EXPORT void oracle_repack_preq_to_preq2(const uint8_t* preq, uint8_t* meta, uint8_t* quant, int rows, int cols) {
+    const int G = cols / 32;
+    const int bands = (rows + 3) / 4;
+    memset(quant, 0, (size_t)bands * G * 64);
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < G; ++g) {
+            const uint8_t* blk = preq + ((size_t)r * G + g) * 20;
+            memcpy(meta + ((size_t)r * G + g) * 4, blk, 4);
+            memcpy(quant + ((size_t)(r / 4) * G + g) * 64 + 16 * (r % 4), blk + 4, 16);
+        }
+}
+
+/* The asymmetric packed weights straight into the preq2 layout at group size
+ * gs (32: the composition repack_q4_32 -> repack_preq2, byte for byte; 128:
+ * the same per-group fp16 (scale, zero) and 4-row bands of 64-byte slots). */
+EXPORT void oracle_repack_asym_to_preq2(const uint8_t* packed, const float* scales, const float* biases,
+                                        uint8_t* meta, uint8_t* quant, int rows, int cols, int gs) {
+    const int G = cols / gs;
+    const int nb = gs / 2;
+    const int bands = (rows + 3) / 4;
+    memset(quant, 0, (size_t)bands * G * 4 * nb);
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < G; ++g) {
+            const size_t gi = (size_t)r * G + g;
+            const double sc = floor_scale(scales[gi]);
+            wr16(meta + gi * 4, double_to_half(sc));
+            wr16(meta + gi * 4 + 2, double_to_half(-(double)biases[gi] / sc));
+            memcpy(quant + ((size_t)(r / 4) * G + g) * 4 * nb + (size_t)nb * (r % 4),
+                   packed + (size_t)r * (cols / 2) + (size_t)g * nb, nb);
+        }
+}
+
+/* _symmetric_quantize_group (asdsl/quantization/repack_q4_128.py:22-31) on
+ * 128 float32 weights: amax = max|w|; below 1e-12 the block is scale 0 and
+ * nibbles 0x88; else scale = amax / 7 and inv = 7 / amax in float64, and
+ * q = clip(round(w * f32(inv)) + 8, 0, 15) in float32 (numpy rounds half to
+ * even); the block is fp16(scale) then the 64 packed nibble bytes. */
+static void q4_128_group(const float* w, uint8_t* blk) {
+    float amax = 0.0f;
+    for (int i = 0; i < 128; ++i) amax = fabsf(w[i]) > amax ? fabsf(w[i]) : amax;
+    if ((double)amax < 1e-12) {
+        wr16(blk, 0);
+        memset(blk + 2, 0x88, 64);
+        return;
+    }
+    const double scale = (double)amax / 7.0;
+    const float inv = (float)(7.0 / (double)amax);
+    uint8_t q[128];
+    for (int i = 0; i < 128; ++i) {
+        float v = nearbyintf(w[i] * inv) + 8.0f;
+        v = v < 0.0f ? 0.0f : (v > 15.0f ? 15.0f : v);
+        q[i] = (uint8_t)v;
+    }
+    wr16(blk, double_to_half(scale));
+    for (int i = 0; i < 64; ++i) blk[2 + i] = (uint8_t)((q[2 * i + 1] << 4) | q[2 * i]);
+}
+
+/* repack_fp32_to_q4_128_blocks (asdsl/quantization/repack_q4_128.py:72-92). */
+EXPORT void oracle_repack_fp32_to_q4_128(const float* w, uint8_t* blocks, int rows, int cols) {
+    const int G = cols / 128;
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < G; ++g)
+            q4_128_group(w + (size_t)r * cols + (size_t)g * 128, blocks + ((size_t)r * G + g) * 66);
+}
+
+/* repack_asymmetric_to_q4_128_blocks (asdsl/quantization/repack_q4_128.py:34-69):
+ * the asymmetric group dequantized as float32 (q - f32(zero)) * f32(scale),
+ * zero = -b / max(s, 1e-8) in float64, then requantized symmetrically. */
+EXPORT void oracle_repack_asym_to_q4_128(const uint8_t* packed, const float* scales, const float* biases,
+                                         uint8_t* blocks, int rows, int cols) {
+    const int G = cols / 128;
+    float wf[128];
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < G; ++g) {
+            const size_t gi = (size_t)r * G + g;
+            const double sc = floor_scale(scales[gi]);
+            const float zero32 = (float)(-(double)biases[gi] / sc);
+            const float sc32 = (float)sc;
+            const uint8_t* pg = packed + (size_t)r * (cols / 2) + (size_t)g * 64;
+            for (int i = 0; i < 128; ++i) wf[i] = ((float)nib(pg, i) - zero32) * sc32;
+            q4_128_group(wf, blocks + gi * 66);
+        }
+}
+
+/* Q4_128 blocks -> preq2-g128 (no reference counterpart): meta = block
+ * scale | fp16 8.0, the 64 nibble bytes into the row's band slot; slots of
+ * rows past `rows` in the last band are zero. */
+EXPORT void oracle_repack_q4_128_to_preq2(const uint8_t* blocks, uint8_t* meta, uint8_t* quant, int rows, int cols) {
+    const int G = cols / 128;
+    const int bands = (rows + 3) / 4;
+    memset(quant, 0, (size_t)bands * G * 256);
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < G; ++g) {
+            const uint8_t* blk = blocks + ((size_t)r * G + g) * 66;
+            uint8_t* m = meta + ((size_t)r * G + g) * 4;
+            m[0] = blk[0];
+            m[1] = blk[1];
+            wr16(m + 2, 0x4800u);
+            memcpy(quant + ((size_t)(r / 4) * G + g) * 256 + 64 * (r % 4), blk + 2, 64);
+        }
+}

@@ -45,3 +45,48 @@ def test_q4_128_block_layout():
     assert b[:2].view(np.float16)[0] == np.float16(0.1)
     assert b[2] == (15 | (1 << 4))  # q0 = 7+8, q1 = -7+8, low nibble first
     assert np.all(b[3:] == 0x88)
+
+
+def _asym(rows, cols, gs, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 16, (rows, cols), dtype=np.uint8)
+    packed = ((q[:, 1::2] << 4) | q[:, 0::2]).astype(np.uint8)
+    sc = rng.uniform(0.01, 0.5, (rows, cols // gs)).astype(np.float32)
+    bi = rng.uniform(-0.1, 0.1, (rows, cols // gs)).astype(np.float32)
+    sc[0, 0], sc[0, 1] = np.float32(1e-8), 0.0
+    return packed, sc, bi
+
+
+def test_host_repackers_match_the_oracle():
+    """The host restatements write the oracle's bytes (tail bands, edge
+    scales, a zero Q4_128 group included)."""
+    import oracle
+    from asdsl.quantization import repack as rp
+
+    rows = 10
+    packed, sc, bi = _asym(rows, 256, 32, 1)
+    assert np.array_equal(rp.repack_asymmetric_to_q4_32_blocks(packed, sc, bi, rows, 256).reshape(-1),
+                          oracle.repack_asym_to_q4_32(packed, sc, bi, rows, 256))
+    for gs in (32, 128):
+        packed, sc, bi = _asym(rows, 512, gs, 2 + gs)
+        got = rp.repack_asymmetric_to_preq2(packed, sc, bi, rows, 512, gs)
+        want = oracle.repack_asym_to_preq2(packed, sc, bi, rows, 512, gs)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    packed, sc, bi = _asym(rows, 512, 128, 3)
+    assert np.array_equal(rp.repack_asymmetric_to_q4_128_blocks(packed, sc, bi, rows, 512).reshape(-1),
+                          oracle.repack_asym_to_q4_128(packed, sc, bi, rows, 512))
+    w = syn.gaussian_weights(rows, 512, 4)
+    w[2, 128:256] = 0.0
+    blocks = rp.repack_fp32_to_q4_128_blocks(w, rows, 512)
+    assert np.array_equal(blocks.reshape(-1), oracle.repack_fp32_to_q4_128(w, rows, 512))
+    got = rp.repack_q4_128_blocks_to_preq2(blocks, rows, 512)
+    want = oracle.repack_q4_128_to_preq2(blocks, rows, 512)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+
+
+def test_reference_module_names():
+    from asdsl.quantization import repack_preq2, repack_q4_128, repack_q4_32
+
+    assert repack_q4_32.BLOCK_SIZE == 20 and repack_q4_128.BLOCK_SIZE == 66 and repack_q4_128.GROUP_SIZE == 128
+    assert repack_preq2.preq2_flat_sizes(10, 256, 32) == (10 * 8 * 4, 3 * 8 * 64)
+    assert callable(repack_q4_32.repack_asymmetric_to_q4_32_blocks)
