@@ -393,13 +393,14 @@ asdsl_status asdsl_repack_asym_to_preq2(const uint8_t* packed, const float* scal
 
 /* fp32 weights[rows][cols] -> 66-byte Q4_128 blocks: fp16(amax/7), levels
  * clip(round_half_even(w * f32(7/amax)) + 8, 0, 15); amax < 1e-12: scale 0,
- * nibbles 0x88.  group_size must be 128; weights 16-byte aligned.
+ * nibbles 0x88.  group_size must be 128; weights 16-byte, blocks 4-byte aligned.
  * Replaces repack_fp32_to_q4_128_blocks (asdsl/quantization/repack_q4_128.py:72-92). */
 asdsl_status asdsl_repack_fp32_to_q4_128(const float* weights, uint8_t* blocks, int rows, int cols, int group_size,
                                          asdsl_stream_t stream);
 
 /* packed + scales + biases (gs 128) -> Q4_128 blocks: each group decoded in
  * float32 as (q - f32(zero)) * f32(max(s, 1e-8)), then requantized as above.
+ * packed 16-byte, scales, biases and blocks 4-byte aligned.
  * Replaces repack_asymmetric_to_q4_128_blocks (asdsl/quantization/repack_q4_128.py:34-69). */
 asdsl_status asdsl_repack_asym_to_q4_128(const uint8_t* packed, const float* scales, const float* biases,
                                          uint8_t* blocks, int rows, int cols, int group_size,
