@@ -661,6 +661,13 @@ def repack_rows(args, oracle) -> list:
         lambda c, o, h: lib.asdsl_repack_preq_to_preq2(P(c["preq"]), P(o["meta"]), P(o["quant"]), M, K, 32, h),
         lambda hc, n: oracle.repack_preq_to_preq2(hc["preq"][: n * G32 * 20], n, K), CR)
 
+    row("F2 repack asym->preq (Q4_32 blocks)", "lm_head 200064x3072 g32", M, K,
+        M * K // 2 + 8 * M * G32 + M * G32 * 20, lambda: asym(M, K, 32), {"blocks": M * G32 * 20},
+        lambda c, o, h: lib.asdsl_repack_asym_to_q4_32(P(c["packed"]), P(c["sc"]), P(c["bi"]), P(o["blocks"]),
+                                                       M, K, 32, h),
+        lambda hc, n: oracle.repack_asym_to_q4_32(hc["packed"][: n * K // 2], hc["sc"][: n * G32],
+                                                  hc["bi"][: n * G32], n, K), CR)
+
     in_b = M * K // 2 + 8 * M * G128
     row("F2 repack asym->preq2 g128", "lm_head 200064x3072", M, K, in_b + M * G128 * 4 + bands * G128 * 256,
         lambda: asym(M, K, 128), {"meta": M * G128 * 4, "quant": bands * G128 * 256},
