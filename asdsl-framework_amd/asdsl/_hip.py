@@ -63,6 +63,9 @@ SIGNATURES: dict[str, list] = {
     "asdsl_attention_f16kv": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "asdsl_decode_work_bytes": [_P],
     "asdsl_decode_token": [_P, _P, _P, _P, _P, _P],
+    "asdsl_decode_verify_work_bytes": [_P, _I],
+    "asdsl_decode_verify": [_P, _P, _I, _P, _P, _P, _P, _P],
+    "asdsl_kv_zero_from": [_P, _P, _I, _I, _I, _I, _P],
     "asdsl_repack_preq_to_preq2": [_P, _P, _P, _I, _I, _I, _P],
     "asdsl_repack_asym_to_q4_32": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_repack_asym_to_preq2": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
@@ -71,7 +74,7 @@ SIGNATURES: dict[str, list] = {
     "asdsl_repack_q4_128_to_preq2": [_P, _P, _P, _I, _I, _P],
 }
 _RESTYPE = {"asdsl_last_error": ctypes.c_char_p, "asdsl_attention_work_floats": ctypes.c_size_t,
-            "asdsl_decode_work_bytes": ctypes.c_size_t}
+            "asdsl_decode_work_bytes": ctypes.c_size_t, "asdsl_decode_verify_work_bytes": ctypes.c_size_t}
 
 
 class HipLibraryMissing(ImportError):

@@ -156,6 +156,11 @@ class DecodeEngine:
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.logits = torch.empty(cfg.vocab, dtype=torch.float32, device=dev)
         self._graph = None
+        # committed KV length and its snapshot stack (UnifiedEngine::kv_seq_len_,
+        # kv_snapshot_stack_), host-side like the reference's
+        self.kv_seq_len = 0
+        self._kv_snapshots: list[int] = []
+        self._verify = None  # work, token, logits and next-token buffers of the verify pass
 
     # ------------------------------------------------------------ building
     @classmethod
@@ -200,6 +205,7 @@ class DecodeEngine:
                     L[n][:, :ctx] = torch.randn((self.cfg.n_kv_heads, ctx, self.cfg.head_dim), generator=gen,
                                                 device=L[n].device, dtype=torch.float32).half()
         self.pos.fill_(ctx)
+        self.kv_seq_len = ctx
 
     # ------------------------------------------------------------ stepping
     def _queue_step(self, stream: int) -> None:
@@ -217,6 +223,7 @@ class DecodeEngine:
         self.token.fill_(token_id)
         self.pos.fill_(pos)
         self._queue_step(_hip.stream_handle())
+        self.kv_seq_len = max(self.kv_seq_len, pos + 1)
         return self.logits
 
     def next_token(self) -> int:
@@ -249,6 +256,88 @@ class DecodeEngine:
         if self._graph is None:
             self.capture()
         self._graph.replay()
+
+    # ------------------------------------------------------------ verify
+    MAX_VERIFY_TOKENS = 16
+
+    def forward_batch_all_logits(self, tokens, start_pos: int):
+        """Logits of every column of a multi-token pass (the speculative
+        verify; the reference's UnifiedEngine::forward_verify_batch and its
+        bridge call forward_batch_all_logits): tokens[i] at position
+        start_pos + i, K/V written at those positions, the projections as
+        batched GEMVs.  Returns a device tensor [n][vocab]; the greedy next
+        token of each column is ``verify_next_tokens()``."""
+        import torch
+
+        toks = [int(t) for t in tokens]
+        n = len(toks)
+        c = self.cfg
+        if not 1 <= n <= self.MAX_VERIFY_TOKENS:
+            raise ValueError(f"forward_batch_all_logits: 1..{self.MAX_VERIFY_TOKENS} tokens, got {n}")
+        if any(not 0 <= t < c.vocab for t in toks):
+            raise ValueError("forward_batch_all_logits: token_id out of vocab range")
+        if not (0 <= start_pos and start_pos + n <= c.max_seq):
+            raise ValueError("forward_batch_all_logits: positions out of kv-cache range")
+        if self._verify is None:
+            dev = self.token.device
+            nbytes = _hip.LIB.asdsl_decode_verify_work_bytes(ctypes.byref(self._model), self.MAX_VERIFY_TOKENS)
+            if nbytes == 0:
+                raise ValueError(f"invalid decode model: {_hip.last_error()}")
+            self._verify = {
+                "work": torch.empty(nbytes, dtype=torch.uint8, device=dev),
+                "tokens": torch.zeros(self.MAX_VERIFY_TOKENS, dtype=torch.int32, device=dev),
+                "next": torch.zeros(self.MAX_VERIFY_TOKENS, dtype=torch.int32, device=dev),
+                "logits": torch.empty((self.MAX_VERIFY_TOKENS, c.vocab), dtype=torch.float32, device=dev),
+            }
+        v = self._verify
+        v["tokens"][:n].copy_(torch.tensor(toks, dtype=torch.int32))
+        self.pos.fill_(start_pos)
+        _hip.check(_hip.LIB.asdsl_decode_verify(ctypes.byref(self._model), _hip.ptr(v["tokens"]), n,
+                                                _hip.ptr(self.pos), _hip.ptr(v["logits"]), _hip.ptr(v["next"]),
+                                                _hip.ptr(v["work"]), _hip.stream_handle()),
+                   "asdsl_decode_verify")
+        self.pos.fill_(start_pos + n)
+        self.kv_seq_len = max(self.kv_seq_len, start_pos + n)
+        self._verify_n = n
+        return v["logits"][:n]
+
+    forward_verify_batch = forward_batch_all_logits
+
+    def verify_next_tokens(self) -> list[int]:
+        """Greedy argmax of each column of the last multi-token pass."""
+        return [int(t) for t in self._verify["next"][: self._verify_n].tolist()]
+
+    # ------------------------------------------------------------ KV bookkeeping
+    def get_kv_seq_len(self) -> int:
+        return self.kv_seq_len
+
+    def truncate_kv(self, new_len: int) -> None:
+        """UnifiedEngine::truncate_kv (unified_engine.cpp:1298-1307): clamp to
+        [0, max_seq], zero every layer's K/V rows from there on, set the
+        committed length (and the device position) to it."""
+        c = self.cfg
+        new_len = min(max(int(new_len), 0), c.max_seq)
+        for L in self.layers:
+            _hip.check(_hip.LIB.asdsl_kv_zero_from(_hip.ptr(L["k_cache"]), _hip.ptr(L["v_cache"]), c.n_kv_heads,
+                                                   c.head_dim, c.max_seq, new_len, _hip.stream_handle()),
+                       "asdsl_kv_zero_from")
+        self.kv_seq_len = new_len
+        self.pos.fill_(new_len)
+
+    def snapshot_kv(self) -> None:
+        """Push the committed KV length (unified_engine.cpp:1285-1287)."""
+        self._kv_snapshots.append(self.kv_seq_len)
+
+    def restore_kv(self) -> None:
+        """Pop the last snapshot and truncate to it; no-op without one
+        (unified_engine.cpp:1289-1296)."""
+        if self._kv_snapshots:
+            self.truncate_kv(self._kv_snapshots.pop())
+
+    def reset_session(self) -> None:
+        """Empty KV cache and snapshot stack (unified_engine.cpp:1325-1337)."""
+        self.truncate_kv(0)
+        self._kv_snapshots.clear()
 
     # ------------------------------------------------------------ accounting
     def weight_bytes(self) -> int:

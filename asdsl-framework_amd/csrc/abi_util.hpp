@@ -74,6 +74,17 @@ asdsl_status device_workspace(hipStream_t stream, size_t bytes, void** out, cons
 // ASDSL_HIP_KSPLIT forces the K split of the preq2 kernels.
 int env_knob(const char* name);
 
+// The batched preq2 GEMV behind asdsl_gemv_preq2_fused_batch.  allow_mfma =
+// false keeps every column on the dot4 kernels.  The MFMA form sums each
+// column's groups in another fp32 order (~1e-7 apart); a consumer that
+// quantizes the result to int8 again (the next layer's GEMV) can see such a
+// difference move one element across a rounding boundary, about 5e-4 of that
+// GEMV's output per flipped level.  A pass that must track the single-token
+// step's arithmetic therefore uses the dot4 form.
+asdsl_status preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X, float* Y,
+                               int out_features, int in_features, int group_size, int n_cols, asdsl_stream_t stream,
+                               bool allow_mfma);
+
 // Workgroups for a streaming kernel: enough tiles for every wave, capped at
 // `per_cu` workgroups per compute unit (waves then loop over tiles).
 inline int stream_grid(long long tiles, int waves_per_wg, int per_cu, int cus) {

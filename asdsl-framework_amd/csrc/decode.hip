@@ -54,120 +54,27 @@ __global__ void finalize_kernel(const unsigned long long* __restrict__ amax, int
     }
 }
 
-// Attention partials of one KV head over positions [s*kSplit, min((s+1)*kSplit, pos+1)).
-// G = query heads per KV head.  Lane l of a wave reads dims 8*(l%16).. of
-// position 4*step + l/16, so every K/V load instruction moves 1 KiB of
-// consecutive positions.  Writes per query head (m, l, acc[128]) with
-// acc = sum_p exp(s_p - m) v_p.  The split holding `pos` also applies RoPE to
-// the new K, rounds K and V to fp16 and stores them in the cache.
-// Each wave keeps its 32 positions' scores in registers and forms its own
-// (max, sum, P.V); the four waves are merged in LDS behind one barrier (a
-// block-wide softmax through LDS took two more barriers and ~2 us longer).
-
-template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
-    const float* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
-    float* __restrict__ part, int n_heads, int n_kv, int max_seq, int rot_half, int nsplit) {
-    __shared__ float q_s[G][kHeadDim];
-    __shared__ float kv_new[2][kHeadDim];
-    __shared__ float wml[kAttnThreads / kWave][G][2];
-    __shared__ float wacc[kAttnThreads / kWave][G][kHeadDim];
-    const int s = static_cast<int>(blockIdx.x);
-    const int kvh = static_cast<int>(blockIdx.y);
-    const int pos = *pos_ptr;
-    const int p0 = s * kSplit;
-    // whole workgroup: this split is past the sequence, or the position is
-    // outside the cache (the combine then writes zeros)
-    if (p0 > pos || pos < 0 || pos >= max_seq) return;
-    const int p1 = min(p0 + kSplit, pos + 1);
+// Scores, split-local softmax and P.V of one split for the G query heads of a
+// KV head, then the merge of the four waves: lane (wave, pg, dc) holds the
+// K/V rows of positions p0 + 4*wave + pg + 16*it in kraw/vraw (dims
+// 8*dc..+8) and its query chunks in qr; positions >= p1 are masked.  With
+// NEW, position `pos` takes its K/V rows from kv_new (LDS) instead.  Writes
+// (m, l, acc[128]) of head hh at part + hh * head_stride.
+template <int G, bool NEW>
+__device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16], const uint4 (&vraw)[kSplit / 16],
+                                                const float (&qr)[G][8], int p0, int p1, int pos,
+                                                const float (*kv_new)[kHeadDim], float (*wml)[G][2],
+                                                float (*wacc)[G][kHeadDim], float* __restrict__ part,
+                                                size_t head_stride) {
+    constexpr int kIt = kSplit / 16;
     const int tid = static_cast<int>(threadIdx.x);
     const float inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(kHeadDim));
     const int lane = tid & (kWave - 1);
     const int wave = tid >> 6;
-    const int pg = lane >> 4;   // position within the wave's four
-    const int dc = lane & 15;   // 8-dim chunk
-    const size_t head_base = static_cast<size_t>(kvh) * max_seq * kHeadDim;
-
-    // RoPE inputs first (small, from L2), then every K and V row this lane
-    // will use (they depend on nothing but pos): loads complete in issue
-    // order, so the rotation waits only for its own inputs and the kernel
-    // waits on HBM once.  Rows of positions 4*wave + pg + 16*it of the split;
-    // `pos` itself comes from LDS.
-    const float* cp = rope_cos + static_cast<size_t>(pos) * rot_half;
-    const float* sp = rope_sin + static_cast<size_t>(pos) * rot_half;
-    constexpr int kRope = ((G + 1) * kHeadDim + kAttnThreads - 1) / kAttnThreads;
-    float rx[kRope][4];
-#pragma unroll
-    for (int r = 0; r < kRope; ++r) {
-        const int e = tid + r * kAttnThreads;
-        const int hh = e / kHeadDim;
-        const int d = e % kHeadDim;
-        if (hh <= G) {
-            const float* src = hh < G ? qkv + static_cast<size_t>(kvh * G + hh) * kHeadDim
-                                      : qkv + static_cast<size_t>(n_heads + kvh) * kHeadDim;
-            if (d < 2 * rot_half) {
-                const int i = d < rot_half ? d : d - rot_half;
-                rx[r][0] = src[i];
-                rx[r][1] = src[i + rot_half];
-                rx[r][2] = cp[i];
-                rx[r][3] = sp[i];
-            } else {
-                rx[r][0] = src[d];
-            }
-        }
-    }
-    const float* vsrc = qkv + static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim;
-    const float vnew = tid < kHeadDim ? vsrc[tid] : 0.0f;
-    constexpr int kIt = kSplit / 16;
-    uint4 kraw[kIt], vraw[kIt];
-#pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-        const int p = p0 + wave * 4 + pg + 16 * it;
-        if (p < p1 && p != pos) {
-            const size_t at = head_base + static_cast<size_t>(p) * kHeadDim + 8 * dc;
-            kraw[it] = *reinterpret_cast<const uint4*>(kc + at);
-            vraw[it] = *reinterpret_cast<const uint4*>(vc + at);
-        } else {
-            kraw[it] = make_uint4(0u, 0u, 0u, 0u);
-            vraw[it] = kraw[it];
-        }
-    }
-
-    // RoPE (half split over the first 2*rot_half dims) on the G query heads
-    // and the KV head's new key; the new value as is.
-#pragma unroll
-    for (int r = 0; r < kRope; ++r) {
-        const int e = tid + r * kAttnThreads;
-        const int hh = e / kHeadDim;
-        const int d = e % kHeadDim;
-        if (hh <= G) {
-            float val;
-            if (d < 2 * rot_half) {
-                const float xf = rx[r][0], xs = rx[r][1], c = rx[r][2], sn = rx[r][3];
-                val = d < rot_half ? fmaf(xf, c, -(xs * sn)) : fmaf(xf, sn, xs * c);
-            } else {
-                val = rx[r][0];
-            }
-            if (hh < G) q_s[hh][d] = val;
-            else kv_new[0][d] = h2f(f2h(val));
-        }
-    }
-    if (tid < kHeadDim) kv_new[1][tid] = h2f(f2h(vnew));
-    __syncthreads();
-    if (pos < p1 && tid < kHeadDim) {
-        kc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
-        vc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[1][tid]);
-    }
-
-    float qr[G][8];
-#pragma unroll
-    for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
-
+    const int pg = lane >> 4;
+    const int dc = lane & 15;
     auto row_of = [&](const uint4& raw, int which, int p, float (&r)[8]) {
-        if (p == pos) {
+        if (NEW && p == pos) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) r[e] = kv_new[which][8 * dc + e];
         } else {
@@ -272,7 +179,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
             const float mw = wml[w][hh][0];
             sum = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wacc[w][hh][d], sum);
         }
-        part[(static_cast<size_t>(kvh * G + hh) * nsplit + s) * kPartStride + 2 + d] = sum;
+        part[hh * head_stride + 2 + d] = sum;
     }
     if (tid < G) {
         float M = wml[0][tid][0];
@@ -284,10 +191,126 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
             const float mw = wml[w][tid][0];
             L = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wml[w][tid][1], L);
         }
-        float* pp = part + (static_cast<size_t>(kvh * G + tid) * nsplit + s) * kPartStride;
+        float* pp = part + tid * head_stride;
         pp[0] = M;
         pp[1] = L;
     }
+}
+
+// Attention partials of one KV head over positions [s*kSplit, min((s+1)*kSplit, pos+1)).
+// G = query heads per KV head.  Lane l of a wave reads dims 8*(l%16).. of
+// position 4*step + l/16, so every K/V load instruction moves 1 KiB of
+// consecutive positions.  Writes per query head (m, l, acc[128]) with
+// acc = sum_p exp(s_p - m) v_p.  The split holding `pos` also applies RoPE to
+// the new K, rounds K and V to fp16 and stores them in the cache.
+// Each wave keeps its 32 positions' scores in registers and forms its own
+// (max, sum, P.V); the four waves are merged in LDS behind one barrier (a
+// block-wide softmax through LDS took two more barriers and ~2 us longer).
+
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
+    const float* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
+    float* __restrict__ part, int n_heads, int n_kv, int max_seq, int rot_half, int nsplit) {
+    __shared__ float q_s[G][kHeadDim];
+    __shared__ float kv_new[2][kHeadDim];
+    __shared__ float wml[kAttnThreads / kWave][G][2];
+    __shared__ float wacc[kAttnThreads / kWave][G][kHeadDim];
+    const int s = static_cast<int>(blockIdx.x);
+    const int kvh = static_cast<int>(blockIdx.y);
+    const int pos = *pos_ptr;
+    const int p0 = s * kSplit;
+    // whole workgroup: this split is past the sequence, or the position is
+    // outside the cache (the combine then writes zeros)
+    if (p0 > pos || pos < 0 || pos >= max_seq) return;
+    const int p1 = min(p0 + kSplit, pos + 1);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWave - 1);
+    const int wave = tid >> 6;
+    const int pg = lane >> 4;   // position within the wave's four
+    const int dc = lane & 15;   // 8-dim chunk
+    const size_t head_base = static_cast<size_t>(kvh) * max_seq * kHeadDim;
+
+    // RoPE inputs first (small, from L2), then every K and V row this lane
+    // will use (they depend on nothing but pos): loads complete in issue
+    // order, so the rotation waits only for its own inputs and the kernel
+    // waits on HBM once.  Rows of positions 4*wave + pg + 16*it of the split;
+    // `pos` itself comes from LDS.
+    const float* cp = rope_cos + static_cast<size_t>(pos) * rot_half;
+    const float* sp = rope_sin + static_cast<size_t>(pos) * rot_half;
+    constexpr int kRope = ((G + 1) * kHeadDim + kAttnThreads - 1) / kAttnThreads;
+    float rx[kRope][4];
+#pragma unroll
+    for (int r = 0; r < kRope; ++r) {
+        const int e = tid + r * kAttnThreads;
+        const int hh = e / kHeadDim;
+        const int d = e % kHeadDim;
+        if (hh <= G) {
+            const float* src = hh < G ? qkv + static_cast<size_t>(kvh * G + hh) * kHeadDim
+                                      : qkv + static_cast<size_t>(n_heads + kvh) * kHeadDim;
+            if (d < 2 * rot_half) {
+                const int i = d < rot_half ? d : d - rot_half;
+                rx[r][0] = src[i];
+                rx[r][1] = src[i + rot_half];
+                rx[r][2] = cp[i];
+                rx[r][3] = sp[i];
+            } else {
+                rx[r][0] = src[d];
+            }
+        }
+    }
+    const float* vsrc = qkv + static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim;
+    const float vnew = tid < kHeadDim ? vsrc[tid] : 0.0f;
+    constexpr int kIt = kSplit / 16;
+    uint4 kraw[kIt], vraw[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int p = p0 + wave * 4 + pg + 16 * it;
+        if (p < p1 && p != pos) {
+            const size_t at = head_base + static_cast<size_t>(p) * kHeadDim + 8 * dc;
+            kraw[it] = *reinterpret_cast<const uint4*>(kc + at);
+            vraw[it] = *reinterpret_cast<const uint4*>(vc + at);
+        } else {
+            kraw[it] = make_uint4(0u, 0u, 0u, 0u);
+            vraw[it] = kraw[it];
+        }
+    }
+
+    // RoPE (half split over the first 2*rot_half dims) on the G query heads
+    // and the KV head's new key; the new value as is.
+#pragma unroll
+    for (int r = 0; r < kRope; ++r) {
+        const int e = tid + r * kAttnThreads;
+        const int hh = e / kHeadDim;
+        const int d = e % kHeadDim;
+        if (hh <= G) {
+            float val;
+            if (d < 2 * rot_half) {
+                const float xf = rx[r][0], xs = rx[r][1], c = rx[r][2], sn = rx[r][3];
+                val = d < rot_half ? fmaf(xf, c, -(xs * sn)) : fmaf(xf, sn, xs * c);
+            } else {
+                val = rx[r][0];
+            }
+            if (hh < G) q_s[hh][d] = val;
+            else kv_new[0][d] = h2f(f2h(val));
+        }
+    }
+    if (tid < kHeadDim) kv_new[1][tid] = h2f(f2h(vnew));
+    __syncthreads();
+    if (pos < p1 && tid < kHeadDim) {
+        kc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
+        vc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[1][tid]);
+    }
+
+    float qr[G][8];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
+
+    attn_split_core<G, true>(kraw, vraw, qr, p0, p1, pos, kv_new, wml, wacc,
+                             part + (static_cast<size_t>(kvh * G) * nsplit + s) * kPartStride,
+                             static_cast<size_t>(nsplit) * kPartStride);
 }
 
 // out[h][d] = sum_s e_s acc_s[d] / sum_s e_s l_s, e_s = exp(m_s - max m).
@@ -295,6 +318,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 // splits (chunks of kChunk loads issued together, a running (max, sum,
 // output) rescaled between chunks); with more than one group the runs are
 // merged in LDS in split order.  One group when the splits fit one chunk.
+// blockIdx.y = column c of a multi-token pass (position *pos_ptr + c; its
+// partials and output follow column c - 1's); the decode step runs one column.
 constexpr int kCombineGroups = 4;
 constexpr int kCombineThreads = kCombineGroups * kHeadDim;
 
@@ -305,10 +330,13 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
     constexpr int kChunk = 16;
     __shared__ float gml[kCombineGroups][2];
     __shared__ float go[kCombineGroups][kHeadDim];
+    const int col = static_cast<int>(blockIdx.y);
     const int h = static_cast<int>(blockIdx.x);
     const int d = static_cast<int>(threadIdx.x) % kHeadDim;
     const int g = static_cast<int>(threadIdx.x) / kHeadDim;
-    const int pos = *pos_ptr;
+    const int pos = *pos_ptr + col;
+    part += static_cast<size_t>(col) * gridDim.x * nsplit * kPartStride;
+    out += static_cast<size_t>(col) * gridDim.x * kHeadDim;
     if (pos < 0 || pos >= max_seq) {  // outside the cache: no partials were written
         if (g == 0) out[static_cast<size_t>(h) * kHeadDim + d] = 0.0f;
         return;
@@ -442,6 +470,260 @@ asdsl_status check_model(const asdsl_decode_model* m) {
     return ASDSL_OK;
 }
 
+
+// ------------------------------------------------------------------ verify
+// A multi-token pass over n tokens at positions pos .. pos + n - 1, the
+// speculative verify of UnifiedEngine::forward_verify_batch
+// (unified_engine.cpp:1774-1789): column c of every activation matrix is
+// token c, the projections run as batched GEMVs (the dot4 form of
+// asdsl_gemv_preq2_fused_batch, whose per-column arithmetic follows the
+// single-column GEMV), and the elementwise steps use the decode step's
+// formulas, so a column tracks the single-token step to fp32 rounding.
+constexpr int kMaxVerifyTokens = 16;
+constexpr int kNormThreads = 512;  // 8 waves, as the fused prologue of the norm-fed GEMVs
+
+// H[c] = embed[tokens[c]] (fp16 -> fp32); clears the n argmax keys.
+__global__ __launch_bounds__(256) void verify_embed_kernel(const uint16_t* __restrict__ embed,
+                                                           const int* __restrict__ tokens, float* __restrict__ H,
+                                                           int hidden, int vocab, unsigned long long* __restrict__ keys) {
+    const int c = static_cast<int>(blockIdx.y);
+    const int t0 = tokens[c];
+    const int t = t0 >= 0 && t0 < vocab ? t0 : 0;
+    const uint16_t* row = embed + static_cast<size_t>(t) * hidden;
+    for (int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); i < hidden;
+         i += static_cast<int>(gridDim.x * blockDim.x))
+        H[static_cast<size_t>(c) * hidden + i] = h2f(row[i]);
+    if (blockIdx.x == 0 && threadIdx.x == 0) keys[c] = 0ull;
+}
+
+// Per column c (one workgroup): h = H[c] + D[c] (D may be null), written back
+// to H[c]; X[c] = (h * inv_rms) * w with inv_rms = 1 / sqrt(sum(h^2)/K + eps)
+// (residual_add_rmsnorm_f32, unified_engine.cpp:499-524).  The sum is formed
+// in the order of the single-token GEMV's fused prologue at 8 waves (the plan
+// of the norm-fed GEMVs at hidden 3072): thread t folds the 8-element chunks
+// t, t + 512, ... element by element, then a xor butterfly per wave and the
+// 8 wave sums in order, so both passes normalize identically.
+__global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __restrict__ H,
+                                                                       const float* __restrict__ D,
+                                                                       const float* __restrict__ w,
+                                                                       float* __restrict__ X, int K, float eps) {
+    __shared__ float red[kNormThreads / kWave];
+    const size_t c = blockIdx.x;
+    float4* h = reinterpret_cast<float4*>(H + c * K);
+    const float4* d = D ? reinterpret_cast<const float4*>(D + c * K) : nullptr;
+    float4* x = reinterpret_cast<float4*>(X + c * K);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int nchunk = K >> 3;
+    float ss = 0.0f;
+    for (int ch = tid; ch < nchunk; ch += kNormThreads) {
+        float v[8];
+        const float4 a = h[2 * ch], b = h[2 * ch + 1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        if (d) {
+            const float4 da = d[2 * ch], db = d[2 * ch + 1];
+            v[0] += da.x; v[1] += da.y; v[2] += da.z; v[3] += da.w;
+            v[4] += db.x; v[5] += db.y; v[6] += db.z; v[7] += db.w;
+            h[2 * ch] = make_float4(v[0], v[1], v[2], v[3]);
+            h[2 * ch + 1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
+    __syncthreads();
+    float tot = red[0];
+#pragma unroll
+    for (int q = 1; q < kNormThreads / kWave; ++q) tot += red[q];
+    const float inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+    for (int ch = tid; ch < nchunk; ch += kNormThreads) {
+        const float4 a = h[2 * ch], b = h[2 * ch + 1];
+        const float4 wa = w4[2 * ch], wb = w4[2 * ch + 1];
+        x[2 * ch] = make_float4((a.x * inv_rms) * wa.x, (a.y * inv_rms) * wa.y, (a.z * inv_rms) * wa.z,
+                               (a.w * inv_rms) * wa.w);
+        x[2 * ch + 1] = make_float4((b.x * inv_rms) * wb.x, (b.y * inv_rms) * wb.y, (b.z * inv_rms) * wb.z,
+                                   (b.w * inv_rms) * wb.w);
+    }
+}
+
+// RoPE of column c's query and key heads at position pos + c (grid: heads x
+// columns, one thread per dimension): rotated q (fp32) to Q[c][head], the
+// key and value rounded to fp16 into the caches at that position, as the
+// decode step does.  Columns past the cache write nothing.
+__global__ __launch_bounds__(kHeadDim) void verify_rope_kv_kernel(const float* __restrict__ QKV,
+                                                                  float* __restrict__ Q, uint16_t* __restrict__ kc,
+                                                                  uint16_t* __restrict__ vc,
+                                                                  const float* __restrict__ rope_cos,
+                                                                  const float* __restrict__ rope_sin,
+                                                                  const int* __restrict__ pos_ptr, int n_heads,
+                                                                  int n_kv, int max_seq, int rot_half) {
+    const int c = static_cast<int>(blockIdx.y);
+    const int hh = static_cast<int>(blockIdx.x);  // query heads, then key heads
+    const int d = static_cast<int>(threadIdx.x);
+    const int pos = *pos_ptr + c;
+    if (pos < 0 || pos >= max_seq) return;
+    const float* row = QKV + static_cast<size_t>(c) * (n_heads + 2 * n_kv) * kHeadDim;
+    const float* src = row + static_cast<size_t>(hh) * kHeadDim;
+    float val;
+    if (d < 2 * rot_half) {
+        const int i = d < rot_half ? d : d - rot_half;
+        const float xf = src[i], xs = src[i + rot_half];
+        const float cs = rope_cos[static_cast<size_t>(pos) * rot_half + i];
+        const float sn = rope_sin[static_cast<size_t>(pos) * rot_half + i];
+        val = d < rot_half ? fmaf(xf, cs, -(xs * sn)) : fmaf(xf, sn, xs * cs);
+    } else {
+        val = src[d];
+    }
+    if (hh < n_heads) {
+        Q[(static_cast<size_t>(c) * n_heads + hh) * kHeadDim + d] = val;
+    } else {
+        const int kvh = hh - n_heads;
+        const size_t at = (static_cast<size_t>(kvh) * max_seq + pos) * kHeadDim + d;
+        kc[at] = f2h(val);
+        vc[at] = f2h(row[static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim + d]);
+    }
+}
+
+// Attention partials of column c (position pos + c) for one KV head and one
+// split, every K/V row from the cache (the pass's own rows are there).
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const float* __restrict__ Q,
+                                                                           const uint16_t* __restrict__ kc,
+                                                                           const uint16_t* __restrict__ vc,
+                                                                           const int* __restrict__ pos_ptr,
+                                                                           float* __restrict__ part, int n_heads,
+                                                                           int max_seq, int nsplit) {
+    __shared__ float q_s[G][kHeadDim];
+    __shared__ float wml[kAttnThreads / kWave][G][2];
+    __shared__ float wacc[kAttnThreads / kWave][G][kHeadDim];
+    const int s = static_cast<int>(blockIdx.x);
+    const int kvh = static_cast<int>(blockIdx.y);
+    const int c = static_cast<int>(blockIdx.z);
+    const int pos = *pos_ptr + c;
+    const int p0 = s * kSplit;
+    if (p0 > pos || pos < 0 || pos >= max_seq) return;
+    const int p1 = min(p0 + kSplit, pos + 1);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWave - 1);
+    const int wave = tid >> 6;
+    const int pg = lane >> 4;
+    const int dc = lane & 15;
+    const size_t head_base = static_cast<size_t>(kvh) * max_seq * kHeadDim;
+    constexpr int kIt = kSplit / 16;
+    uint4 kraw[kIt], vraw[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int p = p0 + wave * 4 + pg + 16 * it;
+        if (p < p1) {
+            const size_t at = head_base + static_cast<size_t>(p) * kHeadDim + 8 * dc;
+            kraw[it] = *reinterpret_cast<const uint4*>(kc + at);
+            vraw[it] = *reinterpret_cast<const uint4*>(vc + at);
+        } else {
+            kraw[it] = make_uint4(0u, 0u, 0u, 0u);
+            vraw[it] = kraw[it];
+        }
+    }
+    const float* qsrc = Q + (static_cast<size_t>(c) * n_heads + kvh * G) * kHeadDim;
+    for (int e = tid; e < G * kHeadDim; e += kAttnThreads) q_s[e / kHeadDim][e % kHeadDim] = qsrc[e];
+    __syncthreads();
+    float qr[G][8];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
+    attn_split_core<G, false>(kraw, vraw, qr, p0, p1, pos, nullptr, wml, wacc,
+                              part + ((static_cast<size_t>(c) * n_heads + kvh * G) * nsplit + s) * kPartStride,
+                              static_cast<size_t>(nsplit) * kPartStride);
+}
+
+// S[c] = SwiGLU(gate, up) of GU[c] = [gate | up] with the FATReLU threshold
+// (swiglu_inplace, unified_engine.cpp:803-857; the decode prologue's formula).
+__global__ __launch_bounds__(256) void verify_swiglu_kernel(const float* __restrict__ GU, float* __restrict__ S,
+                                                            int ffn, float thr) {
+    const size_t c = blockIdx.y;
+    for (int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); i < ffn;
+         i += static_cast<int>(gridDim.x * blockDim.x))
+        S[c * ffn + i] = swiglu_ref(GU[c * 2 * ffn + i], GU[c * 2 * ffn + ffn + i], thr);
+}
+
+// keys[c] = max over rows of argmax_key(logits[c][row], row): the largest
+// logit, the first row among equals (argmax_f32_avx2, unified_engine.cpp:207-233).
+__global__ __launch_bounds__(256) void verify_argmax_kernel(const float* __restrict__ logits, int vocab,
+                                                            unsigned long long* __restrict__ keys) {
+    __shared__ unsigned long long red[256 / kWave];
+    const size_t c = blockIdx.y;
+    unsigned long long best = 0ull;
+    for (int r = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); r < vocab;
+         r += static_cast<int>(gridDim.x * blockDim.x)) {
+        const unsigned long long k = argmax_key(logits[c * vocab + r], r);
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long other = __shfl_xor(best, o, kWave);
+        best = other > best ? other : best;
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long tot = red[0];
+#pragma unroll
+        for (int q = 1; q < 256 / kWave; ++q) tot = red[q] > tot ? red[q] : tot;
+        atomicMax(keys + c, tot);
+    }
+}
+
+__global__ void verify_tokens_kernel(const unsigned long long* __restrict__ keys, int* __restrict__ next, int n) {
+    const int c = static_cast<int>(threadIdx.x);
+    if (c < n) next[c] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(keys[c]));
+}
+
+// Zero the cache rows [from, max_seq) of every KV head (zero_kv_from,
+// unified_engine.cpp:1263-1283), 16-byte stores.
+__global__ __launch_bounds__(256) void kv_zero_kernel(uint4* __restrict__ k, uint4* __restrict__ v, int n_kv,
+                                                      int max_seq, int from) {
+    const size_t per_head = static_cast<size_t>(max_seq - from) * (kHeadDim / 8);
+    const size_t total = per_head * n_kv;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const size_t h = i / per_head;
+        const size_t at = (h * max_seq + from) * (kHeadDim / 8) + (i - h * per_head);
+        k[at] = make_uint4(0u, 0u, 0u, 0u);
+        v[at] = make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
+// Work buffer layout of a verify pass of up to n tokens (offsets in floats).
+struct VerifyWork {
+    size_t H, X, QKV, Q, part, att, O, GU, S, keys, total;
+};
+
+VerifyWork verify_work(const asdsl_decode_model& m, int n) {
+    VerifyWork w{};
+    size_t at = 0;
+    auto take = [&](size_t cnt) {
+        const size_t here = at;
+        at += align64(cnt);
+        return here;
+    };
+    const size_t N = static_cast<size_t>(n);
+    const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
+    w.H = take(N * m.hidden);
+    w.X = take(N * (m.hidden > m.ffn ? m.hidden : m.ffn));
+    w.QKV = take(N * qkv_dim);
+    w.Q = take(N * m.n_heads * m.head_dim);
+    w.part = take(N * m.n_heads * attn_splits(m.max_seq) * kPartStride);
+    w.att = take(N * m.n_heads * m.head_dim);
+    w.O = take(N * m.hidden);
+    w.GU = take(N * 2 * m.ffn);
+    w.S = take(N * m.ffn);
+    w.keys = take(2 * N);
+    w.total = at;
+    return w;
+}
+
 }  // namespace
 }  // namespace asdsl
 
@@ -543,4 +825,108 @@ extern "C" asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int*
     if (st != ASDSL_OK) return st;
     return launch("finalize_kernel", finalize_kernel, dim3(1), dim3(64), 0, s,
                   static_cast<const unsigned long long*>(amax), token, pos);
+}
+
+extern "C" size_t asdsl_decode_verify_work_bytes(const asdsl_decode_model* model, int max_tokens) {
+    if (check_model(model) != ASDSL_OK || max_tokens < 1 || max_tokens > kMaxVerifyTokens) return 0;
+    return verify_work(*model, max_tokens).total * sizeof(float);
+}
+
+extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, const int* tokens, int n_tokens,
+                                            const int* pos, float* logits, int* next_tokens, void* work,
+                                            asdsl_stream_t stream) {
+    const asdsl_status cs = check_model(model);
+    if (cs != ASDSL_OK) return cs;
+    ASDSL_CHECK_ARG(tokens && pos && logits && next_tokens && work, "decode_verify: null pointer");
+    ASDSL_CHECK_ARG(n_tokens >= 1 && n_tokens <= kMaxVerifyTokens, "decode_verify: n_tokens must be in [1, %d]",
+                    kMaxVerifyTokens);
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(work) % 256 == 0, "decode_verify: work must be 256-byte aligned");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(logits) % 16 == 0, "decode_verify: logits must be 16-byte aligned");
+    const asdsl_decode_model& m = *model;
+    const int n = n_tokens;
+    const VerifyWork w = verify_work(m, n);
+    float* base = static_cast<float*>(work);
+    float* H = base + w.H;
+    float* X = base + w.X;
+    float* QKV = base + w.QKV;
+    float* Q = base + w.Q;
+    float* part = base + w.part;
+    float* att = base + w.att;
+    float* O = base + w.O;
+    float* GU = base + w.GU;
+    float* S = base + w.S;
+    auto* keys = reinterpret_cast<unsigned long long*>(base + w.keys);
+    hipStream_t s = as_hip(stream);
+    const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
+    const int q_dim = m.n_heads * m.head_dim;
+    const int nsplit = attn_splits(m.max_seq);
+    const int G = m.n_heads / m.n_kv_heads;
+
+    asdsl_status st = launch("verify_embed_kernel", verify_embed_kernel, dim3((m.hidden + 1023) / 1024, n), dim3(256),
+                             0, s, m.embed, tokens, H, m.hidden, m.vocab, keys);
+    if (st != ASDSL_OK) return st;
+    // H carries the residual stream of every column; O (attention output
+    // projection) and S -> O (down projection) are added in by the next norm.
+    const float* pending = nullptr;
+    for (int l = 0; l < m.n_layers; ++l) {
+        const asdsl_decode_layer& L = m.layers[l];
+        st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H, pending,
+                    L.rms_att, X, m.hidden, m.rms_eps);
+        if (st != ASDSL_OK) return st;
+        st = preq2_fused_batch(L.qkv_meta, L.qkv_quant, X, QKV, qkv_dim, m.hidden, m.gs_attn, n, stream, false);
+        if (st != ASDSL_OK) return st;
+        st = launch("verify_rope_kv_kernel", verify_rope_kv_kernel, dim3(m.n_heads + m.n_kv_heads, n), dim3(kHeadDim),
+                    0, s, static_cast<const float*>(QKV), Q, L.k_cache, L.v_cache, m.rope_cos, m.rope_sin, pos,
+                    m.n_heads, m.n_kv_heads, m.max_seq, m.rotary_dim / 2);
+        if (st != ASDSL_OK) return st;
+        const dim3 pgrid(nsplit, m.n_kv_heads, n);
+        switch (G) {
+            case 1: st = launch("verify_attn_partial_kernel", verify_attn_partial_kernel<1>, pgrid, dim3(kAttnThreads), 0, s, static_cast<const float*>(Q), static_cast<const uint16_t*>(L.k_cache), static_cast<const uint16_t*>(L.v_cache), pos, part, m.n_heads, m.max_seq, nsplit); break;
+            case 2: st = launch("verify_attn_partial_kernel", verify_attn_partial_kernel<2>, pgrid, dim3(kAttnThreads), 0, s, static_cast<const float*>(Q), static_cast<const uint16_t*>(L.k_cache), static_cast<const uint16_t*>(L.v_cache), pos, part, m.n_heads, m.max_seq, nsplit); break;
+            case 3: st = launch("verify_attn_partial_kernel", verify_attn_partial_kernel<3>, pgrid, dim3(kAttnThreads), 0, s, static_cast<const float*>(Q), static_cast<const uint16_t*>(L.k_cache), static_cast<const uint16_t*>(L.v_cache), pos, part, m.n_heads, m.max_seq, nsplit); break;
+            default: st = launch("verify_attn_partial_kernel", verify_attn_partial_kernel<4>, pgrid, dim3(kAttnThreads), 0, s, static_cast<const float*>(Q), static_cast<const uint16_t*>(L.k_cache), static_cast<const uint16_t*>(L.v_cache), pos, part, m.n_heads, m.max_seq, nsplit); break;
+        }
+        if (st != ASDSL_OK) return st;
+        st = launch("attn_combine_kernel", attn_combine_kernel, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
+                    static_cast<const float*>(part), pos, att, nsplit, m.max_seq);
+        if (st != ASDSL_OK) return st;
+        st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, false);
+        if (st != ASDSL_OK) return st;
+        st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H,
+                    static_cast<const float*>(O), L.rms_ffn, X, m.hidden, m.rms_eps);
+        if (st != ASDSL_OK) return st;
+        st = preq2_fused_batch(L.gu_meta, L.gu_quant, X, GU, 2 * m.ffn, m.hidden, m.gs_ffn, n, stream, false);
+        if (st != ASDSL_OK) return st;
+        st = launch("verify_swiglu_kernel", verify_swiglu_kernel, dim3((m.ffn + 1023) / 1024, n), dim3(256), 0, s,
+                    static_cast<const float*>(GU), S, m.ffn, L.fatrelu_threshold);
+        if (st != ASDSL_OK) return st;
+        st = preq2_fused_batch(L.down_meta, L.down_quant, S, O, m.hidden, m.ffn, m.gs_ffn, n, stream, false);
+        if (st != ASDSL_OK) return st;
+        pending = O;
+    }
+    st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H, pending,
+                m.rms_out, X, m.hidden, m.rms_eps);
+    if (st != ASDSL_OK) return st;
+    st = preq2_fused_batch(m.lm_meta, m.lm_quant, X, logits, m.vocab, m.hidden, m.gs_lm, n, stream, false);
+    if (st != ASDSL_OK) return st;
+    st = launch("verify_argmax_kernel", verify_argmax_kernel, dim3(64, n), dim3(256), 0, s,
+                static_cast<const float*>(logits), m.vocab, keys);
+    if (st != ASDSL_OK) return st;
+    return launch("verify_tokens_kernel", verify_tokens_kernel, dim3(1), dim3(kWave), 0, s,
+                  static_cast<const unsigned long long*>(keys), next_tokens, n);
+}
+
+extern "C" asdsl_status asdsl_kv_zero_from(uint16_t* k_cache, uint16_t* v_cache, int n_kv_heads, int head_dim,
+                                           int max_seq, int from_pos, asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(k_cache && v_cache, "kv_zero_from: null pointer");
+    ASDSL_CHECK_ARG(head_dim == kHeadDim, "kv_zero_from: head_dim must be 128");
+    ASDSL_CHECK_ARG(n_kv_heads > 0 && max_seq > 0, "kv_zero_from: invalid dimensions");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && reinterpret_cast<uintptr_t>(v_cache) % 16 == 0,
+                    "kv_zero_from: caches must be 16-byte aligned");
+    const int from = from_pos < 0 ? 0 : from_pos;
+    if (from >= max_seq) return ASDSL_OK;  // nothing past the cache (zero_kv_from returns too)
+    const size_t total = static_cast<size_t>(max_seq - from) * (kHeadDim / 8) * n_kv_heads;
+    const unsigned grid = static_cast<unsigned>(total / 256 + 1 < 4096 ? total / 256 + 1 : 4096);
+    return launch("kv_zero_kernel", kv_zero_kernel, dim3(grid), dim3(256), 0, as_hip(stream),
+                  reinterpret_cast<uint4*>(k_cache), reinterpret_cast<uint4*>(v_cache), n_kv_heads, max_seq, from);
 }

@@ -65,37 +65,6 @@ struct ProArgs {
     float thr = 0.0f;
 };
 
-// The reference's exp polynomial (fast_exp_avx2, unified_engine.cpp:781-801):
-// clamp to [-87.3, 87.3], x*log2(e) split into round-to-nearest integer i and
-// fraction f, 2^f by a degree-5 polynomial, 2^i by exponent bits.
-__device__ __forceinline__ float fast_exp_ref(float x) {
-    x = fmaxf(x, -87.3f);
-    x = fminf(x, 87.3f);
-    x = x * 1.4426950408889634f;
-    const float fi = __builtin_rintf(x);
-    const int i = static_cast<int>(fi);
-    const float f = x - fi;
-    float p = fmaf(0.001333838100523091f, f, 0.009618129107628477f);
-    p = fmaf(p, f, 0.05550410866482158f);
-    p = fmaf(p, f, 0.2402265069591007f);
-    p = fmaf(p, f, 0.6931471805599453f);
-    p = fmaf(p, f, 1.0f);
-    return p * __builtin_bit_cast(float, (i + 127) << 23);
-}
-
-__device__ __forceinline__ float swiglu_ref(float g, float u, float thr) {
-    const float sigmoid = 1.0f / (1.0f + fast_exp_ref(0.0f - g));
-    float v = (g * sigmoid) * u;
-    if (thr > 0.0f && !(fabsf(v) >= thr)) v = 0.0f;
-    return v;
-}
-
-__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
-    const uint32_t b = __builtin_bit_cast(uint32_t, v);
-    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return (static_cast<unsigned long long>(k) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(row));
-}
-
 template <int WAVES>
 __device__ __forceinline__ float block_sum_fixed(float v, float* s_red) {
 #pragma unroll

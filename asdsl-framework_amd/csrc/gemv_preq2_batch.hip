@@ -521,9 +521,12 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused(const uint8_t* meta, const uint8_
                                                int out_features, int in_features, int group_size,
                                                asdsl_stream_t stream);
 
-extern "C" asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X,
-                                                     float* Y, int out_features, int in_features, int group_size,
-                                                     int n_cols, asdsl_stream_t stream) {
+// allow_mfma = false keeps every column on the dot4 kernels, whose
+// per-column arithmetic follows the single-column GEMV; the multi-token
+// decode pass uses that form (see preq2_fused_batch in abi_util.hpp).
+asdsl_status asdsl::preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X, float* Y,
+                                      int out_features, int in_features, int group_size, int n_cols,
+                                      asdsl_stream_t stream, bool allow_mfma) {
     ASDSL_CHECK_ARG(meta && quant && X && Y, "gemv_preq2_fused_batch: null pointer");
     ASDSL_CHECK_ARG(group_size == 32 || group_size == 128,
                     "gemv_preq2_fused_batch: group_size must be 32 (preq2) or 128 (preq2-g128)");
@@ -545,7 +548,7 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const 
     static const int mfma_knob = env_knob("ASDSL_HIP_BATCH_MFMA_MIN_N");
     const int mfma_min = mfma_knob > 0 ? mfma_knob : (in_features >= 4096 ? 3 : 4);
     const MfmaPlan mp = plan_mfma(M, K, cus);
-    if (group_size == 32 && n_cols >= mfma_min && mp.ok && reinterpret_cast<uintptr_t>(meta) % 16 == 0 &&
+    if (allow_mfma && group_size == 32 && n_cols >= mfma_min && mp.ok && reinterpret_cast<uintptr_t>(meta) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(quant) % 4 == 0) {
         const int G = K / 32;
         const size_t img_bytes = static_cast<size_t>(G) * kMfmaCols * 32;
@@ -591,4 +594,10 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const 
         if (st != ASDSL_OK) return st;
     }
     return ASDSL_OK;
+}
+
+extern "C" asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X,
+                                                     float* Y, int out_features, int in_features, int group_size,
+                                                     int n_cols, asdsl_stream_t stream) {
+    return preq2_fused_batch(meta, quant, X, Y, out_features, in_features, group_size, n_cols, stream, true);
 }

@@ -357,6 +357,32 @@ size_t asdsl_decode_work_bytes(const asdsl_decode_model* model);
 asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int* pos, float* logits,
                                 void* work, asdsl_stream_t stream);
 
+/* Bytes of device work buffer asdsl_decode_verify needs for up to max_tokens
+ * tokens (1..16); 0 for an invalid model or count. */
+size_t asdsl_decode_verify_work_bytes(const asdsl_decode_model* model, int max_tokens);
+
+/* Queues one multi-token pass (speculative verify): tokens[0..n) (device) at
+ * positions *pos .. *pos + n - 1 (device int, not advanced) run through every
+ * layer with the projections as batched GEMVs over the n columns; each
+ * column's K/V are written to the caches at its position and its attention
+ * covers positions <= its own; logits[n][vocab] (16-byte aligned) and
+ * next_tokens[n] = the greedy argmax of each column (first on ties).  Columns
+ * at or past max_seq produce zero attention and write no K/V.  1 <= n <= 16;
+ * work: asdsl_decode_verify_work_bytes(model, >= n) bytes, 256-byte aligned.
+ * Replaces UnifiedEngine::forward_verify_batch
+ * (asdsl/kernels/native/unified_engine.cpp:1774-1789), whose preq2 path falls
+ * back to serial forward_token calls. */
+asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, const int* tokens, int n_tokens, const int* pos,
+                                 float* logits, int* next_tokens, void* work, asdsl_stream_t stream);
+
+/* Zeroes rows [from_pos, max_seq) of every head of one layer's fp16 K and V
+ * caches ([n_kv_heads][max_seq][head_dim], 16-byte aligned); from_pos < 0
+ * counts as 0, from_pos >= max_seq does nothing.
+ * Replaces UnifiedEngine::zero_kv_from (asdsl/kernels/native/unified_engine.cpp:1263-1283),
+ * used by truncate_kv / restore_kv (1285-1307). */
+asdsl_status asdsl_kv_zero_from(uint16_t* k_cache, uint16_t* v_cache, int n_kv_heads, int head_dim, int max_seq,
+                                int from_pos, asdsl_stream_t stream);
+
 /* ------------------------------------------------------------- repackers
  * Load-time conversions of the quantized store's weights into the layouts
  * above, on the GPU; every output byte equals the reference's.  Inputs are
