@@ -861,6 +861,12 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     const int q_dim = m.n_heads * m.head_dim;
     const int nsplit = attn_splits(m.max_seq);
     const int G = m.n_heads / m.n_kv_heads;
+    // ASDSL_HIP_VERIFY_MFMA=1 lets the g32 projections take the MFMA batched
+    // GEMV (faster from 4 columns on, but its fp32 summation order differs
+    // from the single-token step's, so a column's int8 activations can round
+    // differently; see preq2_fused_batch)
+    static const int mfma_knob = env_knob("ASDSL_HIP_VERIFY_MFMA");
+    const bool mfma = mfma_knob > 0;
 
     asdsl_status st = launch("verify_embed_kernel", verify_embed_kernel, dim3((m.hidden + 1023) / 1024, n), dim3(256),
                              0, s, m.embed, tokens, H, m.hidden, m.vocab, keys);
@@ -873,7 +879,7 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H, pending,
                     L.rms_att, X, m.hidden, m.rms_eps);
         if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.qkv_meta, L.qkv_quant, X, QKV, qkv_dim, m.hidden, m.gs_attn, n, stream, false);
+        st = preq2_fused_batch(L.qkv_meta, L.qkv_quant, X, QKV, qkv_dim, m.hidden, m.gs_attn, n, stream, mfma);
         if (st != ASDSL_OK) return st;
         st = launch("verify_rope_kv_kernel", verify_rope_kv_kernel, dim3(m.n_heads + m.n_kv_heads, n), dim3(kHeadDim),
                     0, s, static_cast<const float*>(QKV), Q, L.k_cache, L.v_cache, m.rope_cos, m.rope_sin, pos,
@@ -890,7 +896,7 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         st = launch("attn_combine_kernel", attn_combine_kernel, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
                     static_cast<const float*>(part), pos, att, nsplit, m.max_seq);
         if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, false);
+        st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma);
         if (st != ASDSL_OK) return st;
         st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H,
                     static_cast<const float*>(O), L.rms_ffn, X, m.hidden, m.rms_eps);

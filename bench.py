@@ -273,9 +273,51 @@ def decode_tokens_per_s(contexts=(128, 1024, 4096), steps: int = 64, n_layers: i
                                     "roofline_tokens_per_s": round(ideal, 1), "frac_of_roofline": round(tps / ideal, 4),
                                     "final_pos": int(eng.pos.item())}
         eng._graph = None
+    out["verify"] = verify_pass_us(eng, ctx=1024, per_token_us=out["per_ctx"].get("1024", {}).get("us_per_token"))
     del eng
     torch.cuda.empty_cache()
     return out
+
+
+def verify_pass_us(eng, ctx: int, per_token_us, counts=(4, 8, 16), reps: int = 20) -> dict:
+    """Multi-token verify pass (asdsl_decode_verify) of N tokens at position
+    ctx, captured in a HIP graph (the token ids and the position already on
+    the device) and replayed: microseconds per pass against N single-token
+    steps at the same context."""
+    import torch
+
+    from asdsl import _hip
+
+    res = {"ctx": ctx}
+    eng.prefill_kv_random(ctx, seed=ctx)
+    for n in counts:
+        eng.forward_batch_all_logits(list(range(1, n + 1)), ctx)  # allocates and warms the pass
+        v = eng._verify
+        eng.pos.fill_(ctx)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            st = _hip.LIB.asdsl_decode_verify(ctypes.byref(eng._model), _hip.ptr(v["tokens"]), n, _hip.ptr(eng.pos),
+                                              _hip.ptr(v["logits"]), _hip.ptr(v["next"]), _hip.ptr(v["work"]),
+                                              int(torch.cuda.current_stream().cuda_stream))
+        if st:
+            raise RuntimeError(_hip.last_error())
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1e3 * e0.elapsed_time(e1) / reps
+        row = {"us_per_pass": round(us, 1), "us_per_token": round(us / n, 1)}
+        if per_token_us:
+            row["serial_us"] = round(n * per_token_us, 1)
+            row["speedup_vs_serial"] = round(n * per_token_us / us, 2)
+        res[str(n)] = row
+        del g
+    return res
 
 
 # --------------------------------------------------------------------------- suite
