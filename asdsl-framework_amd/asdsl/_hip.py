@@ -47,6 +47,8 @@ SIGNATURES: dict[str, list] = {
     "asdsl_gemv_q4_128_fused": [_P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_q8": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4km_q8": [_P, _P, _P, _I, _I, _P],
+    "asdsl_gemv_q4_s256": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "asdsl_gemv_q4_s256_fused": [_P, _P, _P, _I, _I, _P],
     "asdsl_gemv_q4_packed": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "asdsl_matmul_batch_q4": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "asdsl_gemm_q4_128": [_P, _P, _P, _I, _I, _I, _I, _P],

@@ -150,6 +150,43 @@ def gemv_q4_128_preq_avx2(blocks, x_q8, x_scales, y, out_features: int, in_featu
     c.run("asdsl_gemv_q4_128_preq", pb, pq, ps, py, out_features, in_features, group_size)
 
 
+def _check_s256(out_features: int, in_features: int, fn: str) -> None:
+    if out_features <= 0 or in_features <= 0:
+        raise ValueError(f"{fn}: invalid dimensions")
+    if in_features % 256:
+        raise ValueError("gemv_q4_s256: in_features must be divisible by 256")
+
+
+def gemv_q4_s256_preq_avx2(blocks, x_q8, x_scales, y, out_features: int, in_features: int,
+                           group_size: int = 32) -> None:
+    """Reference: gemv_q4_s256_preq_avx2 (gemv_q4_s256.cpp:79-209): 144-byte
+    superblocks of 8 fp16 sub-scales + 128 nibble bytes, activation
+    pre-quantized per 32 (group_size is the activation group, must be 32).
+    The reference exposes it to its engine only (unified_engine.h:127)."""
+    fn = "gemv_q4_s256_preq_avx2"
+    _check_gs(group_size, (32,), fn)
+    _check_s256(out_features, in_features, fn)
+    c = DeviceCall(fn)
+    pb = c.input(blocks, np.uint8, out_features * (in_features // 256) * 144, "blocks")
+    pq = c.input(x_q8, np.int8, in_features, "x_q8")
+    ps = c.input(x_scales, np.float32, in_features // 32, "x_scales")
+    py = c.output(y, np.float32, out_features, "y")
+    c.run("asdsl_gemv_q4_s256", pb, pq, ps, py, out_features, in_features, group_size)
+
+
+def gemv_q4_s256_fused(blocks, x_fp32, y, out_features: int, in_features: int) -> None:
+    """Q4_S256 GEMV that quantizes the fp32 activation per 32 (A1 rule) inside
+    the call (the engine's quantize + gemv_q4_s256_preq_avx2 pair,
+    unified_engine.cpp:1414-1416)."""
+    fn = "gemv_q4_s256_fused"
+    _check_s256(out_features, in_features, fn)
+    c = DeviceCall(fn)
+    pb = c.input(blocks, np.uint8, out_features * (in_features // 256) * 144, "blocks")
+    px = c.input(x_fp32, np.float32, in_features, "x_fp32")
+    py = c.output(y, np.float32, out_features, "y")
+    c.run("asdsl_gemv_q4_s256_fused", pb, px, py, out_features, in_features)
+
+
 def gemv_q4_128_fused(blocks, x_fp32, y, out_features: int, in_features: int, group_size: int = 128) -> None:
     """Q4_128 GEMV that quantizes the fp32 activation per 128 inside the call
     (the engine's quantize + gemv_q4_128_preq_avx2 pair, unified_engine.cpp:1646-1653)."""

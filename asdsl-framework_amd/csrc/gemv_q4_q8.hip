@@ -43,3 +43,38 @@ extern "C" asdsl_status asdsl_gemv_q4km_q8(const uint8_t* weights_q4km, const fl
     return launch_rowblk<RowLayout::kQ4K, 32, false>(weights_q4km, nullptr, x, nullptr, nullptr, y, out_features,
                                                       in_features, as_hip(stream), cus);
 }
+
+// Q4_S256 superblock GEMV (asdsl/kernels/native/gemv_q4_s256.cpp:79-209):
+// y[r] = sum_sub s_sub * xs_sub * (sum q*x8 - 8 * sum x8) over 32-weight
+// sub-blocks, with the activation quantized per 32 (A1 rule) -- given as
+// x_q8/x_scales (the reference's interface) or quantized inside (_fused).
+static asdsl_status check_s256(const uint8_t* blocks, float* y, int out_features, int in_features, const char* fn) {
+    ASDSL_CHECK_ARG(blocks && y, "%s: null pointer", fn);
+    ASDSL_CHECK_ARG(out_features > 0 && in_features > 0, "%s: invalid dimensions", fn);
+    ASDSL_CHECK_ARG(in_features % 256 == 0, "gemv_q4_s256: in_features must be divisible by 256");
+    ASDSL_CHECK_ARG(in_features <= 20480, "%s: in_features must be <= 20480", fn);
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(blocks) % 16 == 0, "%s: blocks must be 16-byte aligned", fn);
+    return ASDSL_OK;
+}
+
+extern "C" asdsl_status asdsl_gemv_q4_s256(const uint8_t* blocks, const int8_t* x_q8, const float* x_scales, float* y,
+                                           int out_features, int in_features, int group_size, asdsl_stream_t stream) {
+    const asdsl_status cs = check_s256(blocks, y, out_features, in_features, "gemv_q4_s256_preq_avx2");
+    if (cs != ASDSL_OK) return cs;
+    ASDSL_CHECK_ARG(x_q8 && x_scales, "gemv_q4_s256_preq_avx2: null pointer");
+    ASDSL_CHECK_ARG(group_size == 32, "gemv_q4_s256_preq_avx2: group_size (activation groups) must be 32");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(x_q8) % 16 == 0, "gemv_q4_s256_preq_avx2: x_q8 must be 16-byte aligned");
+    ASDSL_CU_COUNT(cus);
+    return launch_rowblk<RowLayout::kQ4S256, 32, true>(blocks, nullptr, nullptr, x_q8, x_scales, y, out_features,
+                                                        in_features, as_hip(stream), cus);
+}
+
+extern "C" asdsl_status asdsl_gemv_q4_s256_fused(const uint8_t* blocks, const float* x, float* y, int out_features,
+                                                 int in_features, asdsl_stream_t stream) {
+    const asdsl_status cs = check_s256(blocks, y, out_features, in_features, "gemv_q4_s256_fused");
+    if (cs != ASDSL_OK) return cs;
+    ASDSL_CHECK_ARG(x != nullptr, "gemv_q4_s256_fused: null pointer");
+    ASDSL_CU_COUNT(cus);
+    return launch_rowblk<RowLayout::kQ4S256, 32, false>(blocks, nullptr, x, nullptr, nullptr, y, out_features,
+                                                         in_features, as_hip(stream), cus);
+}

@@ -43,7 +43,7 @@
 
 namespace asdsl {
 
-enum class RowLayout { kPreq, kQ4_128, kPacked, kQ4K };
+enum class RowLayout { kPreq, kQ4_128, kPacked, kQ4K, kQ4S256 };
 
 // kBlockBytes: bytes per block; kUnitsPerBlock: 16-byte units per block;
 // kDataOffset: offset of the first unit in a block.
@@ -70,6 +70,17 @@ struct RowFmt<RowLayout::kQ4K> {
     static constexpr int kBlockBytes = 144, kUnitsPerBlock = 8, kDataOffset = 16;
 };
 
+// Q4_S256: 8 fp16 sub-scales (one per 32 weights) then 128 nibble bytes,
+// symmetric about 8 (gemv_q4_s256.cpp:3-8).
+template <>
+struct RowFmt<RowLayout::kQ4S256> {
+    static constexpr int kBlockBytes = 144, kUnitsPerBlock = 8, kDataOffset = 16;
+};
+
+// Blocks whose 16-byte header serves all 8 units.
+template <RowLayout L>
+constexpr bool kWideHeader = L == RowLayout::kQ4K || L == RowLayout::kQ4S256;
+
 // 6-bit field idx of the Q4_K scale bitstream held in 3 dwords (12 bytes,
 // LSB-first), as get_6bit_packed reads it (gemv_q4_avx2.cpp:110-120).
 __device__ __forceinline__ uint32_t q4k_field(uint32_t b0, uint32_t b1, uint32_t b2, int idx) {
@@ -92,7 +103,7 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
                                                                    float* __restrict__ y, int M, int K,
                                                                    int llpr) {
     using F = RowFmt<L>;
-    using Hd = typename std::conditional<L == RowLayout::kQ4K, uint4, uint32_t>::type;
+    using Hd = typename std::conditional<kWideHeader<L>, uint4, uint32_t>::type;
     constexpr int UPG = GSX / 32;  // units per activation group
     constexpr QRule kRule = L == RowLayout::kQ4K ? QRule::kRoundAway : QRule::kRne;
     extern __shared__ __align__(16) uint32_t lds[];
@@ -137,7 +148,7 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
     // lm_head 80.3 -> 61.7 us, Q4_K gate_up 10.4 -> 10.2 us; for preq (one
     // unit per block) it was slower (gate_up 8.1 -> 10.0 us), so preq keeps
     // per-unit loads.
-    constexpr bool STAGE = (L == RowLayout::kQ4_128 || L == RowLayout::kQ4K) && !MULTI;
+    constexpr bool STAGE = (L == RowLayout::kQ4_128 || kWideHeader<L>) && !MULTI;
     constexpr int kStageLoads = STAGE ? (NU * kWave * F::kBlockBytes / F::kUnitsPerBlock + 32 + 16 * kWave - 1) /
                                             (16 * kWave) : 1;
     uint4 cw[kStageLoads];
@@ -181,7 +192,7 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
             w[i] = make_uint4(v.x, v.y, v.z, v.w);
             if constexpr (L == RowLayout::kPreq) hd[i] = *reinterpret_cast<const uint32_t*>(bp);
             else if constexpr (L == RowLayout::kQ4_128) hd[i] = *reinterpret_cast<const uint16_t*>(bp);
-            else if constexpr (L == RowLayout::kQ4K) hd[i] = *reinterpret_cast<const uint4*>(bp);
+            else if constexpr (kWideHeader<L>) hd[i] = *reinterpret_cast<const uint4*>(bp);
         }
     };
     // Unconditional loads at clamped, in-bounds rows; rows >= M are never stored.
@@ -246,7 +257,14 @@ __global__ __launch_bounds__(WAVES * kWave) void rowblk_gemv_kernel(const uint8_
                 const uint32_t(&xv)[8] = MULTI ? xt : xr[ii];
                 const float xsv = MULTI ? sc : xs[ii];
                 const int d = unit_dot(w[i], xv);
-                if constexpr (L == RowLayout::kQ4K) {
+                if constexpr (L == RowLayout::kQ4S256) {
+                    const uint4 h = hd[i];
+                    const int sb = tu[i] % 8;
+                    const uint32_t pair = sb < 2 ? h.x : (sb < 4 ? h.y : (sb < 6 ? h.z : h.w));
+                    const float s = half_bits_to_float(pair >> (16 * (sb & 1)));
+                    acc = fmaf(static_cast<float>(d), s * xsv, acc);
+                    acc = fmaf(-(8.0f * s), MULTI ? us : xu[ii], acc);
+                } else if constexpr (L == RowLayout::kQ4K) {
                     const uint4 h = hd[i];
                     const int sb = tu[i] % 8;
                     const float sub_scale = half_bits_to_float(h.x) * static_cast<float>(q4k_field(h.y, h.z, h.w, sb));
@@ -316,7 +334,7 @@ template <RowLayout L, int GSX, int WAVES, int NCH, bool Q8, bool EXACT, bool MU
 asdsl_status launch_rowblk_exact(const RowPlan& p, const uint8_t* blocks, const float* side, const float* x,
                                  const int8_t* xq8, const float* xsc, float* y, int M, int K, hipStream_t stream) {
     using F = RowFmt<L>;
-    constexpr bool STAGE = (L == RowLayout::kQ4_128 || L == RowLayout::kQ4K) && !MULTI;
+    constexpr bool STAGE = (L == RowLayout::kQ4_128 || kWideHeader<L>) && !MULTI;
     const size_t row_bytes = static_cast<size_t>(K / 32 / F::kUnitsPerBlock) * F::kBlockBytes;
     const size_t stage = STAGE ? WAVES * (((static_cast<size_t>(kWave >> p.llpr) * row_bytes) + 47) & ~static_cast<size_t>(15))
                                : 0;

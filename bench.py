@@ -613,6 +613,23 @@ def run_suite(args) -> int:
                 sd_cpu if spm else None,
                 note="reference result races beyond one pool chunk; rel_l2 compares against it as is")
 
+    # Q4_S256 superblocks (weight_format 1 of the reference engine)
+    sys.path.insert(0, str(REPO / "tests" / "golden"))
+    from make_golden import s256_blocks
+
+    s256 = torch.from_numpy(s256_blocks(M, K, 5)).cuda()
+    xs8 = torch.empty(K, dtype=torch.int8, device="cuda")
+    xss = torch.empty(K // 32, dtype=torch.float32, device="cuda")
+    lib.asdsl_quantize_activation(P(x), P(xs8), P(xss), K, 32, int(torch.cuda.current_stream().cuda_stream))
+    ref_s256 = oracle.reference_q4_s256()
+
+    def s256_cpu(hc):
+        return ref_s256(hc["b"], hc["xq"], hc["xs"], M, K)
+    measure("F4 Q4_S256 GEMV (pre-quantized x)", "gate_up 16384x3072", M * (K // 256) * 144 + K + 4 * (K // 32) + 4 * M,
+            lambda: {"b": s256.clone(), "xq": xs8, "xs": xss},
+            lambda c, y, h: lib.asdsl_gemv_q4_s256(P(c["b"]), P(c["xq"]), P(c["xs"]), P(y), M, K, 32, h), (M,),
+            s256_cpu if ref_s256 else None)
+
     xb = torch.randn(8192, generator=gen, device="cuda")
     mask = torch.empty(256, dtype=torch.int32, device="cuda")
 

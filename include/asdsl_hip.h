@@ -383,6 +383,20 @@ asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, const int* tok
 asdsl_status asdsl_kv_zero_from(uint16_t* k_cache, uint16_t* v_cache, int n_kv_heads, int head_dim, int max_seq,
                                 int from_pos, asdsl_stream_t stream);
 
+/* Q4_S256 superblock GEMV: blocks[out][in/256][144] = 8 fp16 sub-scales
+ * (one per 32 weights) then 128 nibble bytes (low nibble = even weight),
+ * weights (q - 8) * s; x_q8/x_scales pre-quantized per 32 (group_size must
+ * be 32; x_q8 16-byte aligned); in_features % 256 == 0, <= 20480; blocks
+ * 16-byte aligned.
+ * Replaces gemv_q4_s256_preq_avx2 (asdsl/kernels/native/gemv_q4_s256.cpp:79-209). */
+asdsl_status asdsl_gemv_q4_s256(const uint8_t* blocks, const int8_t* x_q8, const float* x_scales, float* y,
+                                int out_features, int in_features, int group_size, asdsl_stream_t stream);
+
+/* The same with the fp32 activation quantized inside (A1 rule, groups of 32),
+ * as the reference's engine does before calling it (unified_engine.cpp:1414-1416). */
+asdsl_status asdsl_gemv_q4_s256_fused(const uint8_t* blocks, const float* x, float* y, int out_features,
+                                      int in_features, asdsl_stream_t stream);
+
 /* ------------------------------------------------------------- repackers
  * Load-time conversions of the quantized store's weights into the layouts
  * above, on the GPU; every output byte equals the reference's.  Inputs are

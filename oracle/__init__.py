@@ -317,3 +317,28 @@ def repack_q4_128_to_preq2(blocks, rows: int, cols: int) -> tuple[np.ndarray, np
     meta, quant = np.empty(mb, np.uint8), np.empty(qb, np.uint8)
     lib().oracle_repack_q4_128_to_preq2(_p(b, _c_u8p), _p(meta, _c_u8p), _p(quant, _c_u8p), rows, cols)
     return meta, quant
+
+
+def gemv_q4_s256(blocks, x_q8, x_scales, M: int, K: int) -> np.ndarray:
+    """gemv_q4_s256_preq_avx2 restated (activation groups of 32)."""
+    b, xq, xs = _u8(blocks), _i8(x_q8), _f32(x_scales).reshape(-1)
+    y = np.empty(M, np.float32)
+    lib().oracle_gemv_q4_s256(_p(b, _c_u8p), _p(xq, _c_i8p), _p(xs, _c_f32p), _p(y, _c_f32p), M, K)
+    return y
+
+
+def reference_q4_s256():
+    """The reference's own Q4_S256 kernel (oracle/_ref/libref_q4_s256.so) as
+    f(blocks, x_q8, x_scales, M, K) -> y, or None when it is not built."""
+    path = REF_DIR / "libref_q4_s256.so"
+    if not path.exists():
+        return None
+    so = ctypes.CDLL(str(path))
+
+    def run(blocks, x_q8, x_scales, M: int, K: int) -> np.ndarray:
+        b, xq, xs = _u8(blocks), _i8(x_q8), _f32(x_scales).reshape(-1)
+        y = np.empty(M, np.float32)
+        so.ref_gemv_q4_s256(_p(b, _c_u8p), _p(xq, _c_i8p), _p(xs, _c_f32p), _p(y, _c_f32p), ctypes.c_int(M),
+                            ctypes.c_int(K))
+        return y
+    return run

@@ -575,3 +575,30 @@ EXPORT void oracle_repack_q4_128_to_preq2(const uint8_t* blocks, uint8_t* meta, 
             memcpy(quant + ((size_t)(r / 4) * G + g) * 256 + 64 * (r % 4), blk + 2, 64);
         }
 }
+
+/* gemv_q4_s256_preq_avx2 (asdsl/kernels/native/gemv_q4_s256.cpp:79-209):
+ * per row, 144-byte superblocks of 8 fp16 sub-scales then 128 nibble bytes
+ * (low nibble = even weight); per 32-weight sub-block k with activation
+ * group g: sc = ws * xs[g] (fp32), y += dot(q, x8) * sc - 8 * sum(x8) * sc.
+ * The sum over sub-blocks is accumulated in double. */
+EXPORT void oracle_gemv_q4_s256(const uint8_t* blocks, const int8_t* xq, const float* xs, float* y, int M, int K) {
+    const int NS = K / 256;
+    for (int r = 0; r < M; ++r) {
+        double acc = 0.0;
+        for (int sb = 0; sb < NS; ++sb) {
+            const uint8_t* blk = blocks + ((size_t)r * NS + sb) * 144;
+            for (int k = 0; k < 8; ++k) {
+                const int g = sb * 8 + k;
+                const float sc = half_to_float(rd16(blk + 2 * k)) * xs[g];
+                const int8_t* x = xq + (size_t)g * 32;
+                int dot = 0, xsum = 0;
+                for (int i = 0; i < 32; ++i) {
+                    dot += nib(blk + 16 + 16 * k, i) * x[i];
+                    xsum += x[i];
+                }
+                acc += (double)dot * sc - 8.0 * (double)xsum * sc;
+            }
+        }
+        y[r] = (float)acc;
+    }
+}

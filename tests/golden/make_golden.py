@@ -151,7 +151,40 @@ def main() -> None:
     np.savez_compressed(HERE / "gemv_q4_reference.npz", **out)
     total = sum(v.nbytes for v in out.values())
     print(f"wrote {HERE / 'gemv_q4_reference.npz'} ({len(out)} arrays, {total} raw bytes)")
+    s256_fixture()
+
+
+def s256_blocks(M: int, K: int, seed: int) -> np.ndarray:
+    """Random Q4_S256 superblocks: 8 fp16 sub-scales (both signs, one zero)
+    then 128 random nibble bytes per 256 weights."""
+    rng = np.random.default_rng(seed)
+    nsb = M * (K // 256)
+    scales = (rng.uniform(0.001, 0.05, (nsb, 8)) * rng.choice([-1.0, 1.0], (nsb, 8))).astype(np.float16)
+    scales[0, 3] = 0.0
+    blocks = np.empty((nsb, 144), np.uint8)
+    blocks[:, :16] = scales.view(np.uint8).reshape(nsb, 16)
+    blocks[:, 16:] = rng.integers(0, 256, (nsb, 128), dtype=np.uint8)
+    return blocks.reshape(-1)
+
+
+def s256_fixture() -> None:
+    """Q4_S256 (gemv_q4_s256.cpp, no Python binding in the reference): the
+    compiled reference kernel through oracle/_ref/libref_q4_s256.so, on 37
+    rows (a tail row past the 4-row loop) x 512, activation quantized by the
+    reference's quantize_activation_avx2."""
+    ng = oracle.load_reference("_native_gemv")
+    ref = oracle.reference_q4_s256()
+    M, K = 37, 512
+    blocks = s256_blocks(M, K, 41)
+    x = tricky_activation(K, 42)
+    x[96:128] = syn.activation(32, 43) * np.float32(1e4)  # large but finite: fp32 sums stay finite
+    xq, xs = np.zeros(K, np.int8), np.zeros(K // 32, np.float32)
+    ng.quantize_activation_avx2(x, xq, xs, K, 32)
+    out = {"s256_blocks": blocks, "s256_xq": xq, "s256_xs": xs, "s256_shape": np.array([M, K]),
+           "s256_y": ref(blocks, xq, xs, M, K)}
+    np.savez_compressed(HERE / "q4_s256_reference.npz", **out)
+    print(f"wrote {HERE / 'q4_s256_reference.npz'}")
 
 
 if __name__ == "__main__":
-    main()
+    s256_fixture() if sys.argv[1:] == ["s256"] else main()
