@@ -23,7 +23,7 @@ namespace asdsl {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kSplit = 128;        // positions per attention workgroup
+constexpr int kSplit = 64;         // positions per attention workgroup
 constexpr int kAttnThreads = 256;  // 4 waves x 4 positions per step
 constexpr int kPartStride = kHeadDim + 2;  // m, l, acc[128]
 
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 // merged in LDS in split order.  One group when the splits fit one chunk.
 // blockIdx.y = column c of a multi-token pass (position *pos_ptr + c; its
 // partials and output follow column c - 1's); the decode step runs one column.
-constexpr int kCombineGroups = 4;
+constexpr int kCombineGroups = 8;
 constexpr int kCombineThreads = kCombineGroups * kHeadDim;
 
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const float* __restrict__ part,

@@ -104,8 +104,9 @@ def test_swiglu_gemv_matches_oracle(gpu, gs, thr):
 @pytest.mark.parametrize("pos,max_seq", [(0, 1600), (1, 1600), (127, 1600), (128, 1600), (129, 1600), (383, 1600),
                                          (1500, 1600), (4100, 4224), (9000, 9100)])
 def test_attention_rope_kv_matches_oracle(gpu, pos, max_seq):
-    """RoPE, the KV write and attention at 1 to 71 splits of 128 positions
-    (past 16 splits the combine folds runs of splits in parallel groups)."""
+    """RoPE, the KV write and attention at 1 to 141 splits of 64 positions
+    (past 16 splits the combine folds runs of splits in up to 8 parallel
+    groups; at 141 each group takes two chunks)."""
     import torch
     from asdsl import _hip
     from asdsl.engine import rope_tables
@@ -187,9 +188,10 @@ def test_decode_steps_match_oracle(gpu):
 
 @pytest.mark.parametrize("ctx", [127, 129, 2100, 4100])
 def test_decode_long_context_matches_oracle(gpu, ctx):
-    """One layer at contexts whose attention spans 1, 2, 17 and 33 splits of
-    128 positions (the combine then merges one, one, two and three chunks of
-    16 splits), two steps each: logits within 1e-3 and the same tokens."""
+    """One layer at contexts whose attention spans 2, 3, 33 and 65 splits of
+    64 positions (the combine folds them in one group, one group, three and
+    five parallel groups of at most 16), two steps each: logits within 1e-3
+    and the same tokens."""
     import torch
 
     eng = _small_engine(n_layers=1, vocab=4096, max_seq=4224, seed=ctx)

@@ -62,7 +62,7 @@ def _oracle_model(eng):
 @pytest.mark.parametrize("ctx,n", [(100, 1), (100, 4), (124, 9), (300, 16)])
 def test_verify_matches_serial_oracle(gpu, ctx, n):
     """n tokens at ctx .. ctx + n - 1 (124 + 9 crosses the 128-position
-    split boundary; 300 spans three splits)."""
+    split boundary; 300 + 16 spans five 64-position splits)."""
     eng = _engine(seed=ctx + n, n_layers=2 if n == 4 else 1)
     eng.prefill_kv_random(ctx, seed=3)
     model = _oracle_model(eng)
