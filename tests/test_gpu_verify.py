@@ -147,3 +147,34 @@ def test_pld_generate_is_greedy(gpu):
     got = pld_generate(eng, prompt, 40, max_draft_k=6, stats=stats)
     assert got == want
     assert stats["verify_passes"] >= 1
+
+
+def test_reference_kv_length_cases(gpu):
+    """The reference's tests/test_unified_kv_snapshot.py and
+    test_unified_kv_truncate.py on this engine (their draft tokens run as
+    ordinary steps: the layer-skipping draft mode is not part of this path)."""
+    from asdsl.inference.unified_bridge import get_kv_seq_len, restore_kv, snapshot_kv, truncate_kv
+
+    eng = _engine(seed=4, max_seq=64)
+    eng.reset_session()
+    for pos, tid in enumerate(range(10)):
+        eng.forward_token(tid, pos)
+    base_len = get_kv_seq_len(eng)
+    assert base_len == 10
+    snapshot_kv(eng)
+    for k in range(3):
+        eng.forward_token(100 + k, base_len + k)
+    assert get_kv_seq_len(eng) == 13
+    restore_kv(eng)
+    assert get_kv_seq_len(eng) == base_len
+
+    eng.reset_session()
+    for pos, tid in enumerate(range(8)):
+        eng.forward_token(tid, pos)
+    committed = get_kv_seq_len(eng)
+    snapshot_kv(eng)
+    for k in range(4):
+        eng.forward_token(200 + k, committed + k)
+    assert get_kv_seq_len(eng) == committed + 4
+    truncate_kv(eng, committed + 2)
+    assert get_kv_seq_len(eng) == committed + 2
