@@ -178,3 +178,36 @@ def test_reference_kv_length_cases(gpu):
     assert get_kv_seq_len(eng) == committed + 4
     truncate_kv(eng, committed + 2)
     assert get_kv_seq_len(eng) == committed + 2
+
+
+def test_columns_past_the_cache_write_nothing(gpu):
+    """Through the C ABI (the Python API refuses it): a pass at pos =
+    max_seq - 2 with 4 tokens.  The two columns inside the cache agree with a
+    pass of just those two tokens (same greedy tokens); the two past it write
+    no K/V (every write and read is guarded by its position) and get finite
+    logits from a zero attention output."""
+    import ctypes
+    import torch
+    from asdsl import _hip
+
+    eng = _engine(seed=8, max_seq=128)
+    eng.prefill_kv_random(120, seed=2)
+    eng.forward_batch_all_logits([1, 2], 126)  # allocates the pass buffers; the two in-cache columns
+    want = _host(eng._verify["logits"][:2]).copy()
+    eng.truncate_kv(126)
+    before = [(_host(L["k_cache"]).copy(), _host(L["v_cache"]).copy()) for L in eng.layers]
+    v = eng._verify
+    v["tokens"][:4].copy_(torch.tensor([1, 2, 3, 4], dtype=torch.int32))
+    eng.pos.fill_(126)
+    _hip.check(_hip.LIB.asdsl_decode_verify(ctypes.byref(eng._model), _hip.ptr(v["tokens"]), 4, _hip.ptr(eng.pos),
+                                            _hip.ptr(v["logits"]), _hip.ptr(v["next"]), _hip.ptr(v["work"]),
+                                            _hip.stream_handle()), "asdsl_decode_verify")
+    torch.cuda.synchronize()
+    got = _host(v["logits"][:4])
+    assert np.all(np.isfinite(got))
+    for c in range(2):  # the same columns through other batched kernels (4 columns, not 2)
+        assert rel_l2(got[c], want[c]) < LOOSE and od.argmax_first(got[c]) == od.argmax_first(want[c])
+    for L, (k0, v0) in zip(eng.layers, before):
+        k1, v1 = _host(L["k_cache"]), _host(L["v_cache"])
+        assert np.array_equal(k1[:, :126], k0[:, :126]) and np.array_equal(v1[:, :126], v0[:, :126])
+        assert k1[:, 126:].any() and v1[:, 126:].any()  # rows 126, 127 written by the in-cache columns
