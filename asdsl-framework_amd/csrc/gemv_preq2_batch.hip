@@ -447,18 +447,22 @@ asdsl_status launch_mfma(const MfmaPlan& p, const uint32_t* m, const uint8_t* q,
 struct BatchPlan {
     int lks, nu, waves, grid, nb;
     bool exact;
+    int cus;
 };
 
 // Tiling: the largest K split (KS <= 8) that divides the band exactly, i.e.
 // the fewest units per lane, since every unit's nibbles stay in registers
 // while all columns are dotted; then columns per launch capped so no
-// instantiation spills (measured VGPRs: 8 waves, NU <= 4: 16 columns within
-// 208 VGPRs; 16 waves: 128-VGPR budget, 8 columns at NU <= 4) and the column
-// images stay within ~96 KB of LDS.
+// instantiation spills and enough waves stay resident (16 waves: 128-VGPR
+// budget, 8 columns at NU <= 4; 8 waves, NU = 3: 16 columns take 208 VGPRs,
+// two waves per SIMD, 8 columns 128, four -- measured at 16 columns, gate_up
+// 16384x3072 g128 36.6 us in two launches of 8 vs 41.4 in one of 16,
+// lm_head 200064x3072 239 vs 383 us) and the column images stay within
+// ~96 KB of LDS.
 BatchPlan plan_batch(int M, int K, int gs, int cus) {
     const int upb = K / 8;
     const int nbands = (M + 3) / 4;
-    BatchPlan p{0, 0, K > 4096 ? 16 : 8, 0, 16, false};
+    BatchPlan p{0, 0, K > 4096 ? 16 : 8, 0, 16, false, cus};
     auto tiles_of = [&](int l) {
         const int bpt = p.waves >> l;
         return (nbands + bpt - 1) / bpt;
@@ -473,14 +477,28 @@ BatchPlan plan_batch(int M, int K, int gs, int cus) {
     p.lks = best;
     p.nu = upb / (kWave << p.lks);
     p.exact = p.nu <= 6;
-    const int cap = cus * (32 / p.waves);
-    const int tiles = tiles_of(p.lks);
-    p.grid = tiles < cap ? tiles : cap;
-    if (p.waves == 8) p.nb = p.nu <= 4 ? 16 : 8;
+    p.grid = tiles_of(p.lks);  // capped at the resident workgroups at launch
+    if (p.waves == 8) p.nb = p.nu <= 2 ? 16 : 8;
     else p.nb = p.nu <= 4 ? 8 : 4;
     const size_t img = batch_image_bytes(K, gs);
     while (p.nb > 2 && static_cast<size_t>(p.nb) * img > 96 * 1024) p.nb >>= 1;
+    static const int nb_knob = env_knob("ASDSL_HIP_BATCH_MAX_COLS");  // tuning: a lower cap
+    while (nb_knob > 0 && p.nb > 2 && p.nb > nb_knob) p.nb >>= 1;
     return p;
+}
+
+// One workgroup per tile up to the workgroups that fit on the chip at once
+// (VGPRs and LDS decide); past that each workgroup loops over tiles, so
+// its column staging is paid once for several tiles.
+template <typename Kern>
+int resident_grid(Kern kern, const BatchPlan& p, int threads, size_t lds) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    static const int knob = env_knob("ASDSL_HIP_BATCH_WG_PER_CU");
+    if (knob > 0 && knob < per_cu) per_cu = knob;
+    const long long cap = static_cast<long long>(p.cus) * per_cu;
+    return p.grid < cap ? p.grid : static_cast<int>(cap);
 }
 
 template <int GS, int WAVES, int NB>
@@ -488,10 +506,12 @@ asdsl_status launch_batch_nb(const BatchPlan& p, const uint32_t* m, const uint4*
                              int K, int ncols, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(NB) * batch_image_bytes(K, GS);
     const dim3 block(WAVES * kWave);
-#define ASDSL_BATCH_NU(N)                                                                                  \
-    case N:                                                                                                \
-        return launch("preq2_gemv_batch_kernel", preq2_gemv_batch_kernel<GS, N, WAVES, NB>, dim3(p.grid),  \
-                      block, lds, stream, m, q, X, Y, M, K, ncols, p.lks);
+#define ASDSL_BATCH_NU(N)                                                                                        \
+    case N: {                                                                                                    \
+        auto* kern = preq2_gemv_batch_kernel<GS, N, WAVES, NB>;                                                 \
+        return launch("preq2_gemv_batch_kernel", kern, dim3(resident_grid(kern, p, WAVES * kWave, lds)), block, \
+                      lds, stream, m, q, X, Y, M, K, ncols, p.lks);                                             \
+    }
     switch (p.nu) {
         ASDSL_BATCH_NU(1)
         ASDSL_BATCH_NU(2)

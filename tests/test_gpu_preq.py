@@ -193,6 +193,30 @@ def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
         assert rel_l2(Yh[n], oracle.gemv_preq2_fused(mh, qh, X[n], M, K, gs)) < TOL, f"column {n}"
 
 
+@pytest.mark.parametrize("M,K", [(16384, 3072), (3072, 8192), (1000, 5120)])
+def test_preq2_batch_columns_do_not_depend_on_the_column_count(gpu, M, K):
+    """g128 dot4 batch: a column's result does not depend on how many columns
+    share the call (another kernel instance, column chunk and grid): the
+    shared columns of 3, 4, 9 and 16-column calls are bit for bit equal."""
+    import torch
+    from asdsl.kernels import _native_gemv as ng
+
+    g = torch.Generator(device="cuda").manual_seed(M + K)
+    w = torch.randn((M, K), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    meta, quant = syn.preq2_from_weights_torch(w, 128)
+    del w
+    X = torch.from_numpy(syn.activation(K, 16, batch=16)).cuda()
+    outs = {}
+    for n in (3, 4, 9, 16):
+        Y = torch.empty((n, M), dtype=torch.float32, device="cuda")
+        ng.gemv_preq2_fused_avx2(meta, quant, X[:n].contiguous(), Y, M, K, 128)
+        torch.cuda.synchronize()
+        outs[n] = Y.cpu().numpy()
+    for n in (4, 9, 16):
+        assert np.array_equal(outs[n][:3], outs[3]), n
+    assert np.array_equal(outs[16][:9], outs[9])
+
+
 def test_forced_ksplit_still_covers_every_unit(gpu, monkeypatch):
     """ASDSL_HIP_KSPLIT=2 on K=8192 would leave 8 units per lane (the kernel
     takes at most 6): the plan raises the split, and the GEMV still matches
