@@ -85,6 +85,17 @@ asdsl_status preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const 
                                int out_features, int in_features, int group_size, int n_cols, asdsl_stream_t stream,
                                bool allow_mfma);
 
+// The decode step's o_proj: gemv_preq2_fused of the attention output, which
+// the GEMV's prologue merges itself from the split partials (part: per head
+// nsplit rows of part_stride floats, m, l, acc[head_dim]) when the position
+// *pos has at most `fold` (<= 4) splits of `split` positions; then the
+// combine kernel skipped that position and `att` is not read.  Otherwise
+// `att` holds the merged output.  Same bits either way.
+asdsl_status preq2_fused_combine(const uint8_t* meta, const uint8_t* quant, const float* att, float* y,
+                                 int out_features, int in_features, int group_size, const float* part, const int* pos,
+                                 int nsplit, int split, int part_stride, int head_dim, int max_seq, int fold,
+                                 asdsl_stream_t stream);
+
 // Workgroups for a streaming kernel: enough tiles for every wave, capped at
 // `per_cu` workgroups per compute unit (waves then loop over tiles).
 inline int stream_grid(long long tiles, int waves_per_wg, int per_cu, int cus) {

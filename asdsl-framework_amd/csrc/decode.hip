@@ -326,7 +326,7 @@ constexpr int kCombineThreads = kCombineGroups * kHeadDim;
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const float* __restrict__ part,
                                                                       const int* __restrict__ pos_ptr,
                                                                       float* __restrict__ out, int nsplit,
-                                                                      int max_seq) {
+                                                                      int max_seq, int fold) {
     constexpr int kChunk = 16;
     __shared__ float gml[kCombineGroups][2];
     __shared__ float go[kCombineGroups][kHeadDim];
@@ -342,6 +342,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
         return;
     }
     const int ns = pos / kSplit + 1;
+    if (ns <= fold) return;  // the consuming GEMV's prologue merges these splits itself
     const int ng = min(kCombineGroups, (ns + kChunk - 1) / kChunk);  // groups with splits
     const int per = (ns + ng - 1) / ng;
     const int s_begin = min(ns, g * per);
@@ -402,7 +403,7 @@ int attn_splits(int max_seq) { return (max_seq + kSplit - 1) / kSplit; }
 
 asdsl_status launch_attention(const float* qkv, uint16_t* kc, uint16_t* vc, const float* rc, const float* rs,
                               const int* pos, float* att, float* part, int n_heads, int n_kv, int rot_half,
-                              int max_seq, hipStream_t s) {
+                              int max_seq, hipStream_t s, int fold = 0) {
     const int nsplit = attn_splits(max_seq);
     const int G = n_heads / n_kv;
     asdsl_status st;
@@ -418,7 +419,7 @@ asdsl_status launch_attention(const float* qkv, uint16_t* kc, uint16_t* vc, cons
     }
     if (st != ASDSL_OK) return st;
     return launch("attn_combine_kernel", attn_combine_kernel, dim3(n_heads), dim3(kCombineThreads), 0, s,
-                  static_cast<const float*>(part), pos, att, nsplit, max_seq);
+                  static_cast<const float*>(part), pos, att, nsplit, max_seq, fold);
 }
 
 // Work buffer layout of one decode step (offsets in floats, 256-byte aligned).
@@ -788,6 +789,11 @@ extern "C" asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int*
     hipStream_t s = as_hip(stream);
     const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
     const int q_dim = m.n_heads * m.head_dim;
+    // Positions with at most 4 attention splits (256 positions) skip the
+    // combine kernel's work: o_proj's prologue merges the splits itself
+    // (same bits).  ASDSL_HIP_NO_COMBINE_FOLD=1 keeps the combine kernel.
+    static const int no_fold = env_knob("ASDSL_HIP_NO_COMBINE_FOLD");
+    const int fold = no_fold > 0 ? 0 : 4;
 
     asdsl_status st = launch("embed_kernel", embed_kernel, dim3((m.hidden + 1023) / 1024), dim3(256), 0, s,
                              m.embed, static_cast<const int*>(token), hA, m.hidden, m.vocab, amax);
@@ -808,9 +814,10 @@ extern "C" asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int*
         }
         if (st != ASDSL_OK) return st;
         st = launch_attention(qkv, L.k_cache, L.v_cache, m.rope_cos, m.rope_sin, pos, att, part, m.n_heads,
-                              m.n_kv_heads, m.rotary_dim / 2, m.max_seq, s);
+                              m.n_kv_heads, m.rotary_dim / 2, m.max_seq, s, fold);
         if (st != ASDSL_OK) return st;
-        st = asdsl_gemv_preq2_fused(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, stream);
+        st = preq2_fused_combine(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, part, pos,
+                                 attn_splits(m.max_seq), kSplit, kPartStride, kHeadDim, m.max_seq, fold, stream);
         if (st != ASDSL_OK) return st;
         st = asdsl_gemv_preq2_rmsnorm(L.gu_meta, L.gu_quant, cur, o, L.rms_ffn, nxt, gu, 2 * m.ffn, m.hidden,
                                       m.gs_ffn, m.rms_eps, nullptr, stream);
@@ -894,7 +901,7 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         }
         if (st != ASDSL_OK) return st;
         st = launch("attn_combine_kernel", attn_combine_kernel, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
-                    static_cast<const float*>(part), pos, att, nsplit, m.max_seq);
+                    static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0);
         if (st != ASDSL_OK) return st;
         st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma);
         if (st != ASDSL_OK) return st;

@@ -48,12 +48,20 @@ constexpr int kThreads = 256;  // helper kernels
 //            (residual_add_rmsnorm_f32 / rmsnorm_f32, unified_engine.cpp:499-524,651-688).
 //   kSwiglu: the GEMV input is silu(x) * up, zeroed where |value| < thr when
 //            thr > 0 (swiglu_inplace with fast_exp_avx2, unified_engine.cpp:803-857).
+//   kCombine: the GEMV input is the attention output, merged here from the
+//            split partials when the position has at most pa.fold splits
+//            (attn_combine_kernel then skipped that position), with that
+//            kernel's single-group arithmetic operation for operation, so the
+//            input is bit for bit the one it would have written; otherwise x,
+//            which it did write.
 //   ARGMAX:  the largest output and its row (first on ties, as argmax_f32_avx2,
 //            unified_engine.cpp:207-233) are folded into *amax with a 64-bit
 //            atomicMax: key = order-preserving float bits << 32 | ~row, so the
 //            result does not depend on workgroup order.  *amax must be zero
 //            before the launch.
-enum class Pro { kPlain, kNorm, kSwiglu };
+enum class Pro { kPlain, kNorm, kSwiglu, kCombine };
+
+constexpr int kMaxFold = 4;  // kCombine: most splits merged in the prologue
 
 struct ProArgs {
     const float* delta = nullptr;
@@ -63,6 +71,11 @@ struct ProArgs {
     unsigned long long* amax = nullptr;
     float eps = 0.0f;
     float thr = 0.0f;
+    // kCombine: partials [head][split][m, l, acc[head_dim]] (part_stride
+    // floats each), the position, positions per split, the fold limit
+    const float* part = nullptr;
+    const int* pos = nullptr;
+    int nsplit = 0, split = 0, part_stride = 0, head_dim = 0, max_seq = 0, fold = 0;
 };
 
 template <int WAVES>
@@ -147,12 +160,42 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     int tile = static_cast<int>(blockIdx.x);
     const int tile_step = static_cast<int>(gridDim.x);
     ActStage<GS, WAVES * kWave, NCH, Q8> act;
-    act.load(x, xq8, xsc, K);  // activation loads first: they retire first
-    constexpr int NX = PRO == Pro::kPlain ? 1 : NCH;
-    float ex[NX][8], ew[NX][8];  // kNorm: delta, norm weight; kSwiglu: up
     const int nchunk = K >> 3;
     const int tid = static_cast<int>(threadIdx.x);
-    if constexpr (PRO != Pro::kPlain) {
+    static_assert(PRO != Pro::kCombine || (NCH == 1 && !Q8), "kCombine: one fp32 chunk per thread");
+    constexpr int NF = PRO == Pro::kCombine ? kMaxFold : 1;
+    float2 fml[NF];    // kCombine: (m, l) of each split
+    float fav[NF][8];  // kCombine: this thread's 8 accumulator values of each split
+    int fns = 0;       // kCombine: splits merged here (0: x holds the merged output)
+    if constexpr (PRO == Pro::kCombine) {
+        const int p = *pa.pos;
+        const int ns = p >= 0 && p < pa.max_seq ? p / pa.split + 1 : 0;
+        fns = ns <= pa.fold ? ns : 0;
+        if (fns > 0) {
+            const int e0 = min(tid, nchunk - 1) * 8;  // this thread's 8 outputs: head h, dims d0..d0+7
+            const int h = e0 / pa.head_dim;
+            const int d0 = e0 - h * pa.head_dim;
+            const float* ph = pa.part + static_cast<size_t>(h) * pa.nsplit * pa.part_stride;
+#pragma unroll
+            for (int sp = 0; sp < NF; ++sp) {
+                if (sp < fns) {
+                    const float* pp = ph + static_cast<size_t>(sp) * pa.part_stride;
+                    fml[sp] = *reinterpret_cast<const float2*>(pp);
+                    const float2* a2 = reinterpret_cast<const float2*>(pp + 2 + d0);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float2 t = a2[k];
+                        fav[sp][2 * k] = t.x;
+                        fav[sp][2 * k + 1] = t.y;
+                    }
+                }
+            }
+        }
+    }
+    if (fns == 0) act.load(x, xq8, xsc, K);  // activation loads first: they retire first
+    constexpr int NX = PRO == Pro::kPlain || PRO == Pro::kCombine ? 1 : NCH;
+    float ex[NX][8], ew[NX][8];  // kNorm: delta, norm weight; kSwiglu: up
+    if constexpr (PRO == Pro::kNorm || PRO == Pro::kSwiglu) {
 #pragma unroll
         for (int i = 0; i < NCH; ++i) {
             const int c = min(i * WAVES * kWave + tid, nchunk - 1);
@@ -212,6 +255,29 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
         for (int i = 0; i < NCH; ++i)
 #pragma unroll
             for (int e = 0; e < 8; ++e) act.v[i][e] = swiglu_ref(act.v[i][e], ex[i][e], pa.thr);
+    } else if constexpr (PRO == Pro::kCombine) {
+        if (fns > 0) {  // one group over splits 0..fns-1: running max, then e-weighted sums
+            float cm = -INFINITY;
+#pragma unroll
+            for (int sp = 0; sp < NF; ++sp)
+                if (sp < fns) cm = fmaxf(cm, fml[sp].x);
+            float L = 0.0f;
+            float o[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[k] = 0.0f;
+#pragma unroll
+            for (int sp = 0; sp < NF; ++sp) {
+                if (sp < fns) {
+                    const float e = expf(fml[sp].x - cm);
+                    L = fmaf(e, fml[sp].y, L);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) o[k] = fmaf(e, fav[sp][k], o[k]);
+                }
+            }
+            const float inv = 1.0f / L;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) act.v[0][k] = o[k] * inv;
+        }
     }
     act.process(K, im);        // quantize while the weights are in flight
     __syncthreads();
@@ -527,6 +593,33 @@ extern "C" asdsl_status asdsl_gemv_preq2_rmsnorm(const uint8_t* meta, const uint
                           : launch_preq2_fused<32, Pro::kNorm, false>(meta, quant, h_in, y, M, K, pa, s, cus);
     return argmax_key ? launch_preq2_fused<128, Pro::kNorm, true>(meta, quant, h_in, y, M, K, pa, s, cus)
                       : launch_preq2_fused<128, Pro::kNorm, false>(meta, quant, h_in, y, M, K, pa, s, cus);
+}
+
+asdsl_status asdsl::preq2_fused_combine(const uint8_t* meta, const uint8_t* quant, const float* att, float* y,
+                                        int out_features, int in_features, int group_size, const float* part,
+                                        const int* pos, int nsplit, int split, int part_stride, int head_dim,
+                                        int max_seq, int fold, asdsl_stream_t stream) {
+    if (check_preq2_args(meta, quant, att, y, out_features, in_features, group_size, "gemv_preq2_combine"))
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    ASDSL_CHECK_ARG(in_features <= 8192, "gemv_preq2_combine: in_features must be <= 8192");
+    ASDSL_CHECK_ARG(part && pos && fold >= 0 && fold <= kMaxFold && split > 0 && head_dim % 8 == 0 &&
+                        in_features % head_dim == 0 && part_stride % 2 == 0 && part_stride >= head_dim + 2 &&
+                        reinterpret_cast<uintptr_t>(part) % 8 == 0,
+                    "gemv_preq2_combine: invalid partial layout");
+    ASDSL_CU_COUNT(cus);
+    ProArgs pa;
+    pa.part = part;
+    pa.pos = pos;
+    pa.nsplit = nsplit;
+    pa.split = split;
+    pa.part_stride = part_stride;
+    pa.head_dim = head_dim;
+    pa.max_seq = max_seq;
+    pa.fold = fold;
+    hipStream_t s = as_hip(stream);
+    if (group_size == 32)
+        return launch_preq2_fused<32, Pro::kCombine, false>(meta, quant, att, y, out_features, in_features, pa, s, cus);
+    return launch_preq2_fused<128, Pro::kCombine, false>(meta, quant, att, y, out_features, in_features, pa, s, cus);
 }
 
 extern "C" asdsl_status asdsl_gemv_preq2_swiglu(const uint8_t* meta, const uint8_t* quant, const float* gate_up,

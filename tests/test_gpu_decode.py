@@ -248,3 +248,48 @@ def test_forward_token_api(gpu):
         eng.forward_token(4096, 0)
     with pytest.raises(ValueError):
         eng.forward_token(0, 256)
+
+
+
+# Eight greedy steps from position 250 of a two-layer model; the logits of
+# every step are saved to OUT (set by the caller).
+_FOLD_RUN = """
+import numpy as np
+import torch
+from asdsl.engine import DecodeConfig, DecodeEngine
+
+eng = DecodeEngine.synthetic(DecodeConfig(n_layers=2, vocab=4096, max_seq=512), seed=6)
+eng.prefill_kv_random(250, seed=3)
+eng.token.fill_(99)
+eng.pos.fill_(250)
+out = []
+for _ in range(8):
+    eng._queue_step(int(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    out.append(eng.logits.cpu().numpy().copy())
+np.save(OUT, np.stack(out))
+"""
+
+
+def test_combine_fold_gives_the_combine_kernels_bits(gpu, tmp_path):
+    """Positions 250..257: up to 255 (at most 4 splits of 64) the o_proj
+    GEMV's prologue merges the attention splits and the combine kernel skips
+    them, from 256 the combine kernel merges them.  A run that leaves the
+    merge to the combine kernel everywhere (ASDSL_HIP_NO_COMBINE_FOLD=1, read
+    once per process, so in a second process) gives the same logits bit for
+    bit at every position."""
+    import os
+    import subprocess
+    import sys
+
+    from conftest import REPO
+
+    here, there = tmp_path / "fold.npy", tmp_path / "nofold.npy"
+    exec(compile(_FOLD_RUN, "fold_run", "exec"), {"OUT": str(here)})
+    env = dict(os.environ, ASDSL_HIP_NO_COMBINE_FOLD="1",
+               PYTHONPATH=os.pathsep.join([str(REPO), str(REPO / "asdsl-framework_amd"),
+                                           os.environ.get("PYTHONPATH", "")]))
+    subprocess.run([sys.executable, "-c", f"OUT = {str(there)!r}\n" + _FOLD_RUN], env=env, check=True, timeout=100)
+    a, b = np.load(here), np.load(there)
+    assert a.shape == (8, 4096) and np.all(np.isfinite(a))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
