@@ -196,6 +196,35 @@ def test_q4_128_closed_form_and_zero_group():
     assert rel_l2(wd @ x.astype(np.float64), w.astype(np.float64) @ x.astype(np.float64)) < 0.3
 
 
+def test_preq2_g128_matches_the_reference_q4_128_gemv_golden(golden):
+    """The reference has no preq2 kernel at group size 128, but preq2-g128
+    repacked from Q4_128 blocks holds the same weights ((q - 8) * s, zero 8),
+    so the preq2 oracle at gs 128 must give the reference's Q4_128 GEMV
+    output (gemv_q4_128_preq_avx2, the golden vectors) on the same input."""
+    M, K = map(int, golden["q128_shape"])
+    meta, quant = oracle.repack_q4_128_to_preq2(golden["q128_blocks"], M, K)
+    y = oracle.gemv_preq2(meta, quant, golden["q128_xq"], golden["q128_xs"], M, K, 128)
+    assert rel_l2(y, golden["q128_y"]) < 1e-6
+
+
+@needs_ref
+@pytest.mark.parametrize("M,K", [(64, 3072), (33, 8192)])
+def test_preq2_g128_fused_vs_reference_q4_128(M, K):
+    """Same identity on random weights and activations against the compiled
+    reference: its activation quantizer at gs 128 and its Q4_128 GEMV."""
+    ng = oracle.load_reference("_native_gemv")
+    rng = np.random.default_rng(M + K)
+    blocks = syn.q4_128_blocks(syn.gaussian_weights(M, K, M * K))
+    x = (rng.standard_normal(K) * 10.0 ** rng.uniform(-3, 3, K // 128).repeat(128)).astype(np.float32)
+    xq_r = np.zeros(K, np.int8)
+    xs_r = np.zeros(K // 128, np.float32)
+    ng.quantize_activation_avx2(x, xq_r, xs_r, K, 128)
+    y_r = np.zeros(M, np.float32)
+    ng.gemv_q4_128_preq_avx2(blocks.reshape(-1), xq_r, xs_r, y_r, M, K, 128)
+    meta, quant = oracle.repack_q4_128_to_preq2(blocks, M, K)
+    assert rel_l2(oracle.gemv_preq2_fused(meta, quant, x, M, K, 128), y_r) < 1e-6
+
+
 def test_gemm_q4_128_is_column_loop():
     M, K, B = 7, 256, 3
     blocks = syn.q4_128_blocks(syn.gaussian_weights(M, K, 5))
