@@ -351,7 +351,8 @@ size_t asdsl_decode_work_bytes(const asdsl_decode_model* model);
  * runs every layer at position *pos (device int), writes logits[vocab], then
  * sets *token to the argmax and increments *pos.  Nothing else changes on
  * the host side between steps, so a HIP graph of one call replays step after
- * step.  work: asdsl_decode_work_bytes() bytes, 256-byte aligned.
+ * step.  work: asdsl_decode_work_bytes() bytes, 256-byte aligned, scratch
+ * whose contents after a call are unspecified.
  * Replaces UnifiedEngine::forward_token + greedy argmax
  * (asdsl/kernels/native/unified_engine.cpp:1339-1688,207-233). */
 asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int* pos, float* logits,
