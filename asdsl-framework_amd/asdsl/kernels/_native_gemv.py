@@ -35,6 +35,60 @@ def _check_dims(M: int, K: int, gs: int, fn: str) -> None:
         raise ValueError(f"{fn}: in_features must be divisible by group_size")
 
 
+# ------------------------------------------------------------ diagnostic counters
+# The reference counts gemv_q4_q8_avx2 calls (gemv_q4_avx2.cpp:129,140) and the
+# preq GEMV's per-(row, group) single-group accumulations
+# (gemv_q4_preq_restored.cpp:22-23,305,325): every group of every row goes
+# through the classic accumulate unless the 4-group inner loop runs
+# (ASDSL_PREQ_G4FUSED=1, or ASDSL_PREQ_G4GATE_UP_ONLY=1 with >= 8192 rows, or
+# the g4fused entry point; gemv_q4_preq_restored.cpp:47-82,350-352), which
+# leaves only the groups past the last multiple of 4.  The x-preloaded
+# accumulate is never called there.  The same counts are kept here per call,
+# so scripts that read them see the reference's values.
+_q8_calls = 0
+_preq_classic = 0
+_preq_xloaded = 0
+
+
+def _g4_inner(out_features: int, forced: bool) -> bool:
+    import os
+
+    if forced:
+        return True
+    if os.environ.get("ASDSL_PREQ_G4GATE_UP_ONLY", "")[:1] == "1":
+        return out_features >= 8192
+    v = os.environ.get("ASDSL_PREQ_G4FUSED", "")
+    return bool(v) and v[0] != "0"
+
+
+def _count_preq_groups(out_features: int, n_groups: int, g4_forced: bool) -> None:
+    global _preq_classic
+    use_g4 = n_groups >= 4 and n_groups % 4 == 0 and _g4_inner(out_features, g4_forced)
+    _preq_classic += out_features * (n_groups - (n_groups // 4) * 4 if use_g4 else n_groups)
+
+
+def get_q8_call_count() -> int:
+    """Calls of gemv_q4_q8_avx2 so far (gemv_q4_avx2.cpp:1442)."""
+    return _q8_calls
+
+
+def get_preq_classic_accum_calls() -> int:
+    """Single-group accumulations of the preq GEMVs since the last reset (gemv_q4_avx2.cpp:1445)."""
+    return _preq_classic
+
+
+def get_preq_xloaded_accum_calls() -> int:
+    """x-preloaded single-group accumulations since the last reset (gemv_q4_avx2.cpp:1448)."""
+    return _preq_xloaded
+
+
+def reset_preq_accum_call_counts() -> None:
+    """Reference: reset_preq_accum_call_counts (gemv_q4_avx2.cpp:1451)."""
+    global _preq_classic, _preq_xloaded
+    _preq_classic = 0
+    _preq_xloaded = 0
+
+
 # ------------------------------------------------------------ activation Q8
 def quantize_activation_avx2(x, x_q8, x_scales, in_features: int, group_size: int = 32) -> None:
     """Reference: quantize_activation_avx2 (gemv_q4_preq_restored.cpp:505-549)."""
@@ -62,9 +116,11 @@ def gemv_q4_32_preq_avx2(blocks, x_q8, x_scales, y, out_features: int, in_featur
     ps = c.input(x_scales, np.float32, G, "x_scales")
     py = c.output(y, np.float32, out_features, "y")
     c.run("asdsl_gemv_q4_32_preq", pb, pq, ps, py, out_features, in_features, group_size)
+    _count_preq_groups(out_features, G, False)
 
 
-def _preq_fused(fn: str, blocks, x_fp32, y, out_features: int, in_features: int, group_size: int) -> None:
+def _preq_fused(fn: str, blocks, x_fp32, y, out_features: int, in_features: int, group_size: int,
+                g4: bool = False) -> None:
     _check_gs(group_size, (32,), fn)
     _check_dims(out_features, in_features, group_size, fn)
     G = in_features // 32
@@ -73,6 +129,7 @@ def _preq_fused(fn: str, blocks, x_fp32, y, out_features: int, in_features: int,
     px = c.input(x_fp32, np.float32, in_features, "x_fp32")
     py = c.output(y, np.float32, out_features, "y")
     c.run("asdsl_gemv_q4_32_preq_fused", pb, px, py, out_features, in_features, group_size)
+    _count_preq_groups(out_features, G, g4)
 
 
 def gemv_q4_32_preq_fused_avx2(blocks, x_fp32, y, out_features: int, in_features: int, group_size: int = 32):
@@ -88,6 +145,21 @@ def gemv_q4_32_preq_4row_avx2(blocks, x_fp32, y, out_features: int, in_features:
 def gemv_q4_32_preq_8row_avx2(blocks, x_fp32, y, out_features: int, in_features: int, group_size: int = 32):
     """Reference: gemv_q4_32_preq_8row_avx2 (gemv_q4_preq_restored.cpp:628-650); same math as fused."""
     _preq_fused("gemv_q4_32_preq_8row_avx2", blocks, x_fp32, y, out_features, in_features, group_size)
+
+
+def gemv_q4_32_preq_g4fused_4row_avx2(blocks, x_fp32, y, out_features: int, in_features: int,
+                                      group_size: int = 32):
+    """Reference: gemv_q4_32_preq_g4fused_4row_avx2 (gemv_q4_preq_restored.cpp:603-626): the
+    4-group inner loop forced on, same math as fused; the group count must be a
+    multiple of 4 (and at most 640), as the reference requires."""
+    fn = "gemv_q4_32_preq_g4fused_4row_avx2"
+    _check_gs(group_size, (32,), fn)
+    if out_features <= 0 or in_features <= 0:
+        raise ValueError(f"{fn}: invalid dimensions")
+    n_groups = in_features // group_size
+    if n_groups > 640 or n_groups % 4:
+        raise ValueError(f"{fn}: n_groups must be <= 640 and divisible by 4")
+    _preq_fused(fn, blocks, x_fp32, y, out_features, in_features, group_size, g4=True)
 
 
 # ------------------------------------------------------------ preq2
@@ -321,6 +393,8 @@ def gemv_q4_q8_avx2(weights_packed, scales, x, y, out_features: int, in_features
     c.run("asdsl_gemv_q4_q8", c.input(weights_packed, np.uint8, out_features * in_features // 2, "weights_packed"),
           c.input(scales, np.float32, out_features * G, "scales"), c.input(x, np.float32, in_features, "x"),
           c.output(y, np.float32, out_features, "y"), out_features, in_features, group_size)
+    global _q8_calls
+    _q8_calls += 1
 
 
 def gemv_q4km_q8_avx2(weights_q4km, x, y, out_features: int, in_features: int) -> None:
@@ -403,3 +477,24 @@ def check_fma() -> bool:
 
 def check_avx512() -> bool:
     return False
+
+
+def check_vnni() -> bool:
+    """The reference's VNNI probe (gemv_q4_avx2.cpp:1461); the integer dot
+    products here run on the GPU's dot4 and MFMA instructions instead."""
+    return False
+
+
+def check_avx_vnni() -> bool:
+    return False
+
+
+def check_avx512_vnni() -> bool:
+    return False
+
+
+def get_cpu_topology() -> dict:
+    """Reference: get_cpu_topology (gemv_q4_avx2.cpp:1470-1493).  Same keys and
+    the values its non-Windows build returns; the compute device is the GPU."""
+    return {"physical_logical_ids": [], "physical_core_count": 0, "pcore_count": 0,
+            "avx_vnni": False, "avx512_vnni": False}

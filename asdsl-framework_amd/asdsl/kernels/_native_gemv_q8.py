@@ -14,6 +14,23 @@ import numpy as np
 from asdsl.kernels._buffers import DeviceCall, new_output, shape_of
 
 has_openmp = False
+# The reference probes the host CPU for AVX2 (gemv_q8_avx2.cpp:208-220,255);
+# the kernels here run on the GPU.
+has_avx2 = False
+
+
+def set_pin_openmp_pcores(enabled: bool = True) -> None:
+    """Reference: set_pin_openmp_pcores (gemv_q8_avx2.cpp:248-252), CPU thread
+    pinning; there are no host threads to pin here."""
+
+
+def detected_pcore_count() -> int:
+    """Reference: detected_pcore_count (gemv_q8_avx2.cpp:204-206,253), the host's
+    physical cores its kernels run on; here the GPU's compute units, as
+    _native_gemv.get_num_threads reports."""
+    from asdsl import _hip
+
+    return _hip.cu_count()
 
 
 def _numel(a) -> int:

@@ -100,6 +100,21 @@ def gemv_preq2(meta, quant, x_q8, x_scales, M: int, K: int, group_size: int = 32
     return y
 
 
+def gemv_preq2_f32sum(meta, quant, x_q8, x_scales, M: int, K: int, group_size: int = 32) -> np.ndarray:
+    """gemv_preq2 with the group terms summed in float32 in group order (a
+    second restatement that differs from gemv_preq2 only in that rounding)."""
+    meta, quant, xq, xs = _u8(meta), _u8(quant), _i8(x_q8), _f32(x_scales)
+    y = np.empty(M, np.float32)
+    lib().oracle_gemv_preq2_f32sum(_p(meta, _c_u8p), _p(quant, _c_u8p), _p(xq, _c_i8p), _p(xs, _c_f32p),
+                                   _p(y, _c_f32p), M, K, group_size)
+    return y
+
+
+def gemv_preq2_fused_f32sum(meta, quant, x, M: int, K: int, group_size: int = 32) -> np.ndarray:
+    xq, xs = quantize_activation(x, group_size)
+    return gemv_preq2_f32sum(meta, quant, xq, xs, M, K, group_size)
+
+
 def gemv_preq2_fused(meta, quant, x, M: int, K: int, group_size: int = 32) -> np.ndarray:
     xq, xs = quantize_activation(x, group_size)
     return gemv_preq2(meta, quant, xq, xs, M, K, group_size)

@@ -5,8 +5,10 @@
  * kernels: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg may load it.  The product path never calls it.
  *
- * Every function restates one reference routine in plain scalar C (no SIMD,
- * no threads).  Integer parts (nibble decode, int8 activation quantization,
+ * Every function restates one reference routine in plain scalar C (no SIMD).
+ * The preq/preq2 GEMVs spread their rows over OpenMP threads (each row's
+ * arithmetic is the same whatever thread runs it), so that a full-size
+ * decode step can be checked in a test.  Integer parts (nibble decode, int8 activation quantization,
  * integer dots) are exact and match the reference bit for bit.  Floating
  * point per-group terms are formed in fp32 in the reference's operand order;
  * the sum over groups is accumulated in double so that the oracle sits at
@@ -103,6 +105,7 @@ static void nib_dot(const uint8_t* packed, const int8_t* xq, int n, int32_t* d, 
  * 551-573): per group term = D*(s*xs), correction = ((z*X)*s)*xs, y = sum - corr. */
 EXPORT void oracle_gemv_preq(const uint8_t* blocks, const int8_t* xq, const float* xs, float* y, int M, int K) {
     const int G = K / 32;
+#pragma omp parallel for schedule(static)
     for (int r = 0; r < M; ++r) {
         double acc = 0.0, corr = 0.0;
         for (int g = 0; g < G; ++g) {
@@ -134,6 +137,7 @@ EXPORT void oracle_gemv_preq2(const uint8_t* meta, const uint8_t* quant, const i
                               float* y, int M, int K, int gs) {
     const int G = K / gs;
     const size_t gbytes = (size_t)gs / 2;
+#pragma omp parallel for schedule(static)
     for (int r = 0; r < M; ++r) {
         const int band = r / 4, slot = r % 4;
         double acc = 0.0;
@@ -151,6 +155,35 @@ EXPORT void oracle_gemv_preq2(const uint8_t* meta, const uint8_t* quant, const i
     }
 }
 
+/* The same GEMV with the per-group terms summed in float32, in group order,
+ * as a plain scalar CPU loop would (the reference sums float32 AVX2 lanes,
+ * gemv_preq2_avx2.cpp:168-194).  A second restatement that differs from
+ * oracle_gemv_preq2 only in the rounding of the sum: the decode tests use
+ * it to measure how far rounding alone moves a deep model's logits. */
+EXPORT void oracle_gemv_preq2_f32sum(const uint8_t* meta, const uint8_t* quant, const int8_t* xq, const float* xs,
+                                     float* y, int M, int K, int gs) {
+    const int G = K / gs;
+    const size_t gbytes = (size_t)gs / 2;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < M; ++r) {
+        const int band = r / 4, slot = r % 4;
+        float acc = 0.0f;
+        for (int g = 0; g < G; ++g) {
+            const uint8_t* m = meta + ((size_t)r * G + g) * 4;
+            const float s = half_to_float(rd16(m));
+            const float z = half_to_float(rd16(m + 2));
+            const uint8_t* q = quant + ((size_t)band * G + g) * 4 * gbytes + slot * gbytes;
+            int32_t d, xsum;
+            nib_dot(q, xq + (size_t)g * gs, gs, &d, &xsum);
+            const float xsum_scaled = (float)xsum * xs[g];
+            const float term = (float)d * (s * xs[g]);
+            acc = acc + term;
+            acc = acc - (z * s) * xsum_scaled;
+        }
+        y[r] = acc;
+    }
+}
+
 EXPORT void oracle_gemv_preq2_fused(const uint8_t* meta, const uint8_t* quant, const float* x, float* y, int M,
                                     int K, int gs, int8_t* scratch_q, float* scratch_s) {
     oracle_quantize_activation(x, scratch_q, scratch_s, K, gs);
@@ -162,6 +195,7 @@ EXPORT void oracle_gemv_preq2_fused(const uint8_t* meta, const uint8_t* quant, c
 EXPORT void oracle_dequant_preq2(const uint8_t* meta, const uint8_t* quant, float* w, int M, int K, int gs) {
     const int G = K / gs;
     const size_t gbytes = (size_t)gs / 2;
+#pragma omp parallel for schedule(static)
     for (int r = 0; r < M; ++r) {
         const int band = r / 4, slot = r % 4;
         for (int g = 0; g < G; ++g) {

@@ -9,15 +9,16 @@ the GEMVs taken from the oracle's C restatement (oracle.gemv_preq2_fused):
         x   = rmsnorm(h, rms_att)                           (rmsnorm_f32, 499-524)
         qkv = gemv_preq2_fused(qkv, x)                      (1399-1401)
         q, k = rope(q), rope(k)                             (rope_apply_inplace, 768-801)
-        cache[pos] = k, v (fp16 here; int8 per 64 in the reference, 859-920)
+        cache[pos] = k, v (fp16, or int8 per 64 as the reference: set_kv_cache, 859-920)
         att = softmax(q.K / sqrt(128)) V over 0..pos         (compute_attention_flash_q8, 922-1027)
         h   = h + gemv_preq2_fused(o, att)                  (1487-1489, residual_add_rmsnorm_f32 651-688)
         gu  = gemv_preq2_fused(gate_up, rmsnorm(h, rms_ffn))
         h   = h + gemv_preq2_fused(down, swiglu(gate, up))  (swiglu_inplace 803-857, vec_add 487-497)
     logits = gemv_preq2_fused(lm_head, rmsnorm(h, rms_out)); next = argmax (207-233)
 
-Every array is float32 as in the reference; the new K/V are rounded to fp16
-before attention, as if read back from the cache.
+Every array is float32 as in the reference; the new K/V are stored in the
+cache (rounded to fp16, or quantized to int8 per 64 dims) before attention,
+which reads them back from there, as the reference does.
 """
 
 from __future__ import annotations
@@ -76,17 +77,45 @@ def swiglu(gate: np.ndarray, up: np.ndarray, threshold: float = 0.0) -> np.ndarr
 
 
 def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_kv: int) -> np.ndarray:
-    """q [n_heads][d]; k, v [n_kv][T][d] (already fp16-rounded floats).
-    out[h] = softmax(q_h . k / sqrt(d)) v of kv head h // (n_heads / n_kv)."""
+    """q [n_heads][d]; k, v [n_kv][T][d] (fp16 or the fp16-rounded floats).
+    out[h] = softmax(q_h . k / sqrt(d)) v of kv head h // (n_heads / n_kv),
+    in float64 (the query heads of one KV head share its converted rows)."""
     n_heads, d = q.shape
     g = n_heads // n_kv
     out = np.empty((n_heads, d), F32)
-    for h in range(n_heads):
-        kk = k[h // g].astype(np.float64)
-        s = kk @ q[h].astype(np.float64) / np.sqrt(d)
-        w = np.exp(s - s.max())
-        out[h] = (w @ v[h // g].astype(np.float64) / w.sum()).astype(F32)
+    for j in range(n_kv):
+        kk = k[j].astype(np.float64)
+        vv = v[j].astype(np.float64)
+        qq = q[j * g:(j + 1) * g].astype(np.float64)
+        s = kk @ qq.T / np.sqrt(d)              # [T][g]
+        w = np.exp(s - s.max(axis=0))
+        out[j * g:(j + 1) * g] = ((w.T @ vv) / w.sum(axis=0)[:, None]).astype(F32)
     return out
+
+
+KV_QBLOCK = 64
+
+
+def kv_quantize_q8(rows: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """set_kv_cache (unified_engine.cpp:859-920) on rows [n][d] (d a multiple of
+    64), as built with -ffast-math: per 64-dim block amax; scale =
+    amax * f32(1/127) (the constant division becomes a reciprocal multiply)
+    when amax > 1e-12, else 1e-12; inv = 1 / scale; q = clip(rne(x * inv),
+    -127, 127).  Returns int8 [n][d] and float32 scales [n][d / 64]."""
+    x = np.ascontiguousarray(rows, F32).reshape(rows.shape[0], -1, KV_QBLOCK)
+    amax = np.abs(x).max(axis=2)
+    scale = np.where(amax > F32(1e-12), (amax * F32(1.0 / 127.0)).astype(F32), F32(1e-12)).astype(F32)
+    inv = (F32(1.0) / scale).astype(F32)
+    q = np.clip(np.rint((x * inv[:, :, None]).astype(F32)), -127, 127).astype(np.int8)
+    return q.reshape(rows.shape), scale
+
+
+def kv_dequant_q8(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """float(q) * scale per 64-dim block in fp32, as compute_attention_flash_q8
+    forms each K/V element (unified_engine.cpp:948-951,981-983)."""
+    lead = q.shape[:-1]
+    qq = q.reshape(*lead, -1, KV_QBLOCK).astype(F32)
+    return (qq * scale.reshape(*lead, -1, 1).astype(F32)).astype(F32).reshape(q.shape)
 
 
 def argmax_first(x: np.ndarray) -> int:
@@ -94,27 +123,85 @@ def argmax_first(x: np.ndarray) -> int:
     return int(np.argmax(x))
 
 
-def decode_step(model: dict, token: int, pos: int, k_cache: list, v_cache: list) -> tuple[np.ndarray, int]:
-    """One greedy step.  model: host copies of the engine's weights (see
-    tests/test_gpu_decode.py); k_cache/v_cache: per layer fp16 arrays
-    [n_kv][max_seq][128], updated at `pos` in place."""
+def layer_forward(model: dict, li: int, h: np.ndarray, pos: int, k_cache: list, v_cache: list,
+                  trace: dict | None = None, gemv=None) -> np.ndarray:
+    """Decoder layer li at position pos on the residual stream h (float32
+    [hidden]); returns the next residual stream.  The layer's K/V row at pos is
+    written into k_cache[li]/v_cache[li] (see decode_step).  trace (a dict),
+    when given, receives this layer's intermediate values: x_att (the normed
+    qkv input), qkv, att, o, h_mid (the stream after the attention residual),
+    x_ffn, gu, s (the SwiGLU output) and down.  gemv replaces
+    oracle.gemv_preq2_fused (same signature)."""
     c = model["cfg"]
+    gemv = gemv or oracle.gemv_preq2_fused
     hd, nh, nkv = c.head_dim, c.n_heads, c.n_kv_heads
     cos_row, sin_row = model["rope_cos"][pos], model["rope_sin"][pos]
-    h = model["embed"][token].astype(F32)
-    for li, L in enumerate(model["layers"]):
-        x = rmsnorm(h, L["rms_att"], c.rms_eps)
-        qkv = oracle.gemv_preq2_fused(*L["qkv"], x, c.qkv_dim, c.hidden, c.gs_attn)
-        q = rope(qkv[: nh * hd].reshape(nh, hd), cos_row, sin_row)
-        k = rope(qkv[nh * hd:(nh + nkv) * hd].reshape(nkv, hd), cos_row, sin_row)
-        v = qkv[(nh + nkv) * hd:].reshape(nkv, hd)
+    L = model["layers"][li]
+    x = rmsnorm(h, L["rms_att"], c.rms_eps)
+    qkv = gemv(*L["qkv"], x, c.qkv_dim, c.hidden, c.gs_attn)
+    q = rope(qkv[: nh * hd].reshape(nh, hd), cos_row, sin_row)
+    k = rope(qkv[nh * hd:(nh + nkv) * hd].reshape(nkv, hd), cos_row, sin_row)
+    v = qkv[(nh + nkv) * hd:].reshape(nkv, hd)
+    if isinstance(k_cache[li], tuple):  # int8 per 64 dims
+        (kq, ks), (vq, vs) = k_cache[li], v_cache[li]
+        kq[:, pos], ks[:, pos] = kv_quantize_q8(k)
+        vq[:, pos], vs[:, pos] = kv_quantize_q8(v)
+        att = attention(q, kv_dequant_q8(kq[:, :pos + 1], ks[:, :pos + 1]),
+                        kv_dequant_q8(vq[:, :pos + 1], vs[:, :pos + 1]), nkv)
+    else:
         k_cache[li][:, pos] = k.astype(np.float16)
         v_cache[li][:, pos] = v.astype(np.float16)
-        att = attention(q, k_cache[li][:, :pos + 1].astype(F32), v_cache[li][:, :pos + 1].astype(F32), nkv)
-        h = (h + oracle.gemv_preq2_fused(*L["o"], att.reshape(-1), c.hidden, nh * hd, c.gs_attn)).astype(F32)
-        gu = oracle.gemv_preq2_fused(*L["gu"], rmsnorm(h, L["rms_ffn"], c.rms_eps), 2 * c.ffn, c.hidden, c.gs_ffn)
-        s = swiglu(gu[: c.ffn], gu[c.ffn:], model.get("fatrelu_threshold", 0.0))
-        h = (h + oracle.gemv_preq2_fused(*L["down"], s, c.hidden, c.ffn, c.gs_ffn)).astype(F32)
-    logits = oracle.gemv_preq2_fused(model["lm_meta"], model["lm_quant"], rmsnorm(h, model["rms_out"], c.rms_eps),
-                                     c.vocab, c.hidden, c.gs_lm)
+        att = attention(q, k_cache[li][:, :pos + 1], v_cache[li][:, :pos + 1], nkv)
+    o = gemv(*L["o"], att.reshape(-1), c.hidden, nh * hd, c.gs_attn)
+    h_mid = (h + o).astype(F32)
+    x_ffn = rmsnorm(h_mid, L["rms_ffn"], c.rms_eps)
+    gu = gemv(*L["gu"], x_ffn, 2 * c.ffn, c.hidden, c.gs_ffn)
+    sw = swiglu(gu[: c.ffn], gu[c.ffn:], model.get("fatrelu_threshold", 0.0))
+    down = gemv(*L["down"], sw, c.hidden, c.ffn, c.gs_ffn)
+    if trace is not None:
+        trace.update(x_att=x, qkv=qkv, att=att.reshape(-1), o=o, h_mid=h_mid, x_ffn=x_ffn, gu=gu, s=sw, down=down)
+    return (h_mid + down).astype(F32)
+
+
+def lm_head_forward(model: dict, h: np.ndarray, gemv=None) -> np.ndarray:
+    """logits = lm_head(rmsnorm(h, rms_out)) (unified_engine.cpp:1634-1648)."""
+    c = model["cfg"]
+    gemv = gemv or oracle.gemv_preq2_fused
+    return gemv(model["lm_meta"], model["lm_quant"], rmsnorm(h, model["rms_out"], c.rms_eps), c.vocab, c.hidden,
+                c.gs_lm)
+
+
+def decode_step(model: dict, token: int, pos: int, k_cache: list, v_cache: list, trace: list | None = None,
+                gemv=None) -> tuple[np.ndarray, int]:
+    """One greedy step.  model: host copies of the engine's weights
+    (host_model); k_cache/v_cache: per layer either an fp16 array
+    [n_kv][max_seq][128] or, for the int8 cache, a pair (int8
+    [n_kv][max_seq][128], float32 scales [n_kv][max_seq][2]); updated at
+    `pos` in place.  trace (a list), when given, receives per layer a dict
+    with the layer's input stream "h" and the values layer_forward traces,
+    then {"h": final stream}.  gemv replaces oracle.gemv_preq2_fused."""
+    h = model["embed"][token].astype(F32)
+    for li in range(len(model["layers"])):
+        t = {"h": h} if trace is not None else None
+        h = layer_forward(model, li, h, pos, k_cache, v_cache, t, gemv)
+        if trace is not None:
+            trace.append(t)
+    if trace is not None:
+        trace.append({"h": h})
+    logits = lm_head_forward(model, h, gemv)
     return logits, argmax_first(logits)
+
+
+def host_model(eng) -> dict:
+    """Host copies of a DecodeEngine's weights in the layout decode_step reads
+    (tensors copied with .cpu().numpy(); nothing else of the engine is used)."""
+    def h(t):
+        return t.cpu().numpy()
+
+    layers = []
+    for L in eng.layers:
+        layers.append({n: (h(L[n][0]), h(L[n][1])) for n in ("qkv", "o", "gu", "down")} |
+                      {"rms_att": h(L["rms_att"]), "rms_ffn": h(L["rms_ffn"])})
+    return {"cfg": eng.cfg, "layers": layers, "embed": h(eng.embed), "rms_out": h(eng.rms_out),
+            "lm_meta": h(eng.lm_meta), "lm_quant": h(eng.lm_quant),
+            "rope_cos": h(eng.rope_cos), "rope_sin": h(eng.rope_sin)}

@@ -142,3 +142,23 @@ def test_sparse_wrappers(gpu):
     want = oracle.gemv_sparse_indices(w, act, s, b, idx, M, K, gs)
     assert rel_l2(gemv_sparse_unpacked(w, act, s, b, mask, M, K, gs), want) < 1e-4
     assert rel_l2(gemv_sparse_with_indices(w, act, s, b, idx, M, K, gs), want) < 1e-4
+
+
+def test_g4fused_entry_and_q8_call_counter(gpu):
+    """gemv_q4_32_preq_g4fused_4row_avx2 computes the fused preq GEMV
+    (gemv_q4_preq_restored.cpp:603-626) and gemv_q4_q8_avx2 calls are counted
+    (gemv_q4_avx2.cpp:140,1442)."""
+    from asdsl.kernels import _native_gemv as ng
+    from asdsl.quantization import synthetic as syn
+
+    M, K = 3072, 3072
+    blocks = syn.preq_blocks(syn.gaussian_weights(M, K, 11))
+    x = syn.activation(K, 12)
+    y = np.full(M, np.nan, np.float32)
+    ng.gemv_q4_32_preq_g4fused_4row_avx2(blocks, x, y, M, K)
+    assert rel_l2(y, oracle.gemv_preq_fused(blocks, x, M, K)) < 1e-4
+    before = ng.get_q8_call_count()
+    w = np.random.default_rng(1).integers(0, 256, M * K // 2, dtype=np.uint8)
+    s = np.full(M * K // 32, 0.01, np.float32)
+    ng.gemv_q4_q8_avx2(w, s, x, np.zeros(M, np.float32), M, K, 32)
+    assert ng.get_q8_call_count() == before + 1

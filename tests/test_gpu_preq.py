@@ -18,7 +18,7 @@ from conftest import GOLDEN, rel_l2
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
 
-SHAPES = [(1, 32), (3, 64), (4, 256), (70, 512), (129, 3072), (66, 8192), (257, 5120), (8, 20480)]
+SHAPES = [(1, 32), (3, 64), (4, 256), (70, 512), (129, 3072), (3072, 3072), (66, 8192), (257, 5120), (8, 20480)]
 
 
 def _dev(a):
@@ -168,11 +168,18 @@ def test_lm_head_preq2_g128_full_size(gpu):
 
 
 @pytest.mark.parametrize("gs", [32, 128])
-@pytest.mark.parametrize("M,K,N", [(16384, 3072, 2), (16384, 3072, 16), (3072, 8192, 4), (3072, 8192, 16),
-                                   (70, 512, 3), (40, 4096, 3), (129, 3072, 8), (257, 5120, 17), (33, 640, 5)])
+@pytest.mark.parametrize("M,K,N", [(16384, 3072, 2), (16384, 3072, 4), (16384, 3072, 8), (16384, 3072, 16),
+                                   (3072, 8192, 2), (3072, 8192, 4), (3072, 8192, 8), (3072, 8192, 16),
+                                   (8192, 8192, 2), (70, 512, 3), (40, 4096, 3), (129, 3072, 8), (257, 5120, 17),
+                                   (33, 640, 5)])
 def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
     """Batched verification GEMV: column n == gemv_preq2_fused(x_n) (each column
-    quantized on its own), against the oracle per column."""
+    quantized on its own), against the oracle per column.  Covers every
+    kernel instance the speculative-verify shapes reach: the 8-wave dot4
+    kernel (K = 3072, N <= 3), the 16-wave dot4 kernel (K = 8192, N = 2),
+    8192 x 8192 at N = 2, whose 1024 tiles exceed the resident workgroups
+    so each workgroup loops over several, and the MFMA kernel (gs 32,
+    N >= 4, N >= 3 once K >= 4096)."""
     if K % gs:
         pytest.skip("K not a multiple of the group size")
     import torch
