@@ -58,6 +58,15 @@ SIGNATURES: dict[str, list] = {
     "asdsl_compute_bitmask": [_P, _P, _I, _F, _P],
     "asdsl_gemv_sparse_unpacked": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_sparse_down_proj_T": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P],
+    "asdsl_sparse_down_work_bytes": [_I],
+    "asdsl_sparse_down_proj_T_ws": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "asdsl_gemv_preq2_fused_batch_work_bytes": [_I],
+    "asdsl_gemv_preq2_fused_batch_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "asdsl_affine_batch_work_bytes": [_I, _I, _I],
+    "asdsl_gemv_q4_packed_ws": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "asdsl_gemv_q4_gs64_ws": [_P, _P, _P, _P, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "asdsl_matmul_batch_q4_ws": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "asdsl_gemm_q4_128_ws": [_P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],
     "asdsl_gemv_sparse_with_indices": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P],
     "asdsl_gemv_preq2_rmsnorm": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P],
     "asdsl_gemv_preq2_swiglu": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
@@ -76,7 +85,10 @@ SIGNATURES: dict[str, list] = {
     "asdsl_repack_q4_128_to_preq2": [_P, _P, _P, _I, _I, _P],
 }
 _RESTYPE = {"asdsl_last_error": ctypes.c_char_p, "asdsl_attention_work_floats": ctypes.c_size_t,
-            "asdsl_decode_work_bytes": ctypes.c_size_t, "asdsl_decode_verify_work_bytes": ctypes.c_size_t}
+            "asdsl_decode_work_bytes": ctypes.c_size_t, "asdsl_decode_verify_work_bytes": ctypes.c_size_t,
+            "asdsl_sparse_down_work_bytes": ctypes.c_size_t,
+            "asdsl_gemv_preq2_fused_batch_work_bytes": ctypes.c_size_t,
+            "asdsl_affine_batch_work_bytes": ctypes.c_size_t}
 
 
 class HipLibraryMissing(ImportError):

@@ -89,6 +89,13 @@ def reset_preq_accum_call_counts() -> None:
     _preq_xloaded = 0
 
 
+def _affine_work(c: DeviceCall, M: int, K: int, group_size: int, batch: int):
+    """A caller-owned work buffer (a device temporary of this call) for the
+    batched fp32-affine GEMMs, or (None, 0) when the call runs per column."""
+    nbytes = int(_hip.LIB.asdsl_affine_batch_work_bytes(M, K, group_size)) if batch > 1 else 0
+    return (c.scratch(nbytes, np.uint8), nbytes) if nbytes else (None, 0)
+
+
 # ------------------------------------------------------------ activation Q8
 def quantize_activation_avx2(x, x_q8, x_scales, in_features: int, group_size: int = 32) -> None:
     """Reference: quantize_activation_avx2 (gemv_q4_preq_restored.cpp:505-549)."""
@@ -184,7 +191,9 @@ def gemv_preq2_fused_avx2(meta, quant, x_fp32, y, out_features: int, in_features
     px = c.input(x_fp32, np.float32, n_cols * in_features, "x_fp32")
     py = c.output(y, np.float32, n_cols * out_features, "y")
     if len(xs) == 2:
-        c.run("asdsl_gemv_preq2_fused_batch", pm, pq, px, py, out_features, in_features, group_size, n_cols)
+        nbytes = int(_hip.LIB.asdsl_gemv_preq2_fused_batch_work_bytes(in_features))
+        c.run("asdsl_gemv_preq2_fused_batch_ws", pm, pq, px, py, out_features, in_features, group_size, n_cols,
+              c.scratch(nbytes, np.uint8), nbytes)
     else:
         c.run("asdsl_gemv_preq2_fused", pm, pq, px, py, out_features, in_features, group_size)
 
@@ -339,10 +348,11 @@ def gemv_q4_packed(w_packed, x, scales, biases, M: int, K: int, group_size: int)
         raise ValueError("group_size must be a multiple of 16 for packed weights")
     y = new_output((M,) if len(shape_of(x)) == 1 else (batch, M), np.float32, w_packed, x)
     c = DeviceCall("gemv_q4_packed")
-    c.run("asdsl_gemv_q4_packed", c.input(w_packed, np.uint8, M * K // 2, "w_packed"),
+    work, nbytes = _affine_work(c, M, K, group_size, batch)
+    c.run("asdsl_gemv_q4_packed_ws", c.input(w_packed, np.uint8, M * K // 2, "w_packed"),
           c.input(x, np.float32, batch * K, "x"), c.input(scales, np.float32, M * (K // group_size), "scales"),
           c.input(biases, np.float32, M * (K // group_size), "biases"), c.output(y, np.float32, batch * M, "y"),
-          M, K, group_size, batch)
+          M, K, group_size, batch, work, nbytes)
     return y
 
 
@@ -375,9 +385,10 @@ def gemv_q4_avx2_gs64(w_packed, x, scales, rows: int, cols: int):
         raise ValueError("x size must equal batch * cols")
     y = new_output((rows,) if len(xs) == 1 else (batch, rows), np.float32, w_packed, x)
     c = DeviceCall("gemv_q4_avx2_gs64")
-    c.run("asdsl_gemv_q4_gs64", c.input(w_packed, np.uint8, rows * cols // 2, "w_packed"),
+    work, nbytes = _affine_work(c, rows, cols, 64, batch)
+    c.run("asdsl_gemv_q4_gs64_ws", c.input(w_packed, np.uint8, rows * cols // 2, "w_packed"),
           c.input(x, np.float32, batch * cols, "x"), c.input(scales, np.float32, rows * (cols // 64), "scales"),
-          c.output(y, np.float32, batch * rows, "y"), rows, cols, batch)
+          c.output(y, np.float32, batch * rows, "y"), rows, cols, batch, work, nbytes)
     return y
 
 
@@ -431,10 +442,11 @@ def matmul_batch_q4(w_packed, scales, biases, X_batch, Y_batch, M: int, K: int, 
         raise ValueError("B must be in [1, 64]")
     G = K // group_size
     c = DeviceCall("matmul_batch_q4")
-    c.run("asdsl_matmul_batch_q4", c.input(w_packed, np.uint8, M * K // 2, "w_packed"),
+    work, nbytes = _affine_work(c, M, K, group_size, B)
+    c.run("asdsl_matmul_batch_q4_ws", c.input(w_packed, np.uint8, M * K // 2, "w_packed"),
           c.input(scales, np.float32, M * G, "scales"), c.input(biases, np.float32, M * G, "biases"),
           c.input(X_batch, np.float32, B * K, "X_batch"), c.output(Y_batch, np.float32, B * M, "Y_batch"),
-          M, K, B, group_size)
+          M, K, B, group_size, work, nbytes)
 
 
 def gemm_q4_128_q8_avx2(blocks, x_batch, y_batch, out_features: int, in_features: int, group_size: int,
@@ -448,10 +460,11 @@ def gemm_q4_128_q8_avx2(blocks, x_batch, y_batch, out_features: int, in_features
         raise ValueError(f"{fn}: batch_size must be in [1, 64]")
     G = in_features // 128
     c = DeviceCall(fn)
-    c.run("asdsl_gemm_q4_128", c.input(blocks, np.uint8, out_features * G * 66, "blocks"),
+    work, nbytes = _affine_work(c, out_features, in_features, 128, batch_size)
+    c.run("asdsl_gemm_q4_128_ws", c.input(blocks, np.uint8, out_features * G * 66, "blocks"),
           c.input(x_batch, np.float32, batch_size * in_features, "x_batch"),
           c.output(y_batch, np.float32, batch_size * out_features, "y_batch"),
-          out_features, in_features, group_size, batch_size)
+          out_features, in_features, group_size, batch_size, work, nbytes)
 
 
 has_openmp = False

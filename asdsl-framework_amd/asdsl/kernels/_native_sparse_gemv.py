@@ -94,9 +94,10 @@ def sparse_down_proj_T(w_T_packed, scales_T, biases_T, sparse_x, active_rows, in
     n = _numel(active_rows)
     y = new_output((out_dim,), np.float32, w_T_packed, sparse_x)
     c = DeviceCall("sparse_down_proj_T")
-    c.run("asdsl_sparse_down_proj_T", c.input(w_T_packed, np.uint8, in_dim * out_dim // 2, "w_T_packed"),
+    nbytes = int(_hip.LIB.asdsl_sparse_down_work_bytes(out_dim))
+    c.run("asdsl_sparse_down_proj_T_ws", c.input(w_T_packed, np.uint8, in_dim * out_dim // 2, "w_T_packed"),
           c.input(scales_T, np.float32, in_dim * G, "scales_T"), c.input(biases_T, np.float32, in_dim * G, "biases_T"),
           c.input(sparse_x, np.float32, in_dim, "sparse_x"),
           c.input(active_rows if n else np.zeros(1, np.int32), np.int32, max(n, 1), "active_rows"), n,
-          c.output(y, np.float32, out_dim, "y"), in_dim, out_dim, group_size)
+          c.output(y, np.float32, out_dim, "y"), in_dim, out_dim, group_size, c.scratch(nbytes, np.uint8), nbytes)
     return y

@@ -99,6 +99,21 @@ asdsl_status device_workspace(hipStream_t stream, size_t bytes, void** out, cons
     return ASDSL_OK;
 }
 
+asdsl_status work_buffer(hipStream_t stream, void* work, size_t work_bytes, size_t need, void** out,
+                         const char* what) {
+    if (work == nullptr) return device_workspace(stream, need, out, what);
+    if (work_bytes < need) {
+        set_error("%s: work buffer of %zu bytes, %zu needed", what, work_bytes, need);
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    }
+    if (reinterpret_cast<uintptr_t>(work) % 256 != 0) {
+        set_error("%s: work buffer must be 256-byte aligned", what);
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    }
+    *out = work;
+    return ASDSL_OK;
+}
+
 int env_knob(const char* name) {
     const char* v = getenv(name);
     if (!v || !*v) return 0;

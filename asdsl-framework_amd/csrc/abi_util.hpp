@@ -68,6 +68,12 @@ asdsl_status launch(const char* what, void (*kernel)(P...), dim3 grid, dim3 bloc
 // (ASDSL_ERR_UNSUPPORTED otherwise).
 asdsl_status device_workspace(hipStream_t stream, size_t bytes, void** out, const char* what);
 
+// The work buffer of one call: the caller's (`work`, `work_bytes`; at least
+// `need` bytes, 256-byte aligned, else ASDSL_ERR_INVALID_ARGUMENT) when
+// `work` is not null, the library-held one (device_workspace) otherwise.
+asdsl_status work_buffer(hipStream_t stream, void* work, size_t work_bytes, size_t need, void** out,
+                         const char* what);
+
 // Integer tuning knob from the environment, read once (0 = unset).  Knobs
 // only change launch shapes (and with them the fp32 summation order), never
 // the formula: ASDSL_HIP_WG_PER_CU caps workgroups per compute unit,
@@ -83,7 +89,7 @@ int env_knob(const char* name);
 // step's arithmetic therefore uses the dot4 form.
 asdsl_status preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X, float* Y,
                                int out_features, int in_features, int group_size, int n_cols, asdsl_stream_t stream,
-                               bool allow_mfma);
+                               bool allow_mfma, void* work = nullptr, size_t work_bytes = 0);
 
 // The decode step's o_proj: gemv_preq2_fused of the attention output, which
 // the GEMV's prologue merges itself from the split partials (part: per head

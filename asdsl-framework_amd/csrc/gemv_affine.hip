@@ -754,9 +754,20 @@ asdsl_status launch_batch_upg(const BatchPlan& p, const uint8_t* w, const float*
 // B columns of X, 16 per weight pass.  Returns ASDSL_ERR_UNSUPPORTED (nothing
 // launched) when the shape has no MFMA tiling; the caller then runs one GEMV
 // per column.
+// Work bytes of affine_batch: the column image (K/32 units x 2 digits x 64 x 16
+// bytes), per-group sums and scale exponents, and the K-slab partial rows.
+size_t affine_batch_work_bytes(int M, int K, int upg, int slabs) {
+    const int U = K / 32;
+    const size_t img_bytes = static_cast<size_t>(U) * 2 * kWave * 16;
+    const size_t sum_bytes = static_cast<size_t>(U / upg) * kBatchCols * 4 + kBatchCols * 4;
+    const size_t part_floats = slabs > 1 ? static_cast<size_t>(slabs) * kBatchCols * M : 0;
+    return img_bytes + sum_bytes + part_floats * 4;
+}
+
 template <bool BIAS, bool Q128 = false>
 asdsl_status affine_batch(const uint8_t* w, const float* s, const float* b, const float* X, float* Y, int M, int K,
-                          int B, int gs, hipStream_t st, int cus, const char* what) {
+                          int B, int gs, hipStream_t st, int cus, const char* what, void* work = nullptr,
+                          size_t work_bytes = 0) {
     const int upg = gs / 32;
     if (gs % 32 != 0 || (upg != 1 && upg != 2 && upg != 4) || reinterpret_cast<uintptr_t>(X) % 16 != 0)
         return ASDSL_ERR_UNSUPPORTED;
@@ -765,9 +776,8 @@ asdsl_status affine_batch(const uint8_t* w, const float* s, const float* b, cons
     const int U = K / 32;
     const size_t img_bytes = static_cast<size_t>(U) * 2 * kWave * 16;
     const size_t sum_bytes = static_cast<size_t>(U / upg) * kBatchCols * 4 + kBatchCols * 4;
-    const size_t part_floats = p.slabs > 1 ? static_cast<size_t>(p.slabs) * kBatchCols * M : 0;
     void* ws = nullptr;
-    asdsl_status r = device_workspace(st, img_bytes + sum_bytes + part_floats * 4, &ws, what);
+    asdsl_status r = work_buffer(st, work, work_bytes, affine_batch_work_bytes(M, K, upg, p.slabs), &ws, what);
     if (r != ASDSL_OK) return r;
     uint4* img = static_cast<uint4*>(ws);
     float* xsum = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + img_bytes);
@@ -853,9 +863,17 @@ int check_affine(const void* w, const void* x, const void* s, const void* y, int
 
 using namespace asdsl;
 
-extern "C" asdsl_status asdsl_gemv_q4_packed(const uint8_t* w_packed, const float* x, const float* scales,
-                                             const float* biases, float* y, int M, int K, int group_size,
-                                             int batch, asdsl_stream_t stream) {
+extern "C" size_t asdsl_affine_batch_work_bytes(int M, int K, int group_size) {
+    if (M <= 0 || K <= 0 || group_size <= 0 || group_size % 32 != 0) return 0;
+    const int upg = group_size / 32;
+    if (upg != 1 && upg != 2 && upg != 4) return 0;
+    const BatchPlan p = plan_affine_batch(M, K, upg, 256);  // the slab count does not depend on the CU count
+    return p.ok ? affine_batch_work_bytes(M, K, upg, p.slabs) : 0;
+}
+
+extern "C" asdsl_status asdsl_gemv_q4_packed_ws(const uint8_t* w_packed, const float* x, const float* scales,
+                                                const float* biases, float* y, int M, int K, int group_size,
+                                                int batch, void* work, size_t work_bytes, asdsl_stream_t stream) {
     if (check_affine(w_packed, x, scales, y, M, K, group_size, batch, "gemv_q4_packed"))
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CHECK_ARG(biases != nullptr, "gemv_q4_packed: null pointer");
@@ -863,7 +881,7 @@ extern "C" asdsl_status asdsl_gemv_q4_packed(const uint8_t* w_packed, const floa
     ASDSL_CU_COUNT(cus);
     if (batch > 1) {
         const asdsl_status st = affine_batch<true>(w_packed, scales, biases, x, y, M, K, batch, group_size,
-                                                   as_hip(stream), cus, "gemv_q4_packed");
+                                                   as_hip(stream), cus, "gemv_q4_packed", work, work_bytes);
         if (st != ASDSL_ERR_UNSUPPORTED) return st;
     }
     for (int bi = 0; bi < batch; ++bi) {
@@ -875,6 +893,12 @@ extern "C" asdsl_status asdsl_gemv_q4_packed(const uint8_t* w_packed, const floa
     return ASDSL_OK;
 }
 
+extern "C" asdsl_status asdsl_gemv_q4_packed(const uint8_t* w_packed, const float* x, const float* scales,
+                                             const float* biases, float* y, int M, int K, int group_size,
+                                             int batch, asdsl_stream_t stream) {
+    return asdsl_gemv_q4_packed_ws(w_packed, x, scales, biases, y, M, K, group_size, batch, nullptr, 0, stream);
+}
+
 extern "C" asdsl_status asdsl_gemv_q4_unpacked(const uint8_t* w, const float* x, const float* scales,
                                                const float* biases, float* y, int M, int K, int group_size,
                                                asdsl_stream_t stream) {
@@ -884,14 +908,15 @@ extern "C" asdsl_status asdsl_gemv_q4_unpacked(const uint8_t* w, const float* x,
     return launch_affine<8, true, false>(w, x, scales, biases, nullptr, y, M, K, group_size, as_hip(stream), cus);
 }
 
-extern "C" asdsl_status asdsl_gemv_q4_gs64(const uint8_t* w_packed, const float* x, const float* scales, float* y,
-                                           int rows, int cols, int batch, asdsl_stream_t stream) {
+extern "C" asdsl_status asdsl_gemv_q4_gs64_ws(const uint8_t* w_packed, const float* x, const float* scales, float* y,
+                                              int rows, int cols, int batch, void* work, size_t work_bytes,
+                                              asdsl_stream_t stream) {
     if (check_affine(w_packed, x, scales, y, rows, cols, 64, batch, "gemv_q4_avx2_gs64"))
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CU_COUNT(cus);
     if (batch > 1) {
         const asdsl_status st = affine_batch<false>(w_packed, scales, nullptr, x, y, rows, cols, batch, 64,
-                                                    as_hip(stream), cus, "gemv_q4_avx2_gs64");
+                                                    as_hip(stream), cus, "gemv_q4_avx2_gs64", work, work_bytes);
         if (st != ASDSL_ERR_UNSUPPORTED) return st;
     }
     for (int bi = 0; bi < batch; ++bi) {
@@ -901,6 +926,11 @@ extern "C" asdsl_status asdsl_gemv_q4_gs64(const uint8_t* w_packed, const float*
         if (st != ASDSL_OK) return st;
     }
     return ASDSL_OK;
+}
+
+extern "C" asdsl_status asdsl_gemv_q4_gs64(const uint8_t* w_packed, const float* x, const float* scales, float* y,
+                                           int rows, int cols, int batch, asdsl_stream_t stream) {
+    return asdsl_gemv_q4_gs64_ws(w_packed, x, scales, y, rows, cols, batch, nullptr, 0, stream);
 }
 
 extern "C" asdsl_status asdsl_gemv_q8_unpacked(const uint8_t* w, const float* x, const float* scales,
@@ -959,9 +989,9 @@ extern "C" asdsl_status asdsl_gemv_sparse_with_indices(const uint8_t* w, const f
     return launch_affine<8, true, true>(w, work_x, scales, biases, work_mask, y, M, K, group_size, s, cus);
 }
 
-extern "C" asdsl_status asdsl_matmul_batch_q4(const uint8_t* w_packed, const float* scales, const float* biases,
-                                              const float* X, float* Y, int M, int K, int B, int group_size,
-                                              asdsl_stream_t stream) {
+extern "C" asdsl_status asdsl_matmul_batch_q4_ws(const uint8_t* w_packed, const float* scales, const float* biases,
+                                                 const float* X, float* Y, int M, int K, int B, int group_size,
+                                                 void* work, size_t work_bytes, asdsl_stream_t stream) {
     if (check_affine(w_packed, X, scales, Y, M, K, group_size, B, "matmul_batch_q4")) return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CHECK_ARG(biases != nullptr, "matmul_batch_q4: null pointer");
     ASDSL_CHECK_ARG(B <= 64, "matmul_batch_q4: B must be <= 64 (the reference's accumulator limit)");
@@ -969,7 +999,7 @@ extern "C" asdsl_status asdsl_matmul_batch_q4(const uint8_t* w_packed, const flo
     ASDSL_CU_COUNT(cus);
     if (B > 1) {
         const asdsl_status st = affine_batch<true>(w_packed, scales, biases, X, Y, M, K, B, group_size,
-                                                   as_hip(stream), cus, "matmul_batch_q4");
+                                                   as_hip(stream), cus, "matmul_batch_q4", work, work_bytes);
         if (st != ASDSL_ERR_UNSUPPORTED) return st;
     }
     for (int bi = 0; bi < B; ++bi) {
@@ -981,8 +1011,15 @@ extern "C" asdsl_status asdsl_matmul_batch_q4(const uint8_t* w_packed, const flo
     return ASDSL_OK;
 }
 
-extern "C" asdsl_status asdsl_gemm_q4_128(const uint8_t* blocks, const float* X, float* Y, int out_features,
-                                          int in_features, int group_size, int batch_size, asdsl_stream_t stream) {
+extern "C" asdsl_status asdsl_matmul_batch_q4(const uint8_t* w_packed, const float* scales, const float* biases,
+                                              const float* X, float* Y, int M, int K, int B, int group_size,
+                                              asdsl_stream_t stream) {
+    return asdsl_matmul_batch_q4_ws(w_packed, scales, biases, X, Y, M, K, B, group_size, nullptr, 0, stream);
+}
+
+extern "C" asdsl_status asdsl_gemm_q4_128_ws(const uint8_t* blocks, const float* X, float* Y, int out_features,
+                                             int in_features, int group_size, int batch_size, void* work,
+                                             size_t work_bytes, asdsl_stream_t stream) {
     ASDSL_CHECK_ARG(blocks && X && Y, "gemm_q4_128_q8_avx2: null pointer");
     ASDSL_CHECK_ARG(group_size == 128, "gemm_q4_128_q8_avx2: group_size must be 128");
     ASDSL_CHECK_ARG(out_features > 0 && in_features > 0 && in_features % 128 == 0,
@@ -994,7 +1031,8 @@ extern "C" asdsl_status asdsl_gemm_q4_128(const uint8_t* blocks, const float* X,
     ASDSL_CU_COUNT(cus);
     if (batch_size > 1) {
         const asdsl_status st = affine_batch<true, true>(blocks, nullptr, nullptr, X, Y, out_features, in_features,
-                                                         batch_size, 128, as_hip(stream), cus, "gemm_q4_128_q8_avx2");
+                                                         batch_size, 128, as_hip(stream), cus, "gemm_q4_128_q8_avx2",
+                                                         work, work_bytes);
         if (st != ASDSL_ERR_UNSUPPORTED) return st;
     }
     for (int bi = 0; bi < batch_size; ++bi) {
@@ -1004,4 +1042,9 @@ extern "C" asdsl_status asdsl_gemm_q4_128(const uint8_t* blocks, const float* X,
         if (st != ASDSL_OK) return st;
     }
     return ASDSL_OK;
+}
+
+extern "C" asdsl_status asdsl_gemm_q4_128(const uint8_t* blocks, const float* X, float* Y, int out_features,
+                                          int in_features, int group_size, int batch_size, asdsl_stream_t stream) {
+    return asdsl_gemm_q4_128_ws(blocks, X, Y, out_features, in_features, group_size, batch_size, nullptr, 0, stream);
 }

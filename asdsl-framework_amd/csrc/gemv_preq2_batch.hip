@@ -546,7 +546,7 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused(const uint8_t* meta, const uint8_
 // decode pass uses that form (see preq2_fused_batch in abi_util.hpp).
 asdsl_status asdsl::preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X, float* Y,
                                       int out_features, int in_features, int group_size, int n_cols,
-                                      asdsl_stream_t stream, bool allow_mfma) {
+                                      asdsl_stream_t stream, bool allow_mfma, void* work, size_t work_bytes) {
     ASDSL_CHECK_ARG(meta && quant && X && Y, "gemv_preq2_fused_batch: null pointer");
     ASDSL_CHECK_ARG(group_size == 32 || group_size == 128,
                     "gemv_preq2_fused_batch: group_size must be 32 (preq2) or 128 (preq2-g128)");
@@ -573,8 +573,9 @@ asdsl_status asdsl::preq2_fused_batch(const uint8_t* meta, const uint8_t* quant,
         const int G = K / 32;
         const size_t img_bytes = static_cast<size_t>(G) * kMfmaCols * 32;
         void* ws = nullptr;
-        const asdsl_status st0 = device_workspace(s, img_bytes + static_cast<size_t>(G) * kMfmaCols * sizeof(float2),
-                                                  &ws, "gemv_preq2_fused_batch");
+        const asdsl_status st0 = work_buffer(s, work, work_bytes,
+                                             img_bytes + static_cast<size_t>(G) * kMfmaCols * sizeof(float2), &ws,
+                                             "gemv_preq2_fused_batch");
         if (st0 != ASDSL_OK) return st0;
         auto* img = static_cast<uint2*>(ws);
         auto* fac = reinterpret_cast<float2*>(static_cast<uint8_t*>(ws) + img_bytes);
@@ -620,4 +621,24 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const 
                                                      float* Y, int out_features, int in_features, int group_size,
                                                      int n_cols, asdsl_stream_t stream) {
     return preq2_fused_batch(meta, quant, X, Y, out_features, in_features, group_size, n_cols, stream, true);
+}
+
+// The MFMA form's column image: per 32-group 16 columns x 32 int8 operands
+// and a (scale, scaled sum) pair.
+extern "C" size_t asdsl_gemv_preq2_fused_batch_work_bytes(int in_features) {
+    if (in_features <= 0 || in_features % 32 != 0) return 0;
+    return static_cast<size_t>(in_features / 32) * kMfmaCols * (32 + sizeof(float2));
+}
+
+extern "C" asdsl_status asdsl_gemv_preq2_fused_batch_ws(const uint8_t* meta, const uint8_t* quant, const float* X,
+                                                        float* Y, int out_features, int in_features, int group_size,
+                                                        int n_cols, void* work, size_t work_bytes,
+                                                        asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(work != nullptr, "gemv_preq2_fused_batch_ws: null work buffer");
+    ASDSL_CHECK_ARG(work_bytes >= asdsl_gemv_preq2_fused_batch_work_bytes(in_features),
+                    "gemv_preq2_fused_batch_ws: work buffer of %zu bytes, "
+                    "asdsl_gemv_preq2_fused_batch_work_bytes gives %zu", work_bytes,
+                    asdsl_gemv_preq2_fused_batch_work_bytes(in_features));
+    return preq2_fused_batch(meta, quant, X, Y, out_features, in_features, group_size, n_cols, stream, true, work,
+                             work_bytes);
 }

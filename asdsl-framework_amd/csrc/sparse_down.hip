@@ -174,10 +174,28 @@ __global__ __launch_bounds__(64) void sparse_down_sum_parts(const float* __restr
 
 using namespace asdsl;
 
-extern "C" asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, const float* scales_T,
-                                                 const float* biases_T, const float* sparse_x,
-                                                 const int32_t* active_rows, int n_active, float* y, int in_dim,
-                                                 int out_dim, int group_size, asdsl_stream_t stream) {
+namespace {
+
+struct SparsePlan {
+    int nslices, nparts, per_part, grid;
+};
+
+SparsePlan plan_sparse_down(int n_active, int out_dim, int cus) {
+    SparsePlan p{};
+    p.nslices = (out_dim + kSliceOut - 1) / kSliceOut;
+    // about 3 workgroups per 4 compute units, at least 32 rows per part
+    int nparts = (3 * cus / 4) / p.nslices;
+    nparts = min(nparts, (n_active + kMinRowsPerPart - 1) / kMinRowsPerPart);
+    p.nparts = max(1, min(nparts, kMaxParts));
+    p.per_part = max(1, (n_active + p.nparts - 1) / p.nparts);
+    const int tiles = p.nslices * p.nparts;
+    p.grid = (tiles + kXcds - 1) / kXcds * kXcds;
+    return p;
+}
+
+asdsl_status check_sparse_down(const uint8_t* w_T_packed, const float* scales_T, const float* biases_T,
+                               const float* sparse_x, const int32_t* active_rows, int n_active, const float* y,
+                               int in_dim, int out_dim, int group_size) {
     ASDSL_CHECK_ARG(in_dim > 0 && out_dim > 0 && group_size > 0, "in_dim, out_dim, group_size must be positive");
     ASDSL_CHECK_ARG(out_dim % group_size == 0, "out_dim must be divisible by group_size");
     ASDSL_CHECK_ARG(w_T_packed && scales_T && biases_T && sparse_x && y, "sparse_down_proj_T: null pointer");
@@ -187,30 +205,61 @@ extern "C" asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, cons
                     "sparse_down_proj_T: out_dim must be a multiple of 32 and group_size of 8");
     ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(w_T_packed) % 16 == 0,
                     "sparse_down_proj_T: w_T_packed must be 16-byte aligned");
-    ASDSL_CU_COUNT(cus);
-    const int nslices = (out_dim + kSliceOut - 1) / kSliceOut;
-    // about 3 workgroups per 4 compute units, at least 32 rows per part
-    int nparts = (3 * cus / 4) / nslices;
-    nparts = min(nparts, (n_active + kMinRowsPerPart - 1) / kMinRowsPerPart);
-    nparts = max(1, min(nparts, kMaxParts));
-    const int per_part = max(1, (n_active + nparts - 1) / nparts);
-    const int tiles = nslices * nparts;
-    const int grid = (tiles + kXcds - 1) / kXcds * kXcds;
-    hipStream_t s = as_hip(stream);
+    return ASDSL_OK;
+}
+
+// The two launches; `part` (nparts x out_dim floats) is only touched when
+// the plan has more than one part.
+asdsl_status run_sparse_down(const SparsePlan& p, const uint8_t* w_T_packed, const float* scales_T,
+                             const float* biases_T, const float* sparse_x, const int32_t* active_rows, int n_active,
+                             float* y, float* part, int in_dim, int out_dim, int group_size, hipStream_t s) {
     auto kernel = group_size % 32 == 0 ? sparse_down_kernel<true> : sparse_down_kernel<false>;
-    if (nparts == 1)
-        return launch("sparse_down_kernel", kernel, dim3(grid), dim3(kWaves * kWave), 0, s, w_T_packed, scales_T,
-                      biases_T, sparse_x, active_rows, n_active, y, in_dim, out_dim, group_size, nslices, nparts,
-                      per_part);
-    void* part = nullptr;
-    const asdsl_status st = device_workspace(s, static_cast<size_t>(nparts) * out_dim * sizeof(float), &part,
-                                             "sparse_down_proj_T");
-    if (st != ASDSL_OK) return st;
-    float* pf = static_cast<float*>(part);
-    const asdsl_status st1 = launch("sparse_down_kernel", kernel, dim3(grid), dim3(kWaves * kWave), 0, s, w_T_packed,
-                                    scales_T, biases_T, sparse_x, active_rows, n_active, pf, in_dim, out_dim,
-                                    group_size, nslices, nparts, per_part);
+    if (p.nparts == 1)
+        return launch("sparse_down_kernel", kernel, dim3(p.grid), dim3(kWaves * kWave), 0, s, w_T_packed, scales_T,
+                      biases_T, sparse_x, active_rows, n_active, y, in_dim, out_dim, group_size, p.nslices, p.nparts,
+                      p.per_part);
+    const asdsl_status st1 = launch("sparse_down_kernel", kernel, dim3(p.grid), dim3(kWaves * kWave), 0, s,
+                                    w_T_packed, scales_T, biases_T, sparse_x, active_rows, n_active, part, in_dim,
+                                    out_dim, group_size, p.nslices, p.nparts, p.per_part);
     if (st1 != ASDSL_OK) return st1;
     return launch("sparse_down_sum_parts", sparse_down_sum_parts, dim3((out_dim + 63) / 64), dim3(64), 0, s,
-                  static_cast<const float*>(pf), y, out_dim, nparts);
+                  static_cast<const float*>(part), y, out_dim, p.nparts);
+}
+
+}  // namespace
+
+extern "C" size_t asdsl_sparse_down_work_bytes(int out_dim) {
+    return out_dim > 0 ? static_cast<size_t>(kMaxParts) * out_dim * sizeof(float) : 0;
+}
+
+extern "C" asdsl_status asdsl_sparse_down_proj_T_ws(const uint8_t* w_T_packed, const float* scales_T,
+                                                    const float* biases_T, const float* sparse_x,
+                                                    const int32_t* active_rows, int n_active, float* y, int in_dim,
+                                                    int out_dim, int group_size, void* work, size_t work_bytes,
+                                                    asdsl_stream_t stream) {
+    const asdsl_status cs = check_sparse_down(w_T_packed, scales_T, biases_T, sparse_x, active_rows, n_active, y,
+                                              in_dim, out_dim, group_size);
+    if (cs != ASDSL_OK) return cs;
+    ASDSL_CHECK_ARG(work == nullptr || work_bytes >= asdsl_sparse_down_work_bytes(out_dim),
+                    "sparse_down_proj_T: work buffer of %zu bytes, asdsl_sparse_down_work_bytes gives %zu", work_bytes,
+                    asdsl_sparse_down_work_bytes(out_dim));
+    ASDSL_CU_COUNT(cus);
+    const SparsePlan p = plan_sparse_down(n_active, out_dim, cus);
+    hipStream_t s = as_hip(stream);
+    void* part = nullptr;
+    if (p.nparts > 1) {
+        const asdsl_status st = work_buffer(s, work, work_bytes, static_cast<size_t>(p.nparts) * out_dim * sizeof(float),
+                                            &part, "sparse_down_proj_T");
+        if (st != ASDSL_OK) return st;
+    }
+    return run_sparse_down(p, w_T_packed, scales_T, biases_T, sparse_x, active_rows, n_active, y,
+                           static_cast<float*>(part), in_dim, out_dim, group_size, s);
+}
+
+extern "C" asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, const float* scales_T,
+                                                 const float* biases_T, const float* sparse_x,
+                                                 const int32_t* active_rows, int n_active, float* y, int in_dim,
+                                                 int out_dim, int group_size, asdsl_stream_t stream) {
+    return asdsl_sparse_down_proj_T_ws(w_T_packed, scales_T, biases_T, sparse_x, active_rows, n_active, y, in_dim,
+                                       out_dim, group_size, nullptr, 0, stream);
 }

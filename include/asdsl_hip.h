@@ -2,14 +2,17 @@
  * asdsl_hip.h — C ABI of the MI355X (gfx950) Q4 GEMV family.
  *
  * Every entry point is stream-ordered and asynchronous: pointers are DEVICE
- * pointers, nothing is allocated (apart from one work buffer per device,
- * grown on first use and kept, which asdsl_sparse_down_proj_T and the batched
- * calls share: asdsl_gemv_preq2_fused_batch with n_cols >= 4 (>= 3 when
- * in_features >= 4096), and with
- * K % 128 == 0 asdsl_matmul_batch_q4, asdsl_gemm_q4_128 and
- * asdsl_gemv_q4_packed / asdsl_gemv_q4_gs64 with batch > 1; calls that
- * overlap on one device on unordered streams race on it), and the call
- * returns as soon as the kernel is queued on `stream` (0 = the null stream).
+ * pointers and the call returns as soon as its kernels are queued on
+ * `stream` (0 = the null stream).  Nothing is allocated, with one exception:
+ * the calls that need a work buffer (asdsl_sparse_down_proj_T, and the
+ * batched GEMVs: asdsl_gemv_preq2_fused_batch with n_cols >= 4 (>= 3 when
+ * in_features >= 4096), asdsl_matmul_batch_q4, asdsl_gemm_q4_128 and
+ * asdsl_gemv_q4_packed / asdsl_gemv_q4_gs64 with batch > 1 and
+ * K % 128 == 0) each have a *_ws form that takes a caller-owned work buffer
+ * (size from the matching *_work_bytes query) and allocates nothing; the
+ * plain forms use one buffer per device that the library grows on first use
+ * and keeps (calls that overlap on one device on unordered streams race on
+ * it; growing is refused under graph capture).
  * Buffers are owned by the
  * caller, exactly as in the reference kernels, which take caller-owned
  * host buffers (asdsl/kernels/native/gemv_q4_kernel.h:25-121).
@@ -49,7 +52,7 @@ typedef enum asdsl_status {
     ASDSL_ERR_UNSUPPORTED = 3       /* valid request outside what the kernels handle */
 } asdsl_status;
 
-#define ASDSL_ABI_VERSION 1
+#define ASDSL_ABI_VERSION 2
 
 /* Library identity and error text. No reference counterpart (pybind11 raises). */
 int asdsl_abi_version(void);
@@ -120,14 +123,31 @@ asdsl_status asdsl_gemv_preq2_fused(const uint8_t* meta, const uint8_t* quant,
 /* Batched preq2 GEMV for speculative verification: X[n_cols][in_features]
  * (16-byte aligned) -> Y[n_cols][out_features]; every column quantized
  * independently, so Y[n] equals asdsl_gemv_preq2_fused on X[n] up to fp32
- * summation order.  Each weight byte is read once per launch of up to 16
- * columns (8 when in_features > 4096).  n_cols in [1, 64].
+ * summation order.  Each weight byte is read once per launch: group size 32
+ * with n_cols >= 4 (>= 3 when in_features >= 4096) runs the MFMA form, 16
+ * columns per launch; otherwise the dot4 form takes 16 columns per launch
+ * when each lane holds at most 2 weight units of a band (8-wave workgroups,
+ * in_features <= 4096), else 8 (16-wave workgroups at most 4 units per lane)
+ * or 4, and fewer when the columns' int8 images would pass 96 KB of LDS
+ * (at in_features 3072: 8 columns; at 8192: 8).  n_cols in [1, 64].
  * No reference counterpart: the reference engine verifies preq2 drafts with
  * serial forward_token calls (asdsl/kernels/native/unified_engine.cpp:1768-1789);
  * this is the batched kernel its forward_verify_batch would call. */
 asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X, float* Y,
                                           int out_features, int in_features, int group_size, int n_cols,
                                           asdsl_stream_t stream);
+
+/* Bytes of work buffer asdsl_gemv_preq2_fused_batch_ws needs for this
+ * in_features (any out_features and n_cols); 0 for an invalid size. */
+size_t asdsl_gemv_preq2_fused_batch_work_bytes(int in_features);
+
+/* asdsl_gemv_preq2_fused_batch with a caller-owned work buffer (256-byte
+ * aligned, at least asdsl_gemv_preq2_fused_batch_work_bytes bytes; contents
+ * after the call unspecified): allocates nothing.  Calls that share a work
+ * buffer must be ordered (one stream, or events). */
+asdsl_status asdsl_gemv_preq2_fused_batch_ws(const uint8_t* meta, const uint8_t* quant, const float* X, float* Y,
+                                             int out_features, int in_features, int group_size, int n_cols,
+                                             void* work, size_t work_bytes, asdsl_stream_t stream);
 
 /* preq2 GEMV on a pre-quantized activation.
  * Replaces gemv_preq2_avx2 (asdsl/kernels/native/gemv_preq2_avx2.cpp:321-337).
@@ -190,6 +210,20 @@ asdsl_status asdsl_gemv_q4_packed(const uint8_t* w_packed, const float* x, const
                                   const float* biases, float* y, int M, int K, int group_size, int batch,
                                   asdsl_stream_t stream);
 
+/* Bytes of work buffer the batched fp32-affine GEMMs need at this shape:
+ * asdsl_gemv_q4_packed_ws, asdsl_gemv_q4_gs64_ws (group_size 64),
+ * asdsl_matmul_batch_q4_ws and asdsl_gemm_q4_128_ws (group_size 128); any
+ * batch.  0 when the shape has no batched form (those calls then run one
+ * GEMV per column and need no buffer) or the arguments are invalid. */
+size_t asdsl_affine_batch_work_bytes(int M, int K, int group_size);
+
+/* The same as asdsl_gemv_q4_packed with a caller-owned work buffer
+ * (256-byte aligned, asdsl_affine_batch_work_bytes(M, K, group_size) bytes;
+ * may be NULL when batch == 1): allocates nothing. */
+asdsl_status asdsl_gemv_q4_packed_ws(const uint8_t* w_packed, const float* x, const float* scales,
+                                     const float* biases, float* y, int M, int K, int group_size, int batch,
+                                     void* work, size_t work_bytes, asdsl_stream_t stream);
+
 /* One byte per value, used as is.  Replaces gemv_q4_unpacked
  * (gemv_q4_avx2.cpp:755-806, pybind 1128-1160). */
 asdsl_status asdsl_gemv_q4_unpacked(const uint8_t* w, const float* x, const float* scales,
@@ -202,6 +236,12 @@ asdsl_status asdsl_gemv_q4_unpacked(const uint8_t* w, const float* x, const floa
 asdsl_status asdsl_gemv_q4_gs64(const uint8_t* w_packed, const float* x, const float* scales, float* y,
                                 int rows, int cols, int batch, asdsl_stream_t stream);
 
+/* The same with a caller-owned work buffer (asdsl_affine_batch_work_bytes(rows,
+ * cols, 64) bytes, 256-byte aligned; may be NULL when batch == 1). */
+asdsl_status asdsl_gemv_q4_gs64_ws(const uint8_t* w_packed, const float* x, const float* scales, float* y,
+                                   int rows, int cols, int batch, void* work, size_t work_bytes,
+                                   asdsl_stream_t stream);
+
 /* ------------------------------------------------------------------ A11 ---
  * Batched fp32 Q4 GEMM over packed weights: Y[b][r] = sum_k dequant(W[r,k]) X[b][k]
  * with dequant = q*s + b per group; X [B][K], Y [B][M] overwritten, B <= 64.
@@ -213,12 +253,25 @@ asdsl_status asdsl_matmul_batch_q4(const uint8_t* w_packed, const float* scales,
                                    const float* X, float* Y, int M, int K, int B, int group_size,
                                    asdsl_stream_t stream);
 
+/* The same with a caller-owned work buffer (asdsl_affine_batch_work_bytes(M, K,
+ * group_size) bytes, 256-byte aligned; may be NULL when B == 1). */
+asdsl_status asdsl_matmul_batch_q4_ws(const uint8_t* w_packed, const float* scales, const float* biases,
+                                      const float* X, float* Y, int M, int K, int B, int group_size, void* work,
+                                      size_t work_bytes, asdsl_stream_t stream);
+
 /* Batched Q4_128 GEMM with an fp32 activation, not quantized:
  * Y[b][r] = sum_g ws * sum_k (q-8) X[b][k]; X [B][K], Y [B][M], B <= 64.
  * Replaces gemm_q4_128_q8_avx2 (asdsl/kernels/native/gemv_q4_128.cpp:262-306),
  * the engine's forward_batch GEMM under g128 (unified_engine.cpp:1153-1158). */
 asdsl_status asdsl_gemm_q4_128(const uint8_t* blocks, const float* X, float* Y, int out_features,
                                int in_features, int group_size, int batch_size, asdsl_stream_t stream);
+
+/* The same with a caller-owned work buffer (asdsl_affine_batch_work_bytes(
+ * out_features, in_features, 128) bytes, 256-byte aligned; may be NULL when
+ * batch_size == 1). */
+asdsl_status asdsl_gemm_q4_128_ws(const uint8_t* blocks, const float* X, float* Y, int out_features,
+                                  int in_features, int group_size, int batch_size, void* work, size_t work_bytes,
+                                  asdsl_stream_t stream);
 
 /* uint8 weights (one per byte), fp32 scale and bias per group.
  * Replaces fused_dequant_gemv / gemv_q8_unpacked
@@ -264,12 +317,26 @@ asdsl_status asdsl_gemv_sparse_with_indices(const uint8_t* w, const float* x, co
  * per device: calls that overlap on one device (unordered streams) race on
  * it.  Sizing it allocates, so under graph capture a call with at least the
  * same n_active and out_dim must have run on the device before (else
- * ASDSL_ERR_UNSUPPORTED).  Repeat calls are bitwise equal.
+ * ASDSL_ERR_UNSUPPORTED); asdsl_sparse_down_proj_T_ws takes the buffer from
+ * the caller instead.  Repeat calls are bitwise equal.
  * Replaces sparse_down_proj_T (asdsl/kernels/native/gemv_sparse_avx2.cpp:273-418),
  * called from experiments/phi4_cpu_run.py:3949-3967. */
 asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, const float* scales_T, const float* biases_T,
                                       const float* sparse_x, const int32_t* active_rows, int n_active, float* y,
                                       int in_dim, int out_dim, int group_size, asdsl_stream_t stream);
+
+/* Bytes of work buffer asdsl_sparse_down_proj_T_ws needs for out_dim outputs
+ * (any list length); 0 for out_dim <= 0. */
+size_t asdsl_sparse_down_work_bytes(int out_dim);
+
+/* asdsl_sparse_down_proj_T with a caller-owned work buffer (256-byte aligned,
+ * asdsl_sparse_down_work_bytes(out_dim) bytes; contents after the call
+ * unspecified): allocates nothing.  Calls that share a work buffer must be
+ * ordered (one stream, or events). */
+asdsl_status asdsl_sparse_down_proj_T_ws(const uint8_t* w_T_packed, const float* scales_T, const float* biases_T,
+                                         const float* sparse_x, const int32_t* active_rows, int n_active, float* y,
+                                         int in_dim, int out_dim, int group_size, void* work, size_t work_bytes,
+                                         asdsl_stream_t stream);
 
 /* Debug dequantization of a preq2 matrix to fp32 W[M][K]: w = (q - z) * s,
  * bit-exact with the reference's dequant (experiments/phi4_cpu_run.py:3450-3467). */

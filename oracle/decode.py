@@ -38,30 +38,40 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     return ((x * inv) * w.astype(F32)).astype(F32)
 
 
+def fma32(a, b, c) -> np.ndarray:
+    """float32 fused multiply-add: a*b is exact in float64, the sum is rounded
+    to float64 and then to float32 (the double rounding can differ from one
+    rounding only when the float64 sum lands exactly halfway between two
+    float32 values)."""
+    return (np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)).astype(F32)
+
+
 def rope(heads: np.ndarray, cos_row: np.ndarray, sin_row: np.ndarray) -> np.ndarray:
-    """Half-split rotation of the first 2*len(cos_row) dims of every head row:
-    (x_i, x_{i+h}) -> (x_i c - x_{i+h} s, x_i s + x_{i+h} c)."""
+    """Half-split rotation of the first 2*len(cos_row) dims of every head row,
+    as rope_apply_inplace forms it (unified_engine.cpp:777-786):
+    x_i' = fma(x_i, c, -(x_{i+h} s)), x_{i+h}' = fma(x_i, s, x_{i+h} c)."""
     out = heads.astype(F32).copy()
     h = cos_row.size
     xf = heads[:, :h].astype(F32)
     xs = heads[:, h:2 * h].astype(F32)
-    out[:, :h] = xf * cos_row - xs * sin_row
-    out[:, h:2 * h] = xf * sin_row + xs * cos_row
+    out[:, :h] = fma32(xf, cos_row, -(xs * sin_row).astype(F32))
+    out[:, h:2 * h] = fma32(xf, sin_row, (xs * cos_row).astype(F32))
     return out
 
 
 def fast_exp(x: np.ndarray) -> np.ndarray:
-    """fast_exp_avx2 (unified_engine.cpp:781-801): clamp to +-87.3, x*log2(e) =
-    i + f with i = round-half-even(x*log2(e)), 2^f by a degree-5 polynomial."""
+    """fast_exp_avx2 (unified_engine.cpp:803-825): clamp to +-87.3, x*log2(e) =
+    i + f with i = round-half-even(x*log2(e)), 2^f by a degree-5 polynomial
+    evaluated with fused multiply-adds (_mm256_fmadd_ps), times 2^i."""
     x = np.clip(x.astype(F32), F32(-87.3), F32(87.3))
     x = (x * F32(1.4426950408889634)).astype(F32)
     fi = np.rint(x).astype(F32)
     f = (x - fi).astype(F32)
-    p = F32(0.001333838100523091) * f + F32(0.009618129107628477)
-    p = p * f + F32(0.05550410866482158)
-    p = p * f + F32(0.2402265069591007)
-    p = p * f + F32(0.6931471805599453)
-    p = p * f + F32(1.0)
+    p = fma32(F32(0.001333838100523091), f, F32(0.009618129107628477))
+    p = fma32(p, f, F32(0.05550410866482158))
+    p = fma32(p, f, F32(0.2402265069591007))
+    p = fma32(p, f, F32(0.6931471805599453))
+    p = fma32(p, f, F32(1.0))
     two_i = ((fi.astype(np.int32) + 127) << 23).astype(np.int32).view(F32)
     return (p.astype(F32) * two_i).astype(F32)
 

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
     missing = [n for n in declared_entry_points() if not _hip.exported(n)]
     assert not missing, f"declared but not exported: {missing}"
-    assert _hip.LIB.asdsl_abi_version() == 1
+    assert _hip.LIB.asdsl_abi_version() == 2
 
 
 def test_python_signatures_cover_header():
@@ -86,3 +86,25 @@ def test_no_cpu_fallback():
     with pytest.raises(RuntimeError):
         ng.gemv_preq2_fused_avx2(np.zeros(32, np.uint8), np.zeros(128, np.uint8),
                                  np.zeros(64, np.float32), np.zeros(4, np.float32), 4, 64, 32)
+
+
+def test_work_buffer_queries_and_checks_without_gpu():
+    """The *_work_bytes queries need no device; a caller buffer below the
+    queried size is an argument error raised before any HIP call."""
+    from asdsl import _hip
+
+    lib = _hip.LIB
+    one = ctypes.c_void_p(256)
+    assert lib.asdsl_sparse_down_work_bytes(3072) == 32 * 3072 * 4
+    assert lib.asdsl_sparse_down_work_bytes(0) == 0
+    assert lib.asdsl_gemv_preq2_fused_batch_work_bytes(3072) == 96 * 16 * 40
+    assert lib.asdsl_gemv_preq2_fused_batch_work_bytes(100) == 0
+    # gate_up 16384 x 3072 at group 32: 96 units, one K slab (8 waves x 12 units): image + sums only
+    assert lib.asdsl_affine_batch_work_bytes(16384, 3072, 32) == 96 * 2 * 64 * 16 + 96 * 16 * 4 + 16 * 4
+    assert lib.asdsl_affine_batch_work_bytes(16384, 3000, 32) == 0
+    assert lib.asdsl_sparse_down_proj_T_ws(one, one, one, one, one, 8, one, 64, 3072, 64, one, 1024,
+                                           None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+    assert "work buffer" in _hip.last_error()
+    assert lib.asdsl_gemv_preq2_fused_batch_ws(one, one, one, one, 64, 3072, 32, 4, one, 100,
+                                               None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+    assert "work buffer" in _hip.last_error()
