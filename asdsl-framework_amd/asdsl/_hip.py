@@ -36,6 +36,8 @@ SIGNATURES: dict[str, list] = {
     "asdsl_device_cu_count": [],
     "asdsl_profile_next_launch": [_P, _P],
     "asdsl_stream_read": [_P, ctypes.c_size_t, _P, _I, _P],
+    "asdsl_grid_sync_probe_work_bytes": [_I],
+    "asdsl_grid_sync_probe": [_I, _I, _I, _P, ctypes.c_size_t, _I, _P],
     "asdsl_quantize_activation": [_P, _P, _P, _I, _I, _P],
     "asdsl_gemv_q4_32_preq": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_gemv_q4_32_preq_fused": [_P, _P, _P, _I, _I, _I, _P],
@@ -86,7 +88,7 @@ SIGNATURES: dict[str, list] = {
 }
 _RESTYPE = {"asdsl_last_error": ctypes.c_char_p, "asdsl_attention_work_floats": ctypes.c_size_t,
             "asdsl_decode_work_bytes": ctypes.c_size_t, "asdsl_decode_verify_work_bytes": ctypes.c_size_t,
-            "asdsl_sparse_down_work_bytes": ctypes.c_size_t,
+            "asdsl_sparse_down_work_bytes": ctypes.c_size_t, "asdsl_grid_sync_probe_work_bytes": ctypes.c_size_t,
             "asdsl_gemv_preq2_fused_batch_work_bytes": ctypes.c_size_t,
             "asdsl_affine_batch_work_bytes": ctypes.c_size_t}
 

@@ -287,26 +287,40 @@ struct ActStage {
 // Decode-step elementwise helpers shared by the fused GEMV prologues and the
 // batched verify pass, so both compute identical values.
 
-// The reference's exp polynomial (fast_exp_avx2, unified_engine.cpp:781-801):
-// clamp to [-87.3, 87.3], x*log2(e) split into round-to-nearest integer i and
-// fraction f, 2^f by a degree-5 polynomial, 2^i by exponent bits.
-__device__ __forceinline__ float fast_exp_ref(float x) {
+// The reference's exp polynomial (fast_exp_avx2, unified_engine.cpp:803-825)
+// in two parts, exp(x) = p * 2^i: clamp to [-87.3, 87.3], t = x*log2(e)
+// rounded to fp32, i = round-to-nearest-even(t), f = t - i, p = the degree-5
+// polynomial in f by fused multiply-adds, 2^i by exponent bits.  Contraction
+// is off here, so the compiler cannot fuse t into f = t - i (the reference
+// rounds t); the fused steps are the explicit fmaf calls.
+__device__ __forceinline__ float fast_exp_poly(float x, float& two_i) {
+#pragma clang fp contract(off)
     x = fmaxf(x, -87.3f);
     x = fminf(x, 87.3f);
-    x = x * 1.4426950408889634f;
-    const float fi = __builtin_rintf(x);
+    const float t = x * 1.4426950408889634f;
+    const float fi = __builtin_rintf(t);
     const int i = static_cast<int>(fi);
-    const float f = x - fi;
+    const float f = t - fi;
     float p = fmaf(0.001333838100523091f, f, 0.009618129107628477f);
     p = fmaf(p, f, 0.05550410866482158f);
     p = fmaf(p, f, 0.2402265069591007f);
     p = fmaf(p, f, 0.6931471805599453f);
     p = fmaf(p, f, 1.0f);
-    return p * __builtin_bit_cast(float, (i + 127) << 23);
+    two_i = __builtin_bit_cast(float, (i + 127) << 23);
+    return p;
 }
 
+// swiglu_inplace (unified_engine.cpp:827-857) as the reference's build
+// evaluates it: the denominator 1 + p*2^i as one fused multiply-add, the
+// quotient correctly rounded (the reference build forms it with a reciprocal
+// estimate and one Newton step, which differs in the last bits and depends on
+// the CPU's estimate table), then (g * sigmoid) * u; zeroed where |v| < thr
+// when thr > 0 (FATReLU).
 __device__ __forceinline__ float swiglu_ref(float g, float u, float thr) {
-    const float sigmoid = 1.0f / (1.0f + fast_exp_ref(0.0f - g));
+#pragma clang fp contract(off)
+    float two_i;
+    const float p = fast_exp_poly(0.0f - g, two_i);
+    const float sigmoid = 1.0f / fmaf(p, two_i, 1.0f);
     float v = (g * sigmoid) * u;
     if (thr > 0.0f && !(fabsf(v) >= thr)) v = 0.0f;
     return v;

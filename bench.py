@@ -640,8 +640,54 @@ def run_suite(args) -> int:
             bm_cpu if spm else None, exact=True)
 
     results.extend(repack_rows(args, oracle))
+    results.extend(sync_rows(args))
     print(json.dumps({"suite": "done", "rows": len(results)}), flush=True)
     return 0
+
+
+def sync_rows(args) -> list:
+    """Cost of one grid-wide handoff inside a kernel (asdsl_grid_sync_probe):
+    one cooperative launch of `grid` workgroups running `rounds` waits for
+    every workgroup, timed with HIP events; µs per wait = elapsed / rounds.
+    Every wait in the probe is bounded (it gives up and exits after its spin
+    limit), and the row reports whether any gave up."""
+    import torch
+
+    from asdsl import _hip
+
+    lib, P = _hip.LIB, _hip.ptr
+    out = []
+    cus = _hip.cu_count()
+    modes = {0: "flag barrier", 1: "flag barrier + 4096-float vector handoff", 2: "atomic counter barrier"}
+    for grid in (cus, 2 * cus):
+        for mode, what in modes.items():
+            name = f"S1 grid handoff: {what}"
+            if args.rows and not any(f in name for f in args.rows.split(",")):
+                continue
+            nbytes = lib.asdsl_grid_sync_probe_work_bytes(grid)
+            work = torch.zeros(nbytes // 4, dtype=torch.int32, device="cuda")
+            h = int(torch.cuda.current_stream().cuda_stream)
+            rounds, spin = 2000, 20000
+            st = lib.asdsl_grid_sync_probe(mode, 20, grid, P(work), nbytes, spin, h)  # warm-up
+            torch.cuda.synchronize()
+            if st != 0 or int(work[0].item()) != 0:
+                row = {"suite_row": name, "grid": grid, "error": _hip.last_error() or "a wait gave up"}
+                print(json.dumps(row), flush=True)
+                out.append(row)
+                continue
+            work.zero_()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            lib.asdsl_grid_sync_probe(mode, rounds, grid, P(work), nbytes, spin, h)
+            e1.record()
+            torch.cuda.synchronize()
+            gave_up = int(work[0].item()) != 0
+            us = 1e3 * e0.elapsed_time(e1) / rounds
+            row = {"suite_row": name, "workload": f"{grid} workgroups x 256 threads, {rounds} waits in one launch",
+                   "us_per_wait": round(us, 3), "gave_up": gave_up}
+            print(json.dumps(row), flush=True)
+            out.append(row)
+    return out
 
 
 def repack_rows(args, oracle) -> list:

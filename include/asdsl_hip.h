@@ -79,6 +79,22 @@ asdsl_status asdsl_profile_next_launch(void* start_event, void* stop_event);
  * the practical ceiling for streaming that many bytes in one launch. */
 asdsl_status asdsl_stream_read(const void* data, size_t bytes, uint32_t* sink, int grid, asdsl_stream_t stream);
 
+/* Calibration, no reference counterpart: the cost of a grid-wide handoff
+ * inside one kernel.  One cooperative launch of `grid` workgroups (256
+ * threads each; all must fit on the device at once, else
+ * ASDSL_ERR_UNSUPPORTED) runs `rounds` waits for every workgroup.  mode 0:
+ * each workgroup stores its own flag word, one wave polls all of them;
+ * mode 1: the same with a 4096-float vector written in slices before the
+ * flags and read whole after (plus a second wait before it is rewritten);
+ * mode 2: one atomic add per workgroup on a shared counter, polled.  Flags
+ * and data use agent-scope atomic loads and stores, no cache flushes.
+ * work: asdsl_grid_sync_probe_work_bytes(grid) bytes, zeroed by the caller
+ * before every call.  Every wait gives up after spin_limit polls: the run
+ * then stops early with word 0 of work set to 1 (0 after a complete run). */
+size_t asdsl_grid_sync_probe_work_bytes(int grid);
+asdsl_status asdsl_grid_sync_probe(int mode, int rounds, int grid, void* work, size_t work_bytes, int spin_limit,
+                                   asdsl_stream_t stream);
+
 /* ------------------------------------------------------------------ A1 ---
  * Per-group int8 activation quantizer.
  * Replaces quantize_activation_avx2

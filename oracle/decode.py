@@ -59,28 +59,40 @@ def rope(heads: np.ndarray, cos_row: np.ndarray, sin_row: np.ndarray) -> np.ndar
     return out
 
 
-def fast_exp(x: np.ndarray) -> np.ndarray:
-    """fast_exp_avx2 (unified_engine.cpp:803-825): clamp to +-87.3, x*log2(e) =
-    i + f with i = round-half-even(x*log2(e)), 2^f by a degree-5 polynomial
-    evaluated with fused multiply-adds (_mm256_fmadd_ps), times 2^i."""
+def fast_exp_parts(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """fast_exp_avx2 (unified_engine.cpp:803-825) as exp(x) = p * 2^i: clamp to
+    +-87.3, t = x*log2(e) rounded to float32, i = round-half-even(t), f = t - i,
+    p = the degree-5 polynomial in f by fused multiply-adds (_mm256_fmadd_ps);
+    returns (p, 2^i)."""
     x = np.clip(x.astype(F32), F32(-87.3), F32(87.3))
-    x = (x * F32(1.4426950408889634)).astype(F32)
-    fi = np.rint(x).astype(F32)
-    f = (x - fi).astype(F32)
+    t = (x * F32(1.4426950408889634)).astype(F32)
+    fi = np.rint(t).astype(F32)
+    f = (t - fi).astype(F32)
     p = fma32(F32(0.001333838100523091), f, F32(0.009618129107628477))
     p = fma32(p, f, F32(0.05550410866482158))
     p = fma32(p, f, F32(0.2402265069591007))
     p = fma32(p, f, F32(0.6931471805599453))
     p = fma32(p, f, F32(1.0))
     two_i = ((fi.astype(np.int32) + 127) << 23).astype(np.int32).view(F32)
-    return (p.astype(F32) * two_i).astype(F32)
+    return p, two_i
+
+
+def fast_exp(x: np.ndarray) -> np.ndarray:
+    p, two_i = fast_exp_parts(x)
+    return (p * two_i).astype(F32)
 
 
 def swiglu(gate: np.ndarray, up: np.ndarray, threshold: float = 0.0) -> np.ndarray:
-    """swiglu_inplace: v = (g * 1/(1 + fast_exp(-g))) * u; |v| < threshold -> 0."""
+    """swiglu_inplace (unified_engine.cpp:827-857) as the reference's build
+    evaluates it: sigmoid = 1 / fma(p, 2^i, 1) with (p, 2^i) = fast_exp_parts(-g)
+    (GCC fuses the polynomial's last product into the 1 + exp add), v = (g *
+    sigmoid) * u; |v| < threshold -> 0.  The quotient is correctly rounded here;
+    the reference build forms it with a reciprocal estimate and one Newton
+    step, which moves the last bits and depends on the CPU's estimate table."""
     g = gate.astype(F32)
-    sig = F32(1.0) / (F32(1.0) + fast_exp(-g))
-    v = ((g * sig) * up.astype(F32)).astype(F32)
+    p, two_i = fast_exp_parts(-g)
+    sig = (F32(1.0) / fma32(p, two_i, F32(1.0))).astype(F32)
+    v = ((g * sig).astype(F32) * up.astype(F32)).astype(F32)
     if threshold > 0.0:
         v[np.abs(v) < F32(threshold)] = F32(0.0)
     return v
