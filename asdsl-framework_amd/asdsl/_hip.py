@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list] = {
     "asdsl_gemv_sparse_unpacked": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_sparse_down_proj_T": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P],
     "asdsl_sparse_down_work_bytes": [_I],
+    "asdsl_sparse_down_proj_T_noalloc": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P],
     "asdsl_sparse_down_proj_T_ws": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, ctypes.c_size_t, _P],
     "asdsl_gemv_preq2_fused_batch_work_bytes": [_I],
     "asdsl_gemv_preq2_fused_batch_ws": [_P, _P, _P, _P, _I, _I, _I, _I, _P, ctypes.c_size_t, _P],

@@ -26,6 +26,8 @@
 // results are reproducible run to run on a device (P follows n and the CU
 // count).  The reference's own per-thread buffers race across pool chunks
 // (gemv_sparse_avx2.cpp:297-300).
+#include <mutex>
+
 #include "abi_util.hpp"
 #include "device_common.hpp"
 
@@ -176,6 +178,44 @@ using namespace asdsl;
 
 namespace {
 
+// Partial rows of the no-allocation entry point: at most kMaxParts rows of
+// kNoAllocMaxOut outputs (2 MiB), one array per device for the life of the
+// process.  In host code `g_sparse_scratch` names a host-side stand-in, not
+// device memory: kernels get the per-device address that
+// hipGetSymbolAddress returns (sparse_scratch_ptr).
+constexpr int kNoAllocMaxOut = 16384;
+static __device__ __align__(256) float g_sparse_scratch[kMaxParts * kNoAllocMaxOut];
+
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch_slots[64];
+
+// Device address of this device's g_sparse_scratch, looked up once per device
+// (with that device current) on its first use.
+asdsl_status sparse_scratch_ptr(float** out) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("sparse_down_proj_T_noalloc: no usable HIP device: %s", hipGetErrorString(e));
+        return ASDSL_ERR_HIP;
+    }
+    ScratchSlot& slot = g_scratch_slots[dev];
+    std::call_once(slot.once, [&] {
+        void* p = nullptr;
+        slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(g_sparse_scratch));
+        slot.ptr = slot.err == hipSuccess ? p : nullptr;
+    });
+    if (slot.err != hipSuccess || slot.ptr == nullptr) {
+        set_error("sparse_down_proj_T_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(slot.err));
+        return ASDSL_ERR_HIP;
+    }
+    *out = static_cast<float*>(slot.ptr);
+    return ASDSL_OK;
+}
+
 struct SparsePlan {
     int nslices, nparts, per_part, grid;
 };
@@ -262,4 +302,25 @@ extern "C" asdsl_status asdsl_sparse_down_proj_T(const uint8_t* w_T_packed, cons
                                                  int out_dim, int group_size, asdsl_stream_t stream) {
     return asdsl_sparse_down_proj_T_ws(w_T_packed, scales_T, biases_T, sparse_x, active_rows, n_active, y, in_dim,
                                        out_dim, group_size, nullptr, 0, stream);
+}
+
+extern "C" asdsl_status asdsl_sparse_down_proj_T_noalloc(const uint8_t* w_T_packed, const float* scales_T,
+                                                         const float* biases_T, const float* sparse_x,
+                                                         const int32_t* active_rows, int n_active, float* y,
+                                                         int in_dim, int out_dim, int group_size,
+                                                         asdsl_stream_t stream) {
+    const asdsl_status cs = check_sparse_down(w_T_packed, scales_T, biases_T, sparse_x, active_rows, n_active, y,
+                                              in_dim, out_dim, group_size);
+    if (cs != ASDSL_OK) return cs;
+    ASDSL_CHECK_ARG(out_dim <= kNoAllocMaxOut, "sparse_down_proj_T_noalloc: out_dim %d exceeds the %d outputs of its "
+                    "device scratch array", out_dim, kNoAllocMaxOut);
+    ASDSL_CU_COUNT(cus);
+    const SparsePlan p = plan_sparse_down(n_active, out_dim, cus);
+    float* part = nullptr;
+    if (p.nparts > 1) {
+        const asdsl_status st = sparse_scratch_ptr(&part);
+        if (st != ASDSL_OK) return st;
+    }
+    return run_sparse_down(p, w_T_packed, scales_T, biases_T, sparse_x, active_rows, n_active, y, part, in_dim,
+                           out_dim, group_size, as_hip(stream));
 }

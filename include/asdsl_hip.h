@@ -354,6 +354,21 @@ asdsl_status asdsl_sparse_down_proj_T_ws(const uint8_t* w_T_packed, const float*
                                          int in_dim, int out_dim, int group_size, void* work, size_t work_bytes,
                                          asdsl_stream_t stream);
 
+/* asdsl_sparse_down_proj_T for callers that cannot allocate at all (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc); no counterpart in the reference.  The partial rows live in a
+ * static device array of this library: 32 rows of at most 16384 outputs
+ * (2 MiB per device, held until the process ends), so out_dim > 16384 is
+ * refused (ASDSL_ERR_INVALID_ARGUMENT).  The array's device address is
+ * looked up once per device on the first call there.  Every call on a
+ * device shares that device's array: calls that overlap on one device
+ * (unordered streams) race on it; calls ordered by one stream or by events
+ * do not.  Same bits as asdsl_sparse_down_proj_T. */
+asdsl_status asdsl_sparse_down_proj_T_noalloc(const uint8_t* w_T_packed, const float* scales_T,
+                                              const float* biases_T, const float* sparse_x,
+                                              const int32_t* active_rows, int n_active, float* y, int in_dim,
+                                              int out_dim, int group_size, asdsl_stream_t stream);
+
 /* Debug dequantization of a preq2 matrix to fp32 W[M][K]: w = (q - z) * s,
  * bit-exact with the reference's dequant (experiments/phi4_cpu_run.py:3450-3467). */
 asdsl_status asdsl_dequant_preq2(const uint8_t* meta, const uint8_t* quant, float* w,
