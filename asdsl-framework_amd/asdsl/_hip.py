@@ -73,10 +73,12 @@ SIGNATURES: dict[str, list] = {
     "asdsl_gemv_sparse_with_indices": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P],
     "asdsl_gemv_preq2_rmsnorm": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P],
     "asdsl_gemv_preq2_swiglu": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
+    "asdsl_gemv_preq2_rmsnorm_swiglu": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _P],
     "asdsl_attention_work_floats": [_I, _I],
     "asdsl_attention_f16kv": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "asdsl_decode_work_bytes": [_P],
     "asdsl_decode_token": [_P, _P, _P, _P, _P, _P],
+    "asdsl_decode_token_upto": [_P, _P, _P, _I, _P, _P, _P],
     "asdsl_decode_verify_work_bytes": [_P, _I],
     "asdsl_decode_verify": [_P, _P, _I, _P, _P, _P, _P, _P],
     "asdsl_kv_zero_from": [_P, _P, _I, _I, _I, _I, _P],

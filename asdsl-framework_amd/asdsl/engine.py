@@ -155,7 +155,8 @@ class DecodeEngine:
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.logits = torch.empty(cfg.vocab, dtype=torch.float32, device=dev)
-        self._graph = None
+        self._graphs: dict[int, object] = {}
+        self._host_pos = 0  # the device position as the host last set or advanced it
         # committed KV length and its snapshot stack (UnifiedEngine::kv_seq_len_,
         # kv_snapshot_stack_), host-side like the reference's
         self.kv_seq_len = 0
@@ -190,6 +191,18 @@ class DecodeEngine:
         lm_meta, lm_quant = packed(cfg.vocab, cfg.hidden, cfg.gs_lm)
         return cls(cfg, layers, embed, norm_w(), lm_meta, lm_quant, fatrelu_threshold)
 
+    # A step is shaped for the positions it serves (asdsl_decode_token_upto):
+    # below 256 the attention splits are merged in o_proj's prologue, beyond
+    # by the combine kernel.  One graph per range.
+    POS_LIMITS = (256,)
+
+    def _pos_limit(self, pos: int) -> int:
+        c = self.cfg
+        for limit in self.POS_LIMITS:
+            if 0 <= pos < limit < c.max_seq:
+                return limit
+        return c.max_seq
+
     def prefill_kv_random(self, ctx: int, seed: int = 1) -> None:
         """Positions [0, ctx) of every layer's cache ~ N(0, 1) in fp16; the
         next step decodes at position ctx."""
@@ -205,13 +218,18 @@ class DecodeEngine:
                     L[n][:, :ctx] = torch.randn((self.cfg.n_kv_heads, ctx, self.cfg.head_dim), generator=gen,
                                                 device=L[n].device, dtype=torch.float32).half()
         self.pos.fill_(ctx)
+        self._host_pos = ctx
         self.kv_seq_len = ctx
 
     # ------------------------------------------------------------ stepping
-    def _queue_step(self, stream: int) -> None:
-        _hip.check(_hip.LIB.asdsl_decode_token(ctypes.byref(self._model), _hip.ptr(self.token), _hip.ptr(self.pos),
-                                               _hip.ptr(self.logits), _hip.ptr(self.work), stream),
-                   "asdsl_decode_token")
+    def _queue_step(self, stream: int, pos_limit: int | None = None) -> None:
+        """Queue one step; the device position must be below pos_limit
+        (default: max_seq, any position)."""
+        limit = self.cfg.max_seq if pos_limit is None else int(pos_limit)
+        _hip.check(_hip.LIB.asdsl_decode_token_upto(ctypes.byref(self._model), _hip.ptr(self.token),
+                                                    _hip.ptr(self.pos), limit, _hip.ptr(self.logits),
+                                                    _hip.ptr(self.work), stream),
+                   "asdsl_decode_token_upto")
 
     def forward_token(self, token_id: int, pos: int):
         """Reference: UnifiedEngine::forward_token(token_id, pos, logits).
@@ -222,7 +240,8 @@ class DecodeEngine:
             raise ValueError("forward_token: pos out of kv-cache range")
         self.token.fill_(token_id)
         self.pos.fill_(pos)
-        self._queue_step(_hip.stream_handle())
+        self._queue_step(_hip.stream_handle(), self._pos_limit(pos))
+        self._host_pos = pos + 1
         self.kv_seq_len = max(self.kv_seq_len, pos + 1)
         return self.logits
 
@@ -230,32 +249,49 @@ class DecodeEngine:
         return int(self.token.item())
 
     def capture(self) -> None:
-        """HIP graph of one step (token and position advance on the device)."""
+        """HIP graph of one step (token and position advance on the device)
+        for the current position's range (POS_LIMITS); the
+        host's copy of the position is read back from the device here."""
         import torch
 
+        self._host_pos = int(self.pos.item())
+        limit = self._pos_limit(self._host_pos)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         tok, pos = self.token.clone(), self.pos.clone()
         with torch.cuda.stream(side):
-            self._queue_step(int(side.cuda_stream))  # warm-up (also the library's one-time set-up)
+            self._queue_step(int(side.cuda_stream), limit)  # warm-up (also the library's one-time set-up)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self.token.copy_(tok)
         self.pos.copy_(pos)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self._queue_step(int(torch.cuda.current_stream().cuda_stream))
+            self._queue_step(int(torch.cuda.current_stream().cuda_stream), limit)
         torch.cuda.synchronize()
         self.token.copy_(tok)
         self.pos.copy_(pos)
-        self._graph = g
+        self._graphs[limit] = g
+
+    @property
+    def _graph(self):
+        return self._graphs.get(self._pos_limit(self._host_pos))
+
+    @_graph.setter
+    def _graph(self, value) -> None:
+        if value is None:
+            self._graphs.clear()
 
     def step(self) -> None:
         """One captured step: consumes self.token at self.pos, leaves the next
-        greedy token and pos + 1."""
+        greedy token and pos + 1.  The position is tracked on the host (set by
+        prefill, forward_token, the verify pass and the KV bookkeeping, read
+        back by capture()); a position set by writing self.pos directly needs
+        a capture() before the next step."""
         if self._graph is None:
             self.capture()
         self._graph.replay()
+        self._host_pos += 1
 
     # ------------------------------------------------------------ verify
     MAX_VERIFY_TOKENS = 16
@@ -297,6 +333,7 @@ class DecodeEngine:
                                                 _hip.ptr(v["work"]), _hip.stream_handle()),
                    "asdsl_decode_verify")
         self.pos.fill_(start_pos + n)
+        self._host_pos = start_pos + n
         self.kv_seq_len = max(self.kv_seq_len, start_pos + n)
         self._verify_n = n
         return v["logits"][:n]
@@ -323,6 +360,7 @@ class DecodeEngine:
                        "asdsl_kv_zero_from")
         self.kv_seq_len = new_len
         self.pos.fill_(new_len)
+        self._host_pos = new_len
 
     def snapshot_kv(self) -> None:
         """Push the committed KV length (unified_engine.cpp:1285-1287)."""

@@ -102,6 +102,14 @@ asdsl_status preq2_fused_combine(const uint8_t* meta, const uint8_t* quant, cons
                                  int nsplit, int split, int part_stride, int head_dim, int max_seq, int fold,
                                  asdsl_stream_t stream);
 
+// The decode step's first qkv GEMV: the RMSNorm prologue reads h as the fp16
+// embedding row of *token (row 0 for a token outside [0, vocab)), workgroup 0
+// stores h to h_out (fp32) and clears *clear_key (may be null).
+asdsl_status preq2_embed_rmsnorm(const uint8_t* meta, const uint8_t* quant, const uint16_t* embed, const int* token,
+                                 int vocab, const float* norm_w, float* h_out, float* y, int out_features,
+                                 int in_features, int group_size, float eps, unsigned long long* clear_key,
+                                 asdsl_stream_t stream);
+
 // Workgroups for a streaming kernel: enough tiles for every wave, capped at
 // `per_cu` workgroups per compute unit (waves then loop over tiles).
 inline int stream_grid(long long tiles, int waves_per_wg, int per_cu, int cus) {

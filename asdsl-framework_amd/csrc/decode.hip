@@ -9,11 +9,16 @@
 //   step keeps them fp16 (the decode workload's KV format); the current
 //   token's K/V are rounded to fp16 before use, as if read back from the cache.
 //
-// Per layer (6 launches): qkv GEMV with residual add + RMSNorm in its
-// prologue, attention partials, attention combine, o_proj GEMV, gate_up GEMV
-// with residual add + RMSNorm, down GEMV with SwiGLU in its prologue.  The
-// token id and position live in device memory, so a captured graph of one
-// step replays token after token with no host work.
+// Per layer: qkv GEMV with residual add + RMSNorm in its prologue (layer 0:
+// the embedding row itself), attention (RoPE, KV write, split partials),
+// o_proj GEMV (below 256 positions it merges the partials in its prologue;
+// beyond, a combine launch precedes it), gate_up GEMV with residual add +
+// RMSNorm in its prologue and SwiGLU in its epilogue, down GEMV.  Four
+// launches per layer at short context, five beyond; then lm_head with the
+// argmax and a one-thread finalize.  The token id and position live in
+// device memory, so a captured graph of one step replays token after token
+// with no host work.  The multi-token verify pass keeps a separate combine
+// launch.
 #include <hip/hip_fp16.h>
 
 #include "abi_util.hpp"
@@ -399,11 +404,335 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
     }
 }
 
+// ------------------------------------------------------------ decode attention
+// The short-context step's attention: workgroup (s, kvh) covers split s of
+// the KV head's positions, tps consecutive tiles of 64 positions (tps = 1
+// below 2048 positions), with the next tile's K/V rows requested before the
+// current tile is used and a running (max, sum, P.V) per wave; the four
+// waves merge in LDS and the partial (m, l, acc) of each query head is
+// stored for the o_proj GEMV's prologue, which merges the splits (at most
+// 4: positions below 256).  The launch covers only the splits of the
+// positions it serves; a position outside the cache gives zero output.
+constexpr int kMaxSplits = 32;
+constexpr int kTile = 64;
+
+__host__ __device__ inline int attn_tiles_per_split(int pos) {
+    const int nt = pos / kTile + 1;
+    return (nt + kMaxSplits - 1) / kMaxSplits;
+}
+
+__host__ __device__ inline int attn_nsplit(int pos) {
+    const int nt = pos / kTile + 1;
+    const int tps = attn_tiles_per_split(pos);
+    return (nt + tps - 1) / tps;
+}
+
+// Most splits any position below pos_limit uses (the launch's grid.x).
+int attn_max_splits(int pos_limit) {
+    int best = 1;
+    for (int nt = 1; (nt - 1) * kTile < pos_limit && nt <= kMaxSplits * 4; ++nt) {
+        const int tps = (nt + kMaxSplits - 1) / kMaxSplits;
+        best = max(best, (nt + tps - 1) / tps);
+    }
+    return best;
+}
+
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
+    const float* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
+    float* __restrict__ part, float* __restrict__ att, int n_heads, int n_kv, int max_seq, int rot_half) {
+    constexpr int kWaves = kAttnThreads / kWave;
+    constexpr int kIt = kTile / 16;
+    __shared__ float q_s[G][kHeadDim];
+    __shared__ float kv_new[2][kHeadDim];
+    __shared__ float wml[kWaves][G][2];
+    __shared__ float wacc[kWaves][G][kHeadDim];
+    const int s = static_cast<int>(blockIdx.x);
+    const int kvh = static_cast<int>(blockIdx.y);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int pos = *pos_ptr;
+    if (pos < 0 || pos >= max_seq) {  // outside the cache: zero output, nothing written to the cache
+        if (s == 0)
+            for (int e = tid; e < G * kHeadDim; e += kAttnThreads) att[static_cast<size_t>(kvh * G) * kHeadDim + e] = 0.0f;
+        return;
+    }
+    const int tps = attn_tiles_per_split(pos);
+    const int ns = attn_nsplit(pos);
+    if (s >= ns) return;
+    const int p0 = s * tps * kTile;
+    const int p1 = min(p0 + tps * kTile, pos + 1);
+    const int lane = tid & (kWave - 1);
+    const int wave = tid >> 6;
+    const int pg = lane >> 4;   // position within the wave's four
+    const int dc = lane & 15;   // 8-dim chunk
+    const size_t head_base = static_cast<size_t>(kvh) * max_seq * kHeadDim;
+
+    // RoPE inputs of the G query heads and the new key (small, first), then
+    // the first tile's K/V rows: loads complete in issue order.
+    const float* cp = rope_cos + static_cast<size_t>(pos) * rot_half;
+    const float* sp = rope_sin + static_cast<size_t>(pos) * rot_half;
+    constexpr int kRope = ((G + 1) * kHeadDim + kAttnThreads - 1) / kAttnThreads;
+    float rx[kRope][4];
+#pragma unroll
+    for (int r = 0; r < kRope; ++r) {
+        const int e = tid + r * kAttnThreads;
+        const int hh = e / kHeadDim;
+        const int d = e % kHeadDim;
+        if (hh <= G) {
+            const float* src = hh < G ? qkv + static_cast<size_t>(kvh * G + hh) * kHeadDim
+                                      : qkv + static_cast<size_t>(n_heads + kvh) * kHeadDim;
+            if (d < 2 * rot_half) {
+                const int i = d < rot_half ? d : d - rot_half;
+                rx[r][0] = src[i];
+                rx[r][1] = src[i + rot_half];
+                rx[r][2] = cp[i];
+                rx[r][3] = sp[i];
+            } else {
+                rx[r][0] = src[d];
+            }
+        }
+    }
+    const float* vsrc = qkv + static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim;
+    const float vnew = tid < kHeadDim ? vsrc[tid] : 0.0f;
+
+    // Unconditional loads (positions past the split read the split's first
+    // row; the row at `pos` is taken from LDS): no branch around a load, so
+    // the rows stay in registers with every load in flight.
+    auto load_tile = [&](int t0, uint4 (&kraw)[kIt], uint4 (&vraw)[kIt]) {
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int p = t0 + wave * 4 + pg + 16 * it;
+            const size_t at = head_base + static_cast<size_t>(p < p1 ? p : p0) * kHeadDim + 8 * dc;
+            kraw[it] = *reinterpret_cast<const uint4*>(kc + at);
+            vraw[it] = *reinterpret_cast<const uint4*>(vc + at);
+        }
+    };
+    uint4 ka[kIt], va[kIt], kb[kIt], vb[kIt];
+    load_tile(p0, ka, va);
+
+#pragma unroll
+    for (int r = 0; r < kRope; ++r) {
+        const int e = tid + r * kAttnThreads;
+        const int hh = e / kHeadDim;
+        const int d = e % kHeadDim;
+        if (hh <= G) {
+            float val;
+            if (d < 2 * rot_half) {
+                const float xf = rx[r][0], xs = rx[r][1], c = rx[r][2], sn = rx[r][3];
+                val = d < rot_half ? fmaf(xf, c, -(xs * sn)) : fmaf(xf, sn, xs * c);
+            } else {
+                val = rx[r][0];
+            }
+            if (hh < G) q_s[hh][d] = val;
+            else kv_new[0][d] = h2f(f2h(val));
+        }
+    }
+    if (tid < kHeadDim) kv_new[1][tid] = h2f(f2h(vnew));
+    __syncthreads();
+    if (pos >= p0 && pos < p1 && tid < kHeadDim) {
+        kc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
+        vc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[1][tid]);
+    }
+    float qr[G][8];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
+
+    // running state of this wave: max (uniform), and this lane's share of
+    // the exp-sum and of P.V (its 8 dims, its positions)
+    const float inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(kHeadDim));
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+        m[hh] = -INFINITY;
+        l[hh] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[hh][e] = 0.0f;
+    }
+    auto row_of = [&](const uint4& raw, int which, int p, float (&r)[8]) {
+        if (p == pos) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) r[e] = kv_new[which][8 * dc + e];
+        } else {
+            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                r[2 * e] = h2f(static_cast<uint16_t>(w[e] & 0xFFFFu));
+                r[2 * e + 1] = h2f(static_cast<uint16_t>(w[e] >> 16));
+            }
+        }
+    };
+    auto process_tile = [&](int t0, const uint4 (&kraw)[kIt], const uint4 (&vraw)[kIt]) {
+        float sr[kIt][G];
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int p = t0 + wave * 4 + pg + 16 * it;
+            float k8[8];
+            row_of(kraw[it], 0, p, k8);
+#pragma unroll
+            for (int hh = 0; hh < G; ++hh) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf(qr[hh][e], k8[e], d);
+                d += dpp<kDppQuadXor1>(d);  // sum over the 16 lanes of the position
+                d += dpp<kDppQuadXor2>(d);
+                d += dpp<kDppRowRor4>(d);
+                d += dpp<kDppRowRor8>(d);
+                sr[it][hh] = p < p1 ? d * inv_sqrt_d : -INFINITY;
+            }
+        }
+        float mn[G], rs[G];
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh) {
+            float v = sr[0][hh];
+#pragma unroll
+            for (int it = 1; it < kIt; ++it) v = fmaxf(v, sr[it][hh]);
+            v = fmaxf(v, swz_xor16(v));
+            v = fmaxf(v, __shfl_xor(v, 32, kWave));
+            mn[hh] = fmaxf(m[hh], v);
+            rs[hh] = m[hh] == -INFINITY ? 0.0f : expf(m[hh] - mn[hh]);
+            m[hh] = mn[hh];
+            l[hh] *= rs[hh];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[hh][e] *= rs[hh];
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int p = t0 + wave * 4 + pg + 16 * it;
+            float v8[8];
+            row_of(vraw[it], 1, p, v8);
+#pragma unroll
+            for (int hh = 0; hh < G; ++hh) {
+                const float w = p < p1 ? expf(sr[it][hh] - m[hh]) : 0.0f;
+                l[hh] += w;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[hh][e] = fmaf(w, v8[e], acc[hh][e]);
+            }
+        }
+    };
+    for (int t = p0; t < p1; t += 2 * kTile) {  // uniform per workgroup
+        if (t + kTile < p1) load_tile(t + kTile, kb, vb);
+        process_tile(t, ka, va);
+        if (t + kTile >= p1) break;
+        if (t + 2 * kTile < p1) load_tile(t + 2 * kTile, ka, va);
+        process_tile(t + kTile, kb, vb);
+    }
+
+    // the wave's sums over its four position groups, then the four waves
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+        l[hh] += swz_xor16(l[hh]);
+        l[hh] += __shfl_xor(l[hh], 32, kWave);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            acc[hh][e] += swz_xor16(acc[hh][e]);
+            acc[hh][e] += __shfl_xor(acc[hh][e], 32, kWave);
+        }
+    }
+    if (pg == 0) {
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wacc[wave][hh][8 * dc + e] = acc[hh][e];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh) {
+            wml[wave][hh][0] = m[hh];
+            wml[wave][hh][1] = l[hh];
+        }
+    }
+    __syncthreads();
+    float* pbase = part + static_cast<size_t>(kvh * G) * kMaxSplits * kPartStride;
+    for (int e = tid; e < G * kHeadDim; e += kAttnThreads) {
+        const int hh = e / kHeadDim;
+        const int d = e % kHeadDim;
+        float M = wml[0][hh][0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][hh][0]);
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = wml[w][hh][0];
+            sum = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wacc[w][hh][d], sum);
+        }
+        pbase[(static_cast<size_t>(hh) * kMaxSplits + s) * kPartStride + 2 + d] = sum;
+    }
+    if (tid < G) {
+        float M = wml[0][tid][0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][tid][0]);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = wml[w][tid][0];
+            L = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wml[w][tid][1], L);
+        }
+        float* dst = pbase + (static_cast<size_t>(tid) * kMaxSplits + s) * kPartStride;
+        dst[0] = M;
+        dst[1] = L;
+    }
+}
+
+int attn_splits(int max_seq);
+asdsl_status launch_attention(const float* qkv, uint16_t* kc, uint16_t* vc, const float* rc, const float* rs,
+                              const int* pos, float* att, float* part, int n_heads, int n_kv, int rot_half,
+                              int max_seq, hipStream_t s, int fold);
+
+// Floats of the decode attention's work area: kMaxSplits partial rows per
+// query head for the short-context form, then the partial rows of the
+// general form (one per 64 positions of max_seq).
+size_t attn_decode_work_floats(int n_heads, int max_seq) {
+    return static_cast<size_t>(n_heads) * kMaxSplits * kPartStride +
+           static_cast<size_t>(n_heads) * attn_splits(max_seq) * kPartStride;
+}
+
+// Positions below pos_limit take the short-context form when they use at
+// most kMaxFold (4) splits: the o_proj GEMV's prologue merges them, no
+// combine launch.  Otherwise the partial kernel over 64-position splits and
+// the combine kernel (up to eight groups of threads folding runs of splits
+// in parallel).  Merging in the attention kernel's last workgroup instead
+// (device-coherent partial stores, an atomic count, device-coherent loads)
+// measured slower than the combine launch: 13.2 us per layer at ctx 1024
+// against 8.0 + 4.0.
+bool attn_fold(int pos_limit, int max_seq) {
+    return attn_max_splits(pos_limit < max_seq ? pos_limit : max_seq) <= 4;
+}
+
+// work: attn_decode_work_floats.  fold: the short-context form (partials at
+// work, kMaxSplits rows per head, for the o_proj prologue); otherwise att
+// receives the merged output.
+asdsl_status launch_attention_decode(const float* qkv, uint16_t* kc, uint16_t* vc, const float* rc, const float* rs,
+                                     const int* pos, float* att, float* work, int n_heads, int n_kv, int rot_half,
+                                     int max_seq, int pos_limit, bool fold, hipStream_t s) {
+    const int G = n_heads / n_kv;
+    if (!fold)
+        return launch_attention(qkv, kc, vc, rc, rs, pos, att, work + static_cast<size_t>(n_heads) * kMaxSplits *
+                                kPartStride, n_heads, n_kv, rot_half, max_seq, s, 0);
+    const dim3 grid(attn_max_splits(pos_limit < max_seq ? pos_limit : max_seq), n_kv);
+#define ASDSL_ATTN_CASE(GG)                                                                                  \
+    case GG:                                                                                                \
+        return launch("attn_decode_kernel", attn_decode_kernel<GG>, grid, dim3(kAttnThreads), 0, s, qkv, kc, vc, \
+                      rc, rs, pos, work, att, n_heads, n_kv, max_seq, rot_half);
+    switch (G) {
+        ASDSL_ATTN_CASE(1)
+        ASDSL_ATTN_CASE(2)
+        ASDSL_ATTN_CASE(3)
+        ASDSL_ATTN_CASE(4)
+        default:
+            set_error("attention: n_heads / n_kv_heads must be 1..4");
+            return ASDSL_ERR_UNSUPPORTED;
+    }
+#undef ASDSL_ATTN_CASE
+}
+
 int attn_splits(int max_seq) { return (max_seq + kSplit - 1) / kSplit; }
 
 asdsl_status launch_attention(const float* qkv, uint16_t* kc, uint16_t* vc, const float* rc, const float* rs,
                               const int* pos, float* att, float* part, int n_heads, int n_kv, int rot_half,
-                              int max_seq, hipStream_t s, int fold = 0) {
+                              int max_seq, hipStream_t s, int fold) {
     const int nsplit = attn_splits(max_seq);
     const int G = n_heads / n_kv;
     asdsl_status st;
@@ -445,7 +774,7 @@ DecodeWork decode_work(const asdsl_decode_model& m) {
     w.o = take(m.hidden);
     w.gu = take(2 * static_cast<size_t>(m.ffn));
     w.down = take(m.hidden);
-    w.part = take(static_cast<size_t>(m.n_heads) * attn_splits(m.max_seq) * kPartStride);
+    w.part = take(attn_decode_work_floats(m.n_heads, m.max_seq));
     w.amax = take(2);
     w.total = at;
     return w;
@@ -740,9 +1069,13 @@ extern "C" asdsl_status asdsl_gemv_preq2_rmsnorm(const uint8_t* meta, const uint
 extern "C" asdsl_status asdsl_gemv_preq2_swiglu(const uint8_t* meta, const uint8_t* quant, const float* gate_up,
                                                 float* y, int out_features, int in_features, int group_size,
                                                 float threshold, asdsl_stream_t stream);
+extern "C" asdsl_status asdsl_gemv_preq2_rmsnorm_swiglu(const uint8_t* meta, const uint8_t* quant, const float* h_in,
+                                                        const float* delta, const float* norm_w, float* h_out,
+                                                        float* s_out, int ffn, int in_features, int group_size,
+                                                        float eps, float threshold, asdsl_stream_t stream);
 
 extern "C" size_t asdsl_attention_work_floats(int n_heads, int max_seq) {
-    return static_cast<size_t>(n_heads) * attn_splits(max_seq) * kPartStride;
+    return n_heads > 0 && max_seq > 0 ? attn_decode_work_floats(n_heads, max_seq) : 0;
 }
 
 extern "C" asdsl_status asdsl_attention_f16kv(const float* qkv, uint16_t* k_cache, uint16_t* v_cache,
@@ -759,8 +1092,8 @@ extern "C" asdsl_status asdsl_attention_f16kv(const float* qkv, uint16_t* k_cach
     ASDSL_CHECK_ARG(max_seq > 0, "attention_f16kv: max_seq must be positive");
     ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && reinterpret_cast<uintptr_t>(v_cache) % 16 == 0,
                     "attention_f16kv: caches must be 16-byte aligned");
-    return launch_attention(qkv, k_cache, v_cache, rope_cos, rope_sin, pos, att_out, work, n_heads, n_kv_heads,
-                            rotary_dim / 2, max_seq, as_hip(stream));
+    return launch_attention_decode(qkv, k_cache, v_cache, rope_cos, rope_sin, pos, att_out, work, n_heads, n_kv_heads,
+                                   rotary_dim / 2, max_seq, max_seq, false, as_hip(stream));
 }
 
 extern "C" size_t asdsl_decode_work_bytes(const asdsl_decode_model* model) {
@@ -768,11 +1101,12 @@ extern "C" size_t asdsl_decode_work_bytes(const asdsl_decode_model* model) {
     return decode_work(*model).total * sizeof(float);
 }
 
-extern "C" asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int* pos, float* logits,
-                                           void* work, asdsl_stream_t stream) {
+extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model, int* token, int* pos, int pos_limit,
+                                                float* logits, void* work, asdsl_stream_t stream) {
     const asdsl_status cs = check_model(model);
     if (cs != ASDSL_OK) return cs;
     ASDSL_CHECK_ARG(token && pos && logits && work, "decode_token: null pointer");
+    ASDSL_CHECK_ARG(pos_limit > 0, "decode_token: pos_limit must be positive");
     ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(work) % 256 == 0, "decode_token: work must be 256-byte aligned");
     const asdsl_decode_model& m = *model;
     const DecodeWork w = decode_work(m);
@@ -789,15 +1123,23 @@ extern "C" asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int*
     hipStream_t s = as_hip(stream);
     const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
     const int q_dim = m.n_heads * m.head_dim;
-    // Positions with at most 4 attention splits (256 positions) skip the
-    // combine kernel's work: o_proj's prologue merges the splits itself
-    // (same bits).  ASDSL_HIP_NO_COMBINE_FOLD=1 keeps the combine kernel.
+    // The attention form follows pos_limit (attn_fold): below 256 o_proj's
+    // prologue merges the splits, beyond the combine kernel does.
+    // ASDSL_HIP_NO_COMBINE_FOLD=1 always takes the combine kernel.
     static const int no_fold = env_knob("ASDSL_HIP_NO_COMBINE_FOLD");
-    const int fold = no_fold > 0 ? 0 : 4;
+    const int limit = pos_limit < m.max_seq ? pos_limit : m.max_seq;
+    const bool fold = no_fold == 0 && attn_fold(limit, m.max_seq);
 
-    asdsl_status st = launch("embed_kernel", embed_kernel, dim3((m.hidden + 1023) / 1024), dim3(256), 0, s,
-                             m.embed, static_cast<const int*>(token), hA, m.hidden, m.vocab, amax);
-    if (st != ASDSL_OK) return st;
+    // Layer 0's qkv GEMV reads the embedding row itself (and stores it to hA,
+    // clearing the argmax key) when the table is 16-byte aligned; otherwise
+    // embed_kernel does that first.
+    const bool embed_fold = reinterpret_cast<uintptr_t>(m.embed) % 16 == 0;
+    asdsl_status st = ASDSL_OK;
+    if (!embed_fold) {
+        st = launch("embed_kernel", embed_kernel, dim3((m.hidden + 1023) / 1024), dim3(256), 0, s, m.embed,
+                    static_cast<const int*>(token), hA, m.hidden, m.vocab, amax);
+        if (st != ASDSL_OK) return st;
+    }
     // The residual stream enters layer l in `cur`; layer l > 0 adds the
     // previous down output in its qkv prologue and writes the sum to `nxt`.
     float* cur = hA;
@@ -808,23 +1150,36 @@ extern "C" asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int*
             st = asdsl_gemv_preq2_rmsnorm(L.qkv_meta, L.qkv_quant, cur, down, L.rms_att, nxt, qkv, qkv_dim,
                                           m.hidden, m.gs_attn, m.rms_eps, nullptr, stream);
             std::swap(cur, nxt);
+        } else if (embed_fold) {
+            st = preq2_embed_rmsnorm(L.qkv_meta, L.qkv_quant, m.embed, static_cast<const int*>(token), m.vocab,
+                                     L.rms_att, hA, qkv, qkv_dim, m.hidden, m.gs_attn, m.rms_eps, amax, stream);
         } else {
             st = asdsl_gemv_preq2_rmsnorm(L.qkv_meta, L.qkv_quant, cur, nullptr, L.rms_att, nullptr, qkv, qkv_dim,
                                           m.hidden, m.gs_attn, m.rms_eps, nullptr, stream);
         }
         if (st != ASDSL_OK) return st;
-        st = launch_attention(qkv, L.k_cache, L.v_cache, m.rope_cos, m.rope_sin, pos, att, part, m.n_heads,
-                              m.n_kv_heads, m.rotary_dim / 2, m.max_seq, s, fold);
+        st = launch_attention_decode(qkv, L.k_cache, L.v_cache, m.rope_cos, m.rope_sin, pos, att, part, m.n_heads,
+                                     m.n_kv_heads, m.rotary_dim / 2, m.max_seq, limit, fold, s);
         if (st != ASDSL_OK) return st;
-        st = preq2_fused_combine(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, part, pos,
-                                 attn_splits(m.max_seq), kSplit, kPartStride, kHeadDim, m.max_seq, fold, stream);
+        st = fold ? preq2_fused_combine(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, part, pos, kMaxSplits,
+                                        kTile, kPartStride, kHeadDim, m.max_seq, 4, stream)
+                  : asdsl_gemv_preq2_fused(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, stream);
         if (st != ASDSL_OK) return st;
-        st = asdsl_gemv_preq2_rmsnorm(L.gu_meta, L.gu_quant, cur, o, L.rms_ffn, nxt, gu, 2 * m.ffn, m.hidden,
-                                      m.gs_ffn, m.rms_eps, nullptr, stream);
-        if (st != ASDSL_OK) return st;
-        std::swap(cur, nxt);
-        st = asdsl_gemv_preq2_swiglu(L.down_meta, L.down_quant, gu, down, m.hidden, m.ffn, m.gs_ffn,
-                                     L.fatrelu_threshold, stream);
+        // gate_up with SwiGLU in its epilogue (gate and up rows in one
+        // workgroup), down on the result; the SwiGLU prologue form otherwise
+        st = asdsl_gemv_preq2_rmsnorm_swiglu(L.gu_meta, L.gu_quant, cur, o, L.rms_ffn, nxt, gu, m.ffn, m.hidden,
+                                             m.gs_ffn, m.rms_eps, L.fatrelu_threshold, stream);
+        if (st == ASDSL_OK) {
+            std::swap(cur, nxt);
+            st = asdsl_gemv_preq2_fused(L.down_meta, L.down_quant, gu, down, m.hidden, m.ffn, m.gs_ffn, stream);
+        } else if (st == ASDSL_ERR_UNSUPPORTED) {
+            st = asdsl_gemv_preq2_rmsnorm(L.gu_meta, L.gu_quant, cur, o, L.rms_ffn, nxt, gu, 2 * m.ffn, m.hidden,
+                                          m.gs_ffn, m.rms_eps, nullptr, stream);
+            if (st != ASDSL_OK) return st;
+            std::swap(cur, nxt);
+            st = asdsl_gemv_preq2_swiglu(L.down_meta, L.down_quant, gu, down, m.hidden, m.ffn, m.gs_ffn,
+                                         L.fatrelu_threshold, stream);
+        }
         if (st != ASDSL_OK) return st;
     }
     st = asdsl_gemv_preq2_rmsnorm(m.lm_meta, m.lm_quant, cur, down, m.rms_out, nullptr, logits, m.vocab, m.hidden,
@@ -832,6 +1187,11 @@ extern "C" asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int*
     if (st != ASDSL_OK) return st;
     return launch("finalize_kernel", finalize_kernel, dim3(1), dim3(64), 0, s,
                   static_cast<const unsigned long long*>(amax), token, pos);
+}
+
+extern "C" asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int* pos, float* logits,
+                                           void* work, asdsl_stream_t stream) {
+    return asdsl_decode_token_upto(model, token, pos, model ? model->max_seq : 1, logits, work, stream);
 }
 
 extern "C" size_t asdsl_decode_verify_work_bytes(const asdsl_decode_model* model, int max_tokens) {

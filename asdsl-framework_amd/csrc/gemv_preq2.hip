@@ -59,7 +59,11 @@ constexpr int kThreads = 256;  // helper kernels
 //            atomicMax: key = order-preserving float bits << 32 | ~row, so the
 //            result does not depend on workgroup order.  *amax must be zero
 //            before the launch.
-enum class Pro { kPlain, kNorm, kSwiglu, kCombine };
+//   kNormEmbed: kNorm whose h is the fp16 embedding row of *pa.token (a
+//            token outside [0, vocab) reads row 0), converted to fp32;
+//            workgroup 0 stores h to h_out and clears *pa.amax (the step's
+//            argmax key) (load_embed_row_f32, unified_engine.cpp:181-197).
+enum class Pro { kPlain, kNorm, kSwiglu, kCombine, kNormEmbed };
 
 constexpr int kMaxFold = 4;  // kCombine: most splits merged in the prologue
 
@@ -76,6 +80,13 @@ struct ProArgs {
     const float* part = nullptr;
     const int* pos = nullptr;
     int nsplit = 0, split = 0, part_stride = 0, head_dim = 0, max_seq = 0, fold = 0;
+    // SWIGLU_EPI: the output rows are [gate F | up F] with F = 4 * fbands;
+    // y receives swiglu(gate, up) (F values, pa.thr applies)
+    int fbands = 0;
+    // kNormEmbed: fp16 embedding table [vocab][K] and the token id (device)
+    const uint16_t* embed = nullptr;
+    const int* token = nullptr;
+    int vocab = 0;
 };
 
 template <int WAVES>
@@ -92,7 +103,7 @@ __device__ __forceinline__ float block_sum_fixed(float v, float* s_red) {
 }
 
 template <int GS, int NU, int WAVES, int NCH, bool Q8, bool EXACT, bool XREG, Pro PRO = Pro::kPlain,
-          bool ARGMAX = false>
+          bool ARGMAX = false, bool SWIGLU_EPI = false>
 __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_t* __restrict__ meta,
                                                                   const uint4* __restrict__ quant,
                                                                   const float* __restrict__ x,
@@ -115,7 +126,15 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     const int bl = wave >> lks;
     const int bpt = WAVES >> lks;      // bands per tile
     const int nbands = (M + 3) >> 2;
-    const int ntiles = (nbands + bpt - 1) / bpt;
+    // SWIGLU_EPI (KS = 1): tile t pairs gate bands t*h .. t*h+h-1 (waves
+    // 0..h-1) with the up bands fbands + t*h .. (waves h..2h-1), h = bpt/2,
+    // so every gate row meets its up row in the workgroup
+    const int hpt = bpt >> 1;
+    const int ntiles = SWIGLU_EPI ? (pa.fbands + hpt - 1) / hpt : (nbands + bpt - 1) / bpt;
+    auto band_of = [&](int t) {
+        if constexpr (SWIGLU_EPI) return bl < hpt ? t * hpt + bl : pa.fbands + t * hpt + (bl - hpt);
+        else return t * bpt + bl;
+    };
     const int upb = K >> 3;            // units per band
     const int c0 = ks * (NU * kWave) + lane;
     const int part = lane % UPS;
@@ -138,7 +157,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     // Loads are unconditional at in-bounds indices; values of rows >= M
     // (tail band) are never stored.
     auto load_tile = [&](int tile) {
-        const int band = min(tile * bpt + bl, nbands - 1);
+        const int band = min(band_of(tile), nbands - 1);
         const uint4* qb = quant + static_cast<size_t>(band) * upb;
         const int row = min(band * 4 + slot, M - 1);
         const uint32_t* mrow = meta + static_cast<size_t>(row) * G;
@@ -192,23 +211,41 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
             }
         }
     }
-    if (fns == 0) act.load(x, xq8, xsc, K);  // activation loads first: they retire first
+    constexpr bool kNormed = PRO == Pro::kNorm || PRO == Pro::kNormEmbed;
+    if constexpr (PRO == Pro::kNormEmbed) {  // the embedding row, fp16 -> fp32
+        const int t0 = *pa.token;
+        const int t = t0 >= 0 && t0 < pa.vocab ? t0 : 0;
+        const uint4* row = reinterpret_cast<const uint4*>(pa.embed + static_cast<size_t>(t) * K);
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const uint4 u = row[min(i * WAVES * kWave + tid, nchunk - 1)];
+            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                act.v[i][2 * e] = half_bits_to_float(w4[e]);
+                act.v[i][2 * e + 1] = half_bits_to_float(w4[e] >> 16);
+            }
+        }
+        if (blockIdx.x == 0 && tid == 0 && pa.amax) *pa.amax = 0ull;
+    } else if (fns == 0) {
+        act.load(x, xq8, xsc, K);  // activation loads first: they retire first
+    }
     constexpr int NX = PRO == Pro::kPlain || PRO == Pro::kCombine ? 1 : NCH;
     float ex[NX][8], ew[NX][8];  // kNorm: delta, norm weight; kSwiglu: up
-    if constexpr (PRO == Pro::kNorm || PRO == Pro::kSwiglu) {
+    if constexpr (kNormed || PRO == Pro::kSwiglu) {
 #pragma unroll
         for (int i = 0; i < NCH; ++i) {
             const int c = min(i * WAVES * kWave + tid, nchunk - 1);
-            const float* src0 = PRO == Pro::kNorm ? pa.delta : pa.up;
+            const float* src0 = kNormed ? pa.delta : pa.up;
 #pragma unroll
             for (int e = 0; e < 8; ++e) ex[i][e] = 0.0f;
-            if (src0) {
+            if (PRO != Pro::kNormEmbed && src0) {
                 const float4 a = reinterpret_cast<const float4*>(src0)[2 * c];
                 const float4 b = reinterpret_cast<const float4*>(src0)[2 * c + 1];
                 ex[i][0] = a.x; ex[i][1] = a.y; ex[i][2] = a.z; ex[i][3] = a.w;
                 ex[i][4] = b.x; ex[i][5] = b.y; ex[i][6] = b.z; ex[i][7] = b.w;
             }
-            if constexpr (PRO == Pro::kNorm) {
+            if constexpr (kNormed) {
                 const float4 a = reinterpret_cast<const float4*>(pa.nw)[2 * c];
                 const float4 b = reinterpret_cast<const float4*>(pa.nw)[2 * c + 1];
                 ew[i][0] = a.x; ew[i][1] = a.y; ew[i][2] = a.z; ew[i][3] = a.w;
@@ -225,7 +262,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     // outstanding.
     if constexpr (WAVES == 16) __syncthreads();
     load_tile(tile);           // grid <= ntiles, so this tile exists
-    if constexpr (PRO == Pro::kNorm) {
+    if constexpr (kNormed) {
         __shared__ float s_red[WAVES];
         float ss = 0.0f;
 #pragma unroll
@@ -319,13 +356,22 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
                 acc = fmaf(-(z * s), XREG ? xu[jj] : us, acc);
             }
         }
-        const int band = tile * bpt + bl;
+        const int band = band_of(tile);
         acc = slot_sum<SB>(acc);
         // next tile's loads after the reduction: issuing them before it keeps
         // ~20 more VGPRs live (measured), costing a workgroup per CU at NU=6
         if (tile + tile_step < ntiles) load_tile(tile + tile_step);
         const int row = band * 4 + slot;
-        if (lks == 0) {
+        if constexpr (SWIGLU_EPI) {
+            // the up waves hand their rows to the gate waves through LDS (two
+            // buffers by tile parity: one barrier per tile suffices)
+            __shared__ float s_up[2][WAVES / 2][4];
+            if (bl >= hpt && writer) s_up[parity][bl - hpt][slot] = acc;
+            __syncthreads();
+            if (bl < hpt && writer && band < pa.fbands)
+                y[row] = swiglu_ref(acc, s_up[parity][bl][slot], pa.thr);
+            parity ^= 1;
+        } else if (lks == 0) {
             if (writer && band < nbands && row < M) {
                 y[row] = acc;
                 if constexpr (ARGMAX) best = max(best, argmax_key(acc, row));
@@ -500,15 +546,16 @@ Plan plan_preq2(int M, int K, int cus) {
     return p;
 }
 
-template <int GS, int WAVES, int NCH, bool Q8, bool EXACT, Pro PRO = Pro::kPlain, bool ARGMAX = false>
+template <int GS, int WAVES, int NCH, bool Q8, bool EXACT, Pro PRO = Pro::kPlain, bool ARGMAX = false,
+          bool SWI = false>
 asdsl_status launch_exact(const Plan& p, const uint32_t* m, const uint4* q, const float* x, const int8_t* xq8,
                           const float* xsc, float* y, int M, int K, hipStream_t stream, const ProArgs& pa = ProArgs{}) {
     constexpr bool XREG = true;
     const size_t lds = x_image_bytes(K, GS);
     const dim3 block(WAVES * kWave);
-#define ASDSL_PREQ2_NU(N)                                                                                       \
-    case N:                                                                                                     \
-        return launch("preq2_gemv_kernel", preq2_gemv_kernel<GS, N, WAVES, NCH, Q8, EXACT, XREG, PRO, ARGMAX>,   \
+#define ASDSL_PREQ2_NU(N)                                                                                         \
+    case N:                                                                                                       \
+        return launch("preq2_gemv_kernel", preq2_gemv_kernel<GS, N, WAVES, NCH, Q8, EXACT, XREG, PRO, ARGMAX, SWI>, \
                       dim3(p.grid), block, lds, stream, m, q, x, xq8, xsc, y, M, K, p.lks, pa);
     switch (p.nu) {
         ASDSL_PREQ2_NU(1)
@@ -526,6 +573,34 @@ asdsl_status launch_waves(const Plan& p, const uint32_t* m, const uint4* q, cons
                           const float* xsc, float* y, int M, int K, hipStream_t stream, const ProArgs& pa = ProArgs{}) {
     if (p.exact) return launch_exact<GS, WAVES, NCH, Q8, true, PRO, ARGMAX>(p, m, q, x, xq8, xsc, y, M, K, stream, pa);
     return launch_exact<GS, WAVES, NCH, Q8, false, PRO, ARGMAX>(p, m, q, x, xq8, xsc, y, M, K, stream, pa);
+}
+
+// gate_up with the residual add + RMSNorm prologue and the SwiGLU epilogue:
+// rows [gate F | up F] -> y[F] = swiglu(gate, up).  Needs one wave per band
+// (KS = 1) and F/4 divisible by half the bands of a tile; returns
+// ASDSL_ERR_UNSUPPORTED (nothing launched) otherwise.
+template <int GS>
+asdsl_status launch_gateup_swiglu(const uint8_t* meta, const uint8_t* quant, const float* x, float* y, int F, int K,
+                                  ProArgs pa, hipStream_t stream, int cus) {
+    Plan p = plan_preq2(2 * F, K, cus);
+    const int hpt = (p.waves >> p.lks) / 2;
+    if (p.lks != 0 || hpt < 1 || F % 4 != 0 || (F / 4) % hpt != 0) return ASDSL_ERR_UNSUPPORTED;
+    pa.fbands = F / 4;
+    const int tiles = (F / 4) / hpt;
+    const int cap = cus * (32 / p.waves);
+    p.grid = tiles < cap ? tiles : cap;
+    const auto* m = reinterpret_cast<const uint32_t*>(meta);
+    const auto* q = reinterpret_cast<const uint4*>(quant);
+    if (p.waves == 8) {
+        return p.exact ? launch_exact<GS, 8, 1, false, true, Pro::kNorm, false, true>(p, m, q, x, nullptr, nullptr, y,
+                                                                                       2 * F, K, stream, pa)
+                       : launch_exact<GS, 8, 1, false, false, Pro::kNorm, false, true>(p, m, q, x, nullptr, nullptr,
+                                                                                        y, 2 * F, K, stream, pa);
+    }
+    return p.exact ? launch_exact<GS, 16, 1, false, true, Pro::kNorm, false, true>(p, m, q, x, nullptr, nullptr, y,
+                                                                                    2 * F, K, stream, pa)
+                   : launch_exact<GS, 16, 1, false, false, Pro::kNorm, false, true>(p, m, q, x, nullptr, nullptr, y,
+                                                                                     2 * F, K, stream, pa);
 }
 
 // Decode-step variants (fp32 activation, one chunk per thread: K <= 8192).
@@ -595,6 +670,31 @@ extern "C" asdsl_status asdsl_gemv_preq2_rmsnorm(const uint8_t* meta, const uint
                       : launch_preq2_fused<128, Pro::kNorm, false>(meta, quant, h_in, y, M, K, pa, s, cus);
 }
 
+asdsl_status asdsl::preq2_embed_rmsnorm(const uint8_t* meta, const uint8_t* quant, const uint16_t* embed,
+                                        const int* token, int vocab, const float* norm_w, float* h_out, float* y,
+                                        int out_features, int in_features, int group_size, float eps,
+                                        unsigned long long* clear_key, asdsl_stream_t stream) {
+    if (check_preq2_args(meta, quant, embed, y, out_features, in_features, group_size, "gemv_preq2_embed_rmsnorm"))
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    ASDSL_CHECK_ARG(norm_w && token && h_out && vocab > 0, "gemv_preq2_embed_rmsnorm: null pointer");
+    ASDSL_CHECK_ARG(in_features <= 8192 && in_features % 8 == 0 && reinterpret_cast<uintptr_t>(embed) % 16 == 0,
+                    "gemv_preq2_embed_rmsnorm: in_features must be <= 8192 and the table 16-byte aligned");
+    ASDSL_CU_COUNT(cus);
+    ProArgs pa;
+    pa.nw = norm_w;
+    pa.h_out = h_out;
+    pa.eps = eps;
+    pa.amax = clear_key;
+    pa.embed = embed;
+    pa.token = token;
+    pa.vocab = vocab;
+    hipStream_t s = as_hip(stream);
+    const float* none = nullptr;
+    if (group_size == 32)
+        return launch_preq2_fused<32, Pro::kNormEmbed, false>(meta, quant, none, y, out_features, in_features, pa, s, cus);
+    return launch_preq2_fused<128, Pro::kNormEmbed, false>(meta, quant, none, y, out_features, in_features, pa, s, cus);
+}
+
 asdsl_status asdsl::preq2_fused_combine(const uint8_t* meta, const uint8_t* quant, const float* att, float* y,
                                         int out_features, int in_features, int group_size, const float* part,
                                         const int* pos, int nsplit, int split, int part_stride, int head_dim,
@@ -620,6 +720,32 @@ asdsl_status asdsl::preq2_fused_combine(const uint8_t* meta, const uint8_t* quan
     if (group_size == 32)
         return launch_preq2_fused<32, Pro::kCombine, false>(meta, quant, att, y, out_features, in_features, pa, s, cus);
     return launch_preq2_fused<128, Pro::kCombine, false>(meta, quant, att, y, out_features, in_features, pa, s, cus);
+}
+
+extern "C" asdsl_status asdsl_gemv_preq2_rmsnorm_swiglu(const uint8_t* meta, const uint8_t* quant, const float* h_in,
+                                                        const float* delta, const float* norm_w, float* h_out,
+                                                        float* s_out, int ffn, int in_features, int group_size,
+                                                        float eps, float threshold, asdsl_stream_t stream) {
+    if (check_preq2_args(meta, quant, h_in, s_out, 2 * ffn, in_features, group_size, "gemv_preq2_rmsnorm_swiglu"))
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    ASDSL_CHECK_ARG(norm_w != nullptr, "gemv_preq2_rmsnorm_swiglu: null norm weight");
+    ASDSL_CHECK_ARG(in_features <= 8192, "gemv_preq2_rmsnorm_swiglu: in_features must be <= 8192");
+    ASDSL_CHECK_ARG(ffn > 0 && ffn % 16 == 0, "gemv_preq2_rmsnorm_swiglu: ffn must be a positive multiple of 16");
+    ASDSL_CHECK_ARG(h_out == nullptr || (h_out != h_in && h_out != delta),
+                    "gemv_preq2_rmsnorm_swiglu: h_out must not alias h_in or delta");
+    ASDSL_CU_COUNT(cus);
+    ProArgs pa;
+    pa.delta = delta;
+    pa.nw = norm_w;
+    pa.h_out = h_out;
+    pa.eps = eps;
+    pa.thr = threshold;
+    hipStream_t s = as_hip(stream);
+    const asdsl_status st = group_size == 32
+                                ? launch_gateup_swiglu<32>(meta, quant, h_in, s_out, ffn, in_features, pa, s, cus)
+                                : launch_gateup_swiglu<128>(meta, quant, h_in, s_out, ffn, in_features, pa, s, cus);
+    if (st == ASDSL_ERR_UNSUPPORTED) set_error("gemv_preq2_rmsnorm_swiglu: no paired gate/up tiling for this shape");
+    return st;
 }
 
 extern "C" asdsl_status asdsl_gemv_preq2_swiglu(const uint8_t* meta, const uint8_t* quant, const float* gate_up,

@@ -402,6 +402,22 @@ asdsl_status asdsl_gemv_preq2_swiglu(const uint8_t* meta, const uint8_t* quant, 
                                      float* y, int out_features, int in_features, int group_size,
                                      float threshold, asdsl_stream_t stream);
 
+/* gate_up GEMV with the residual add + RMSNorm prologue of
+ * asdsl_gemv_preq2_rmsnorm and SwiGLU in its epilogue: the weight rows are
+ * [gate ffn | up ffn] x in_features (preq2), and s_out[ffn] =
+ * swiglu(gate, up) with the reference's polynomial exp and the FATReLU
+ * threshold, bit for bit what asdsl_gemv_preq2_rmsnorm followed by the
+ * SwiGLU prologue of asdsl_gemv_preq2_swiglu computes.  A workgroup takes
+ * gate and up rows together, so the 2*ffn outputs never reach memory.
+ * ffn % 16 == 0, in_features <= 8192; ASDSL_ERR_UNSUPPORTED when the shape
+ * has no paired tiling (nothing is launched then).
+ * Replaces residual_add_rmsnorm_f32 + the gate_up GEMV + swiglu_inplace
+ * (unified_engine.cpp:651-688,1524-1575). */
+asdsl_status asdsl_gemv_preq2_rmsnorm_swiglu(const uint8_t* meta, const uint8_t* quant, const float* h_in,
+                                             const float* delta, const float* norm_w, float* h_out, float* s_out,
+                                             int ffn, int in_features, int group_size, float eps, float threshold,
+                                             asdsl_stream_t stream);
+
 /* Floats of device work buffer asdsl_attention_f16kv needs. */
 size_t asdsl_attention_work_floats(int n_heads, int max_seq);
 
@@ -411,7 +427,8 @@ size_t asdsl_attention_work_floats(int n_heads, int max_seq);
  * (x[i], x[i+rotary_dim/2]) with rope_cos/rope_sin[pos][rotary_dim/2].  The new
  * k, v are rounded to fp16 and stored at [kv_head][pos] of the caches
  * (fp16 [n_kv_heads][max_seq][128]); att_out[h] = softmax(q_h.K/sqrt(128)) V
- * over positions 0..pos of kv head h / (n_heads/n_kv_heads).  head_dim = 128.
+ * over positions 0..pos of kv head h / (n_heads/n_kv_heads).  head_dim = 128,
+ * work: asdsl_attention_work_floats floats of scratch.
  * Replaces rope_apply_inplace + set_kv_cache + compute_attention_flash_q8
  * (unified_engine.cpp:768-801,859-1027), with an fp16 instead of int8 cache. */
 asdsl_status asdsl_attention_f16kv(const float* qkv, uint16_t* k_cache, uint16_t* v_cache,
@@ -455,6 +472,16 @@ size_t asdsl_decode_work_bytes(const asdsl_decode_model* model);
  * (asdsl/kernels/native/unified_engine.cpp:1339-1688,207-233). */
 asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int* pos, float* logits,
                                 void* work, asdsl_stream_t stream);
+
+/* The same step for a position *pos < pos_limit (the caller guarantees it;
+ * asdsl_decode_token is pos_limit = max_seq).  The launch is shaped for that
+ * range: below 256 the attention grid covers only the (at most 4) splits
+ * such positions use and the o_proj GEMV merges them in its prologue, with
+ * no combine launch (same bits as the combine kernel).  A HIP graph of one call then
+ * replays for every position below pos_limit.  No reference counterpart (the
+ * reference passes the position by value, unified_engine.cpp:1339). */
+asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model, int* token, int* pos, int pos_limit,
+                                     float* logits, void* work, asdsl_stream_t stream);
 
 /* Bytes of device work buffer asdsl_decode_verify needs for up to max_tokens
  * tokens (1..16); 0 for an invalid model or count. */

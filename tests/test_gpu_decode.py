@@ -84,6 +84,37 @@ def test_argmax_epilogue_first_row_on_ties(gpu):
     assert yh[700] == yh[900]
 
 
+@pytest.mark.parametrize("gs,F,K,thr", [(128, 8192, 3072, 0.0), (32, 8192, 3072, 0.05), (128, 1024, 640, 0.0)])
+def test_gateup_swiglu_epilogue(gpu, gs, F, K, thr):
+    """gate_up with the residual + RMSNorm prologue and SwiGLU epilogue: the
+    residual stream bit-exact, s bit for bit swiglu of the plain norm-fed
+    GEMV's [gate | up] outputs (same rows, same per-row arithmetic), and
+    within 1e-4 of the oracle."""
+    import torch
+    from asdsl import _hip
+
+    meta, quant = _packed(2 * F, K, gs, F + K + gs)
+    rng = np.random.default_rng(F)
+    h = rng.standard_normal(K).astype(np.float32) * 3
+    d = rng.standard_normal(K).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    dh, dd, dw = (torch.from_numpy(a).cuda() for a in (h, d, w))
+    hout = torch.empty(K, device="cuda")
+    s_out = torch.empty(F, device="cuda")
+    gu = torch.empty(2 * F, device="cuda")
+    P, st = _hip.ptr, _hip.stream_handle()
+    _hip.call("asdsl_gemv_preq2_rmsnorm_swiglu", P(meta), P(quant), P(dh), P(dd), P(dw), P(hout), P(s_out), F, K, gs,
+              1e-5, thr, st)
+    _hip.call("asdsl_gemv_preq2_rmsnorm", P(meta), P(quant), P(dh), P(dd), P(dw), None, P(gu), 2 * F, K, gs, 1e-5,
+              None, st)
+    torch.cuda.synchronize()
+    assert np.array_equal(_host(hout).view(np.uint32), (h + d).view(np.uint32))
+    g = _host(gu)
+    assert np.array_equal(_host(s_out).view(np.uint32), od.swiglu(g[:F], g[F:], thr).view(np.uint32))
+    want_gu = oracle.gemv_preq2_fused(_host(meta), _host(quant), od.rmsnorm(h + d, w, 1e-5), 2 * F, K, gs)
+    assert rel_l2(_host(s_out), od.swiglu(want_gu[:F], want_gu[F:], thr)) < TOL
+
+
 @pytest.mark.parametrize("gs,thr", [(128, 0.0), (32, 0.0), (128, 0.05)])
 def test_swiglu_gemv_matches_oracle(gpu, gs, thr):
     import torch
@@ -120,7 +151,7 @@ def test_attention_rope_kv_matches_oracle(gpu, pos, max_seq):
     d = {k: torch.from_numpy(v).cuda() for k, v in dict(qkv=qkv, kc=kc, vc=vc, cos=cos, sin=sin).items()}
     dpos = torch.tensor([pos], dtype=torch.int32, device="cuda")
     att = torch.empty(nh * hd, device="cuda")
-    work = torch.empty(_hip.LIB.asdsl_attention_work_floats(nh, max_seq), device="cuda")
+    work = torch.zeros(_hip.LIB.asdsl_attention_work_floats(nh, max_seq), device="cuda")
     _hip.call("asdsl_attention_f16kv", _hip.ptr(d["qkv"]), _hip.ptr(d["kc"]), _hip.ptr(d["vc"]), _hip.ptr(d["cos"]),
               _hip.ptr(d["sin"]), _hip.ptr(dpos), _hip.ptr(att), _hip.ptr(work), nh, nkv, hd, rot, max_seq,
               _hip.stream_handle())
@@ -212,11 +243,16 @@ def test_decode_long_context_matches_oracle(gpu, ctx):
         tok = want_next
 
 
-def test_graph_replay_matches_eager_steps(gpu):
+@pytest.mark.parametrize("max_seq,ctx", [(300, 150), (1600, 1400), (3000, 2500)])
+def test_graph_replay_matches_eager_steps(gpu, max_seq, ctx):
+    """Eager steps (the general step, any position: the combine kernel)
+    against a captured graph replayed three times: at 150 the graph holds the
+    short-context step (splits merged in o_proj's prologue; same bits), at
+    1400 and 2500 the general step."""
     import torch
 
-    eng = _small_engine(n_layers=1, vocab=4096, max_seq=300, seed=9)
-    eng.prefill_kv_random(150, seed=2)
+    eng = _small_engine(n_layers=1, vocab=4096, max_seq=max_seq, seed=9)
+    eng.prefill_kv_random(ctx, seed=2)
     snap = [(L["k_cache"].clone(), L["v_cache"].clone()) for L in eng.layers]
     eng.token.fill_(17)
     eager = []
@@ -228,14 +264,14 @@ def test_graph_replay_matches_eager_steps(gpu):
         L["k_cache"].copy_(k)
         L["v_cache"].copy_(v)
     eng.token.fill_(17)
-    eng.pos.fill_(150)
+    eng.pos.fill_(ctx)
     eng.capture()
     for i in range(3):
         eng.step()
         torch.cuda.synchronize()
         assert torch.equal(eng.logits, eager[i][0]), i
         assert eng.next_token() == eager[i][1]
-    assert int(eng.pos.item()) == 153
+    assert int(eng.pos.item()) == ctx + 3
 
 
 def test_forward_token_api(gpu):
@@ -263,8 +299,8 @@ eng.prefill_kv_random(250, seed=3)
 eng.token.fill_(99)
 eng.pos.fill_(250)
 out = []
-for _ in range(8):
-    eng._queue_step(int(torch.cuda.current_stream().cuda_stream))
+for i in range(8):
+    eng._queue_step(int(torch.cuda.current_stream().cuda_stream), eng._pos_limit(250 + i))
     torch.cuda.synchronize()
     out.append(eng.logits.cpu().numpy().copy())
 np.save(OUT, np.stack(out))
@@ -272,9 +308,9 @@ np.save(OUT, np.stack(out))
 
 
 def test_combine_fold_gives_the_combine_kernels_bits(gpu, tmp_path):
-    """Positions 250..257: up to 255 (at most 4 splits of 64) the o_proj
-    GEMV's prologue merges the attention splits and the combine kernel skips
-    them, from 256 the combine kernel merges them.  A run that leaves the
+    """Positions 250..257: up to 255 (at most 4 splits of 64) a step shaped
+    for short contexts lets the o_proj GEMV's prologue merge the attention
+    splits; from 256 the combine kernel merges them.  A run that leaves the
     merge to the combine kernel everywhere (ASDSL_HIP_NO_COMBINE_FOLD=1, read
     once per process, so in a second process) gives the same logits bit for
     bit at every position."""
