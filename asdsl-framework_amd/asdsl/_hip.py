@@ -76,12 +76,14 @@ SIGNATURES: dict[str, list] = {
     "asdsl_gemv_preq2_rmsnorm_swiglu": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F, _P],
     "asdsl_attention_work_floats": [_I, _I],
     "asdsl_attention_f16kv": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "asdsl_attention_q8kv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "asdsl_decode_work_bytes": [_P],
     "asdsl_decode_token": [_P, _P, _P, _P, _P, _P],
     "asdsl_decode_token_upto": [_P, _P, _P, _I, _P, _P, _P],
     "asdsl_decode_verify_work_bytes": [_P, _I],
     "asdsl_decode_verify": [_P, _P, _I, _P, _P, _P, _P, _P],
     "asdsl_kv_zero_from": [_P, _P, _I, _I, _I, _I, _P],
+    "asdsl_kv_zero_from_q8": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "asdsl_repack_preq_to_preq2": [_P, _P, _P, _I, _I, _I, _P],
     "asdsl_repack_asym_to_q4_32": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_repack_asym_to_preq2": [_P, _P, _P, _P, _P, _I, _I, _I, _P],

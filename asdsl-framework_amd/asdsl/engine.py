@@ -44,6 +44,9 @@ class DecodeConfig:
     gs_lm: int = 128
     rms_eps: float = 1e-5
     rope_theta: float = 10000.0
+    # "int8": the reference's KV cache (int8 codes, one fp32 scale per 64
+    # dims; UnifiedEngine::set_kv_cache); "fp16": fp16 rows
+    kv_format: str = "fp16"
 
     @property
     def qkv_dim(self) -> int:
@@ -53,14 +56,19 @@ class DecodeConfig:
 class _Layer(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "qkv_meta", "qkv_quant", "o_meta", "o_quant", "gu_meta", "gu_quant", "down_meta", "down_quant",
-        "rms_att", "rms_ffn", "k_cache", "v_cache")] + [("fatrelu_threshold", ctypes.c_float)]
+        "rms_att", "rms_ffn", "k_cache", "v_cache")] + [("fatrelu_threshold", ctypes.c_float)] + [
+        (n, ctypes.c_void_p) for n in ("k_scale", "v_scale")]
 
 
 class _Model(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "hidden", "ffn", "vocab", "n_layers", "n_heads", "n_kv_heads", "head_dim", "rotary_dim", "max_seq",
         "gs_attn", "gs_ffn", "gs_lm")] + [("rms_eps", ctypes.c_float), ("layers", ctypes.POINTER(_Layer))] + [
-        (n, ctypes.c_void_p) for n in ("embed", "rms_out", "lm_meta", "lm_quant", "rope_cos", "rope_sin")]
+        (n, ctypes.c_void_p) for n in ("embed", "rms_out", "lm_meta", "lm_quant", "rope_cos", "rope_sin")] + [
+        ("kv_format", ctypes.c_int)]
+
+KV_FORMATS = {"fp16": 0, "int8": 1}
+KV_QBLOCK = 64  # dims per int8 cache scale
 
 
 def rope_tables(max_seq: int, rotary_dim: int, theta: float = 10000.0) -> tuple[np.ndarray, np.ndarray]:
@@ -125,10 +133,18 @@ class DecodeEngine:
         cos, sin = rope_tables(cfg.max_seq, cfg.rotary_dim, cfg.rope_theta)
         self.rope_cos = torch.from_numpy(cos).to(dev)
         self.rope_sin = torch.from_numpy(sin).to(dev)
+        if cfg.kv_format not in KV_FORMATS:
+            raise ValueError(f"kv_format must be one of {sorted(KV_FORMATS)}")
+        self.kv_int8 = cfg.kv_format == "int8"
         for L in layers:
             if "k_cache" not in L:
-                L["k_cache"] = torch.zeros((cfg.n_kv_heads, cfg.max_seq, cfg.head_dim), dtype=torch.float16, device=dev)
+                shape = (cfg.n_kv_heads, cfg.max_seq, cfg.head_dim)
+                L["k_cache"] = torch.zeros(shape, dtype=torch.int8 if self.kv_int8 else torch.float16, device=dev)
                 L["v_cache"] = torch.zeros_like(L["k_cache"])
+                if self.kv_int8:  # zero_kv_from's state: codes 0, scales 1.0
+                    L["k_scale"] = torch.ones(shape[:2] + (cfg.head_dim // KV_QBLOCK,), dtype=torch.float32,
+                                              device=dev)
+                    L["v_scale"] = torch.ones_like(L["k_scale"])
         self._c_layers = (_Layer * cfg.n_layers)()
         for i, L in enumerate(layers):
             c = self._c_layers[i]
@@ -137,6 +153,8 @@ class DecodeEngine:
                 setattr(c, f"{n}_quant", _hip.ptr(L[n][1]))
             c.rms_att, c.rms_ffn = _hip.ptr(L["rms_att"]), _hip.ptr(L["rms_ffn"])
             c.k_cache, c.v_cache = _hip.ptr(L["k_cache"]), _hip.ptr(L["v_cache"])
+            if self.kv_int8:
+                c.k_scale, c.v_scale = _hip.ptr(L["k_scale"]), _hip.ptr(L["v_scale"])
             c.fatrelu_threshold = float(fatrelu_threshold)
         m = _Model()
         for n in ("hidden", "ffn", "vocab", "n_layers", "n_heads", "n_kv_heads", "head_dim", "rotary_dim",
@@ -147,6 +165,7 @@ class DecodeEngine:
         m.embed, m.rms_out = _hip.ptr(embed), _hip.ptr(rms_out)
         m.lm_meta, m.lm_quant = _hip.ptr(lm_meta), _hip.ptr(lm_quant)
         m.rope_cos, m.rope_sin = _hip.ptr(self.rope_cos), _hip.ptr(self.rope_sin)
+        m.kv_format = KV_FORMATS[cfg.kv_format]
         self._model = m
         nbytes = _hip.LIB.asdsl_decode_work_bytes(ctypes.byref(m))
         if nbytes == 0:
@@ -204,19 +223,28 @@ class DecodeEngine:
         return c.max_seq
 
     def prefill_kv_random(self, ctx: int, seed: int = 1) -> None:
-        """Positions [0, ctx) of every layer's cache ~ N(0, 1) in fp16; the
-        next step decodes at position ctx."""
+        """Positions [0, ctx) of every layer's cache ~ N(0, 1) (fp16 rows, or
+        int8 codes and scales quantized per 64 dims); the rest zeroed as
+        truncate_kv leaves it.  The next step decodes at position ctx."""
         import torch
 
         if not 0 <= ctx < self.cfg.max_seq:
             raise ValueError(f"ctx must be in [0, {self.cfg.max_seq})")
         gen = torch.Generator(device=_hip.device()).manual_seed(seed)
         for L in self.layers:
-            for n in ("k_cache", "v_cache"):
-                L[n].zero_()
-                if ctx:
-                    L[n][:, :ctx] = torch.randn((self.cfg.n_kv_heads, ctx, self.cfg.head_dim), generator=gen,
-                                                device=L[n].device, dtype=torch.float32).half()
+            for n in ("k", "v"):
+                cache = L[f"{n}_cache"]
+                cache.zero_()
+                if self.kv_int8:
+                    L[f"{n}_scale"].fill_(1.0)
+                if not ctx:
+                    continue
+                rows = torch.randn((self.cfg.n_kv_heads, ctx, self.cfg.head_dim), generator=gen,
+                                   device=cache.device, dtype=torch.float32)
+                if self.kv_int8:
+                    cache[:, :ctx], L[f"{n}_scale"][:, :ctx] = kv_quantize_int8(rows)
+                else:
+                    cache[:, :ctx] = rows.half()
         self.pos.fill_(ctx)
         self._host_pos = ctx
         self.kv_seq_len = ctx
@@ -355,9 +383,17 @@ class DecodeEngine:
         c = self.cfg
         new_len = min(max(int(new_len), 0), c.max_seq)
         for L in self.layers:
-            _hip.check(_hip.LIB.asdsl_kv_zero_from(_hip.ptr(L["k_cache"]), _hip.ptr(L["v_cache"]), c.n_kv_heads,
-                                                   c.head_dim, c.max_seq, new_len, _hip.stream_handle()),
-                       "asdsl_kv_zero_from")
+            if self.kv_int8:
+                _hip.check(_hip.LIB.asdsl_kv_zero_from_q8(_hip.ptr(L["k_cache"]), _hip.ptr(L["v_cache"]),
+                                                          _hip.ptr(L["k_scale"]), _hip.ptr(L["v_scale"]),
+                                                          c.n_kv_heads, c.head_dim, c.max_seq, new_len,
+                                                          _hip.stream_handle()),
+                           "asdsl_kv_zero_from_q8")
+            else:
+                _hip.check(_hip.LIB.asdsl_kv_zero_from(_hip.ptr(L["k_cache"]), _hip.ptr(L["v_cache"]),
+                                                       c.n_kv_heads, c.head_dim, c.max_seq, new_len,
+                                                       _hip.stream_handle()),
+                           "asdsl_kv_zero_from")
         self.kv_seq_len = new_len
         self.pos.fill_(new_len)
         self._host_pos = new_len
@@ -388,11 +424,29 @@ class DecodeEngine:
 
     def bytes_per_token(self, pos: int) -> int:
         """HBM bytes one step must move at position pos: every weight once,
-        the K and V cache rows of positions 0..pos (fp16), one embedding row;
-        activations and logits are included for completeness."""
+        the K and V cache rows of positions 0..pos (fp16: 2 bytes a dim; int8:
+        1 byte a dim and 4 bytes per 64 dims), one embedding row; activations
+        and logits are included for completeness."""
         c = self.cfg
-        kv = c.n_layers * 2 * c.n_kv_heads * (pos + 1) * c.head_dim * 2
+        row = c.head_dim + 4 * (c.head_dim // KV_QBLOCK) if self.kv_int8 else 2 * c.head_dim
+        kv = c.n_layers * 2 * c.n_kv_heads * (pos + 1) * row
         return self.weight_bytes() + kv + 2 * c.hidden + 4 * c.vocab
+
+
+def kv_quantize_int8(rows):
+    """set_kv_cache's rule (unified_engine.cpp:859-920) on a float32 device
+    tensor [..., d] (d a multiple of 64): per 64-dim block scale = amax *
+    float32(1/127) (1e-12 when amax <= 1e-12), code = round-half-even(x *
+    (1/scale)) clamped to [-127, 127].  Returns (int8 codes [..., d], float32
+    scales [..., d/64])."""
+    import torch
+
+    x = rows.float().reshape(*rows.shape[:-1], -1, KV_QBLOCK)
+    amax = x.abs().amax(dim=-1)
+    scale = torch.where(amax > 1e-12, amax * float(np.float32(1.0 / 127.0)), torch.full_like(amax, 1e-12))
+    inv = 1.0 / scale
+    q = torch.round(x * inv.unsqueeze(-1)).clamp_(-127, 127).to(torch.int8)
+    return q.reshape(rows.shape), scale
 
 
 def ideal_tokens_per_s(bytes_per_token: int, peak_gbs: float = 8000.0) -> float:

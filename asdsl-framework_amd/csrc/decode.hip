@@ -5,9 +5,10 @@
 // Reference: UnifiedEngine::forward_token (asdsl/kernels/native/unified_engine.cpp:1339-1688)
 //   with its helpers load_embed_row_f32 (181-197), rope_apply_inplace (768-801),
 //   set_kv_cache (859-920), compute_attention_flash_q8 (922-1027),
-//   argmax_f32_avx2 (207-233).  The reference caches K/V as int8 per 64; this
-//   step keeps them fp16 (the decode workload's KV format); the current
-//   token's K/V are rounded to fp16 before use, as if read back from the cache.
+//   argmax_f32_avx2 (207-233).  The cache is either the reference's form
+//   (int8 codes with one fp32 scale per 64 dims; the current token's K/V are
+//   quantized and dequantized before use, as the reference reads them back)
+//   or fp16 rows (the current token's K/V rounded to fp16 before use).
 //
 // Per layer: qkv GEMV with residual add + RMSNorm in its prologue (layer 0:
 // the embedding row itself), attention (RoPE, KV write, split partials),
@@ -34,6 +35,65 @@ constexpr int kPartStride = kHeadDim + 2;  // m, l, acc[128]
 
 __device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_as_half(b)); }
 __device__ __forceinline__ uint16_t f2h(float v) { return __half_as_ushort(__float2half_rn(v)); }
+
+// One layer's KV cache as the attention kernels address it: rows of 128
+// dims at [kv_head][position], either fp16 or int8 with one fp32 scale per
+// 64 dims (scales [kv_head][position][2]; set_kv_cache,
+// unified_engine.cpp:859-920).
+struct KvCache {
+    void* k;
+    void* v;
+    float* ks;  // int8 form only
+    float* vs;
+};
+
+constexpr float kInv127 = 1.0f / 127.0f;
+
+// Dims 8*dc .. 8*dc+7 of cache row `row` (kv_head * max_seq + position) in
+// 16 bytes: fp16 as stored; int8 as the 8 codes, then the block's scale.
+template <bool Q8>
+__device__ __forceinline__ uint4 kv_load8(const void* base, const float* scales, size_t row, int dc) {
+    if constexpr (Q8) {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(base) + row * kHeadDim + 8 * dc);
+        return make_uint4(u.x, u.y, __float_as_uint(scales[row * 2 + (dc >> 3)]), 0u);
+    } else {
+        return *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + row * kHeadDim + 8 * dc);
+    }
+}
+
+// kv_load8's 16 bytes as 8 floats: fp16 -> fp32, or float(code) * scale
+// (compute_attention_flash_q8's dequantization, unified_engine.cpp:948-951).
+template <bool Q8>
+__device__ __forceinline__ void kv_unpack8(const uint4& raw, float (&r)[8]) {
+    if constexpr (Q8) {
+        const float sc = __uint_as_float(raw.z);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            r[e] = static_cast<float>(static_cast<int8_t>(raw.x >> (8 * e))) * sc;
+            r[4 + e] = static_cast<float>(static_cast<int8_t>(raw.y >> (8 * e))) * sc;
+        }
+    } else {
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            r[2 * e] = h2f(static_cast<uint16_t>(w[e] & 0xFFFFu));
+            r[2 * e + 1] = h2f(static_cast<uint16_t>(w[e] >> 16));
+        }
+    }
+}
+
+// set_kv_cache's rule on one 64-dim block held one value per lane of a wave:
+// scale = amax * (1/127) if amax > 1e-12, else 1e-12; returns the code
+// round-half-even(x * (1 / scale)) clamped to [-127, 127].
+__device__ __forceinline__ int kv_q8_code(float x, float& scale) {
+    float a = fabsf(x);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, kWave));
+    scale = a > 1e-12f ? a * kInv127 : 1e-12f;
+    const float inv = 1.0f / scale;
+    const float q = __builtin_rintf(x * inv);
+    return static_cast<int>(fminf(fmaxf(q, -127.0f), 127.0f));
+}
 
 // h[0:hidden] = embed[token] (fp16 -> fp32); also clears the argmax slot for
 // this step's lm_head.  A token outside [0, vocab) reads row 0 (the host
@@ -65,7 +125,7 @@ __global__ void finalize_kernel(const unsigned long long* __restrict__ amax, int
 // 8*dc..+8) and its query chunks in qr; positions >= p1 are masked.  With
 // NEW, position `pos` takes its K/V rows from kv_new (LDS) instead.  Writes
 // (m, l, acc[128]) of head hh at part + hh * head_stride.
-template <int G, bool NEW>
+template <int G, bool NEW, bool Q8>
 __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16], const uint4 (&vraw)[kSplit / 16],
                                                 const float (&qr)[G][8], int p0, int p1, int pos,
                                                 const float (*kv_new)[kHeadDim], float (*wml)[G][2],
@@ -83,12 +143,7 @@ __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16]
 #pragma unroll
             for (int e = 0; e < 8; ++e) r[e] = kv_new[which][8 * dc + e];
         } else {
-            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                r[2 * e] = h2f(static_cast<uint16_t>(w[e] & 0xFFFFu));
-                r[2 * e + 1] = h2f(static_cast<uint16_t>(w[e] >> 16));
-            }
+            kv_unpack8<Q8>(raw, r);
         }
     };
 
@@ -202,6 +257,27 @@ __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16]
     }
 }
 
+// int8 cache: the new position's rotated key and value (kv_new, fp32)
+// become their codes.  Each of the four waves takes one 64-dim block (waves
+// 0-1: the key's blocks, 2-3: the value's), leaves the dequantized values in
+// kv_new (what a later step reads back) and, when `store`, writes the codes
+// and the scale to cache row `row`.
+static_assert(kAttnThreads == 4 * kWave, "kv_quantize_new: one wave per 64-dim block of K and V");
+__device__ __forceinline__ void kv_quantize_new(float (*kv_new)[kHeadDim], const KvCache& kv, size_t row,
+                                                bool store) {
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid >> 6;
+    const int which = wave >> 1;
+    const int d = (wave & 1) * kWave + (tid & (kWave - 1));
+    float scale;
+    const int q = kv_q8_code(kv_new[which][d], scale);
+    kv_new[which][d] = static_cast<float>(q) * scale;
+    if (store) {
+        static_cast<int8_t*>(which ? kv.v : kv.k)[row * kHeadDim + d] = static_cast<int8_t>(q);
+        if ((tid & (kWave - 1)) == 0) (which ? kv.vs : kv.ks)[row * 2 + (wave & 1)] = scale;
+    }
+}
+
 // Attention partials of one KV head over positions [s*kSplit, min((s+1)*kSplit, pos+1)).
 // G = query heads per KV head.  Lane l of a wave reads dims 8*(l%16).. of
 // position 4*step + l/16, so every K/V load instruction moves 1 KiB of
@@ -212,9 +288,9 @@ __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16]
 // (max, sum, P.V); the four waves are merged in LDS behind one barrier (a
 // block-wide softmax through LDS took two more barriers and ~2 us longer).
 
-template <int G>
+template <int G, bool Q8>
 __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
-    const float* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    const float* __restrict__ qkv, KvCache kv,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
     float* __restrict__ part, int n_heads, int n_kv, int max_seq, int rot_half, int nsplit) {
     __shared__ float q_s[G][kHeadDim];
@@ -234,7 +310,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const int wave = tid >> 6;
     const int pg = lane >> 4;   // position within the wave's four
     const int dc = lane & 15;   // 8-dim chunk
-    const size_t head_base = static_cast<size_t>(kvh) * max_seq * kHeadDim;
+    const size_t row0 = static_cast<size_t>(kvh) * max_seq;  // cache row of position 0
 
     // RoPE inputs first (small, from L2), then every K and V row this lane
     // will use (they depend on nothing but pos): loads complete in issue
@@ -272,9 +348,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     for (int it = 0; it < kIt; ++it) {
         const int p = p0 + wave * 4 + pg + 16 * it;
         if (p < p1 && p != pos) {
-            const size_t at = head_base + static_cast<size_t>(p) * kHeadDim + 8 * dc;
-            kraw[it] = *reinterpret_cast<const uint4*>(kc + at);
-            vraw[it] = *reinterpret_cast<const uint4*>(vc + at);
+            kraw[it] = kv_load8<Q8>(kv.k, kv.ks, row0 + p, dc);
+            vraw[it] = kv_load8<Q8>(kv.v, kv.vs, row0 + p, dc);
         } else {
             kraw[it] = make_uint4(0u, 0u, 0u, 0u);
             vraw[it] = kraw[it];
@@ -297,14 +372,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
                 val = rx[r][0];
             }
             if (hh < G) q_s[hh][d] = val;
-            else kv_new[0][d] = h2f(f2h(val));
+            else kv_new[0][d] = Q8 ? val : h2f(f2h(val));
         }
     }
-    if (tid < kHeadDim) kv_new[1][tid] = h2f(f2h(vnew));
+    if (tid < kHeadDim) kv_new[1][tid] = Q8 ? vnew : h2f(f2h(vnew));
     __syncthreads();
-    if (pos < p1 && tid < kHeadDim) {
-        kc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
-        vc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[1][tid]);
+    if constexpr (Q8) {
+        kv_quantize_new(kv_new, kv, row0 + pos, pos < p1);
+        __syncthreads();
+    } else if (pos < p1 && tid < kHeadDim) {
+        static_cast<uint16_t*>(kv.k)[(row0 + pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
+        static_cast<uint16_t*>(kv.v)[(row0 + pos) * kHeadDim + tid] = f2h(kv_new[1][tid]);
     }
 
     float qr[G][8];
@@ -313,7 +391,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
 
-    attn_split_core<G, true>(kraw, vraw, qr, p0, p1, pos, kv_new, wml, wacc,
+    attn_split_core<G, true, Q8>(kraw, vraw, qr, p0, p1, pos, kv_new, wml, wacc,
                              part + (static_cast<size_t>(kvh * G) * nsplit + s) * kPartStride,
                              static_cast<size_t>(nsplit) * kPartStride);
 }
@@ -437,9 +515,9 @@ int attn_max_splits(int pos_limit) {
     return best;
 }
 
-template <int G>
+template <int G, bool Q8>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
-    const float* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    const float* __restrict__ qkv, KvCache kv,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
     float* __restrict__ part, float* __restrict__ att, int n_heads, int n_kv, int max_seq, int rot_half) {
     constexpr int kWaves = kAttnThreads / kWave;
@@ -466,7 +544,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     const int wave = tid >> 6;
     const int pg = lane >> 4;   // position within the wave's four
     const int dc = lane & 15;   // 8-dim chunk
-    const size_t head_base = static_cast<size_t>(kvh) * max_seq * kHeadDim;
+    const size_t row0 = static_cast<size_t>(kvh) * max_seq;  // cache row of position 0
 
     // RoPE inputs of the G query heads and the new key (small, first), then
     // the first tile's K/V rows: loads complete in issue order.
@@ -503,9 +581,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
             const int p = t0 + wave * 4 + pg + 16 * it;
-            const size_t at = head_base + static_cast<size_t>(p < p1 ? p : p0) * kHeadDim + 8 * dc;
-            kraw[it] = *reinterpret_cast<const uint4*>(kc + at);
-            vraw[it] = *reinterpret_cast<const uint4*>(vc + at);
+            const size_t row = row0 + (p < p1 ? p : p0);
+            kraw[it] = kv_load8<Q8>(kv.k, kv.ks, row, dc);
+            vraw[it] = kv_load8<Q8>(kv.v, kv.vs, row, dc);
         }
     };
     uint4 ka[kIt], va[kIt], kb[kIt], vb[kIt];
@@ -525,14 +603,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
                 val = rx[r][0];
             }
             if (hh < G) q_s[hh][d] = val;
-            else kv_new[0][d] = h2f(f2h(val));
+            else kv_new[0][d] = Q8 ? val : h2f(f2h(val));
         }
     }
-    if (tid < kHeadDim) kv_new[1][tid] = h2f(f2h(vnew));
+    if (tid < kHeadDim) kv_new[1][tid] = Q8 ? vnew : h2f(f2h(vnew));
     __syncthreads();
-    if (pos >= p0 && pos < p1 && tid < kHeadDim) {
-        kc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
-        vc[head_base + static_cast<size_t>(pos) * kHeadDim + tid] = f2h(kv_new[1][tid]);
+    if constexpr (Q8) {
+        kv_quantize_new(kv_new, kv, row0 + pos, pos >= p0 && pos < p1);
+        __syncthreads();
+    } else if (pos >= p0 && pos < p1 && tid < kHeadDim) {
+        static_cast<uint16_t*>(kv.k)[(row0 + pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
+        static_cast<uint16_t*>(kv.v)[(row0 + pos) * kHeadDim + tid] = f2h(kv_new[1][tid]);
     }
     float qr[G][8];
 #pragma unroll
@@ -556,12 +637,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
 #pragma unroll
             for (int e = 0; e < 8; ++e) r[e] = kv_new[which][8 * dc + e];
         } else {
-            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                r[2 * e] = h2f(static_cast<uint16_t>(w[e] & 0xFFFFu));
-                r[2 * e + 1] = h2f(static_cast<uint16_t>(w[e] >> 16));
-            }
+            kv_unpack8<Q8>(raw, r);
         }
     };
     auto process_tile = [&](int t0, const uint4 (&kraw)[kIt], const uint4 (&vraw)[kIt]) {
@@ -677,7 +753,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
 }
 
 int attn_splits(int max_seq);
-asdsl_status launch_attention(const float* qkv, uint16_t* kc, uint16_t* vc, const float* rc, const float* rs,
+asdsl_status launch_attention(const float* qkv, const KvCache& kv, bool q8, const float* rc, const float* rs,
                               const int* pos, float* att, float* part, int n_heads, int n_kv, int rot_half,
                               int max_seq, hipStream_t s, int fold);
 
@@ -704,48 +780,57 @@ bool attn_fold(int pos_limit, int max_seq) {
 // work: attn_decode_work_floats.  fold: the short-context form (partials at
 // work, kMaxSplits rows per head, for the o_proj prologue); otherwise att
 // receives the merged output.
-asdsl_status launch_attention_decode(const float* qkv, uint16_t* kc, uint16_t* vc, const float* rc, const float* rs,
-                                     const int* pos, float* att, float* work, int n_heads, int n_kv, int rot_half,
-                                     int max_seq, int pos_limit, bool fold, hipStream_t s) {
-    const int G = n_heads / n_kv;
-    if (!fold)
-        return launch_attention(qkv, kc, vc, rc, rs, pos, att, work + static_cast<size_t>(n_heads) * kMaxSplits *
-                                kPartStride, n_heads, n_kv, rot_half, max_seq, s, 0);
-    const dim3 grid(attn_max_splits(pos_limit < max_seq ? pos_limit : max_seq), n_kv);
-#define ASDSL_ATTN_CASE(GG)                                                                                  \
-    case GG:                                                                                                \
-        return launch("attn_decode_kernel", attn_decode_kernel<GG>, grid, dim3(kAttnThreads), 0, s, qkv, kc, vc, \
-                      rc, rs, pos, work, att, n_heads, n_kv, max_seq, rot_half);
-    switch (G) {
-        ASDSL_ATTN_CASE(1)
-        ASDSL_ATTN_CASE(2)
-        ASDSL_ATTN_CASE(3)
-        ASDSL_ATTN_CASE(4)
+// The kernel instance for G query heads per KV head (1..4) and the cache
+// form: f(kernel) is called with the matching instantiation.
+template <template <int, bool> class K, typename F>
+asdsl_status with_attn_kernel(int G, bool q8, F&& f) {
+    switch (G * 2 + (q8 ? 1 : 0)) {
+        case 2: return f(K<1, false>::fn());
+        case 3: return f(K<1, true>::fn());
+        case 4: return f(K<2, false>::fn());
+        case 5: return f(K<2, true>::fn());
+        case 6: return f(K<3, false>::fn());
+        case 7: return f(K<3, true>::fn());
+        case 8: return f(K<4, false>::fn());
+        case 9: return f(K<4, true>::fn());
         default:
             set_error("attention: n_heads / n_kv_heads must be 1..4");
             return ASDSL_ERR_UNSUPPORTED;
     }
-#undef ASDSL_ATTN_CASE
+}
+template <int G, bool Q8>
+struct DecodeAttnK {
+    static auto fn() { return attn_decode_kernel<G, Q8>; }
+};
+template <int G, bool Q8>
+struct PartialAttnK {
+    static auto fn() { return attn_partial_kernel<G, Q8>; }
+};
+
+asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q8, const float* rc, const float* rs,
+                                     const int* pos, float* att, float* work, int n_heads, int n_kv, int rot_half,
+                                     int max_seq, int pos_limit, bool fold, hipStream_t s) {
+    if (!fold)
+        return launch_attention(qkv, kv, q8, rc, rs, pos, att, work + static_cast<size_t>(n_heads) * kMaxSplits *
+                                kPartStride, n_heads, n_kv, rot_half, max_seq, s, 0);
+    const dim3 grid(attn_max_splits(pos_limit < max_seq ? pos_limit : max_seq), n_kv);
+    return with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, [&](auto kern) {
+        return launch("attn_decode_kernel", kern, grid, dim3(kAttnThreads), 0, s, qkv, kv, rc, rs, pos, work, att,
+                      n_heads, n_kv, max_seq, rot_half);
+    });
 }
 
 int attn_splits(int max_seq) { return (max_seq + kSplit - 1) / kSplit; }
 
-asdsl_status launch_attention(const float* qkv, uint16_t* kc, uint16_t* vc, const float* rc, const float* rs,
+asdsl_status launch_attention(const float* qkv, const KvCache& kv, bool q8, const float* rc, const float* rs,
                               const int* pos, float* att, float* part, int n_heads, int n_kv, int rot_half,
                               int max_seq, hipStream_t s, int fold) {
     const int nsplit = attn_splits(max_seq);
-    const int G = n_heads / n_kv;
-    asdsl_status st;
     const dim3 grid(nsplit, n_kv);
-    switch (G) {
-        case 1: st = launch("attn_partial_kernel", attn_partial_kernel<1>, grid, dim3(kAttnThreads), 0, s, qkv, kc, vc, rc, rs, pos, part, n_heads, n_kv, max_seq, rot_half, nsplit); break;
-        case 2: st = launch("attn_partial_kernel", attn_partial_kernel<2>, grid, dim3(kAttnThreads), 0, s, qkv, kc, vc, rc, rs, pos, part, n_heads, n_kv, max_seq, rot_half, nsplit); break;
-        case 3: st = launch("attn_partial_kernel", attn_partial_kernel<3>, grid, dim3(kAttnThreads), 0, s, qkv, kc, vc, rc, rs, pos, part, n_heads, n_kv, max_seq, rot_half, nsplit); break;
-        case 4: st = launch("attn_partial_kernel", attn_partial_kernel<4>, grid, dim3(kAttnThreads), 0, s, qkv, kc, vc, rc, rs, pos, part, n_heads, n_kv, max_seq, rot_half, nsplit); break;
-        default:
-            set_error("attention: n_heads / n_kv_heads must be 1..4");
-            return ASDSL_ERR_UNSUPPORTED;
-    }
+    const asdsl_status st = with_attn_kernel<PartialAttnK>(n_heads / n_kv, q8, [&](auto kern) {
+        return launch("attn_partial_kernel", kern, grid, dim3(kAttnThreads), 0, s, qkv, kv, rc, rs, pos, part,
+                      n_heads, n_kv, max_seq, rot_half, nsplit);
+    });
     if (st != ASDSL_OK) return st;
     return launch("attn_combine_kernel", attn_combine_kernel, dim3(n_heads), dim3(kCombineThreads), 0, s,
                   static_cast<const float*>(part), pos, att, nsplit, max_seq, fold);
@@ -797,6 +882,16 @@ asdsl_status check_model(const asdsl_decode_model* m) {
     ASDSL_CHECK_ARG(m->n_layers > 0 && m->layers && m->embed && m->rms_out && m->lm_meta && m->lm_quant &&
                         m->rope_cos && m->rope_sin && m->vocab > 0 && m->max_seq > 0,
                     "decode: incomplete model description");
+    ASDSL_CHECK_ARG(m->kv_format == ASDSL_KV_FP16 || m->kv_format == ASDSL_KV_INT8,
+                    "decode: kv_format must be ASDSL_KV_FP16 or ASDSL_KV_INT8");
+    for (int l = 0; l < m->n_layers; ++l) {
+        const asdsl_decode_layer& L = m->layers[l];
+        ASDSL_CHECK_ARG(L.k_cache && L.v_cache && reinterpret_cast<uintptr_t>(L.k_cache) % 16 == 0 &&
+                            reinterpret_cast<uintptr_t>(L.v_cache) % 16 == 0,
+                        "decode: layer %d: K/V caches must be non-null and 16-byte aligned", l);
+        ASDSL_CHECK_ARG(m->kv_format != ASDSL_KV_INT8 || (L.k_scale && L.v_scale),
+                        "decode: layer %d: the int8 cache needs its scale arrays", l);
+    }
     return ASDSL_OK;
 }
 
@@ -880,11 +975,12 @@ __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __
 
 // RoPE of column c's query and key heads at position pos + c (grid: heads x
 // columns, one thread per dimension): rotated q (fp32) to Q[c][head], the
-// key and value rounded to fp16 into the caches at that position, as the
-// decode step does.  Columns past the cache write nothing.
+// key and value into the caches at that position as the decode step stores
+// them (fp16, or int8 codes and scales with one wave per 64-dim block).
+// Columns past the cache write nothing.
+template <bool Q8>
 __global__ __launch_bounds__(kHeadDim) void verify_rope_kv_kernel(const float* __restrict__ QKV,
-                                                                  float* __restrict__ Q, uint16_t* __restrict__ kc,
-                                                                  uint16_t* __restrict__ vc,
+                                                                  float* __restrict__ Q, KvCache kv,
                                                                   const float* __restrict__ rope_cos,
                                                                   const float* __restrict__ rope_sin,
                                                                   const int* __restrict__ pos_ptr, int n_heads,
@@ -910,18 +1006,29 @@ __global__ __launch_bounds__(kHeadDim) void verify_rope_kv_kernel(const float* _
         Q[(static_cast<size_t>(c) * n_heads + hh) * kHeadDim + d] = val;
     } else {
         const int kvh = hh - n_heads;
-        const size_t at = (static_cast<size_t>(kvh) * max_seq + pos) * kHeadDim + d;
-        kc[at] = f2h(val);
-        vc[at] = f2h(row[static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim + d]);
+        const size_t crow = static_cast<size_t>(kvh) * max_seq + pos;
+        const float vv = row[static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim + d];
+        if constexpr (Q8) {
+            float sk, sv;
+            const int qk = kv_q8_code(val, sk);
+            const int qv = kv_q8_code(vv, sv);
+            static_cast<int8_t*>(kv.k)[crow * kHeadDim + d] = static_cast<int8_t>(qk);
+            static_cast<int8_t*>(kv.v)[crow * kHeadDim + d] = static_cast<int8_t>(qv);
+            if ((d & (kWave - 1)) == 0) {
+                kv.ks[crow * 2 + d / kWave] = sk;
+                kv.vs[crow * 2 + d / kWave] = sv;
+            }
+        } else {
+            static_cast<uint16_t*>(kv.k)[crow * kHeadDim + d] = f2h(val);
+            static_cast<uint16_t*>(kv.v)[crow * kHeadDim + d] = f2h(vv);
+        }
     }
 }
 
 // Attention partials of column c (position pos + c) for one KV head and one
 // split, every K/V row from the cache (the pass's own rows are there).
-template <int G>
-__global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const float* __restrict__ Q,
-                                                                           const uint16_t* __restrict__ kc,
-                                                                           const uint16_t* __restrict__ vc,
+template <int G, bool Q8>
+__global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const float* __restrict__ Q, KvCache kv,
                                                                            const int* __restrict__ pos_ptr,
                                                                            float* __restrict__ part, int n_heads,
                                                                            int max_seq, int nsplit) {
@@ -940,16 +1047,15 @@ __global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const
     const int wave = tid >> 6;
     const int pg = lane >> 4;
     const int dc = lane & 15;
-    const size_t head_base = static_cast<size_t>(kvh) * max_seq * kHeadDim;
+    const size_t row0 = static_cast<size_t>(kvh) * max_seq;
     constexpr int kIt = kSplit / 16;
     uint4 kraw[kIt], vraw[kIt];
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
         const int p = p0 + wave * 4 + pg + 16 * it;
         if (p < p1) {
-            const size_t at = head_base + static_cast<size_t>(p) * kHeadDim + 8 * dc;
-            kraw[it] = *reinterpret_cast<const uint4*>(kc + at);
-            vraw[it] = *reinterpret_cast<const uint4*>(vc + at);
+            kraw[it] = kv_load8<Q8>(kv.k, kv.ks, row0 + p, dc);
+            vraw[it] = kv_load8<Q8>(kv.v, kv.vs, row0 + p, dc);
         } else {
             kraw[it] = make_uint4(0u, 0u, 0u, 0u);
             vraw[it] = kraw[it];
@@ -963,7 +1069,7 @@ __global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const
     for (int hh = 0; hh < G; ++hh)
 #pragma unroll
         for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
-    attn_split_core<G, false>(kraw, vraw, qr, p0, p1, pos, nullptr, wml, wacc,
+    attn_split_core<G, false, Q8>(kraw, vraw, qr, p0, p1, pos, nullptr, wml, wacc,
                               part + ((static_cast<size_t>(c) * n_heads + kvh * G) * nsplit + s) * kPartStride,
                               static_cast<size_t>(nsplit) * kPartStride);
 }
@@ -1025,6 +1131,34 @@ __global__ __launch_bounds__(256) void kv_zero_kernel(uint4* __restrict__ k, uin
     }
 }
 
+// The int8 cache's rows [from, max_seq): codes 0 and scales 1.0, as
+// zero_kv_from leaves them (unified_engine.cpp:1263-1283).
+__global__ __launch_bounds__(256) void kv_zero_q8_kernel(uint4* __restrict__ k, uint4* __restrict__ v,
+                                                         float* __restrict__ ks, float* __restrict__ vs, int n_kv,
+                                                         int max_seq, int from) {
+    constexpr int kU = kHeadDim / 16;  // 16-byte units per row
+    const size_t rows = static_cast<size_t>(max_seq - from);
+    const size_t total = rows * n_kv * kU;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const size_t h = i / (rows * kU);
+        const size_t r = (i - h * rows * kU) / kU;
+        const size_t u = i % kU;
+        const size_t crow = h * max_seq + from + r;
+        k[crow * kU + u] = make_uint4(0u, 0u, 0u, 0u);
+        v[crow * kU + u] = make_uint4(0u, 0u, 0u, 0u);
+        if (u < 2) {
+            ks[crow * 2 + u] = 1.0f;
+            vs[crow * 2 + u] = 1.0f;
+        }
+    }
+}
+
+template <int G, bool Q8>
+struct VerifyAttnK {
+    static auto fn() { return verify_attn_partial_kernel<G, Q8>; }
+};
+
 // Work buffer layout of a verify pass of up to n tokens (offsets in floats).
 struct VerifyWork {
     size_t H, X, QKV, Q, part, att, O, GU, S, keys, total;
@@ -1078,21 +1212,47 @@ extern "C" size_t asdsl_attention_work_floats(int n_heads, int max_seq) {
     return n_heads > 0 && max_seq > 0 ? attn_decode_work_floats(n_heads, max_seq) : 0;
 }
 
+namespace {
+asdsl_status check_attention_args(const char* what, const void* qkv, const void* k_cache, const void* v_cache,
+                                  const void* rope_cos, const void* rope_sin, const void* pos, const void* att_out,
+                                  const void* work, int n_heads, int n_kv_heads, int head_dim, int rotary_dim,
+                                  int max_seq) {
+    ASDSL_CHECK_ARG(qkv && k_cache && v_cache && rope_cos && rope_sin && pos && att_out && work,
+                    "%s: null pointer", what);
+    ASDSL_CHECK_ARG(head_dim == kHeadDim, "%s: head_dim must be 128", what);
+    ASDSL_CHECK_ARG(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 4,
+                    "%s: n_heads must be a multiple (1..4x) of n_kv_heads", what);
+    ASDSL_CHECK_ARG(rotary_dim > 0 && rotary_dim % 2 == 0 && rotary_dim <= head_dim,
+                    "%s: rotary_dim must be even and <= head_dim", what);
+    ASDSL_CHECK_ARG(max_seq > 0, "%s: max_seq must be positive", what);
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && reinterpret_cast<uintptr_t>(v_cache) % 16 == 0,
+                    "%s: caches must be 16-byte aligned", what);
+    return ASDSL_OK;
+}
+}  // namespace
+
 extern "C" asdsl_status asdsl_attention_f16kv(const float* qkv, uint16_t* k_cache, uint16_t* v_cache,
                                               const float* rope_cos, const float* rope_sin, const int* pos,
                                               float* att_out, float* work, int n_heads, int n_kv_heads,
                                               int head_dim, int rotary_dim, int max_seq, asdsl_stream_t stream) {
-    ASDSL_CHECK_ARG(qkv && k_cache && v_cache && rope_cos && rope_sin && pos && att_out && work,
-                    "attention_f16kv: null pointer");
-    ASDSL_CHECK_ARG(head_dim == kHeadDim, "attention_f16kv: head_dim must be 128");
-    ASDSL_CHECK_ARG(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 4,
-                    "attention_f16kv: n_heads must be a multiple (1..4x) of n_kv_heads");
-    ASDSL_CHECK_ARG(rotary_dim > 0 && rotary_dim % 2 == 0 && rotary_dim <= head_dim,
-                    "attention_f16kv: rotary_dim must be even and <= head_dim");
-    ASDSL_CHECK_ARG(max_seq > 0, "attention_f16kv: max_seq must be positive");
-    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && reinterpret_cast<uintptr_t>(v_cache) % 16 == 0,
-                    "attention_f16kv: caches must be 16-byte aligned");
-    return launch_attention_decode(qkv, k_cache, v_cache, rope_cos, rope_sin, pos, att_out, work, n_heads, n_kv_heads,
+    const asdsl_status cs = check_attention_args("attention_f16kv", qkv, k_cache, v_cache, rope_cos, rope_sin, pos,
+                                                 att_out, work, n_heads, n_kv_heads, head_dim, rotary_dim, max_seq);
+    if (cs != ASDSL_OK) return cs;
+    const KvCache kv{k_cache, v_cache, nullptr, nullptr};
+    return launch_attention_decode(qkv, kv, false, rope_cos, rope_sin, pos, att_out, work, n_heads, n_kv_heads,
+                                   rotary_dim / 2, max_seq, max_seq, false, as_hip(stream));
+}
+
+extern "C" asdsl_status asdsl_attention_q8kv(const float* qkv, int8_t* k_cache, int8_t* v_cache, float* k_scale,
+                                             float* v_scale, const float* rope_cos, const float* rope_sin,
+                                             const int* pos, float* att_out, float* work, int n_heads, int n_kv_heads,
+                                             int head_dim, int rotary_dim, int max_seq, asdsl_stream_t stream) {
+    const asdsl_status cs = check_attention_args("attention_q8kv", qkv, k_cache, v_cache, rope_cos, rope_sin, pos,
+                                                 att_out, work, n_heads, n_kv_heads, head_dim, rotary_dim, max_seq);
+    if (cs != ASDSL_OK) return cs;
+    ASDSL_CHECK_ARG(k_scale && v_scale, "attention_q8kv: null scale array");
+    const KvCache kv{k_cache, v_cache, k_scale, v_scale};
+    return launch_attention_decode(qkv, kv, true, rope_cos, rope_sin, pos, att_out, work, n_heads, n_kv_heads,
                                    rotary_dim / 2, max_seq, max_seq, false, as_hip(stream));
 }
 
@@ -1129,6 +1289,7 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
     static const int no_fold = env_knob("ASDSL_HIP_NO_COMBINE_FOLD");
     const int limit = pos_limit < m.max_seq ? pos_limit : m.max_seq;
     const bool fold = no_fold == 0 && attn_fold(limit, m.max_seq);
+    const bool q8 = m.kv_format == ASDSL_KV_INT8;
 
     // Layer 0's qkv GEMV reads the embedding row itself (and stores it to hA,
     // clearing the argmax key) when the table is 16-byte aligned; otherwise
@@ -1158,7 +1319,8 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
                                           m.hidden, m.gs_attn, m.rms_eps, nullptr, stream);
         }
         if (st != ASDSL_OK) return st;
-        st = launch_attention_decode(qkv, L.k_cache, L.v_cache, m.rope_cos, m.rope_sin, pos, att, part, m.n_heads,
+        const KvCache kv{L.k_cache, L.v_cache, L.k_scale, L.v_scale};
+        st = launch_attention_decode(qkv, kv, q8, m.rope_cos, m.rope_sin, pos, att, part, m.n_heads,
                                      m.n_kv_heads, m.rotary_dim / 2, m.max_seq, limit, fold, s);
         if (st != ASDSL_OK) return st;
         st = fold ? preq2_fused_combine(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, part, pos, kMaxSplits,
@@ -1228,6 +1390,7 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     const int q_dim = m.n_heads * m.head_dim;
     const int nsplit = attn_splits(m.max_seq);
     const int G = m.n_heads / m.n_kv_heads;
+    const bool q8 = m.kv_format == ASDSL_KV_INT8;
     // ASDSL_HIP_VERIFY_MFMA=1 lets the g32 projections take the MFMA batched
     // GEMV (faster from 4 columns on, but its fp32 summation order differs
     // from the single-token step's, so a column's int8 activations can round
@@ -1248,17 +1411,16 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         if (st != ASDSL_OK) return st;
         st = preq2_fused_batch(L.qkv_meta, L.qkv_quant, X, QKV, qkv_dim, m.hidden, m.gs_attn, n, stream, mfma);
         if (st != ASDSL_OK) return st;
-        st = launch("verify_rope_kv_kernel", verify_rope_kv_kernel, dim3(m.n_heads + m.n_kv_heads, n), dim3(kHeadDim),
-                    0, s, static_cast<const float*>(QKV), Q, L.k_cache, L.v_cache, m.rope_cos, m.rope_sin, pos,
-                    m.n_heads, m.n_kv_heads, m.max_seq, m.rotary_dim / 2);
+        const KvCache kv{L.k_cache, L.v_cache, L.k_scale, L.v_scale};
+        st = launch("verify_rope_kv_kernel", q8 ? verify_rope_kv_kernel<true> : verify_rope_kv_kernel<false>,
+                    dim3(m.n_heads + m.n_kv_heads, n), dim3(kHeadDim), 0, s, static_cast<const float*>(QKV), Q, kv,
+                    m.rope_cos, m.rope_sin, pos, m.n_heads, m.n_kv_heads, m.max_seq, m.rotary_dim / 2);
         if (st != ASDSL_OK) return st;
         const dim3 pgrid(nsplit, m.n_kv_heads, n);
-        switch (G) {
-            case 1: st = launch("verify_attn_partial_kernel", verify_attn_partial_kernel<1>, pgrid, dim3(kAttnThreads), 0, s, static_cast<const float*>(Q), static_cast<const uint16_t*>(L.k_cache), static_cast<const uint16_t*>(L.v_cache), pos, part, m.n_heads, m.max_seq, nsplit); break;
-            case 2: st = launch("verify_attn_partial_kernel", verify_attn_partial_kernel<2>, pgrid, dim3(kAttnThreads), 0, s, static_cast<const float*>(Q), static_cast<const uint16_t*>(L.k_cache), static_cast<const uint16_t*>(L.v_cache), pos, part, m.n_heads, m.max_seq, nsplit); break;
-            case 3: st = launch("verify_attn_partial_kernel", verify_attn_partial_kernel<3>, pgrid, dim3(kAttnThreads), 0, s, static_cast<const float*>(Q), static_cast<const uint16_t*>(L.k_cache), static_cast<const uint16_t*>(L.v_cache), pos, part, m.n_heads, m.max_seq, nsplit); break;
-            default: st = launch("verify_attn_partial_kernel", verify_attn_partial_kernel<4>, pgrid, dim3(kAttnThreads), 0, s, static_cast<const float*>(Q), static_cast<const uint16_t*>(L.k_cache), static_cast<const uint16_t*>(L.v_cache), pos, part, m.n_heads, m.max_seq, nsplit); break;
-        }
+        st = with_attn_kernel<VerifyAttnK>(G, q8, [&](auto kern) {
+            return launch("verify_attn_partial_kernel", kern, pgrid, dim3(kAttnThreads), 0, s,
+                          static_cast<const float*>(Q), kv, pos, part, m.n_heads, m.max_seq, nsplit);
+        });
         if (st != ASDSL_OK) return st;
         st = launch("attn_combine_kernel", attn_combine_kernel, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
                     static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0);
@@ -1302,4 +1464,21 @@ extern "C" asdsl_status asdsl_kv_zero_from(uint16_t* k_cache, uint16_t* v_cache,
     const unsigned grid = static_cast<unsigned>(total / 256 + 1 < 4096 ? total / 256 + 1 : 4096);
     return launch("kv_zero_kernel", kv_zero_kernel, dim3(grid), dim3(256), 0, as_hip(stream),
                   reinterpret_cast<uint4*>(k_cache), reinterpret_cast<uint4*>(v_cache), n_kv_heads, max_seq, from);
+}
+
+extern "C" asdsl_status asdsl_kv_zero_from_q8(int8_t* k_cache, int8_t* v_cache, float* k_scale, float* v_scale,
+                                              int n_kv_heads, int head_dim, int max_seq, int from_pos,
+                                              asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(k_cache && v_cache && k_scale && v_scale, "kv_zero_from_q8: null pointer");
+    ASDSL_CHECK_ARG(head_dim == kHeadDim, "kv_zero_from_q8: head_dim must be 128");
+    ASDSL_CHECK_ARG(n_kv_heads > 0 && max_seq > 0, "kv_zero_from_q8: invalid dimensions");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 && reinterpret_cast<uintptr_t>(v_cache) % 16 == 0,
+                    "kv_zero_from_q8: caches must be 16-byte aligned");
+    const int from = from_pos < 0 ? 0 : from_pos;
+    if (from >= max_seq) return ASDSL_OK;
+    const size_t total = static_cast<size_t>(max_seq - from) * (kHeadDim / 16) * n_kv_heads;
+    const unsigned grid = static_cast<unsigned>(total / 256 + 1 < 4096 ? total / 256 + 1 : 4096);
+    return launch("kv_zero_q8_kernel", kv_zero_q8_kernel, dim3(grid), dim3(256), 0, as_hip(stream),
+                  reinterpret_cast<uint4*>(k_cache), reinterpret_cast<uint4*>(v_cache), k_scale, v_scale, n_kv_heads,
+                  max_seq, from);
 }

@@ -52,7 +52,7 @@ typedef enum asdsl_status {
     ASDSL_ERR_UNSUPPORTED = 3       /* valid request outside what the kernels handle */
 } asdsl_status;
 
-#define ASDSL_ABI_VERSION 2
+#define ASDSL_ABI_VERSION 3
 
 /* Library identity and error text. No reference counterpart (pybind11 raises). */
 int asdsl_abi_version(void);
@@ -418,7 +418,7 @@ asdsl_status asdsl_gemv_preq2_rmsnorm_swiglu(const uint8_t* meta, const uint8_t*
                                              int ffn, int in_features, int group_size, float eps, float threshold,
                                              asdsl_stream_t stream);
 
-/* Floats of device work buffer asdsl_attention_f16kv needs. */
+/* Floats of device work buffer asdsl_attention_f16kv / _q8kv need. */
 size_t asdsl_attention_work_floats(int n_heads, int max_seq);
 
 /* RoPE + KV write + attention for one token at position *pos (device int):
@@ -436,6 +436,23 @@ asdsl_status asdsl_attention_f16kv(const float* qkv, uint16_t* k_cache, uint16_t
                                    float* att_out, float* work, int n_heads, int n_kv_heads,
                                    int head_dim, int rotary_dim, int max_seq, asdsl_stream_t stream);
 
+/* The same with the reference's cache form: int8 codes [n_kv_heads][max_seq][128]
+ * and one fp32 scale per 64 dims, k_scale/v_scale [n_kv_heads][max_seq][2].
+ * The new k and v are quantized per 64-dim block as set_kv_cache does
+ * (scale = amax * (1/127), or 1e-12 when amax <= 1e-12; code =
+ * round-half-even(x / scale) clamped to [-127, 127]) and every K/V element
+ * of the attention, the new row's included, is float(code) * scale.
+ * Replaces rope_apply_inplace + set_kv_cache + compute_attention_flash_q8
+ * (unified_engine.cpp:768-801,859-1027). */
+asdsl_status asdsl_attention_q8kv(const float* qkv, int8_t* k_cache, int8_t* v_cache, float* k_scale,
+                                  float* v_scale, const float* rope_cos, const float* rope_sin, const int* pos,
+                                  float* att_out, float* work, int n_heads, int n_kv_heads, int head_dim,
+                                  int rotary_dim, int max_seq, asdsl_stream_t stream);
+
+/* KV cache forms of asdsl_decode_model.kv_format. */
+#define ASDSL_KV_FP16 0 /* fp16 rows */
+#define ASDSL_KV_INT8 1 /* int8 rows + fp32 scale per 64 dims (the reference's form) */
+
 /* Weights of one decoder layer (device pointers). */
 typedef struct asdsl_decode_layer {
     const uint8_t* qkv_meta;  const uint8_t* qkv_quant;   /* preq2, [(h + 2 kv) * 128] x hidden, gs_attn */
@@ -443,8 +460,11 @@ typedef struct asdsl_decode_layer {
     const uint8_t* gu_meta;   const uint8_t* gu_quant;    /* preq2, [gate ffn | up ffn] x hidden, gs_ffn */
     const uint8_t* down_meta; const uint8_t* down_quant;  /* preq2, hidden x ffn, gs_ffn */
     const float* rms_att;     const float* rms_ffn;       /* [hidden] */
-    uint16_t* k_cache;        uint16_t* v_cache;          /* fp16 [n_kv_heads][max_seq][128] */
+    void* k_cache;            void* v_cache;              /* [n_kv_heads][max_seq][128], fp16 or int8
+                                                             (kv_format), 16-byte aligned */
     float fatrelu_threshold;                              /* 0: plain SwiGLU */
+    float* k_scale;           float* v_scale;             /* int8 cache: fp32 [n_kv_heads][max_seq][2];
+                                                             unused (may be null) for fp16 */
 } asdsl_decode_layer;
 
 /* A Phi-4-shaped decoder (layers is a HOST array of n_layers entries). */
@@ -457,6 +477,7 @@ typedef struct asdsl_decode_model {
     const float* rms_out;                                 /* [hidden] */
     const uint8_t* lm_meta;   const uint8_t* lm_quant;    /* preq2, vocab x hidden, gs_lm */
     const float* rope_cos;    const float* rope_sin;      /* fp32 [max_seq][rotary_dim/2] */
+    int kv_format;                                        /* ASDSL_KV_FP16 or ASDSL_KV_INT8 */
 } asdsl_decode_model;
 
 /* Bytes of device work buffer asdsl_decode_token needs (0 for an invalid model). */
@@ -500,6 +521,12 @@ size_t asdsl_decode_verify_work_bytes(const asdsl_decode_model* model, int max_t
  * back to serial forward_token calls. */
 asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, const int* tokens, int n_tokens, const int* pos,
                                  float* logits, int* next_tokens, void* work, asdsl_stream_t stream);
+
+/* The int8 cache's form of asdsl_kv_zero_from: codes 0 and scales 1.0 in rows
+ * [from_pos, max_seq), as zero_kv_from leaves them
+ * (asdsl/kernels/native/unified_engine.cpp:1263-1283). */
+asdsl_status asdsl_kv_zero_from_q8(int8_t* k_cache, int8_t* v_cache, float* k_scale, float* v_scale,
+                                   int n_kv_heads, int head_dim, int max_seq, int from_pos, asdsl_stream_t stream);
 
 /* Zeroes rows [from_pos, max_seq) of every head of one layer's fp16 K and V
  * caches ([n_kv_heads][max_seq][head_dim], 16-byte aligned); from_pos < 0

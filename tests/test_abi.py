@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
     missing = [n for n in declared_entry_points() if not _hip.exported(n)]
     assert not missing, f"declared but not exported: {missing}"
-    assert _hip.LIB.asdsl_abi_version() == 2
+    assert _hip.LIB.asdsl_abi_version() == 3
 
 
 def test_python_signatures_cover_header():
@@ -108,3 +108,34 @@ def test_work_buffer_queries_and_checks_without_gpu():
     assert lib.asdsl_gemv_preq2_fused_batch_ws(one, one, one, one, 64, 3072, 32, 4, one, 100,
                                                None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
     assert "work buffer" in _hip.last_error()
+
+
+def test_decode_structs_match_the_header(tmp_path):
+    """The engine's ctypes mirrors of asdsl_decode_layer / asdsl_decode_model
+    have the header's field offsets and sizes (a C program built with gcc
+    from the header prints them)."""
+    import shutil
+    import subprocess
+
+    from asdsl.engine import _Layer, _Model
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    fields = {"asdsl_decode_layer": [n for n, _ in _Layer._fields_],
+              "asdsl_decode_model": [n for n, _ in _Model._fields_]}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "asdsl_hip.h"', "int main(void) {"]
+    for st, names in fields.items():
+        lines.append(f'printf("{st} %zu\\n", sizeof({st}));')
+        for n in names:
+            lines.append(f'printf("{st}.{n} %zu\\n", offsetof({st}, {n}));')
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-x", "c", f"-I{REPO / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                       text=True).stdout.splitlines())
+    for st, cls in (("asdsl_decode_layer", _Layer), ("asdsl_decode_model", _Model)):
+        assert int(got[st]) == ctypes.sizeof(cls), st
+        for n in fields[st]:
+            assert int(got[f"{st}.{n}"]) == getattr(cls, n).offset, (st, n)
