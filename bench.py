@@ -54,11 +54,12 @@ LAYER = [("qkv", 5120, 3072), ("o_proj", 3072, 3072), ("gate_up", 16384, 3072), 
 GS = 32
 LM_HEAD = (200064, 3072, 128)
 # HBM bytes per gate_up launch measured by rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on `bench.py --pmc-probe`, each scaled by the same counter on a
-# 64 MiB device copy (fetch x1.9993, write x1.0); see
-# profiles/preq2_gemv_phi4_layer_g32.md.  A property of the kernel's access
-# pattern: re-measure when the kernel's loads change.
-GATE_UP_TRAFFIC_BYTES = 31_681_704
+# WRITE_SIZE on `bench.py --pmc-probe gate_up` at commit 343f414 (median of
+# 50 dispatches: 31,615,144 fetched + 65,536 written), each scaled by the same
+# counter on a 64 MiB device copy (fetch x1.9993, write x1.0); see
+# profiles/hbm_traffic_gemv_decode_sparse_down.md.  A property of the
+# kernel's access pattern: re-measure when the kernel's loads change.
+GATE_UP_TRAFFIC_BYTES = 31_680_680
 
 
 def gemv_bytes(M: int, K: int, gs: int = GS) -> int:
@@ -117,15 +118,76 @@ def build_layers(n_layers: int, seed: int):
     return layers, xs, ys
 
 
-def cpu_baseline(layers, xs, ys_gpu, seconds: float):
+def cpu_topology() -> dict:
+    """The host CPU as the CPU baselines see it: lscpu's physical cores
+    (distinct core/socket pairs), logical CPUs, the CPUs this process may
+    run on, and the cgroup CPU quota when one is set."""
+    import subprocess
+
+    info = {"logical_cpus": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0)), "physical_cores": None}
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, timeout=20,
+                             check=True).stdout
+        info["physical_cores"] = len({ln for ln in out.splitlines() if ln and not ln.startswith("#")})
+        name = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20, check=True).stdout
+        for ln in name.splitlines():
+            if ln.startswith("Model name:"):
+                info["model"] = ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if quota != "max":
+            info["cgroup_cpu_quota"] = int(quota) / int(period)
+    except (OSError, ValueError):
+        pass
+    return info
+
+
+def cpu_thread_counts(topo: dict) -> list[int]:
+    """The reference protocol's two thread counts: every physical core the
+    process may use, and 12 (the reference's own runs); distinct."""
+    usable = topo["usable_cpus"]
+    allc = min(topo["physical_cores"] or usable, usable)
+    return sorted({allc, min(12, usable)}, reverse=True)
+
+
+def omp_runtime():
+    """The OpenMP runtime of the reference's compiled kernels (oracle/_ref is
+    built with g++ -fopenmp, so libgomp): its parallel regions take the
+    calling thread's omp_set_num_threads."""
+    lib = ctypes.CDLL("libgomp.so.1")
+    lib.omp_get_max_threads.restype = ctypes.c_int
+    lib.omp_set_num_threads.argtypes = [ctypes.c_int]
+    return lib
+
+
+def _median_timed(fn, warm: int, iters: int, min_seconds: float) -> tuple[float, int]:
+    """warm untimed calls, then at least `iters` timed calls (and at least
+    min_seconds of them); returns (median seconds per call, calls timed)."""
+    for _ in range(warm):
+        fn()
+    times = []
+    t_begin = time.perf_counter()
+    while len(times) < iters or time.perf_counter() - t_begin < min_seconds:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(layers, xs, ys_gpu, seconds: float, topo: dict):
     """Reference CPU path (oracle/_ref) over the same rotated layers as the GPU
     (so the host's last-level cache cannot hold the weights); layer 0's
-    outputs double as a parity spot check."""
+    outputs double as a parity spot check.  One run per thread count
+    (cpu_thread_counts): 3 warm-up steps, then at least 10 timed steps and
+    seconds / (number of counts) of them; the median step time."""
     sys.path.insert(0, str(REPO))
     import oracle
 
     host = [{n: (m.cpu().numpy(), q.cpu().numpy()) for n, (m, q) in layer.items()} for layer in layers]
     xh = {n: x.cpu().numpy() for n, x in xs.items()}
+    ng = None
     if oracle.reference_available("_native_gemv"):
         ng = oracle.load_reference("_native_gemv")
         kind = "reference"
@@ -144,27 +206,116 @@ def cpu_baseline(layers, xs, ys_gpu, seconds: float):
     for n, M, K in LAYER:
         g = ys_gpu[n]
         parity[n] = float(np.linalg.norm(g - ys[n]) / np.linalg.norm(ys[n]))
-    t0 = time.perf_counter()
-    steps = 0
-    while True:
-        li = steps % len(host)
+    step_bytes = sum(gemv_bytes(M, K) for _, M, K in LAYER)
+    omp = omp_runtime() if kind == "reference" else None
+    omp_default = omp.omp_get_max_threads() if omp else 1
+    counts = cpu_thread_counts(topo) if omp else [1]
+    cursor = [0]
+
+    def one_step():
+        li = cursor[0] % len(host)
+        cursor[0] += 1
         for n, M, K in LAYER:
             run(li, n, M, K, ys[n])
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    step_bytes = sum(gemv_bytes(M, K) for _, M, K in LAYER)
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)) if kind == "reference" else 1
+
+    runs = []
+    for nt in counts:
+        if omp:
+            omp.omp_set_num_threads(nt)
+        med, n_timed = _median_timed(one_step, 3, 10, seconds / len(counts))
+        runs.append({"threads": nt, "median_ms_per_step": round(1e3 * med, 3),
+                     "GB/s": round(step_bytes / med / 1e9, 3), "steps_timed": n_timed})
+    if omp:
+        omp.omp_set_num_threads(omp_default)
+    head = runs[0]
     return {
-        "value": round(step_bytes * steps / el / 1e9, 3),
+        "value": head["GB/s"],
         "unit": "GB/s",
-        "cores": threads,
+        "cores": head["threads"],
         "kind": kind,
-        "sample": f"{steps} steps of one layer's 4 preq2 g32 GEMVs (gemv_preq2_fused_avx2, OpenMP) "
-                  f"rotating over {len(host)} layers ({len(host) * step_bytes / 1e9:.2f} GB) "
-                  f"in {el:.1f} s, ms_per_step={1e3 * el / steps:.3f}",
+        "sample": f"one layer's 4 preq2 g32 GEMVs (gemv_preq2_fused_avx2, OpenMP) per step, rotating over "
+                  f"{len(host)} layers ({len(host) * step_bytes / 1e9:.2f} GB); per thread count 3 warm-up "
+                  f"and >= 10 timed steps over ~{seconds / len(counts):.0f} s, median",
+        "runs": runs,
+        "host": topo,
+        "omp_max_threads_default": omp_default,
+        "reference_get_num_threads": int(ng.get_num_threads()) if ng is not None else None,
     }, parity
+
+
+def cpu_decode_baseline(eng, topo: dict, ctx: int = 128, warm: int = 3, iters: int = 10) -> dict | None:
+    """The reference's own decode step, UnifiedEngine::forward_token
+    (unified_engine.cpp:1339-1688, compiled into oracle/_ref), at ctx on the
+    host cores: the GPU engine's shape, its qkv/o preq2 g32 weights and its
+    embedding (also the tied output projection, which the reference
+    quantizes to Q4_128 at load: lm_head_group_size 128), gate_up/down as
+    Q4_128 blocks of separately drawn N(0, 0.02) weights (the reference's
+    g128 MLP path, ASDSL_C01=1), its int8 KV cache.  Median of `iters`
+    tokens after `warm`, per thread count (cpu_thread_counts)."""
+    import torch
+
+    sys.path.insert(0, str(REPO))
+    import oracle
+    from asdsl.quantization.synthetic import q4_128_from_weights_torch
+
+    if not oracle.reference_available("_native_unified"):
+        return None
+    ue = oracle.load_reference("_native_unified")
+    c = eng.cfg
+    max_seq = ctx + warm + iters + 8
+
+    def host(t):
+        return t.cpu().numpy()
+
+    gen = torch.Generator(device="cuda").manual_seed(12345)
+    layers = {}
+    for li, L in enumerate(eng.layers):
+        R = {"rms_att": host(L["rms_att"]), "rms_ffn": host(L["rms_ffn"])}
+        for n, name in (("qkv", "qkv_proj"), ("o", "o_proj")):
+            R[name + "_meta"], R[name + "_quant"] = host(L[n][0]), host(L[n][1])
+        for name, M, K in (("gate_up_proj", 2 * c.ffn, c.hidden), ("down_proj", c.hidden, c.ffn)):
+            w = torch.randn((M, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+            R[name + "_g128"] = host(q4_128_from_weights_torch(w))
+            del w
+        # the engine binds a preq-block array per projection; this profile
+        # never reads them (zero pages, not resident)
+        for name, M, K in (("qkv_proj", c.qkv_dim, c.hidden), ("o_proj", c.hidden, c.hidden),
+                           ("gate_up_proj", 2 * c.ffn, c.hidden), ("down_proj", c.hidden, c.ffn)):
+            R[name] = np.zeros(M * K // 32 * 20, np.uint8)
+        layers[li] = R
+    embed = host(eng.embed)
+    ec = ue.EngineConfig()
+    ec.num_layers, ec.hidden_size, ec.num_heads, ec.num_kv_heads = c.n_layers, c.hidden, c.n_heads, c.n_kv_heads
+    ec.head_dim, ec.intermediate_size, ec.vocab_size, ec.rms_norm_eps = c.head_dim, c.ffn, c.vocab, c.rms_eps
+    ec.group_size, ec.lm_head_group_size, ec.max_seq_len = 32, 128, max_seq
+    ec.rotary_dim, ec.weight_format = c.rotary_dim, 0
+    os.environ["ASDSL_C01"] = "1"
+    t0 = time.perf_counter()
+    engine = ue.UnifiedEngine(ec, embed, host(eng.rms_out), embed, host(eng.rope_cos)[:max_seq].copy(),
+                              host(eng.rope_sin)[:max_seq].copy(), layers)
+    load_s = time.perf_counter() - t0
+    omp = omp_runtime()
+    omp_default = omp.omp_get_max_threads()
+    runs = []
+    for nt in cpu_thread_counts(topo):
+        omp.omp_set_num_threads(nt)
+        pos = [ctx]
+
+        def one_token():
+            engine.forward_token(1, pos[0])
+            pos[0] += 1
+
+        med, n_timed = _median_timed(one_token, warm, iters, 0.0)
+        runs.append({"threads": nt, "median_ms_per_token": round(1e3 * med, 2),
+                     "tokens_per_s": round(1.0 / med, 3), "tokens_timed": n_timed})
+    omp.omp_set_num_threads(omp_default)
+    del engine, layers, embed
+    head = runs[0]
+    return {"value": head["tokens_per_s"], "unit": "tokens/s", "cores": head["threads"], "kind": "reference",
+            "sample": f"UnifiedEngine::forward_token (oracle/_ref, ASDSL_C01=1: qkv/o preq2 g32, gate_up/down/"
+                      f"lm_head Q4_128, int8 KV) at positions {ctx}.. of the 32-layer vocab-{c.vocab} model; "
+                      f"{warm} warm-up and {iters} timed tokens per thread count, median",
+            "runs": runs, "load_s": round(load_s, 1), "host": topo, "omp_max_threads_default": omp_default}
 
 
 def lm_head_kernel(lib, capture, timed_replays):
@@ -233,14 +384,17 @@ def stream_floor_us(lib, nbytes: int, launches: int = 64) -> dict:
 
 # --------------------------------------------------------------------------- decode
 def decode_tokens_per_s(contexts=(128, 1024, 4096), steps: int = 64, n_layers: int = 32, seed: int = 11,
-                        with_verify: bool = True):
+                        with_verify: bool = True, cpu_topo: dict | None = None, int8_kv: bool = True):
     """Greedy batch-1 decode of a Phi-4-shaped model (32 layers, hidden 3072,
     FFN 8192, vocab 200064, 24/8 heads, head_dim 128; qkv/o preq2 g32,
     gate_up/down/lm_head preq2 g128; random weights) at each context length:
     the KV cache holds `ctx` random fp16 positions, then `steps` captured
     steps replay back to back (each consumes the previous step's argmax and
     advances the position).  bytes/token = every weight once + the K/V rows
-    read (fp16) + one embedding row + the logits."""
+    read (fp16) + one embedding row + the logits.  int8_kv: the same steps
+    over the reference's int8 cache form (per_ctx_int8_kv).  cpu_topo: also
+    time the reference's own engine on the host cores at ctx 128
+    (cpu_decode_baseline)."""
     import torch
 
     from asdsl.engine import DecodeConfig, DecodeEngine
@@ -248,7 +402,30 @@ def decode_tokens_per_s(contexts=(128, 1024, 4096), steps: int = 64, n_layers: i
     cfg = DecodeConfig(n_layers=n_layers, max_seq=max(contexts) + steps + 8)
     eng = DecodeEngine.synthetic(cfg, seed=seed)
     out = {"model": "phi4-shaped 32L h3072 ffn8192 v200064 24/8 heads, preq2 g32 attn / g128 mlp+lm_head, fp16 KV",
-           "weight_bytes": eng.weight_bytes(), "steps_per_ctx": steps, "per_ctx": {}}
+           "weight_bytes": eng.weight_bytes(), "steps_per_ctx": steps}
+    out["per_ctx"] = _decode_contexts(eng, contexts, steps)
+    if with_verify:
+        out["verify"] = verify_pass_us(eng, ctx=1024, per_token_us=out["per_ctx"].get("1024", {}).get("us_per_token"))
+    if cpu_topo is not None:
+        out["cpu_baseline"] = cpu_decode_baseline(eng, cpu_topo)
+    if int8_kv:
+        layers = [{k: v for k, v in L.items() if k not in ("k_cache", "v_cache")} for L in eng.layers]
+        q8 = DecodeEngine(DecodeConfig(n_layers=n_layers, max_seq=cfg.max_seq, kv_format="int8"), layers, eng.embed,
+                          eng.rms_out, eng.lm_meta, eng.lm_quant)
+        del eng
+        torch.cuda.empty_cache()
+        out["per_ctx_int8_kv"] = _decode_contexts(q8, contexts, steps)
+        eng = q8
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
+def _decode_contexts(eng, contexts, steps: int) -> dict:
+    """Captured greedy steps at each context (see decode_tokens_per_s)."""
+    import torch
+
+    res = {}
     for ctx in contexts:
         eng.prefill_kv_random(ctx, seed=ctx)
         eng.token.fill_(1)
@@ -269,16 +446,12 @@ def decode_tokens_per_s(contexts=(128, 1024, 4096), steps: int = 64, n_layers: i
         bpt = eng.bytes_per_token(mid)
         tps = 1e6 / us
         ideal = HBM_PEAK_GBS * 1e9 / bpt
-        out["per_ctx"][str(ctx)] = {"us_per_token": round(us, 2), "tokens_per_s": round(tps, 1),
-                                    "bytes_per_token": bpt, "GB/s": round(bpt / (us * 1e-6) / 1e9, 1),
-                                    "roofline_tokens_per_s": round(ideal, 1), "frac_of_roofline": round(tps / ideal, 4),
-                                    "final_pos": int(eng.pos.item())}
-        eng._graph = None
-    if with_verify:
-        out["verify"] = verify_pass_us(eng, ctx=1024, per_token_us=out["per_ctx"].get("1024", {}).get("us_per_token"))
-    del eng
-    torch.cuda.empty_cache()
-    return out
+        res[str(ctx)] = {"us_per_token": round(us, 2), "tokens_per_s": round(tps, 1),
+                         "bytes_per_token": bpt, "GB/s": round(bpt / (us * 1e-6) / 1e9, 1),
+                         "roofline_tokens_per_s": round(ideal, 1), "frac_of_roofline": round(tps / ideal, 4),
+                         "final_pos": int(eng.pos.item())}
+        eng._graphs.clear()
+    return res
 
 
 def verify_pass_us(eng, ctx: int, per_token_us, counts=(4, 8, 16), reps: int = 20) -> dict:
@@ -812,6 +985,65 @@ def repack_rows(args, oracle) -> list:
     return out
 
 
+def _copy_reference() -> int:
+    """50 plain 64 MiB device copies: what FETCH_SIZE / WRITE_SIZE read for a
+    known byte count."""
+    import torch
+
+    src = torch.ones(16 << 20, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(50):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return src.numel() * 4
+
+
+def pmc_probe(mode: str) -> int:
+    """Kernels for a rocprofv3 --pmc pass (see --pmc-probe), then the copy
+    reference; one JSON line naming what ran."""
+    import torch
+
+    from asdsl import _hip
+
+    lib = _hip.LIB
+    h = int(torch.cuda.current_stream().cuda_stream)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    info = {"pmc_probe": mode}
+    if mode == "sparse_down":
+        IN, OUT = 8192, 3072
+        xs_ = torch.clamp(torch.randn(IN, generator=gen, device="cuda") - 0.841621, min=0.0)
+        rows = torch.nonzero(xs_).to(torch.int32).view(-1).contiguous()
+        na = int(rows.numel())
+        copies = [{"w": _dev_bytes(IN * OUT // 2, gen), "s": _dev_f32(IN * OUT // 32, gen, 0.01, 1e-3),
+                   "b": _dev_f32(IN * OUT // 32, gen, -0.08, 0.0)} for _ in range(8)]
+        y = torch.empty(OUT, device="cuda")
+        work = torch.empty(lib.asdsl_sparse_down_work_bytes(OUT), dtype=torch.uint8, device="cuda")
+        P = _hip.ptr
+        for i in range(50):
+            c = copies[i % len(copies)]
+            _hip.check(lib.asdsl_sparse_down_proj_T_ws(P(c["w"]), P(c["s"]), P(c["b"]), P(xs_), P(rows), na, P(y),
+                                                       IN, OUT, 32, P(work), work.numel(), h),
+                       "asdsl_sparse_down_proj_T_ws")
+        torch.cuda.synchronize()
+        info.update(active_rows=na, algorithmic_bytes=na * (OUT // 2 + 2 * (OUT // 32) * 4 + 8) + 4 * OUT)
+    else:
+        from asdsl.engine import DecodeConfig, DecodeEngine
+
+        ctx = 128 if mode == "decode128" else 4096
+        eng = DecodeEngine.synthetic(DecodeConfig(max_seq=ctx + 16), seed=11)
+        eng.prefill_kv_random(ctx, seed=ctx)
+        eng.token.fill_(1)
+        for i in range(4):
+            eng._queue_step(h, eng._pos_limit(ctx + i))
+        torch.cuda.synchronize()
+        info.update(ctx=ctx, steps=4, bytes_per_token=eng.bytes_per_token(ctx))
+        del eng
+        torch.cuda.empty_cache()
+    info["copy_bytes"] = _copy_reference()
+    print(json.dumps(info), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -829,9 +1061,12 @@ def main() -> int:
     ap.add_argument("--cpu-seconds-per-row", type=float, default=1.0)
     ap.add_argument("--rows", default="", help="--suite: only rows whose name contains one of these "
                                                 "comma-separated strings")
-    ap.add_argument("--pmc-probe", action="store_true",
-                    help="for rocprofv3 --pmc runs: 50 gate_up GEMVs over rotated weights, then 50 plain "
-                         "64 MiB device copies (the counter scale reference); prints nothing else")
+    ap.add_argument("--pmc-probe", nargs="?", const="gate_up", default=None,
+                    choices=["gate_up", "sparse_down", "decode128", "decode4096"],
+                    help="for rocprofv3 --pmc runs: the named kernels (gate_up: 50 g32 GEMVs over rotated "
+                         "weights; sparse_down: 50 FATReLU down-projections at 80%% zeros over rotated "
+                         "weights; decode128/decode4096: 4 eager 32-layer decode steps at that context), "
+                         "then 50 plain 64 MiB device copies (the counter scale reference)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this GEMV path runs on a "
@@ -840,10 +1075,13 @@ def main() -> int:
 
     if args.suite:
         return run_suite(args)
+    if args.pmc_probe and args.pmc_probe != "gate_up":
+        return pmc_probe(args.pmc_probe)
     if args.decode:
         import torch  # noqa: F401
 
-        print(json.dumps({"decode": decode_tokens_per_s()}), flush=True)
+        topo = None if args.no_cpu else cpu_topology()
+        print(json.dumps({"decode": decode_tokens_per_s(cpu_topo=topo)}), flush=True)
         return 0
 
     import torch
@@ -857,7 +1095,7 @@ def main() -> int:
     ptrs = [{n: (_hip.ptr(m), _hip.ptr(q)) for n, (m, q) in L.items()} for L in layers]
     xp = {n: _hip.ptr(x) for n, x in xs.items()}
     yp = {n: _hip.ptr(y) for n, y in ys.items()}
-    if args.pmc_probe:
+    if args.pmc_probe == "gate_up":
         n, M, K = LAYER[2]
         for i in range(50):
             p = ptrs[i % len(ptrs)]
@@ -942,12 +1180,13 @@ def main() -> int:
         lm["frac_of_floor"] = round(lf["us"] / lm["kernel_us"], 4)
 
     cpu, parity = (None, None)
+    topo = None if args.no_cpu else cpu_topology()
     if not args.no_cpu:
-        cpu, parity = cpu_baseline(layers, xs, ys_host, args.cpu_seconds)
+        cpu, parity = cpu_baseline(layers, xs, ys_host, args.cpu_seconds, topo)
     if not args.no_decode:
         del layers
         torch.cuda.empty_cache()
-        extra["decode"] = decode_tokens_per_s()
+        extra["decode"] = decode_tokens_per_s(cpu_topo=topo)
 
     out = {
         "metric": METRIC,
