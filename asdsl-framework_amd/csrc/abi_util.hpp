@@ -93,13 +93,13 @@ asdsl_status preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const 
 
 // The decode step's o_proj: gemv_preq2_fused of the attention output, which
 // the GEMV's prologue merges itself from the split partials (part: per head
-// nsplit rows of part_stride floats, m, l, acc[head_dim]) when the position
-// *pos has at most `fold` (<= 4) splits of `split` positions; then the
-// combine kernel skipped that position and `att` is not read.  Otherwise
-// `att` holds the merged output.  Same bits either way.
+// nsplit rows of part_stride floats, m, l, acc[head_dim]) of a position
+// *pos in [0, max_seq): nt = pos / tile + 1 tiles in splits of
+// ceil(nt / max_splits) tiles (max_splits <= 8).  A position outside the
+// cache reads `att` (the attention kernel zeroed it).
 asdsl_status preq2_fused_combine(const uint8_t* meta, const uint8_t* quant, const float* att, float* y,
                                  int out_features, int in_features, int group_size, const float* part, const int* pos,
-                                 int nsplit, int split, int part_stride, int head_dim, int max_seq, int fold,
+                                 int nsplit, int tile, int max_splits, int part_stride, int head_dim, int max_seq,
                                  asdsl_stream_t stream);
 
 // The decode step's first qkv GEMV: the RMSNorm prologue reads h as the fp16

@@ -262,7 +262,7 @@ __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16]
 // 0-1: the key's blocks, 2-3: the value's), leaves the dequantized values in
 // kv_new (what a later step reads back) and, when `store`, writes the codes
 // and the scale to cache row `row`.
-static_assert(kAttnThreads == 4 * kWave, "kv_quantize_new: one wave per 64-dim block of K and V");
+// (called by the first four waves of a workgroup)
 __device__ __forceinline__ void kv_quantize_new(float (*kv_new)[kHeadDim], const KvCache& kv, size_t row,
                                                 bool store) {
     const int tid = static_cast<int>(threadIdx.x);
@@ -483,45 +483,65 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
 }
 
 // ------------------------------------------------------------ decode attention
-// The short-context step's attention: workgroup (s, kvh) covers split s of
-// the KV head's positions, tps consecutive tiles of 64 positions (tps = 1
-// below 2048 positions), with the next tile's K/V rows requested before the
-// current tile is used and a running (max, sum, P.V) per wave; the four
-// waves merge in LDS and the partial (m, l, acc) of each query head is
-// stored for the o_proj GEMV's prologue, which merges the splits (at most
-// 4: positions below 256).  The launch covers only the splits of the
-// positions it serves; a position outside the cache gives zero output.
-constexpr int kMaxSplits = 32;
-constexpr int kTile = 64;
+// The short-context step's attention, whose split partials the o_proj
+// GEMV's prologue merges (no combine launch).  Workgroup (s, kvh) of WAVES
+// waves covers split s of the KV head's positions: tps consecutive tiles of
+// tile = 16 * WAVES positions (a wave takes 4 positions per step, 4 steps a
+// tile), at most max_splits splits, the next tile's K/V rows requested
+// before the current tile is used and a running (max, sum, P.V) per wave;
+// the waves merge in LDS and the partial (m, l, acc) of each query head is
+// stored.  Used below 256 positions: 4 waves, tiles of 64, at most 4 splits
+// of one tile.  Beyond, the partial kernel over 64-position splits and the
+// combine kernel: a folded form for long contexts (8 waves, tiles of 128,
+// at most 8 splits merged in the prologue) measured slower, 1436 against
+// 1275 us per 32-layer step at ctx 4096 and 1167 against 1150 at 1024, as
+// its 56-64 workgroups keep only two tiles each in flight.  The launch
+// covers only the splits of the positions it serves; a position outside the
+// cache gives zero output.
+constexpr int kMaxSplits = 32;  // partial rows reserved per query head
+constexpr int kShortLimit = 256;
+struct FoldForm {
+    int waves, tile, max_splits;
+};
+constexpr FoldForm kShortForm{4, 64, 4};
+static_assert(kShortForm.max_splits <= 8, "o_proj's prologue folds at most 8 splits");
 
-__host__ __device__ inline int attn_tiles_per_split(int pos) {
-    const int nt = pos / kTile + 1;
-    return (nt + kMaxSplits - 1) / kMaxSplits;
+__host__ __device__ inline int attn_fold_tps(int pos, int tile, int max_splits) {
+    const int nt = pos / tile + 1;
+    return (nt + max_splits - 1) / max_splits;
 }
 
-__host__ __device__ inline int attn_nsplit(int pos) {
-    const int nt = pos / kTile + 1;
-    const int tps = attn_tiles_per_split(pos);
+__host__ __device__ inline int attn_fold_splits(int pos, int tile, int max_splits) {
+    const int nt = pos / tile + 1;
+    const int tps = (nt + max_splits - 1) / max_splits;
     return (nt + tps - 1) / tps;
 }
 
+// Positions below pos_limit take the folded form when pos_limit <= 256.
+bool attn_fold(int pos_limit) { return pos_limit <= kShortLimit; }
+
 // Most splits any position below pos_limit uses (the launch's grid.x).
-int attn_max_splits(int pos_limit) {
+int attn_max_splits(int pos_limit, const FoldForm& f) {
     int best = 1;
-    for (int nt = 1; (nt - 1) * kTile < pos_limit && nt <= kMaxSplits * 4; ++nt) {
-        const int tps = (nt + kMaxSplits - 1) / kMaxSplits;
+    for (int nt = 1; (nt - 1) * f.tile < pos_limit; ++nt) {
+        const int tps = (nt + f.max_splits - 1) / f.max_splits;
         best = max(best, (nt + tps - 1) / tps);
+        if (best == f.max_splits) break;
     }
     return best;
 }
 
-template <int G, bool Q8>
-__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
+template <int G, bool Q8, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
     const float* __restrict__ qkv, KvCache kv,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
-    float* __restrict__ part, float* __restrict__ att, int n_heads, int n_kv, int max_seq, int rot_half) {
-    constexpr int kWaves = kAttnThreads / kWave;
-    constexpr int kIt = kTile / 16;
+    float* __restrict__ part, float* __restrict__ att, int n_heads, int n_kv, int max_seq, int rot_half,
+    int max_splits) {
+    constexpr int kWaves = WAVES;
+    constexpr int kThreads = WAVES * kWave;
+    constexpr int kTile = 16 * WAVES;  // positions per tile
+    constexpr int kStep = 4 * WAVES;   // positions per step of all waves
+    constexpr int kIt = kTile / kStep;
     __shared__ float q_s[G][kHeadDim];
     __shared__ float kv_new[2][kHeadDim];
     __shared__ float wml[kWaves][G][2];
@@ -532,11 +552,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) {  // outside the cache: zero output, nothing written to the cache
         if (s == 0)
-            for (int e = tid; e < G * kHeadDim; e += kAttnThreads) att[static_cast<size_t>(kvh * G) * kHeadDim + e] = 0.0f;
+            for (int e = tid; e < G * kHeadDim; e += kThreads) att[static_cast<size_t>(kvh * G) * kHeadDim + e] = 0.0f;
         return;
     }
-    const int tps = attn_tiles_per_split(pos);
-    const int ns = attn_nsplit(pos);
+    const int tps = attn_fold_tps(pos, kTile, max_splits);
+    const int ns = attn_fold_splits(pos, kTile, max_splits);
     if (s >= ns) return;
     const int p0 = s * tps * kTile;
     const int p1 = min(p0 + tps * kTile, pos + 1);
@@ -550,11 +570,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     // the first tile's K/V rows: loads complete in issue order.
     const float* cp = rope_cos + static_cast<size_t>(pos) * rot_half;
     const float* sp = rope_sin + static_cast<size_t>(pos) * rot_half;
-    constexpr int kRope = ((G + 1) * kHeadDim + kAttnThreads - 1) / kAttnThreads;
+    constexpr int kRope = ((G + 1) * kHeadDim + kThreads - 1) / kThreads;
     float rx[kRope][4];
 #pragma unroll
     for (int r = 0; r < kRope; ++r) {
-        const int e = tid + r * kAttnThreads;
+        const int e = tid + r * kThreads;
         const int hh = e / kHeadDim;
         const int d = e % kHeadDim;
         if (hh <= G) {
@@ -580,7 +600,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     auto load_tile = [&](int t0, uint4 (&kraw)[kIt], uint4 (&vraw)[kIt]) {
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
-            const int p = t0 + wave * 4 + pg + 16 * it;
+            const int p = t0 + wave * 4 + pg + kStep * it;
             const size_t row = row0 + (p < p1 ? p : p0);
             kraw[it] = kv_load8<Q8>(kv.k, kv.ks, row, dc);
             vraw[it] = kv_load8<Q8>(kv.v, kv.vs, row, dc);
@@ -591,7 +611,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
 
 #pragma unroll
     for (int r = 0; r < kRope; ++r) {
-        const int e = tid + r * kAttnThreads;
+        const int e = tid + r * kThreads;
         const int hh = e / kHeadDim;
         const int d = e % kHeadDim;
         if (hh <= G) {
@@ -609,7 +629,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     if (tid < kHeadDim) kv_new[1][tid] = Q8 ? vnew : h2f(f2h(vnew));
     __syncthreads();
     if constexpr (Q8) {
-        kv_quantize_new(kv_new, kv, row0 + pos, pos >= p0 && pos < p1);
+        if (wave < 4) kv_quantize_new(kv_new, kv, row0 + pos, pos >= p0 && pos < p1);
         __syncthreads();
     } else if (pos >= p0 && pos < p1 && tid < kHeadDim) {
         static_cast<uint16_t*>(kv.k)[(row0 + pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
@@ -644,7 +664,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
         float sr[kIt][G];
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
-            const int p = t0 + wave * 4 + pg + 16 * it;
+            const int p = t0 + wave * 4 + pg + kStep * it;
             float k8[8];
             row_of(kraw[it], 0, p, k8);
 #pragma unroll
@@ -676,7 +696,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
         }
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
-            const int p = t0 + wave * 4 + pg + 16 * it;
+            const int p = t0 + wave * 4 + pg + kStep * it;
             float v8[8];
             row_of(vraw[it], 1, p, v8);
 #pragma unroll
@@ -696,7 +716,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
         process_tile(t + kTile, kb, vb);
     }
 
-    // the wave's sums over its four position groups, then the four waves
+    // the wave's sums over its four position groups, then the waves
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
         l[hh] += swz_xor16(l[hh]);
@@ -722,7 +742,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     }
     __syncthreads();
     float* pbase = part + static_cast<size_t>(kvh * G) * kMaxSplits * kPartStride;
-    for (int e = tid; e < G * kHeadDim; e += kAttnThreads) {
+    for (int e = tid; e < G * kHeadDim; e += kThreads) {
         const int hh = e / kHeadDim;
         const int d = e % kHeadDim;
         float M = wml[0][hh][0];
@@ -758,28 +778,20 @@ asdsl_status launch_attention(const float* qkv, const KvCache& kv, bool q8, cons
                               int max_seq, hipStream_t s, int fold);
 
 // Floats of the decode attention's work area: kMaxSplits partial rows per
-// query head for the short-context form, then the partial rows of the
-// general form (one per 64 positions of max_seq).
+// query head for the folded forms, then the partial rows of the unfolded
+// form (one per 64 positions of max_seq).
 size_t attn_decode_work_floats(int n_heads, int max_seq) {
     return static_cast<size_t>(n_heads) * kMaxSplits * kPartStride +
            static_cast<size_t>(n_heads) * attn_splits(max_seq) * kPartStride;
 }
 
-// Positions below pos_limit take the short-context form when they use at
-// most kMaxFold (4) splits: the o_proj GEMV's prologue merges them, no
-// combine launch.  Otherwise the partial kernel over 64-position splits and
-// the combine kernel (up to eight groups of threads folding runs of splits
-// in parallel).  Merging in the attention kernel's last workgroup instead
-// (device-coherent partial stores, an atomic count, device-coherent loads)
-// measured slower than the combine launch: 13.2 us per layer at ctx 1024
-// against 8.0 + 4.0.
-bool attn_fold(int pos_limit, int max_seq) {
-    return attn_max_splits(pos_limit < max_seq ? pos_limit : max_seq) <= 4;
-}
-
-// work: attn_decode_work_floats.  fold: the short-context form (partials at
-// work, kMaxSplits rows per head, for the o_proj prologue); otherwise att
-// receives the merged output.
+// The unfolded form (the standalone attention entries, the verify pass and
+// ASDSL_HIP_NO_COMBINE_FOLD=1): the partial kernel over 64-position splits
+// and the combine kernel (up to eight groups of threads folding runs of
+// splits in parallel).  Merging in the attention kernel's last workgroup
+// instead (device-coherent partial stores, an atomic count, device-coherent
+// loads) measured slower than the combine launch: 13.2 us per layer at ctx
+// 1024 against 8.0 + 4.0.
 // The kernel instance for G query heads per KV head (1..4) and the cache
 // form: f(kernel) is called with the matching instantiation.
 template <template <int, bool> class K, typename F>
@@ -800,23 +812,30 @@ asdsl_status with_attn_kernel(int G, bool q8, F&& f) {
 }
 template <int G, bool Q8>
 struct DecodeAttnK {
-    static auto fn() { return attn_decode_kernel<G, Q8>; }
+    static auto fn() { return attn_decode_kernel<G, Q8, kShortForm.waves>; }
 };
 template <int G, bool Q8>
 struct PartialAttnK {
     static auto fn() { return attn_partial_kernel<G, Q8>; }
 };
 
+// work: attn_decode_work_floats.  fold: the folded form for positions below
+// pos_limit <= 256 (partials at work, kMaxSplits rows per head, for the
+// o_proj prologue); otherwise the unfolded form, att receiving the merged
+// output.
 asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q8, const float* rc, const float* rs,
                                      const int* pos, float* att, float* work, int n_heads, int n_kv, int rot_half,
                                      int max_seq, int pos_limit, bool fold, hipStream_t s) {
     if (!fold)
         return launch_attention(qkv, kv, q8, rc, rs, pos, att, work + static_cast<size_t>(n_heads) * kMaxSplits *
                                 kPartStride, n_heads, n_kv, rot_half, max_seq, s, 0);
-    const dim3 grid(attn_max_splits(pos_limit < max_seq ? pos_limit : max_seq), n_kv);
+    const int limit = pos_limit < max_seq ? pos_limit : max_seq;
+    const dim3 grid(attn_max_splits(limit, kShortForm), n_kv);
+    const dim3 block(kShortForm.waves * kWave);
+    const int max_splits = kShortForm.max_splits;
     return with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, [&](auto kern) {
-        return launch("attn_decode_kernel", kern, grid, dim3(kAttnThreads), 0, s, qkv, kv, rc, rs, pos, work, att,
-                      n_heads, n_kv, max_seq, rot_half);
+        return launch("attn_decode_kernel", kern, grid, block, 0, s, qkv, kv, rc, rs, pos, work, att, n_heads, n_kv,
+                      max_seq, rot_half, max_splits);
     });
 }
 
@@ -1283,12 +1302,13 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
     hipStream_t s = as_hip(stream);
     const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
     const int q_dim = m.n_heads * m.head_dim;
-    // The attention form follows pos_limit (attn_fold): below 256 o_proj's
+    // The attention form follows pos_limit (attn_fold): up to 256 o_proj's
     // prologue merges the splits, beyond the combine kernel does.
     // ASDSL_HIP_NO_COMBINE_FOLD=1 always takes the combine kernel.
     static const int no_fold = env_knob("ASDSL_HIP_NO_COMBINE_FOLD");
     const int limit = pos_limit < m.max_seq ? pos_limit : m.max_seq;
-    const bool fold = no_fold == 0 && attn_fold(limit, m.max_seq);
+    const bool fold = no_fold == 0 && attn_fold(limit);
+    const FoldForm& form = kShortForm;
     const bool q8 = m.kv_format == ASDSL_KV_INT8;
 
     // Layer 0's qkv GEMV reads the embedding row itself (and stores it to hA,
@@ -1324,7 +1344,7 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
                                      m.n_kv_heads, m.rotary_dim / 2, m.max_seq, limit, fold, s);
         if (st != ASDSL_OK) return st;
         st = fold ? preq2_fused_combine(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, part, pos, kMaxSplits,
-                                        kTile, kPartStride, kHeadDim, m.max_seq, 4, stream)
+                                        form.tile, form.max_splits, kPartStride, kHeadDim, m.max_seq, stream)
                   : asdsl_gemv_preq2_fused(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, stream);
         if (st != ASDSL_OK) return st;
         // gate_up with SwiGLU in its epilogue (gate and up rows in one

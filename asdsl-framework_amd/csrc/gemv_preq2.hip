@@ -65,7 +65,7 @@ constexpr int kThreads = 256;  // helper kernels
 //            argmax key) (load_embed_row_f32, unified_engine.cpp:181-197).
 enum class Pro { kPlain, kNorm, kSwiglu, kCombine, kNormEmbed };
 
-constexpr int kMaxFold = 4;  // kCombine: most splits merged in the prologue
+constexpr int kMaxFold = 8;  // kCombine: most splits merged in the prologue
 
 struct ProArgs {
     const float* delta = nullptr;
@@ -76,10 +76,12 @@ struct ProArgs {
     float eps = 0.0f;
     float thr = 0.0f;
     // kCombine: partials [head][split][m, l, acc[head_dim]] (part_stride
-    // floats each), the position, positions per split, the fold limit
+    // floats each, nsplit rows per head), the position and the split policy:
+    // nt = pos / tile + 1 tiles, tps = ceil(nt / max_splits) tiles per split,
+    // ceil(nt / tps) splits
     const float* part = nullptr;
     const int* pos = nullptr;
-    int nsplit = 0, split = 0, part_stride = 0, head_dim = 0, max_seq = 0, fold = 0;
+    int nsplit = 0, tile = 0, max_splits = 0, part_stride = 0, head_dim = 0, max_seq = 0;
     // SWIGLU_EPI: the output rows are [gate F | up F] with F = 4 * fbands;
     // y receives swiglu(gate, up) (F values, pa.thr applies)
     int fbands = 0;
@@ -188,8 +190,11 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     int fns = 0;       // kCombine: splits merged here (0: x holds the merged output)
     if constexpr (PRO == Pro::kCombine) {
         const int p = *pa.pos;
-        const int ns = p >= 0 && p < pa.max_seq ? p / pa.split + 1 : 0;
-        fns = ns <= pa.fold ? ns : 0;
+        if (p >= 0 && p < pa.max_seq) {
+            const int nt = p / pa.tile + 1;
+            const int tps = (nt + pa.max_splits - 1) / pa.max_splits;
+            fns = (nt + tps - 1) / tps;  // <= max_splits <= kMaxFold
+        }
         if (fns > 0) {
             const int e0 = min(tid, nchunk - 1) * 8;  // this thread's 8 outputs: head h, dims d0..d0+7
             const int h = e0 / pa.head_dim;
@@ -697,25 +702,25 @@ asdsl_status asdsl::preq2_embed_rmsnorm(const uint8_t* meta, const uint8_t* quan
 
 asdsl_status asdsl::preq2_fused_combine(const uint8_t* meta, const uint8_t* quant, const float* att, float* y,
                                         int out_features, int in_features, int group_size, const float* part,
-                                        const int* pos, int nsplit, int split, int part_stride, int head_dim,
-                                        int max_seq, int fold, asdsl_stream_t stream) {
+                                        const int* pos, int nsplit, int tile, int max_splits, int part_stride,
+                                        int head_dim, int max_seq, asdsl_stream_t stream) {
     if (check_preq2_args(meta, quant, att, y, out_features, in_features, group_size, "gemv_preq2_combine"))
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CHECK_ARG(in_features <= 8192, "gemv_preq2_combine: in_features must be <= 8192");
-    ASDSL_CHECK_ARG(part && pos && fold >= 0 && fold <= kMaxFold && split > 0 && head_dim % 8 == 0 &&
-                        in_features % head_dim == 0 && part_stride % 2 == 0 && part_stride >= head_dim + 2 &&
-                        reinterpret_cast<uintptr_t>(part) % 8 == 0,
+    ASDSL_CHECK_ARG(part && pos && max_splits >= 1 && max_splits <= kMaxFold && max_splits <= nsplit && tile > 0 &&
+                        head_dim % 8 == 0 && in_features % head_dim == 0 && part_stride % 2 == 0 &&
+                        part_stride >= head_dim + 2 && reinterpret_cast<uintptr_t>(part) % 8 == 0,
                     "gemv_preq2_combine: invalid partial layout");
     ASDSL_CU_COUNT(cus);
     ProArgs pa;
     pa.part = part;
     pa.pos = pos;
     pa.nsplit = nsplit;
-    pa.split = split;
+    pa.tile = tile;
+    pa.max_splits = max_splits;
     pa.part_stride = part_stride;
     pa.head_dim = head_dim;
     pa.max_seq = max_seq;
-    pa.fold = fold;
     hipStream_t s = as_hip(stream);
     if (group_size == 32)
         return launch_preq2_fused<32, Pro::kCombine, false>(meta, quant, att, y, out_features, in_features, pa, s, cus);

@@ -245,10 +245,10 @@ def test_decode_long_context_matches_oracle(gpu, ctx):
 
 @pytest.mark.parametrize("max_seq,ctx", [(300, 150), (1600, 1400), (3000, 2500)])
 def test_graph_replay_matches_eager_steps(gpu, max_seq, ctx):
-    """Eager steps (the general step, any position: the combine kernel)
-    against a captured graph replayed three times: at 150 the graph holds the
-    short-context step (splits merged in o_proj's prologue; same bits), at
-    1400 and 2500 the general step."""
+    """Eager steps, each queued for its position's range as the engine
+    captures it (below 256 the splits merged in o_proj's prologue, beyond the
+    combine kernel), against a captured graph replayed three times: bitwise
+    equal."""
     import torch
 
     eng = _small_engine(n_layers=1, vocab=4096, max_seq=max_seq, seed=9)
@@ -256,8 +256,8 @@ def test_graph_replay_matches_eager_steps(gpu, max_seq, ctx):
     snap = [(L["k_cache"].clone(), L["v_cache"].clone()) for L in eng.layers]
     eng.token.fill_(17)
     eager = []
-    for _ in range(3):
-        eng._queue_step(int(torch.cuda.current_stream().cuda_stream))
+    for i in range(3):
+        eng._queue_step(int(torch.cuda.current_stream().cuda_stream), eng._pos_limit(ctx + i))
         eager.append((eng.logits.clone(), eng.next_token()))
     # reset and replay a captured step three times
     for L, (k, v) in zip(eng.layers, snap):
@@ -272,6 +272,32 @@ def test_graph_replay_matches_eager_steps(gpu, max_seq, ctx):
         assert torch.equal(eng.logits, eager[i][0]), i
         assert eng.next_token() == eager[i][1]
     assert int(eng.pos.item()) == ctx + 3
+
+
+@pytest.mark.parametrize("ctx", [0, 130, 255])
+def test_short_form_gives_the_general_steps_bits(gpu, ctx):
+    """A position below 256 through the step queued for positions below 256
+    (attention splits merged in o_proj's prologue) and through the general
+    step (queued for any position: the partial and combine kernels), two
+    layers: the same logits, token and K/V rows bit for bit."""
+    import torch
+
+    eng = _small_engine(n_layers=2, vocab=4096, max_seq=600, seed=ctx + 1)
+    eng.prefill_kv_random(ctx, seed=9)
+    snap = [(L["k_cache"].clone(), L["v_cache"].clone()) for L in eng.layers]
+    out = []
+    for limit in (256, 600):
+        for L, (k, v) in zip(eng.layers, snap):
+            L["k_cache"].copy_(k)
+            L["v_cache"].copy_(v)
+        eng.token.fill_(33)
+        eng.pos.fill_(ctx)
+        eng._queue_step(int(torch.cuda.current_stream().cuda_stream), limit)
+        torch.cuda.synchronize()
+        out.append((_host(eng.logits), eng.next_token(), [_host(L["k_cache"][:, ctx]) for L in eng.layers]))
+    (la, ta, ka), (lb, tb, kb) = out
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)) and ta == tb
+    assert all(np.array_equal(x, y) for x, y in zip(ka, kb))
 
 
 def test_forward_token_api(gpu):

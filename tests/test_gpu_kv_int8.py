@@ -131,7 +131,7 @@ def test_graph_replay_matches_eager_steps(gpu):
             if graph:
                 eng.step()
             else:
-                eng._queue_step(int(torch.cuda.current_stream().cuda_stream))
+                eng._queue_step(int(torch.cuda.current_stream().cuda_stream), eng._pos_limit(int(eng.pos.item())))
             torch.cuda.synchronize()
             seq.append((_host(eng.logits).copy(), eng.next_token()))
         L = eng.layers[0]
