@@ -1180,7 +1180,7 @@ struct VerifyAttnK {
 
 // Work buffer layout of a verify pass of up to n tokens (offsets in floats).
 struct VerifyWork {
-    size_t H, X, QKV, Q, part, att, O, GU, S, keys, total;
+    size_t H, X, QKV, Q, part, att, O, GU, S, keys, mimg, mimg_bytes, total;
 };
 
 VerifyWork verify_work(const asdsl_decode_model& m, int n) {
@@ -1203,6 +1203,9 @@ VerifyWork verify_work(const asdsl_decode_model& m, int n) {
     w.GU = take(N * 2 * m.ffn);
     w.S = take(N * m.ffn);
     w.keys = take(2 * N);
+    // the MFMA batched GEMV's column image (the widest input, K = max(hidden, ffn))
+    w.mimg_bytes = asdsl_gemv_preq2_fused_batch_work_bytes(m.hidden > m.ffn ? m.hidden : m.ffn);
+    w.mimg = take((w.mimg_bytes + sizeof(float) - 1) / sizeof(float));
     w.total = at;
     return w;
 }
@@ -1405,18 +1408,20 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     float* GU = base + w.GU;
     float* S = base + w.S;
     auto* keys = reinterpret_cast<unsigned long long*>(base + w.keys);
+    void* mimg = base + w.mimg;
     hipStream_t s = as_hip(stream);
     const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
     const int q_dim = m.n_heads * m.head_dim;
     const int nsplit = attn_splits(m.max_seq);
     const int G = m.n_heads / m.n_kv_heads;
     const bool q8 = m.kv_format == ASDSL_KV_INT8;
-    // ASDSL_HIP_VERIFY_MFMA=1 lets the g32 projections take the MFMA batched
-    // GEMV (faster from 4 columns on, but its fp32 summation order differs
-    // from the single-token step's, so a column's int8 activations can round
-    // differently; see preq2_fused_batch)
-    static const int mfma_knob = env_knob("ASDSL_HIP_VERIFY_MFMA");
-    const bool mfma = mfma_knob > 0;
+    // The projections take the MFMA batched GEMV (16 columns per launch, so
+    // each weight byte streams once per pass; from 4 columns on, 3 once
+    // K >= 4096).  Its fp32 summation order differs from the single-token
+    // step's GEMVs, so a column's downstream int8 activations can round
+    // differently.  ASDSL_HIP_VERIFY_DOT4=1 (read per call) keeps the dot4
+    // forms, whose per-column arithmetic follows the single-token step.
+    const bool mfma = env_knob("ASDSL_HIP_VERIFY_DOT4") <= 0;
 
     asdsl_status st = launch("verify_embed_kernel", verify_embed_kernel, dim3((m.hidden + 1023) / 1024, n), dim3(256),
                              0, s, m.embed, tokens, H, m.hidden, m.vocab, keys);
@@ -1429,7 +1434,8 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H, pending,
                     L.rms_att, X, m.hidden, m.rms_eps);
         if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.qkv_meta, L.qkv_quant, X, QKV, qkv_dim, m.hidden, m.gs_attn, n, stream, mfma);
+        st = preq2_fused_batch(L.qkv_meta, L.qkv_quant, X, QKV, qkv_dim, m.hidden, m.gs_attn, n, stream, mfma, mimg,
+                           w.mimg_bytes);
         if (st != ASDSL_OK) return st;
         const KvCache kv{L.k_cache, L.v_cache, L.k_scale, L.v_scale};
         st = launch("verify_rope_kv_kernel", q8 ? verify_rope_kv_kernel<true> : verify_rope_kv_kernel<false>,
@@ -1445,24 +1451,28 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         st = launch("attn_combine_kernel", attn_combine_kernel, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
                     static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0);
         if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma);
+        st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma, mimg,
+                           w.mimg_bytes);
         if (st != ASDSL_OK) return st;
         st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H,
                     static_cast<const float*>(O), L.rms_ffn, X, m.hidden, m.rms_eps);
         if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.gu_meta, L.gu_quant, X, GU, 2 * m.ffn, m.hidden, m.gs_ffn, n, stream, false);
+        st = preq2_fused_batch(L.gu_meta, L.gu_quant, X, GU, 2 * m.ffn, m.hidden, m.gs_ffn, n, stream, mfma, mimg,
+                           w.mimg_bytes);
         if (st != ASDSL_OK) return st;
         st = launch("verify_swiglu_kernel", verify_swiglu_kernel, dim3((m.ffn + 1023) / 1024, n), dim3(256), 0, s,
                     static_cast<const float*>(GU), S, m.ffn, L.fatrelu_threshold);
         if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.down_meta, L.down_quant, S, O, m.hidden, m.ffn, m.gs_ffn, n, stream, false);
+        st = preq2_fused_batch(L.down_meta, L.down_quant, S, O, m.hidden, m.ffn, m.gs_ffn, n, stream, mfma, mimg,
+                           w.mimg_bytes);
         if (st != ASDSL_OK) return st;
         pending = O;
     }
     st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H, pending,
                 m.rms_out, X, m.hidden, m.rms_eps);
     if (st != ASDSL_OK) return st;
-    st = preq2_fused_batch(m.lm_meta, m.lm_quant, X, logits, m.vocab, m.hidden, m.gs_lm, n, stream, false);
+    st = preq2_fused_batch(m.lm_meta, m.lm_quant, X, logits, m.vocab, m.hidden, m.gs_lm, n, stream, mfma, mimg,
+                           w.mimg_bytes);
     if (st != ASDSL_OK) return st;
     st = launch("verify_argmax_kernel", verify_argmax_kernel, dim3(64, n), dim3(256), 0, s,
                 static_cast<const float*>(logits), m.vocab, keys);

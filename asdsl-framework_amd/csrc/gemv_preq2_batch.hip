@@ -159,10 +159,13 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_batch_kernel(const u
 }
 
 // ---------------------------------------------------------------- MFMA path
-// For gs = 32 the batch is a sum over groups of int8 matrix products, one
-// v_mfma_i32_16x16x32_i8 per (group, 16-row tile) for 16 columns at once:
+// The batch is a sum over groups of int8 matrix products, GS/32
+// v_mfma_i32_16x16x32_i8 per (group, 16-row tile) for 16 columns at once,
+// accumulated in one exact int32 tile (the 32-element K slices of a 128-group
+// chain through the MFMA's accumulator), then one fp32 epilogue per group:
 //   D[n][r] = sum_{k in g} xq[n][k] * q[r][k]      (exact int32)
-//   Y[n][r] += D*(s_r*xs_n) - (z_r*s_r)*(X_n*xs_n)  (the fp32 epilogue above)
+//   Y[n][r] += D*(s_r*xs_n) - (z_r*s_r)*(X_n*xs_n)  (the reference's per-group
+//                                                     term, X_n = sum_g xq[n])
 // The MFMA's A operand is the activations (its rows = columns n), B the
 // weights (its columns = rows r), so lane l ends with rows r0 + l%16 and
 // columns 4*(l/16) + v, v = 0..3: one row's (s, z) per lane per group.  Any
@@ -170,18 +173,20 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_batch_kernel(const u
 // so the weight operand is the nibble split (lo: even elements, hi: odd) and
 // the activation operand the split order (even elements, odd elements).
 //
-// Pass 1 quantizes the 16 columns once (A1 rule; zero columns past ncols)
-// into a group-major image in a device buffer:
-//   img[g][n][4] uint2 : split-order int8 of column n in group g, per chunk
-//   fac[g][n]    float2: (xs, X*xs), X = sum of the group's int8
+// Pass 1 quantizes the 16 columns once (A1 rule per GS-group; zero columns
+// past ncols) into a slice-major image in a device buffer:
+//   img[t][n][4] uint2 : split-order int8 of column n in 32-element slice t, per chunk
+//   fac[g][n]    float2: (xs, X*xs), X = sum of group g's int8
 // Pass 2: workgroup = W waves over all groups of a 16-row tile (wave w:
 // groups [w*GPW, (w+1)*GPW), their activation operands held in registers);
 // the W partial tiles are added in LDS in fixed order.  Quantizing inside
 // pass 2 instead was measured slower: every workgroup re-reads all of X.
 constexpr int kMfmaCols = 16;
 
+template <int GS>
 __global__ __launch_bounds__(256) void batch_quantize_kernel(const float* __restrict__ X, uint2* __restrict__ img,
                                                              float2* __restrict__ fac, int K, int ncols) {
+    constexpr int kLanes = GS / 8;
     const int n = static_cast<int>(blockIdx.y);
     const int c = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
     const int nchunk = K >> 3;  // a multiple of 4: lanes past the end form whole groups
@@ -196,41 +201,44 @@ __global__ __launch_bounds__(256) void batch_quantize_kernel(const float* __rest
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     }
-    const QChunk q = quantize8<32>(v);
+    const QChunk q = quantize8<GS>(v);
+    const int gsum = kLanes == 4 ? q.usum : group_sum<kLanes>(sum4_i8(q.even) + sum4_i8(q.odd));
     if (c < nchunk) {
-        const int g = c >> 2;
-        img[(static_cast<size_t>(g) * kMfmaCols + n) * 4 + (c & 3)] = make_uint2(q.even, q.odd);
-        if ((c & 3) == 0)
-            fac[static_cast<size_t>(g) * kMfmaCols + n] = make_float2(q.scale, static_cast<float>(q.usum) * q.scale);
+        img[(static_cast<size_t>(c >> 2) * kMfmaCols + n) * 4 + (c & 3)] = make_uint2(q.even, q.odd);
+        if ((c & (kLanes - 1)) == 0)
+            fac[static_cast<size_t>(c / kLanes) * kMfmaCols + n] =
+                make_float2(q.scale, static_cast<float>(gsum) * q.scale);
     }
 }
 
 typedef int v4i32 __attribute__((ext_vector_type(4)));
 
-// LDS bytes of one band's GPW groups in a wave's staging area, padded by 64 B
-// so that the four bands of a tile fall on different LDS banks.
-__host__ __device__ constexpr int mfma_band_bytes(int gpw) { return gpw * 64 + 64; }
+// LDS bytes of one band's GPW groups (GS/2 bytes each: 4 rows x GS/32
+// 16-byte slices) in a wave's staging area, padded by 64 B so that the four
+// bands of a tile fall on different LDS banks.
+__host__ __device__ constexpr int mfma_band_bytes(int gs, int gpw) { return gpw * (gs * 2) + 64; }
 // Per wave: the weight staging area (4 bands of one tile) and the wave's
 // (xs, X*xs) pairs (GPW groups x 16 columns x 8 B); per workgroup: two
 // buffers of the fixed-order K-slice sum.
-__host__ __device__ constexpr int mfma_wave_bytes(int gpw) { return 4 * mfma_band_bytes(gpw) + gpw * 128; }
-__host__ __device__ constexpr size_t mfma_lds_bytes(int gpw, int waves) {
-    return static_cast<size_t>(waves) * mfma_wave_bytes(gpw) + 2 * static_cast<size_t>(waves) * 4 * kWave * 4;
+__host__ __device__ constexpr int mfma_wave_bytes(int gs, int gpw) { return 4 * mfma_band_bytes(gs, gpw) + gpw * 128; }
+__host__ __device__ constexpr size_t mfma_lds_bytes(int gs, int gpw, int waves) {
+    return static_cast<size_t>(waves) * mfma_wave_bytes(gs, gpw) + 2 * static_cast<size_t>(waves) * 4 * kWave * 4;
 }
 
 // Workgroups loop over 16-row tiles (tile = blockIdx.x, += gridDim.x).  With
 // PF each wave requests the next tile's weights and (s, z) pairs before it
 // computes the current one, so HBM streams while the fp32 epilogue runs;
 // without PF (one tile per workgroup) the second register set is not needed.
-template <int GPW, int W, bool PF>
+template <int GS, int GPW, int W, bool PF>
 __global__ __launch_bounds__(W * kWave) void preq2_batch_mfma_kernel(const uint32_t* __restrict__ meta,
                                                                     const uint8_t* __restrict__ quant,
                                                                     const uint2* __restrict__ img,
                                                                     const float2* __restrict__ fac,
                                                                     float* __restrict__ Y, int M, int K, int ncols) {
-    static_assert(GPW % 4 == 0, "(s, z) pairs are read 4 groups at a time");
-    constexpr int kBand = mfma_band_bytes(GPW);
-    constexpr int kUnits = GPW * 4;                 // 16-byte units per band
+    constexpr int UPS = GS / 32;                    // 32-element slices per group
+    constexpr int kBand = mfma_band_bytes(GS, GPW);
+    constexpr int kGroupBytes = GS * 2;             // one group of a band: 4 rows x UPS slices x 16 B
+    constexpr int kUnits = GPW * 4 * UPS;           // 16-byte units per band
     constexpr int kLoads = (4 * kUnits) / kWave;    // dwordx4 loads per lane per tile
     static_assert((4 * kUnits) % kWave == 0, "a tile's four bands are whole wave loads");
     extern __shared__ __align__(16) uint32_t lds_words[];
@@ -239,33 +247,41 @@ __global__ __launch_bounds__(W * kWave) void preq2_batch_mfma_kernel(const uint3
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const int r16 = lane & 15;
     const int q = lane >> 4;
-    const int G = K >> 5;  // == W * GPW (the plan guarantees it)
+    const int G = K / GS;  // == W * GPW (the plan guarantees it)
     const int g0 = wave * GPW;
     const int ntiles = (M + 15) >> 4;
     const int nbands = (M + 3) >> 2;
-    uint8_t* stage = lds + static_cast<size_t>(wave) * mfma_wave_bytes(GPW);
+    uint8_t* stage = lds + static_cast<size_t>(wave) * mfma_wave_bytes(GS, GPW);
     uint8_t* wfac = stage + 4 * kBand;
-    float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(W) * mfma_wave_bytes(GPW));  // [2][W][4][kWave]
+    float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(W) * mfma_wave_bytes(GS, GPW));  // [2][W][4][kWave]
 
-    // Weights: a tile's four bands x GPW groups are contiguous runs of GPW*64
-    // bytes in HBM, read with whole 16-byte lanes.
+    // Weights: a tile's four bands x GPW groups are contiguous runs of
+    // GPW*GS*2 bytes in HBM (within a group, 16-byte unit r*UPS + t holds
+    // slice t of the band's row r), read with whole 16-byte lanes.
     auto load_tile = [&](uint4 (&wv)[kLoads], uint32_t (&mt)[GPW], int tile) {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
             const int e = i * kWave + lane;
             const int band = min(tile * 4 + e / kUnits, nbands - 1);  // past M: the last band, never stored
-            wv[i] = load_stream16(reinterpret_cast<const uint4*>(quant + (static_cast<size_t>(band) * G + g0) * 64) +
-                                  e % kUnits);
+            wv[i] = load_stream16(
+                reinterpret_cast<const uint4*>(quant + (static_cast<size_t>(band) * G + g0) * kGroupBytes) +
+                e % kUnits);
         }
         const int row = min(tile * 16 + r16, M - 1);
-        const uint4* mp = reinterpret_cast<const uint4*>(meta + static_cast<size_t>(row) * G + g0);
+        const uint32_t* mrow = meta + static_cast<size_t>(row) * G + g0;
+        if constexpr (GPW % 4 == 0) {
+            const uint4* mp = reinterpret_cast<const uint4*>(mrow);
 #pragma unroll
-        for (int j4 = 0; j4 < GPW / 4; ++j4) {
-            const uint4 m4 = mp[j4];
-            mt[4 * j4 + 0] = m4.x;
-            mt[4 * j4 + 1] = m4.y;
-            mt[4 * j4 + 2] = m4.z;
-            mt[4 * j4 + 3] = m4.w;
+            for (int j4 = 0; j4 < GPW / 4; ++j4) {
+                const uint4 m4 = mp[j4];
+                mt[4 * j4 + 0] = m4.x;
+                mt[4 * j4 + 1] = m4.y;
+                mt[4 * j4 + 2] = m4.z;
+                mt[4 * j4 + 3] = m4.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < GPW; ++j) mt[j] = mrow[j];
         }
     };
 
@@ -276,14 +292,16 @@ __global__ __launch_bounds__(W * kWave) void preq2_batch_mfma_kernel(const uint3
     uint4 w0[kLoads], w1[PF ? kLoads : 1];
     uint32_t m0[GPW], m1[PF ? GPW : 1];
 
-    // activation operands (column r16, chunk q of each of the wave's groups)
-    // and the wave's (xs, X*xs) pairs (GPW*128 contiguous bytes, to LDS)
-    long a[GPW];
+    // activation operands (column r16, chunk q of each slice of the wave's
+    // groups) and the wave's (xs, X*xs) pairs (GPW*128 contiguous bytes, to LDS)
+    long a[GPW][UPS];
 #pragma unroll
-    for (int j = 0; j < GPW; ++j) {
-        const uint2 t = img[(static_cast<size_t>(g0 + j) * kMfmaCols + r16) * 4 + q];
-        a[j] = static_cast<long>(static_cast<uint64_t>(t.x) | (static_cast<uint64_t>(t.y) << 32));
-    }
+    for (int j = 0; j < GPW; ++j)
+#pragma unroll
+        for (int t = 0; t < UPS; ++t) {
+            const uint2 v = img[(static_cast<size_t>((g0 + j) * UPS + t) * kMfmaCols + r16) * 4 + q];
+            a[j][t] = static_cast<long>(static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32));
+        }
     constexpr int kFacLoads = (GPW * 8 + kWave - 1) / kWave;
     uint4 fv[kFacLoads];
     const uint4* fsrc = reinterpret_cast<const uint4*>(fac + static_cast<size_t>(g0) * kMfmaCols);
@@ -295,7 +313,7 @@ __global__ __launch_bounds__(W * kWave) void preq2_batch_mfma_kernel(const uint3
         if (i * kWave + lane < GPW * 8) reinterpret_cast<uint4*>(wfac)[i * kWave + lane] = fv[i];
 
     const v4i32 zero = {0, 0, 0, 0};
-    const int rd = (r16 >> 2) * kBand + (r16 & 3) * 16 + q * 4;  // row r16, chunk q
+    const int rd = (r16 >> 2) * kBand + (r16 & 3) * (UPS * 16) + q * 4;  // row r16, chunk q of slice 0
     auto run_tile = [&](auto prefetch, uint4 (&wc)[kLoads], uint32_t (&mc)[GPW], auto& wn, auto& mn, int parity) {
         // stage this tile's weights (the wave reads back only what it wrote;
         // LDS operations of a wave complete in order), then request the next
@@ -326,9 +344,14 @@ __global__ __launch_bounds__(W * kWave) void preq2_batch_mfma_kernel(const uint3
             const float4 f1 = reinterpret_cast<const float4*>(wfac + j * 128 + q * 32)[1];
             const float xs[4] = {f0.x, f0.z, f1.x, f1.z};
             const float xx[4] = {f0.y, f0.w, f1.y, f1.w};
-            const uint32_t w = *reinterpret_cast<const uint32_t*>(stage + rd + j * 64);
-            const uint64_t b = static_cast<uint64_t>(w & 0x0F0F0F0Fu) | (static_cast<uint64_t>((w >> 4) & 0x0F0F0F0Fu) << 32);
-            const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j], static_cast<long>(b), zero, 0, 0, 0);
+            v4i32 d = zero;
+#pragma unroll
+            for (int t = 0; t < UPS; ++t) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(stage + rd + j * kGroupBytes + t * 16);
+                const uint64_t b = static_cast<uint64_t>(w & 0x0F0F0F0Fu) |
+                                   (static_cast<uint64_t>((w >> 4) & 0x0F0F0F0Fu) << 32);
+                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[j][t], static_cast<long>(b), d, 0, 0, 0);
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 acc[v] = fmaf(static_cast<float>(d[v]), sf[j] * xs[v], acc[v]);
@@ -389,21 +412,23 @@ struct MfmaPlan {
     bool ok = false, prefetch = false;
 };
 
-// Waves x groups-per-wave cover the K/32 groups exactly; the grid holds
+// Waves x groups-per-wave cover the K/GS groups exactly; the grid holds
 // ASDSL_HIP_BATCH_WG_PER_CU workgroups per compute unit (default 1), capped
 // at the tile count.
-MfmaPlan plan_mfma(int M, int K, int cus) {
+MfmaPlan plan_mfma(int M, int K, int gs, int cus) {
     MfmaPlan p;
     if (K % 128 != 0) return p;
-    const int G = K / 32;
-    static const int pairs[][2] = {{8, 12}, {16, 16}, {8, 16}, {16, 12}, {8, 8}, {16, 8}, {8, 20}, {4, 16}, {4, 8}};
-    for (const auto& wg : pairs) {
-        if (wg[0] * wg[1] == G) {
-            p.waves = wg[0];
-            p.gpw = wg[1];
-            break;
-        }
-    }
+    const int G = K / gs;
+    static const int pairs32[][2] = {{8, 12}, {16, 16}, {8, 16}, {16, 12}, {8, 8}, {16, 8}, {8, 20}, {4, 16}, {4, 8}};
+    static const int pairs128[][2] = {{8, 3}, {16, 4}, {8, 4}, {8, 5}, {4, 4}};
+    auto pick = [&](const auto& pairs) {
+        for (const auto& wg : pairs)
+            if (wg[0] * wg[1] == G) return std::pair<int, int>(wg[0], wg[1]);
+        return std::pair<int, int>(0, 0);
+    };
+    const auto wg = gs == 32 ? pick(pairs32) : pick(pairs128);
+    p.waves = wg.first;
+    p.gpw = wg.second;
     if (p.waves == 0) return p;
     static const int knob = env_knob("ASDSL_HIP_BATCH_WG_PER_CU");
     const int per_cu = knob > 0 ? knob : 1;
@@ -414,31 +439,37 @@ MfmaPlan plan_mfma(int M, int K, int cus) {
     return p;
 }
 
-template <int GPW, int W>
+template <int GS, int GPW, int W>
 asdsl_status launch_mfma_shape(const MfmaPlan& p, const uint32_t* m, const uint8_t* q, const uint2* img,
                                const float2* fac, float* Y, int M, int K, int ncols, hipStream_t s) {
     if constexpr (W < 16) {  // 16 waves: 128 registers, no room for the second register set
         if (p.prefetch)
-            return launch("preq2_batch_mfma_kernel", preq2_batch_mfma_kernel<GPW, W, true>, dim3(p.grid),
-                          dim3(W * kWave), mfma_lds_bytes(GPW, W), s, m, q, img, fac, Y, M, K, ncols);
+            return launch("preq2_batch_mfma_kernel", preq2_batch_mfma_kernel<GS, GPW, W, true>, dim3(p.grid),
+                          dim3(W * kWave), mfma_lds_bytes(GS, GPW, W), s, m, q, img, fac, Y, M, K, ncols);
     }
-    return launch("preq2_batch_mfma_kernel", preq2_batch_mfma_kernel<GPW, W, false>, dim3(p.grid), dim3(W * kWave),
-                  mfma_lds_bytes(GPW, W), s, m, q, img, fac, Y, M, K, ncols);
+    return launch("preq2_batch_mfma_kernel", preq2_batch_mfma_kernel<GS, GPW, W, false>, dim3(p.grid),
+                  dim3(W * kWave), mfma_lds_bytes(GS, GPW, W), s, m, q, img, fac, Y, M, K, ncols);
 }
 
-asdsl_status launch_mfma(const MfmaPlan& p, const uint32_t* m, const uint8_t* q, const uint2* img, const float2* fac,
-                         float* Y, int M, int K, int ncols, hipStream_t s) {
-#define ASDSL_MFMA_CASE(W_, GPW_) \
-    if (p.waves == W_ && p.gpw == GPW_) return launch_mfma_shape<GPW_, W_>(p, m, q, img, fac, Y, M, K, ncols, s);
-    ASDSL_MFMA_CASE(8, 12)
-    ASDSL_MFMA_CASE(16, 16)
-    ASDSL_MFMA_CASE(8, 16)
-    ASDSL_MFMA_CASE(16, 12)
-    ASDSL_MFMA_CASE(8, 8)
-    ASDSL_MFMA_CASE(16, 8)
-    ASDSL_MFMA_CASE(8, 20)
-    ASDSL_MFMA_CASE(4, 16)
-    ASDSL_MFMA_CASE(4, 8)
+asdsl_status launch_mfma(const MfmaPlan& p, int gs, const uint32_t* m, const uint8_t* q, const uint2* img,
+                         const float2* fac, float* Y, int M, int K, int ncols, hipStream_t s) {
+#define ASDSL_MFMA_CASE(GS_, W_, GPW_)          \
+    if (gs == GS_ && p.waves == W_ && p.gpw == GPW_) \
+        return launch_mfma_shape<GS_, GPW_, W_>(p, m, q, img, fac, Y, M, K, ncols, s);
+    ASDSL_MFMA_CASE(32, 8, 12)
+    ASDSL_MFMA_CASE(32, 16, 16)
+    ASDSL_MFMA_CASE(32, 8, 16)
+    ASDSL_MFMA_CASE(32, 16, 12)
+    ASDSL_MFMA_CASE(32, 8, 8)
+    ASDSL_MFMA_CASE(32, 16, 8)
+    ASDSL_MFMA_CASE(32, 8, 20)
+    ASDSL_MFMA_CASE(32, 4, 16)
+    ASDSL_MFMA_CASE(32, 4, 8)
+    ASDSL_MFMA_CASE(128, 8, 3)
+    ASDSL_MFMA_CASE(128, 16, 4)
+    ASDSL_MFMA_CASE(128, 8, 4)
+    ASDSL_MFMA_CASE(128, 8, 5)
+    ASDSL_MFMA_CASE(128, 4, 4)
 #undef ASDSL_MFMA_CASE
     set_error("gemv_preq2_fused_batch: no MFMA tiling for this shape");
     return ASDSL_ERR_UNSUPPORTED;
@@ -561,31 +592,33 @@ asdsl_status asdsl::preq2_fused_batch(const uint8_t* meta, const uint8_t* quant,
     const BatchPlan p = plan_batch(out_features, in_features, group_size, cus);
     const int M = out_features, K = in_features;
     const auto* m = reinterpret_cast<const uint32_t*>(meta);
-    // gs = 32 with at least ASDSL_HIP_BATCH_MFMA_MIN_N columns: 16 columns per
-    // pass.  Default where the MFMA path was measured to overtake the dot4
-    // kernel: N >= 4 (gate_up 16384x3072: 13.0 vs 13.9 us; N = 3: 12.9 vs
-    // 12.1), N >= 3 once K >= 4096 (down 3072x8192, N = 3: 10.9 vs 12.2 us).
+    // At least ASDSL_HIP_BATCH_MFMA_MIN_N columns: 16 columns per pass.
+    // Default where the MFMA path was measured to overtake the dot4 kernel:
+    // N >= 4 (gate_up 16384x3072 g32: 13.0 vs 13.9 us; N = 3: 12.9 vs 12.1),
+    // N >= 3 once K >= 4096 (down 3072x8192, N = 3: 10.9 vs 12.2 us).
     static const int mfma_knob = env_knob("ASDSL_HIP_BATCH_MFMA_MIN_N");
     const int mfma_min = mfma_knob > 0 ? mfma_knob : (in_features >= 4096 ? 3 : 4);
-    const MfmaPlan mp = plan_mfma(M, K, cus);
-    if (allow_mfma && group_size == 32 && n_cols >= mfma_min && mp.ok && reinterpret_cast<uintptr_t>(meta) % 16 == 0 &&
+    const MfmaPlan mp = plan_mfma(M, K, group_size, cus);
+    if (allow_mfma && n_cols >= mfma_min && mp.ok && reinterpret_cast<uintptr_t>(meta) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(quant) % 4 == 0) {
-        const int G = K / 32;
-        const size_t img_bytes = static_cast<size_t>(G) * kMfmaCols * 32;
+        const size_t img_bytes = static_cast<size_t>(K / 32) * kMfmaCols * 32;
         void* ws = nullptr;
-        const asdsl_status st0 = work_buffer(s, work, work_bytes,
-                                             img_bytes + static_cast<size_t>(G) * kMfmaCols * sizeof(float2), &ws,
-                                             "gemv_preq2_fused_batch");
+        const asdsl_status st0 = work_buffer(
+            s, work, work_bytes, img_bytes + static_cast<size_t>(K / group_size) * kMfmaCols * sizeof(float2), &ws,
+            "gemv_preq2_fused_batch");
         if (st0 != ASDSL_OK) return st0;
         auto* img = static_cast<uint2*>(ws);
         auto* fac = reinterpret_cast<float2*>(static_cast<uint8_t*>(ws) + img_bytes);
         for (int n0 = 0; n0 < n_cols; n0 += kMfmaCols) {
             const int nc = n_cols - n0 < kMfmaCols ? n_cols - n0 : kMfmaCols;
-            asdsl_status st = launch("batch_quantize_kernel", batch_quantize_kernel,
-                                     dim3((K / 8 + 255) / 256, kMfmaCols), dim3(256), 0, s,
-                                     X + static_cast<size_t>(n0) * K, img, fac, K, nc);
+            const dim3 qgrid((K / 8 + 255) / 256, kMfmaCols);
+            asdsl_status st = group_size == 32
+                                  ? launch("batch_quantize_kernel", batch_quantize_kernel<32>, qgrid, dim3(256), 0, s,
+                                           X + static_cast<size_t>(n0) * K, img, fac, K, nc)
+                                  : launch("batch_quantize_kernel", batch_quantize_kernel<128>, qgrid, dim3(256), 0, s,
+                                           X + static_cast<size_t>(n0) * K, img, fac, K, nc);
             if (st != ASDSL_OK) return st;
-            st = launch_mfma(mp, m, quant, img, fac, Y + static_cast<size_t>(n0) * M, M, K, nc, s);
+            st = launch_mfma(mp, group_size, m, quant, img, fac, Y + static_cast<size_t>(n0) * M, M, K, nc, s);
             if (st != ASDSL_OK) return st;
         }
         return ASDSL_OK;

@@ -492,7 +492,34 @@ def verify_pass_us(eng, ctx: int, per_token_us, counts=(4, 8, 16), reps: int = 2
             row["speedup_vs_serial"] = round(n * per_token_us / us, 2)
         res[str(n)] = row
         del g
+    res["mfma_vs_dot4"] = verify_flip_rate(eng, ctx, max(counts))
     return res
+
+
+def verify_flip_rate(eng, ctx: int, n: int) -> dict:
+    """The verify pass of tokens 1..n at ctx with the projections as MFMA
+    batched GEMVs (the default) and as the dot4 forms
+    (ASDSL_HIP_VERIFY_DOT4=1, whose per-column arithmetic follows the
+    single-token step): how often the greedy tokens agree and the logits'
+    relative L2 distance, plus the dot4 pass's time (eager, one pass)."""
+    import torch
+
+    toks = list(range(1, n + 1))
+    mf = eng.forward_batch_all_logits(toks, ctx).float().cpu().numpy()
+    mt = eng.verify_next_tokens()
+    os.environ["ASDSL_HIP_VERIFY_DOT4"] = "1"
+    try:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        d4 = eng.forward_batch_all_logits(toks, ctx).float().cpu().numpy()
+        dot4_ms = 1e3 * (time.perf_counter() - t0)
+        dt = eng.verify_next_tokens()
+    finally:
+        del os.environ["ASDSL_HIP_VERIFY_DOT4"]
+    errs = [float(np.linalg.norm(mf[c] - d4[c]) / np.linalg.norm(d4[c])) for c in range(n)]
+    return {"columns": n, "same_token_share": sum(a == b for a, b in zip(mt, dt)) / n,
+            "rel_l2_median": float(np.median(errs)), "rel_l2_max": float(max(errs)),
+            "dot4_eager_pass_ms": round(dot4_ms, 2)}
 
 
 # --------------------------------------------------------------------------- suite

@@ -178,8 +178,9 @@ def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
     kernel instance the speculative-verify shapes reach: the 8-wave dot4
     kernel (K = 3072, N <= 3), the 16-wave dot4 kernel (K = 8192, N = 2),
     8192 x 8192 at N = 2, whose 1024 tiles exceed the resident workgroups
-    so each workgroup loops over several, and the MFMA kernel (gs 32,
-    N >= 4, N >= 3 once K >= 4096)."""
+    so each workgroup loops over several, and the MFMA kernels (N >= 4,
+    N >= 3 once K >= 4096; at g128 four 32-element slices per group in one
+    int32 accumulator)."""
     if K % gs:
         pytest.skip("K not a multiple of the group size")
     import torch
@@ -202,9 +203,11 @@ def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
 
 @pytest.mark.parametrize("M,K", [(16384, 3072), (3072, 8192), (1000, 5120)])
 def test_preq2_batch_columns_do_not_depend_on_the_column_count(gpu, M, K):
-    """g128 dot4 batch: a column's result does not depend on how many columns
-    share the call (another kernel instance, column chunk and grid): the
-    shared columns of 3, 4, 9 and 16-column calls are bit for bit equal."""
+    """g128 batch: a column's result does not depend on how many columns
+    share the call: the shared columns of 4, 9 and 16-column calls (the MFMA
+    kernel, 16-column passes) are bit for bit equal, and a 3-column call
+    (the dot4 kernel at K = 3072, another fp32 summation order) agrees to
+    1e-5 relative."""
     import torch
     from asdsl.kernels import _native_gemv as ng
 
@@ -219,9 +222,11 @@ def test_preq2_batch_columns_do_not_depend_on_the_column_count(gpu, M, K):
         ng.gemv_preq2_fused_avx2(meta, quant, X[:n].contiguous(), Y, M, K, 128)
         torch.cuda.synchronize()
         outs[n] = Y.cpu().numpy()
-    for n in (4, 9, 16):
-        assert np.array_equal(outs[n][:3], outs[3]), n
+    for n in (9, 16):
+        assert np.array_equal(outs[n][:4], outs[4]), n
     assert np.array_equal(outs[16][:9], outs[9])
+    for c in range(3):
+        assert rel_l2(outs[4][c], outs[3][c]) < 1e-5, c
 
 
 def test_forced_ksplit_still_covers_every_unit(gpu, monkeypatch):

@@ -88,9 +88,14 @@ def test_verify_matches_serial_oracle(gpu, ctx, n):
         assert np.array_equal(gk[:, :ctx], kc[li][:, :ctx]) and not gk[:, ctx + n:].any()
 
 
-def test_verify_matches_single_token_steps(gpu):
+@pytest.mark.parametrize("form", ["mfma", "dot4"])
+def test_verify_matches_single_token_steps(gpu, form, monkeypatch):
     """The batched pass against the engine's own single-token step at the
-    same positions (K/V rolled back in between): 1e-5, same tokens."""
+    same positions (K/V rolled back in between): 1e-5, same tokens, with the
+    projections as MFMA batched GEMVs (the default) and as the dot4 forms
+    (ASDSL_HIP_VERIFY_DOT4=1)."""
+    if form == "dot4":
+        monkeypatch.setenv("ASDSL_HIP_VERIFY_DOT4", "1")
     eng = _engine(seed=7)
     eng.prefill_kv_random(200, seed=1)
     toks = [11, 22, 33, 44, 55, 66, 77, 88]
