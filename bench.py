@@ -406,6 +406,7 @@ def decode_tokens_per_s(contexts=(128, 1024, 4096), steps: int = 64, n_layers: i
     out["per_ctx"] = _decode_contexts(eng, contexts, steps)
     if with_verify:
         out["verify"] = verify_pass_us(eng, ctx=1024, per_token_us=out["per_ctx"].get("1024", {}).get("us_per_token"))
+        out["pld"] = pld_tokens_per_s(eng)
     if cpu_topo is not None:
         out["cpu_baseline"] = cpu_decode_baseline(eng, cpu_topo)
     if int8_kv:
@@ -493,6 +494,55 @@ def verify_pass_us(eng, ctx: int, per_token_us, counts=(4, 8, 16), reps: int = 2
         res[str(n)] = row
         del g
     res["mfma_vs_dot4"] = verify_flip_rate(eng, ctx, max(counts))
+    return res
+
+
+def pld_tokens_per_s(eng, new_tokens: int = 96, max_draft_k: int = 8) -> dict:
+    """Prompt Lookup Decoding against serial greedy decoding on the same
+    engine (asdsl.inference.unified_bridge): a 64-token prompt repeating a
+    16-token pattern, `new_tokens` generated; wall-clock tokens/s of the
+    generation (prompt included in the clock: both loops run it serially),
+    PLD with the reference's serial re-run of committed tokens and without
+    it, their draft statistics, and whether their tokens equal greedy's; then
+    the same two loops with a drafter that proposes greedy's own
+    continuation (every draft accepted: the verify path's upper bound)."""
+    import torch
+
+    from asdsl.inference.unified_bridge import greedy_generate, pld_generate
+
+    prompt = [100 + (i % 16) for i in range(64)]
+    res = {"prompt": "64 tokens, a 16-token pattern x 4", "new_tokens": new_tokens, "max_draft_k": max_draft_k}
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks = fn()
+        torch.cuda.synchronize()
+        return toks, time.perf_counter() - t0
+
+    greedy_generate(eng, prompt, 4)  # warm
+    want, tg = timed(lambda: greedy_generate(eng, prompt, new_tokens, eos=()))
+    res["greedy"] = {"tokens_per_s": round((len(want) - len(prompt)) / tg, 1), "s": round(tg, 3)}
+    for name, rerun in (("pld_rerun", True), ("pld_no_rerun", False)):
+        st = {}
+        got, t = timed(lambda: pld_generate(eng, prompt, new_tokens, max_draft_k=max_draft_k, eos=(), stats=st,
+                                            rerun=rerun))
+        res[name] = {"tokens_per_s": round((len(got) - len(prompt)) / t, 1), "s": round(t, 3),
+                     "same_as_greedy": got == want, **st}
+
+    class GreedyDraft:
+        """Drafts greedy decoding's own continuation: every draft is accepted
+        (up to rounding), the most the verify path can give."""
+
+        def lookup(self, tokens):
+            return want[len(tokens):len(tokens) + max_draft_k]
+
+    for name, rerun in (("oracle_draft_rerun", True), ("oracle_draft_no_rerun", False)):
+        st = {}
+        got, t = timed(lambda: pld_generate(eng, prompt, new_tokens, max_draft_k=max_draft_k, eos=(), stats=st,
+                                            rerun=rerun, decoder=GreedyDraft()))
+        res[name] = {"tokens_per_s": round((len(got) - len(prompt)) / t, 1), "s": round(t, 3),
+                     "same_as_greedy": got == want, **st}
     return res
 
 

@@ -140,18 +140,102 @@ def test_snapshot_restore_truncate(gpu):
         eng.forward_batch_all_logits([1, 2], 255)
 
 
-def test_pld_generate_is_greedy(gpu):
-    """A repetitive prompt gives the lookup drafts to verify; the generated
-    tokens are exactly those of serial greedy decoding."""
+class _ListDraft:
+    """Drafts tokens[len(context):] of a fixed sequence (greedy decoding's
+    own continuation: every draft is accepted), or with every other drafted
+    token replaced (rejections and corrections)."""
+
+    def __init__(self, seq, k, corrupt=False):
+        self.seq, self.k, self.corrupt = seq, k, corrupt
+
+    def lookup(self, context):
+        d = list(self.seq[len(context):len(context) + self.k])
+        if self.corrupt:
+            d = [t if i % 2 == 0 else (t + 1) % 4096 for i, t in enumerate(d)]
+        return d
+
+
+def _assert_greedy_up_to_ties(eng, got, want):
+    """got equals want, or first differs where greedy's own step has got's
+    token within 2 % of the largest |logit| of the top logit (a near-tie
+    that the batched pass's rounding can turn)."""
+    i = next((k for k, (a, b) in enumerate(zip(got, want)) if a != b), None)
+    if i is None:
+        assert got == want
+        return
+    eng.reset_session()
+    for p, t in enumerate(want[:i]):
+        logits = eng.forward_token(t, p)
+    lg = _host(logits)
+    assert lg[got[i]] >= lg.max() - 0.02 * np.abs(lg).max(), (i, float(lg.max()), float(lg[got[i]]))
+
+
+@pytest.mark.parametrize("rerun", [True, False])
+@pytest.mark.parametrize("drafter", ["lookup", "greedy", "corrupt"])
+def test_pld_generate_is_greedy(gpu, rerun, drafter):
+    """Prompt Lookup Decoding with the prompt-lookup drafter on a repetitive
+    prompt, a drafter proposing greedy's own continuation (drafts accepted)
+    and one proposing it with every other token wrong (rejections,
+    corrections).  With the reference's serial re-run the tokens are exactly
+    serial greedy decoding's; keeping the verify pass's K/V and argmax they
+    are greedy's up to a near-tie the batched pass's rounding turns."""
     from asdsl.inference.unified_bridge import greedy_generate, pld_generate
 
     eng = _engine(seed=5, vocab=4096, max_seq=256)
     prompt = [5, 17, 42, 99, 5, 17, 42, 99, 5, 17]
     want = greedy_generate(eng, prompt, 40)
+    dec = None if drafter == "lookup" else _ListDraft(want, 6, corrupt=drafter == "corrupt")
     stats = {}
-    got = pld_generate(eng, prompt, 40, max_draft_k=6, stats=stats)
-    assert got == want
-    assert stats["verify_passes"] >= 1
+    got = pld_generate(eng, prompt, 40, max_draft_k=6, stats=stats, rerun=rerun, decoder=dec)
+    if rerun:
+        assert got == want
+    else:
+        _assert_greedy_up_to_ties(eng, got, want)
+    if drafter != "lookup":
+        assert stats["verify_passes"] >= 1 and stats["accepted"] >= 1
+    if drafter == "greedy" and rerun:  # (without the re-run, a turned near-tie ends the drafter's matches)
+        assert stats["accepted"] >= stats["drafted"] // 2
+
+
+@pytest.mark.parametrize("rerun", [True, False])
+def test_pld_stops_before_end_of_sequence(gpu, rerun):
+    """An end-of-sequence id that greedy decoding produces mid-way (taken
+    from an unbounded run): greedy stops before it and so does PLD, whether
+    it comes from the draft, the correction or a serial step."""
+    from asdsl.inference.unified_bridge import greedy_generate, pld_generate
+
+    eng = _engine(seed=5, vocab=4096, max_seq=256)
+    prompt = [5, 17, 42, 99, 5, 17, 42, 99, 5, 17]
+    free = greedy_generate(eng, prompt, 40, eos=())
+    gen = free[len(prompt):]
+    stop = gen[12]
+    want = greedy_generate(eng, prompt, 40, eos=(stop,))
+    assert stop not in want[len(prompt):] and len(want) < len(free)
+    got = pld_generate(eng, prompt, 40, max_draft_k=6, eos=(stop,), rerun=rerun)
+    if rerun:
+        assert got == want
+    else:
+        _assert_greedy_up_to_ties(eng, got, want)
+    assert stop not in got[len(prompt):]
+
+
+@pytest.mark.parametrize("rerun", [True, False])
+def test_pld_near_the_end_of_the_cache(gpu, rerun):
+    """Generation up to the last cache position: drafts are cut at the
+    cache's end (the verify pass would refuse positions past it), and the
+    tokens are greedy decoding's."""
+    from asdsl.inference.unified_bridge import greedy_generate, pld_generate
+
+    eng = _engine(seed=6, vocab=4096, max_seq=64)
+    prompt = [7, 8, 9, 10, 7, 8, 9, 10, 7, 8]
+    n = 64 - len(prompt)
+    want = greedy_generate(eng, prompt, n, eos=())
+    got = pld_generate(eng, prompt, n, max_draft_k=8, eos=(), rerun=rerun, decoder=_ListDraft(want, 8))
+    assert len(got) == 64
+    if rerun:
+        assert got == want
+    else:
+        _assert_greedy_up_to_ties(eng, got, want)
 
 
 def test_reference_kv_length_cases(gpu):
