@@ -1132,6 +1132,9 @@ def main() -> int:
     ap.add_argument("--no-lm-head", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the 32-layer decode tokens/s measurement")
     ap.add_argument("--decode", action="store_true", help="only the decode tokens/s measurement (one JSON line)")
+    ap.add_argument("--decode-steps", type=int, default=64, help="captured steps per context in the decode phase")
+    ap.add_argument("--no-verify", action="store_true", help="decode phase: skip the verify pass, PLD rows")
+    ap.add_argument("--no-int8-kv", action="store_true", help="decode phase: skip the int8 KV cache rows")
     ap.add_argument("--suite", action="store_true",
                     help="one JSON line per hot-path row: kernel at its workload vs the HBM roofline, "
                          "with the reference's compiled CPU kernel timed on the same inputs")
@@ -1158,7 +1161,8 @@ def main() -> int:
         import torch  # noqa: F401
 
         topo = None if args.no_cpu else cpu_topology()
-        print(json.dumps({"decode": decode_tokens_per_s(cpu_topo=topo)}), flush=True)
+        print(json.dumps({"decode": decode_tokens_per_s(steps=args.decode_steps, with_verify=not args.no_verify,
+                                                        cpu_topo=topo, int8_kv=not args.no_int8_kv)}), flush=True)
         return 0
 
     import torch
@@ -1263,7 +1267,8 @@ def main() -> int:
     if not args.no_decode:
         del layers
         torch.cuda.empty_cache()
-        extra["decode"] = decode_tokens_per_s(cpu_topo=topo)
+        extra["decode"] = decode_tokens_per_s(steps=args.decode_steps, with_verify=not args.no_verify, cpu_topo=topo,
+                                              int8_kv=not args.no_int8_kv)
 
     out = {
         "metric": METRIC,
