@@ -119,6 +119,70 @@ __global__ void finalize_kernel(const unsigned long long* __restrict__ amax, int
     }
 }
 
+// The end of a split's attention in a workgroup of NT threads: every lane
+// holds its own running (m, l, acc) over the positions it scanned; the 16
+// lanes of one position slot of one wave (a group) share m and l, and each
+// holds acc for its 8 dims.  The NG = NT/16 groups merge in LDS in fixed
+// order, with no cross-lane reduction: M = max_k m_k, e_k = exp(m_k - M) (0
+// for a group that saw no position), acc = sum_k e_k acc_k, l = sum_k e_k l_k;
+// writes (M, l, acc[128]) of head hh at part + hh * head_stride.  (Folding the
+// slots of a wave first with swizzles and permutes measured ~40 % of the
+// kernel: 5.4 against 2.0 us for its loads alone at ctx 128.)
+template <int G, int NT>
+__device__ __forceinline__ void merge_position_groups(const float (&m)[G], const float (&l)[G],
+                                                      const float (&acc)[G][8], float (*gml)[G][2],
+                                                      float (*gacc)[G][kHeadDim], float (*ge)[NT / 16],
+                                                      float* __restrict__ part, size_t head_stride) {
+#pragma clang fp contract(off)
+    constexpr int NG = NT / 16;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int k = tid >> 4;  // group: wave * 4 + position slot
+    const int dc = tid & 15;
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+        float4* dst = reinterpret_cast<float4*>(&gacc[k][hh][8 * dc]);
+        dst[0] = make_float4(acc[hh][0], acc[hh][1], acc[hh][2], acc[hh][3]);
+        dst[1] = make_float4(acc[hh][4], acc[hh][5], acc[hh][6], acc[hh][7]);
+    }
+    if (dc == 0) {
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh) {
+            gml[k][hh][0] = m[hh];
+            gml[k][hh][1] = l[hh];
+        }
+    }
+    __syncthreads();
+    if (tid < G * NG) {  // e_k of every (head, group)
+        const int hh = tid / NG;
+        const int kk = tid % NG;
+        float M = gml[0][hh][0];
+#pragma unroll
+        for (int j = 1; j < NG; ++j) M = fmaxf(M, gml[j][hh][0]);
+        const float mk = gml[kk][hh][0];
+        ge[hh][kk] = mk == -INFINITY ? 0.0f : expf(mk - M);
+    }
+    __syncthreads();
+    for (int e = tid; e < G * kHeadDim; e += NT) {
+        const int hh = e / kHeadDim;
+        const int d = e % kHeadDim;
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) sum = fmaf(ge[hh][j], gacc[j][hh][d], sum);
+        part[hh * head_stride + 2 + d] = sum;
+    }
+    if (tid < G) {
+        float M = gml[0][tid][0];
+#pragma unroll
+        for (int j = 1; j < NG; ++j) M = fmaxf(M, gml[j][tid][0]);
+        float L = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) L = fmaf(ge[tid][j], gml[j][tid][1], L);
+        float* pp = part + tid * head_stride;
+        pp[0] = M;
+        pp[1] = L;
+    }
+}
+
 // Scores, split-local softmax and P.V of one split for the G query heads of a
 // KV head, then the merge of the four waves: lane (wave, pg, dc) holds the
 // K/V rows of positions p0 + 4*wave + pg + 16*it in kraw/vraw (dims
@@ -128,9 +192,12 @@ __global__ void finalize_kernel(const unsigned long long* __restrict__ amax, int
 template <int G, bool NEW, bool Q8>
 __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16], const uint4 (&vraw)[kSplit / 16],
                                                 const float (&qr)[G][8], int p0, int p1, int pos,
-                                                const float (*kv_new)[kHeadDim], float (*wml)[G][2],
-                                                float (*wacc)[G][kHeadDim], float* __restrict__ part,
-                                                size_t head_stride) {
+                                                const float (*kv_new)[kHeadDim], float (*gml)[G][2],
+                                                float (*gacc)[G][kHeadDim], float (*ge)[kAttnThreads / 16],
+                                                float* __restrict__ part, size_t head_stride) {
+    // no implicit fused multiply-adds: the folded form's kernel computes the
+    // same scores and weights and must round them alike
+#pragma clang fp contract(off)
     constexpr int kIt = kSplit / 16;
     const int tid = static_cast<int>(threadIdx.x);
     const float inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(kHeadDim));
@@ -167,18 +234,15 @@ __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16]
             sr[it][hh] = p < p1 ? d * inv_sqrt_d : -INFINITY;
         }
     }
-    // the wave's max and exp-sum per head (over its iterations, then over the
-    // four position groups: lanes 16 apart); a wave with no position keeps
-    // m = -inf and l = 0
+    // this lane's max and exp-sum per head over its iterations; a lane with
+    // no position keeps m = -inf and l = 0
     float m[G], l[G];
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
         float v = sr[0][hh];
 #pragma unroll
         for (int it = 1; it < kIt; ++it) v = fmaxf(v, sr[it][hh]);
-        v = fmaxf(v, swz_xor16(v));
-        v = fmaxf(v, __shfl_xor(v, 32, kWave));
-        m[hh] = v;
+        m[hh] = v;  // this lane's positions (the 16 lanes of its slot agree)
     }
     float acc[G][8];
 #pragma unroll
@@ -200,61 +264,7 @@ __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16]
             for (int e = 0; e < 8; ++e) acc[hh][e] = fmaf(w, v8[e], acc[hh][e]);
         }
     }
-#pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-        l[hh] += swz_xor16(l[hh]);
-        l[hh] += __shfl_xor(l[hh], 32, kWave);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            acc[hh][e] += swz_xor16(acc[hh][e]);
-            acc[hh][e] += __shfl_xor(acc[hh][e], 32, kWave);
-        }
-    }
-    if (pg == 0) {
-#pragma unroll
-        for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) wacc[wave][hh][8 * dc + e] = acc[hh][e];
-    }
-    if (lane == 0) {  // m and l are uniform across the wave
-#pragma unroll
-        for (int hh = 0; hh < G; ++hh) {
-            wml[wave][hh][0] = m[hh];
-            wml[wave][hh][1] = l[hh];
-        }
-    }
-    __syncthreads();
-
-    // merge the waves: M = max m_w, acc = sum_w exp(m_w - M) acc_w, L likewise
-    constexpr int kWaves = kAttnThreads / kWave;
-    for (int e = tid; e < G * kHeadDim; e += kAttnThreads) {
-        const int hh = e / kHeadDim;
-        const int d = e % kHeadDim;
-        float M = wml[0][hh][0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][hh][0]);
-        float sum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = wml[w][hh][0];
-            sum = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wacc[w][hh][d], sum);
-        }
-        part[hh * head_stride + 2 + d] = sum;
-    }
-    if (tid < G) {
-        float M = wml[0][tid][0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][tid][0]);
-        float L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = wml[w][tid][0];
-            L = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wml[w][tid][1], L);
-        }
-        float* pp = part + tid * head_stride;
-        pp[0] = M;
-        pp[1] = L;
-    }
+    merge_position_groups<G, kAttnThreads>(m, l, acc, gml, gacc, ge, part, head_stride);
 }
 
 // int8 cache: the new position's rotated key and value (kv_new, fp32)
@@ -295,8 +305,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     float* __restrict__ part, int n_heads, int n_kv, int max_seq, int rot_half, int nsplit) {
     __shared__ float q_s[G][kHeadDim];
     __shared__ float kv_new[2][kHeadDim];
-    __shared__ float wml[kAttnThreads / kWave][G][2];
-    __shared__ float wacc[kAttnThreads / kWave][G][kHeadDim];
+    __shared__ float gml[kAttnThreads / 16][G][2];
+    __shared__ __align__(16) float gacc[kAttnThreads / 16][G][kHeadDim];
+    __shared__ float ge[G][kAttnThreads / 16];
     const int s = static_cast<int>(blockIdx.x);
     const int kvh = static_cast<int>(blockIdx.y);
     const int pos = *pos_ptr;
@@ -391,7 +402,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
 
-    attn_split_core<G, true, Q8>(kraw, vraw, qr, p0, p1, pos, kv_new, wml, wacc,
+    attn_split_core<G, true, Q8>(kraw, vraw, qr, p0, p1, pos, kv_new, gml, gacc, ge,
                              part + (static_cast<size_t>(kvh * G) * nsplit + s) * kPartStride,
                              static_cast<size_t>(nsplit) * kPartStride);
 }
@@ -544,8 +555,9 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
     constexpr int kIt = kTile / kStep;
     __shared__ float q_s[G][kHeadDim];
     __shared__ float kv_new[2][kHeadDim];
-    __shared__ float wml[kWaves][G][2];
-    __shared__ float wacc[kWaves][G][kHeadDim];
+    __shared__ float gml[kThreads / 16][G][2];
+    __shared__ __align__(16) float gacc[kThreads / 16][G][kHeadDim];
+    __shared__ float ge[G][kThreads / 16];
     const int s = static_cast<int>(blockIdx.x);
     const int kvh = static_cast<int>(blockIdx.y);
     const int tid = static_cast<int>(threadIdx.x);
@@ -641,8 +653,8 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
 
-    // running state of this wave: max (uniform), and this lane's share of
-    // the exp-sum and of P.V (its 8 dims, its positions)
+    // running state of this lane over its positions: max, exp-sum and P.V
+    // (its 8 dims; the 16 lanes of its position slot share max and sum)
     const float inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(kHeadDim));
     float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -661,6 +673,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
         }
     };
     auto process_tile = [&](int t0, const uint4 (&kraw)[kIt], const uint4 (&vraw)[kIt]) {
+#pragma clang fp contract(off)  // rounds as attn_split_core does
         float sr[kIt][G];
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
@@ -685,8 +698,6 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
             float v = sr[0][hh];
 #pragma unroll
             for (int it = 1; it < kIt; ++it) v = fmaxf(v, sr[it][hh]);
-            v = fmaxf(v, swz_xor16(v));
-            v = fmaxf(v, __shfl_xor(v, 32, kWave));
             mn[hh] = fmaxf(m[hh], v);
             rs[hh] = m[hh] == -INFINITY ? 0.0f : expf(m[hh] - mn[hh]);
             m[hh] = mn[hh];
@@ -716,60 +727,9 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
         process_tile(t + kTile, kb, vb);
     }
 
-    // the wave's sums over its four position groups, then the waves
-#pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-        l[hh] += swz_xor16(l[hh]);
-        l[hh] += __shfl_xor(l[hh], 32, kWave);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            acc[hh][e] += swz_xor16(acc[hh][e]);
-            acc[hh][e] += __shfl_xor(acc[hh][e], 32, kWave);
-        }
-    }
-    if (pg == 0) {
-#pragma unroll
-        for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) wacc[wave][hh][8 * dc + e] = acc[hh][e];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int hh = 0; hh < G; ++hh) {
-            wml[wave][hh][0] = m[hh];
-            wml[wave][hh][1] = l[hh];
-        }
-    }
-    __syncthreads();
-    float* pbase = part + static_cast<size_t>(kvh * G) * kMaxSplits * kPartStride;
-    for (int e = tid; e < G * kHeadDim; e += kThreads) {
-        const int hh = e / kHeadDim;
-        const int d = e % kHeadDim;
-        float M = wml[0][hh][0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][hh][0]);
-        float sum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = wml[w][hh][0];
-            sum = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wacc[w][hh][d], sum);
-        }
-        pbase[(static_cast<size_t>(hh) * kMaxSplits + s) * kPartStride + 2 + d] = sum;
-    }
-    if (tid < G) {
-        float M = wml[0][tid][0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, wml[w][tid][0]);
-        float L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = wml[w][tid][0];
-            L = fmaf(mw == -INFINITY ? 0.0f : expf(mw - M), wml[w][tid][1], L);
-        }
-        float* dst = pbase + (static_cast<size_t>(tid) * kMaxSplits + s) * kPartStride;
-        dst[0] = M;
-        dst[1] = L;
-    }
+    merge_position_groups<G, kThreads>(m, l, acc, gml, gacc, ge,
+                                       part + (static_cast<size_t>(kvh * G) * kMaxSplits + s) * kPartStride,
+                                       static_cast<size_t>(kMaxSplits) * kPartStride);
 }
 
 int attn_splits(int max_seq);
@@ -1052,8 +1012,9 @@ __global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const
                                                                            float* __restrict__ part, int n_heads,
                                                                            int max_seq, int nsplit) {
     __shared__ float q_s[G][kHeadDim];
-    __shared__ float wml[kAttnThreads / kWave][G][2];
-    __shared__ float wacc[kAttnThreads / kWave][G][kHeadDim];
+    __shared__ float gml[kAttnThreads / 16][G][2];
+    __shared__ __align__(16) float gacc[kAttnThreads / 16][G][kHeadDim];
+    __shared__ float ge[G][kAttnThreads / 16];
     const int s = static_cast<int>(blockIdx.x);
     const int kvh = static_cast<int>(blockIdx.y);
     const int c = static_cast<int>(blockIdx.z);
@@ -1088,7 +1049,7 @@ __global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const
     for (int hh = 0; hh < G; ++hh)
 #pragma unroll
         for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
-    attn_split_core<G, false, Q8>(kraw, vraw, qr, p0, p1, pos, nullptr, wml, wacc,
+    attn_split_core<G, false, Q8>(kraw, vraw, qr, p0, p1, pos, nullptr, gml, gacc, ge,
                               part + ((static_cast<size_t>(c) * n_heads + kvh * G) * nsplit + s) * kPartStride,
                               static_cast<size_t>(nsplit) * kPartStride);
 }
