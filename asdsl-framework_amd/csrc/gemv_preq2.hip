@@ -45,7 +45,9 @@ constexpr int kThreads = 256;  // helper kernels
 //   kNorm:   h = x (+ delta); workgroup 0 writes h to h_out (the new residual
 //            stream); the GEMV input is rmsnorm(h) = (h * inv_rms) * nw with
 //            inv_rms = 1/sqrt(sum(h^2)/K + eps)
-//            (residual_add_rmsnorm_f32 / rmsnorm_f32, unified_engine.cpp:499-524,651-688).
+//            (residual_add_rmsnorm_f32 / rmsnorm_f32, unified_engine.cpp:499-524,651-688),
+//            computed as inv_rms * GEMV(h * nw) (the factor moved past the
+//            quantizer, see the prologue).
 //   kSwiglu: the GEMV input is silu(x) * up, zeroed where |value| < thr when
 //            thr > 0 (swiglu_inplace with fast_exp_avx2, unified_engine.cpp:803-857).
 //   kCombine: the GEMV input is the attention output, merged here from the
@@ -91,13 +93,17 @@ struct ProArgs {
     int vocab = 0;
 };
 
-template <int WAVES>
-__device__ __forceinline__ float block_sum_fixed(float v, float* s_red) {
+// Block sum in fixed order, in two halves around a barrier the caller
+// already has: each wave's butterfly sum to s_red[wave], then, after the
+// barrier, the waves' sums in wave order.
+__device__ __forceinline__ void wave_sum_to_lds(float v, float* s_red) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-    const int wave = static_cast<int>(threadIdx.x) >> 6;
-    if ((threadIdx.x & (kWave - 1)) == 0) s_red[wave] = v;
-    __syncthreads();
+    if ((threadIdx.x & (kWave - 1)) == 0) s_red[threadIdx.x >> 6] = v;
+}
+
+template <int WAVES>
+__device__ __forceinline__ float sum_waves(const float* s_red) {
     float t = s_red[0];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) t += s_red[w];
@@ -267,8 +273,17 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     // outstanding.
     if constexpr (WAVES == 16) __syncthreads();
     load_tile(tile);           // grid <= ntiles, so this tile exists
+    // kNorm: 1/rms is one positive factor of the whole input, so the int8
+    // codes of (h * inv_rms) * nw are those of h * nw (each group's scale is
+    // amax / 127 and takes the factor once) and the output of the GEMV on
+    // h * nw is inv_rms times that of the GEMV on the normed input.  The GEMV
+    // therefore quantizes h * nw right away and scales its outputs by
+    // inv_rms: the sum of squares is reduced behind the staging barrier and
+    // the norm adds no barrier or dependent step before the dot products.
+    // (Equal to the normed form up to fp32 rounding; an element whose
+    // quotient lies within rounding of a .5 boundary can take the other code.)
+    __shared__ float s_red[kNormed ? WAVES : 1];
     if constexpr (kNormed) {
-        __shared__ float s_red[WAVES];
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < NCH; ++i) {
@@ -285,13 +300,10 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
                         make_float4(act.v[i][4], act.v[i][5], act.v[i][6], act.v[i][7]);
                 }
             }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) act.v[i][e] *= ew[i][e];
         }
-        ss = block_sum_fixed<WAVES>(ss, s_red);
-        const float inv_rms = 1.0f / sqrtf(ss / static_cast<float>(K) + pa.eps);
-#pragma unroll
-        for (int i = 0; i < NCH; ++i)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) act.v[i][e] = (act.v[i][e] * inv_rms) * ew[i][e];
+        wave_sum_to_lds(ss, s_red);
     } else if constexpr (PRO == Pro::kSwiglu) {
 #pragma unroll
         for (int i = 0; i < NCH; ++i)
@@ -323,6 +335,8 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     }
     act.process(K, im);        // quantize while the weights are in flight
     __syncthreads();
+    float inv_rms = 1.0f;
+    if constexpr (kNormed) inv_rms = 1.0f / sqrtf(sum_waves<WAVES>(s_red) / static_cast<float>(K) + pa.eps);
 
     // XREG: this lane's activation units are copied from LDS into registers
     // once and reused for every tile; otherwise they are read per tile.
@@ -363,6 +377,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
         }
         const int band = band_of(tile);
         acc = slot_sum<SB>(acc);
+        if constexpr (kNormed) acc *= inv_rms;
         // next tile's loads after the reduction: issuing them before it keeps
         // ~20 more VGPRs live (measured), costing a workgroup per CU at NU=6
         if (tile + tile_step < ntiles) load_tile(tile + tile_step);

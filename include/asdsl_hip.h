@@ -380,7 +380,11 @@ asdsl_status asdsl_dequant_preq2(const uint8_t* meta, const uint8_t* quant, floa
  *
  * preq2 GEMV whose fp32 input is rmsnorm(h) with h = h_in + delta (delta may
  * be NULL): inv_rms = 1/sqrt(sum(h^2)/K + eps), x = (h*inv_rms)*norm_w, then
- * quantized inside as asdsl_gemv_preq2_fused.  If h_out is not NULL, h is
+ * quantized inside as asdsl_gemv_preq2_fused.  The positive factor inv_rms
+ * leaves the int8 codes unchanged and scales every group scale, so it is
+ * applied to the outputs instead: y = inv_rms * GEMV(h*norm_w), equal to the
+ * normed form up to fp32 rounding (a value within rounding of a code
+ * boundary may take the neighbouring code).  If h_out is not NULL, h is
  * stored there (the new residual stream; must not alias h_in or delta).  If
  * argmax_key is not NULL (zeroed before the call), the largest y and its row
  * (first on ties) are folded into it: key = order-preserving float bits << 32
