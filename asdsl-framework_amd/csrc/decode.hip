@@ -548,7 +548,6 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
     float* __restrict__ part, float* __restrict__ att, int n_heads, int n_kv, int max_seq, int rot_half,
     int max_splits) {
-    constexpr int kWaves = WAVES;
     constexpr int kThreads = WAVES * kWave;
     constexpr int kTile = 16 * WAVES;  // positions per tile
     constexpr int kStep = 4 * WAVES;   // positions per step of all waves
