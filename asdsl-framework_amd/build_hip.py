@@ -2,6 +2,10 @@
 
 Compiles every ``csrc/*.hip`` with hipcc into ``_build/`` and links the shared
 library into ``lib/``.  Run ``python build_hip.py`` or call :func:`build`.
+``timeline=True`` (``--timeline``) builds the timing variant
+``lib/libasdsl_hip_timeline.so`` (``-DASDSL_WG_TIMELINE``, objects in
+``_build_timeline/``): the same kernels, with the decode step's kernels
+stamping a per-workgroup wall-clock timeline (``bench.py --decode-timeline``).
 """
 
 from __future__ import annotations
@@ -17,6 +21,8 @@ REPO_ROOT = PKG_ROOT.parent
 CSRC = PKG_ROOT / "csrc"
 BUILD = PKG_ROOT / "_build"
 LIB = PKG_ROOT / "lib" / "libasdsl_hip.so"
+BUILD_TIMELINE = PKG_ROOT / "_build_timeline"
+LIB_TIMELINE = PKG_ROOT / "lib" / "libasdsl_hip_timeline.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -35,9 +41,9 @@ COMMON_FLAGS = [
 ]
 
 
-def _compile(src: Path, verbose: bool) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, verbose: bool, build_dir: Path = BUILD, extra: tuple = ()) -> Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -51,38 +57,42 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-def _stale(src: Path, headers: list[Path]) -> bool:
-    obj = BUILD / (src.stem + ".o")
+def _stale(src: Path, headers: list[Path], build_dir: Path = BUILD) -> bool:
+    obj = build_dir / (src.stem + ".o")
     if not obj.exists():
         return True
     t = obj.stat().st_mtime
     return src.stat().st_mtime > t or any(h.stat().st_mtime > t for h in headers)
 
 
-def build(verbose: bool = False, incremental: bool = False) -> Path:
-    """Compile all HIP sources and link lib/libasdsl_hip.so; returns its path.
-    incremental=True recompiles only sources newer than their objects (or any
-    header); the default rebuilds everything."""
-    BUILD.mkdir(exist_ok=True)
-    LIB.parent.mkdir(exist_ok=True)
+def build(verbose: bool = False, incremental: bool = False, timeline: bool = False) -> Path:
+    """Compile all HIP sources and link lib/libasdsl_hip.so (timeline=True:
+    lib/libasdsl_hip_timeline.so); returns its path.  incremental=True
+    recompiles only sources newer than their objects (or any header); the
+    default rebuilds everything."""
+    build_dir = BUILD_TIMELINE if timeline else BUILD
+    lib = LIB_TIMELINE if timeline else LIB
+    extra = ("-DASDSL_WG_TIMELINE",) if timeline else ()
+    build_dir.mkdir(exist_ok=True)
+    lib.parent.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     headers = sorted(CSRC.glob("*.hpp")) + sorted((REPO_ROOT / "include").glob("*.h"))
-    todo = [s for s in sources if not incremental or _stale(s, headers)]
+    todo = [s for s in sources if not incremental or _stale(s, headers, build_dir)]
     with cf.ThreadPoolExecutor(max_workers=min(8, max(1, len(todo)))) as ex:
-        list(ex.map(lambda s: _compile(s, verbose), todo))
-    objs = [BUILD / (s.stem + ".o") for s in sources]
-    tmp = LIB.with_suffix(".so.tmp")
+        list(ex.map(lambda s: _compile(s, verbose, build_dir, extra), todo))
+    objs = [build_dir / (s.stem + ".o") for s in sources]
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv, incremental="-i" in sys.argv))
+    print(build(verbose="-v" in sys.argv, incremental="-i" in sys.argv, timeline="--timeline" in sys.argv))

@@ -110,6 +110,11 @@ asdsl_status preq2_embed_rmsnorm(const uint8_t* meta, const uint8_t* quant, cons
                                  int in_features, int group_size, float eps, unsigned long long* clear_key,
                                  asdsl_stream_t stream);
 
+#ifdef ASDSL_WG_TIMELINE
+// Timing build: the preq2 GEMVs' timeline buffer (see device_common.hpp).
+asdsl_status timeline_set_preq2(void* buf);
+#endif
+
 // Workgroups for a streaming kernel: enough tiles for every wave, capped at
 // `per_cu` workgroups per compute unit (waves then loop over tiles).
 inline int stream_grid(long long tiles, int waves_per_wg, int per_cu, int cus) {

@@ -110,6 +110,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
     if (blockIdx.x == 0 && threadIdx.x == 0 && amax) *amax = 0ull;
 }
 
+ASDSL_TIMELINE_BUFFER
+
 // Next token = the argmax row; position + 1.
 __global__ void finalize_kernel(const unsigned long long* __restrict__ amax, int* __restrict__ token,
                                 int* __restrict__ pos) {
@@ -316,6 +318,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     // outside the cache (the combine then writes zeros)
     if (p0 > pos || pos < 0 || pos >= max_seq) return;
     const int p1 = min(p0 + kSplit, pos + 1);
+    const int tl_wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
+    ASDSL_TIMELINE_STAMP(5, tl_wg, 0);
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & (kWave - 1);
     const int wave = tid >> 6;
@@ -387,6 +391,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         }
     }
     if (tid < kHeadDim) kv_new[1][tid] = Q8 ? vnew : h2f(f2h(vnew));
+    ASDSL_TIMELINE_STAMP(5, tl_wg, 1);
     __syncthreads();
     if constexpr (Q8) {
         kv_quantize_new(kv_new, kv, row0 + pos, pos < p1);
@@ -402,9 +407,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
 
+    ASDSL_TIMELINE_STAMP(5, tl_wg, 2);
     attn_split_core<G, true, Q8>(kraw, vraw, qr, p0, p1, pos, kv_new, gml, gacc, ge,
                              part + (static_cast<size_t>(kvh * G) * nsplit + s) * kPartStride,
                              static_cast<size_t>(nsplit) * kPartStride);
+    ASDSL_TIMELINE_STAMP(5, tl_wg, 4);
 }
 
 // out[h][d] = sum_s e_s acc_s[d] / sum_s e_s l_s, e_s = exp(m_s - max m).
@@ -437,6 +444,8 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
     }
     const int ns = pos / kSplit + 1;
     if (ns <= fold) return;  // the consuming GEMV's prologue merges these splits itself
+    const int tl_slot = col == 0 ? 6 : -1;
+    ASDSL_TIMELINE_STAMP(tl_slot, h, 0);
     const int ng = min(kCombineGroups, (ns + kChunk - 1) / kChunk);  // groups with splits
     const int per = (ns + ng - 1) / ng;
     const int s_begin = min(ns, g * per);
@@ -469,8 +478,10 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
         }
         M = cm;
     }
+    ASDSL_TIMELINE_STAMP(tl_slot, h, 3);
     if (ng == 1) {  // uniform: group 0 holds every split
         if (g == 0) out[static_cast<size_t>(h) * kHeadDim + d] = o * (1.0f / L);
+        ASDSL_TIMELINE_STAMP(tl_slot, h, 4);
         return;
     }
     go[g][d] = o;
@@ -491,6 +502,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
         }
         out[static_cast<size_t>(h) * kHeadDim + d] = sum * (1.0f / Ls);
     }
+    ASDSL_TIMELINE_STAMP(tl_slot, h, 4);
 }
 
 // ------------------------------------------------------------ decode attention
@@ -560,6 +572,8 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
     const int s = static_cast<int>(blockIdx.x);
     const int kvh = static_cast<int>(blockIdx.y);
     const int tid = static_cast<int>(threadIdx.x);
+    const int tl_wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
+    ASDSL_TIMELINE_STAMP(4, tl_wg, 0);
     const int pos = *pos_ptr;
     if (pos < 0 || pos >= max_seq) {  // outside the cache: zero output, nothing written to the cache
         if (s == 0)
@@ -638,6 +652,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
         }
     }
     if (tid < kHeadDim) kv_new[1][tid] = Q8 ? vnew : h2f(f2h(vnew));
+    ASDSL_TIMELINE_STAMP(4, tl_wg, 1);
     __syncthreads();
     if constexpr (Q8) {
         if (wave < 4) kv_quantize_new(kv_new, kv, row0 + pos, pos >= p0 && pos < p1);
@@ -718,6 +733,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
             }
         }
     };
+    ASDSL_TIMELINE_STAMP(4, tl_wg, 2);
     for (int t = p0; t < p1; t += 2 * kTile) {  // uniform per workgroup
         if (t + kTile < p1) load_tile(t + kTile, kb, vb);
         process_tile(t, ka, va);
@@ -726,9 +742,11 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
         process_tile(t + kTile, kb, vb);
     }
 
+    ASDSL_TIMELINE_STAMP(4, tl_wg, 3);
     merge_position_groups<G, kThreads>(m, l, acc, gml, gacc, ge,
                                        part + (static_cast<size_t>(kvh * G) * kMaxSplits + s) * kPartStride,
                                        static_cast<size_t>(kMaxSplits) * kPartStride);
+    ASDSL_TIMELINE_STAMP(4, tl_wg, 4);
 }
 
 int attn_splits(int max_seq);
@@ -1472,3 +1490,18 @@ extern "C" asdsl_status asdsl_kv_zero_from_q8(int8_t* k_cache, int8_t* v_cache, 
                   reinterpret_cast<uint4*>(k_cache), reinterpret_cast<uint4*>(v_cache), k_scale, v_scale, n_kv_heads,
                   max_seq, from);
 }
+
+#ifdef ASDSL_WG_TIMELINE
+// Timing build only (lib/libasdsl_hip_timeline.so), no reference counterpart:
+// the decode step's kernels stamp their workgroup timeline into buf
+// (kTimelineSlots * kTimelineWgs * 8 uint64, layout in device_common.hpp);
+// null switches the stamps off.
+extern "C" asdsl_status asdsl_timeline_set_buffer(void* buf) {
+    const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(asdsl::g_timeline), &buf, sizeof(buf));
+    if (e != hipSuccess) {
+        asdsl::set_error("timeline: %s", hipGetErrorString(e));
+        return ASDSL_ERR_HIP;
+    }
+    return asdsl::timeline_set_preq2(buf);
+}
+#endif

@@ -332,4 +332,31 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
     return (static_cast<unsigned long long>(k) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(row));
 }
 
+// Workgroup timeline of the decode step's kernels, compiled in only by the
+// timing build (-DASDSL_WG_TIMELINE, lib/libasdsl_hip_timeline.so): thread 0
+// of workgroup wg stores the 100 MHz wall clock at fixed point k of its kernel
+// to tl[(slot * kTimelineWgs + wg) * 8 + k] of the buffer set with
+// asdsl_timeline_set_buffer.  Slots: 0 o_proj with the split merge, 1 gate_up
+// with SwiGLU, 2 norm-fed GEMV (qkv), 3 plain 16-wave GEMV (down), 4 short-form
+// attention, 5 attention partials, 6 attention combine, 7 plain 8-wave GEMV
+// (o_proj beyond 256 positions).
+constexpr int kTimelineSlots = 8;
+constexpr int kTimelineWgs = 1024;
+#ifdef ASDSL_WG_TIMELINE
+#define ASDSL_TIMELINE_BUFFER __device__ unsigned long long* g_timeline;
+#define ASDSL_TIMELINE_STAMP(slot, wg, k)                                                                  \
+    do {                                                                                                   \
+        if ((slot) >= 0 && g_timeline && (wg) < kTimelineWgs && threadIdx.x == 0)                          \
+            g_timeline[(static_cast<size_t>(slot) * kTimelineWgs + (wg)) * 8 + (k)] =                      \
+                static_cast<unsigned long long>(wall_clock64());                                           \
+    } while (0)
+#else
+#define ASDSL_TIMELINE_BUFFER
+#define ASDSL_TIMELINE_STAMP(slot, wg, k) \
+    do {                                  \
+        (void)(slot);                     \
+        (void)(wg);                       \
+    } while (0)
+#endif
+
 }  // namespace asdsl

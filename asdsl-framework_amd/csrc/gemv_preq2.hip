@@ -40,6 +40,7 @@ namespace asdsl {
 namespace {
 
 constexpr int kThreads = 256;  // helper kernels
+ASDSL_TIMELINE_BUFFER
 
 // Decode-step work fused into the GEMV's activation prologue / epilogue.
 //   kNorm:   h = x (+ delta); workgroup 0 writes h to h_out (the new residual
@@ -121,6 +122,13 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
                                                                   ProArgs pa) {
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ float s_part[2][WAVES][4];
+    constexpr int kTl = PRO == Pro::kCombine                 ? 0
+                        : SWIGLU_EPI                         ? 1
+                        : (PRO == Pro::kNorm && !ARGMAX)     ? 2
+                        : (PRO == Pro::kPlain && !Q8)        ? (WAVES == 16 ? 3 : 7)
+                                                             : -1;
+    const int tl_wg = static_cast<int>(blockIdx.x);
+    ASDSL_TIMELINE_STAMP(kTl, tl_wg, 0);
     constexpr int UPS = GS / 32;       // units per (row, group)
     constexpr int UPG4 = 4 * UPS;      // units per (band, group)
     constexpr int SB = UPS == 1 ? 0 : 2;
@@ -334,7 +342,9 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
         }
     }
     act.process(K, im);        // quantize while the weights are in flight
+    ASDSL_TIMELINE_STAMP(kTl, tl_wg, 1);
     __syncthreads();
+    ASDSL_TIMELINE_STAMP(kTl, tl_wg, 2);
     float inv_rms = 1.0f;
     if constexpr (kNormed) inv_rms = 1.0f / sqrtf(sum_waves<WAVES>(s_red) / static_cast<float>(K) + pa.eps);
 
@@ -375,6 +385,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
                 acc = fmaf(-(z * s), XREG ? xu[jj] : us, acc);
             }
         }
+        if (tile == static_cast<int>(blockIdx.x)) ASDSL_TIMELINE_STAMP(kTl, tl_wg, 3);
         const int band = band_of(tile);
         acc = slot_sum<SB>(acc);
         if constexpr (kNormed) acc *= inv_rms;
@@ -408,6 +419,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
             parity ^= 1;
         }
     }
+    ASDSL_TIMELINE_STAMP(kTl, tl_wg, 4);
     if constexpr (ARGMAX) {
         // max is order-free: any reduction order gives the same key.  One
         // atomic per workgroup (one per wave serialized on the single address:
@@ -657,6 +669,17 @@ asdsl_status launch_preq2(const uint8_t* meta, const uint8_t* quant, const float
 }
 
 }  // namespace
+
+#ifdef ASDSL_WG_TIMELINE
+asdsl_status timeline_set_preq2(void* buf) {
+    const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), &buf, sizeof(buf));
+    if (e != hipSuccess) {
+        set_error("timeline: %s", hipGetErrorString(e));
+        return ASDSL_ERR_HIP;
+    }
+    return ASDSL_OK;
+}
+#endif
 
 }  // namespace asdsl
 

@@ -1121,6 +1121,79 @@ def pmc_probe(mode: str) -> int:
     return 0
 
 
+# Workgroup timeline of one decode layer (timing build): the kernels of the
+# step stamp a 100 MHz wall clock at fixed points of every workgroup
+# (slots and stamp points: csrc/device_common.hpp, ASDSL_TIMELINE_STAMP).
+TIMELINE_KERNELS = {0: "o_proj (split merge)", 1: "gate_up (SwiGLU)", 2: "qkv (norm)", 3: "down",
+                    4: "attention (short form)", 5: "attention partials", 6: "attention combine", 7: "o_proj"}
+_GEMV_PHASES = ((0, 1, "prologue"), (1, 2, "staging barrier"), (2, 3, "first tile"), (3, 4, "tail"))
+TIMELINE_PHASES = {0: _GEMV_PHASES, 1: _GEMV_PHASES, 2: _GEMV_PHASES, 3: _GEMV_PHASES, 7: _GEMV_PHASES,
+                   4: ((0, 1, "loads and RoPE"), (1, 2, "barrier and K/V store"), (2, 3, "scores, softmax, P.V"),
+                       (3, 4, "merge")),
+                   5: ((0, 1, "loads and RoPE"), (1, 2, "barrier and K/V store"), (2, 4, "split")),
+                   6: ((0, 3, "fold"), (3, 4, "merge and store"))}
+
+
+def decode_timeline(ctx: int, n_layers: int = 32, steps: int = 8, seed: int = 11) -> dict:
+    """Per-workgroup timeline of the last layer of the last of `steps`
+    captured steps at context `ctx` (each layer overwrites the stamps).  Needs
+    the timing build (ASDSL_HIP_LIB=asdsl-framework_amd/lib/libasdsl_hip_timeline.so).
+    Per kernel: workgroups, first start and last end (us from the layer's
+    first kernel start), gap from the previous kernel's last end to this
+    kernel's first start, and the median / max of each phase."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from asdsl import _hip
+    from asdsl.engine import DecodeConfig, DecodeEngine
+
+    try:
+        setter = _hip.LIB.asdsl_timeline_set_buffer
+    except AttributeError:
+        raise SystemExit("--decode-timeline needs the timing build: "
+                         "ASDSL_HIP_LIB=asdsl-framework_amd/lib/libasdsl_hip_timeline.so") from None
+    setter.argtypes = [ctypes.c_void_p]
+    setter.restype = ctypes.c_int
+    cfg = DecodeConfig(n_layers=n_layers, max_seq=ctx + steps + 64)
+    eng = DecodeEngine.synthetic(cfg, seed=seed)
+    eng.prefill_kv_random(ctx, seed=ctx)
+    eng.token.fill_(1)
+    eng.capture()
+    eng.step()
+    torch.cuda.synchronize()
+    buf = torch.zeros(8 * 1024 * 8, dtype=torch.int64, device="cuda")
+    _hip.check(setter(ctypes.c_void_p(buf.data_ptr())), "asdsl_timeline_set_buffer")
+    for _ in range(steps):
+        eng.step()
+    torch.cuda.synchronize()
+    _hip.check(setter(None), "asdsl_timeline_set_buffer")
+    t = buf.cpu().numpy().reshape(8, 1024, 8).astype(np.float64)
+    rows = []
+    for slot in range(8):
+        a = t[slot]
+        a = a[(a[:, 0] > 0) & (a[:, 4] > 0)]  # workgroups that ran to the end
+        if len(a):
+            rows.append((a[:, 0].min(), slot, a))
+    rows.sort(key=lambda r: r[0])
+    base = rows[0][0]
+    kernels, prev_end = [], None
+    for t0, slot, a in rows:
+        us = (a - base) * 0.01  # 100 MHz ticks -> us
+        k = {"kernel": TIMELINE_KERNELS[slot], "workgroups": int(len(a)),
+             "first_start_us": round(float(us[:, 0].min()), 2), "last_end_us": round(float(us[:, 4].max()), 2)}
+        if prev_end is not None:
+            k["gap_us"] = round(float(us[:, 0].min()) - prev_end, 2)
+        for i0, i1, name in TIMELINE_PHASES[slot]:
+            d = (a[:, i1] - a[:, i0]) * 0.01
+            k[name + "_us"] = [round(float(np.median(d)), 2), round(float(d.max()), 2)]
+        prev_end = float(us[:, 4].max())
+        kernels.append(k)
+    return {"ctx": ctx, "layer": n_layers - 1, "steps": steps, "phases": "[median, max] over workgroups",
+            "kernels": kernels}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1135,6 +1208,9 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=64, help="captured steps per context in the decode phase")
     ap.add_argument("--no-verify", action="store_true", help="decode phase: skip the verify pass, PLD rows")
     ap.add_argument("--no-int8-kv", action="store_true", help="decode phase: skip the int8 KV cache rows")
+    ap.add_argument("--decode-timeline", type=int, nargs="+", default=None, metavar="CTX",
+                    help="per-workgroup timeline of one decode layer at these contexts (needs the timing "
+                         "build: ASDSL_HIP_LIB=asdsl-framework_amd/lib/libasdsl_hip_timeline.so)")
     ap.add_argument("--suite", action="store_true",
                     help="one JSON line per hot-path row: kernel at its workload vs the HBM roofline, "
                          "with the reference's compiled CPU kernel timed on the same inputs")
@@ -1155,6 +1231,10 @@ def main() -> int:
 
     if args.suite:
         return run_suite(args)
+    if args.decode_timeline:
+        for ctx in args.decode_timeline:
+            print(json.dumps({"decode_timeline": decode_timeline(ctx)}), flush=True)
+        return 0
     if args.pmc_probe and args.pmc_probe != "gate_up":
         return pmc_probe(args.pmc_probe)
     if args.decode:
