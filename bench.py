@@ -1211,6 +1211,7 @@ def main() -> int:
     ap.add_argument("--decode-timeline", type=int, nargs="+", default=None, metavar="CTX",
                     help="per-workgroup timeline of one decode layer at these contexts (needs the timing "
                          "build: ASDSL_HIP_LIB=asdsl-framework_amd/lib/libasdsl_hip_timeline.so)")
+    ap.add_argument("--timeline-layers", type=int, default=32, help="--decode-timeline: layers of the model")
     ap.add_argument("--suite", action="store_true",
                     help="one JSON line per hot-path row: kernel at its workload vs the HBM roofline, "
                          "with the reference's compiled CPU kernel timed on the same inputs")
@@ -1233,7 +1234,7 @@ def main() -> int:
         return run_suite(args)
     if args.decode_timeline:
         for ctx in args.decode_timeline:
-            print(json.dumps({"decode_timeline": decode_timeline(ctx)}), flush=True)
+            print(json.dumps({"decode_timeline": decode_timeline(ctx, n_layers=args.timeline_layers)}), flush=True)
         return 0
     if args.pmc_probe and args.pmc_probe != "gate_up":
         return pmc_probe(args.pmc_probe)
