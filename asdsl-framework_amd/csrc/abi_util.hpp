@@ -91,6 +91,18 @@ asdsl_status preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const 
                                int out_features, int in_features, int group_size, int n_cols, asdsl_stream_t stream,
                                bool allow_mfma, void* work = nullptr, size_t work_bytes = 0);
 
+// The MFMA form of preq2_fused_batch (up to 16 columns) on an activation
+// image another kernel already wrote at `image` (image_store8 layout: img,
+// then fac at image + in_features * 16 bytes; columns past n_cols zero).
+// preq2_batch_image_applies says whether preq2_fused_batch would take the
+// MFMA form for this call (allow_mfma included); only then is
+// preq2_batch_mfma_image valid (ASDSL_ERR_INVALID_ARGUMENT otherwise).
+bool preq2_batch_image_applies(const uint8_t* meta, const uint8_t* quant, int out_features, int in_features,
+                               int group_size, int n_cols, bool allow_mfma);
+asdsl_status preq2_batch_mfma_image(const uint8_t* meta, const uint8_t* quant, const void* image, float* Y,
+                                    int out_features, int in_features, int group_size, int n_cols,
+                                    asdsl_stream_t stream);
+
 // The decode step's o_proj: gemv_preq2_fused of the attention output, which
 // the GEMV's prologue merges itself from the split partials (part: per head
 // nsplit rows of part_stride floats, m, l, acc[head_dim]) of a position

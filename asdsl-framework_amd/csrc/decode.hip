@@ -924,18 +924,34 @@ __global__ __launch_bounds__(256) void verify_embed_kernel(const uint16_t* __res
 // of the norm-fed GEMVs at hidden 3072): thread t folds the 8-element chunks
 // t, t + 512, ... element by element, then a xor butterfly per wave and the
 // 8 wave sums in order, so both passes normalize identically.
+// IMG_GS (32 or 128): X[c] is also quantized into the next batched GEMV's
+// int8 image (image_store8, the values batch_quantize_kernel would form from
+// X), and workgroups c >= ncols (the grid covers kImageCols columns) write
+// that image's zero columns, so the GEMV needs no quantize launch of its own.
+template <int IMG_GS>
 __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __restrict__ H,
                                                                        const float* __restrict__ D,
                                                                        const float* __restrict__ w,
-                                                                       float* __restrict__ X, int K, float eps) {
+                                                                       float* __restrict__ X, int K, float eps,
+                                                                       int ncols, uint2* __restrict__ img,
+                                                                       float2* __restrict__ fac) {
     __shared__ float red[kNormThreads / kWave];
-    const size_t c = blockIdx.x;
+    const int col = static_cast<int>(blockIdx.x);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int nchunk = K >> 3;
+    if constexpr (IMG_GS != 0) {
+        if (col >= ncols) {
+            const float z[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            for (int base = 0; base < nchunk; base += kNormThreads)  // uniform per workgroup
+                image_store8<IMG_GS>(z, base + tid, col, base + tid < nchunk, img, fac);
+            return;
+        }
+    }
+    const size_t c = static_cast<size_t>(col);
     float4* h = reinterpret_cast<float4*>(H + c * K);
     const float4* d = D ? reinterpret_cast<const float4*>(D + c * K) : nullptr;
     float4* x = reinterpret_cast<float4*>(X + c * K);
     const float4* w4 = reinterpret_cast<const float4*>(w);
-    const int tid = static_cast<int>(threadIdx.x);
-    const int nchunk = K >> 3;
     float ss = 0.0f;
     for (int ch = tid; ch < nchunk; ch += kNormThreads) {
         float v[8];
@@ -959,13 +975,22 @@ __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __
 #pragma unroll
     for (int q = 1; q < kNormThreads / kWave; ++q) tot += red[q];
     const float inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
-    for (int ch = tid; ch < nchunk; ch += kNormThreads) {
-        const float4 a = h[2 * ch], b = h[2 * ch + 1];
-        const float4 wa = w4[2 * ch], wb = w4[2 * ch + 1];
-        x[2 * ch] = make_float4((a.x * inv_rms) * wa.x, (a.y * inv_rms) * wa.y, (a.z * inv_rms) * wa.z,
-                               (a.w * inv_rms) * wa.w);
-        x[2 * ch + 1] = make_float4((b.x * inv_rms) * wb.x, (b.y * inv_rms) * wb.y, (b.z * inv_rms) * wb.z,
-                                   (b.w * inv_rms) * wb.w);
+    // the loop is uniform per workgroup (every lane of a quantization group
+    // takes part); chunks past the end quantize a copy of the last chunk and
+    // store nothing
+    for (int base = 0; base < nchunk; base += kNormThreads) {
+        const int ch = base + tid;
+        const int cc = min(ch, nchunk - 1);
+        const float4 a = h[2 * cc], b = h[2 * cc + 1];
+        const float4 wa = w4[2 * cc], wb = w4[2 * cc + 1];
+        const float v[8] = {(a.x * inv_rms) * wa.x, (a.y * inv_rms) * wa.y, (a.z * inv_rms) * wa.z,
+                            (a.w * inv_rms) * wa.w, (b.x * inv_rms) * wb.x, (b.y * inv_rms) * wb.y,
+                            (b.z * inv_rms) * wb.z, (b.w * inv_rms) * wb.w};
+        if (ch < nchunk) {
+            x[2 * ch] = make_float4(v[0], v[1], v[2], v[3]);
+            x[2 * ch + 1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, ch, col, ch < nchunk, img, fac);
     }
 }
 
@@ -1073,12 +1098,34 @@ __global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const
 
 // S[c] = SwiGLU(gate, up) of GU[c] = [gate | up] with the FATReLU threshold
 // (swiglu_inplace, unified_engine.cpp:803-857; the decode prologue's formula).
+// S[c] = swiglu(GU[c][0:ffn], GU[c][ffn:2ffn]), one 8-element chunk per
+// thread (grid: ceil(ffn / 2048) x columns).  IMG_GS: also the down GEMV's
+// int8 image of S (image_store8), with zero image columns for c >= ncols (the
+// grid then covers kImageCols columns).
+template <int IMG_GS>
 __global__ __launch_bounds__(256) void verify_swiglu_kernel(const float* __restrict__ GU, float* __restrict__ S,
-                                                            int ffn, float thr) {
-    const size_t c = blockIdx.y;
-    for (int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); i < ffn;
-         i += static_cast<int>(gridDim.x * blockDim.x))
-        S[c * ffn + i] = swiglu_ref(GU[c * 2 * ffn + i], GU[c * 2 * ffn + ffn + i], thr);
+                                                            int ffn, float thr, int ncols, uint2* __restrict__ img,
+                                                            float2* __restrict__ fac) {
+    const int col = static_cast<int>(blockIdx.y);
+    const size_t c = static_cast<size_t>(col);
+    const int nchunk = ffn >> 3;
+    const int ch = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+    const int cc = min(ch, nchunk - 1);
+    float v[8];
+    if (IMG_GS != 0 && col >= ncols) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+    } else {
+        const float* g = GU + c * 2 * ffn + 8 * cc;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = swiglu_ref(g[e], g[ffn + e], thr);
+        if (ch < nchunk) {
+            float4* sp = reinterpret_cast<float4*>(S + c * ffn + 8 * ch);
+            sp[0] = make_float4(v[0], v[1], v[2], v[3]);
+            sp[1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+    }
+    if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, ch, col, ch < nchunk, img, fac);
 }
 
 // keys[c] = max over rows of argmax_key(logits[c][row], row): the largest
@@ -1404,16 +1451,34 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     asdsl_status st = launch("verify_embed_kernel", verify_embed_kernel, dim3((m.hidden + 1023) / 1024, n), dim3(256),
                              0, s, m.embed, tokens, H, m.hidden, m.vocab, keys);
     if (st != ASDSL_OK) return st;
+    // The norm and SwiGLU kernels write the next projection's int8 image
+    // themselves when that projection takes the MFMA form, which then runs
+    // without its quantize launch.
+    auto* img = static_cast<uint2*>(mimg);
+    auto fac_of = [&](int K) { return reinterpret_cast<float2*>(static_cast<uint8_t*>(mimg) + static_cast<size_t>(K) * 16); };
+    auto norm_then_gemv = [&](const float* D, const float* nw, const uint8_t* meta, const uint8_t* quant, float* Y,
+                              int M, int gs) -> asdsl_status {
+        const int K = m.hidden;
+        if (preq2_batch_image_applies(meta, quant, M, K, gs, n, mfma)) {
+            asdsl_status r = launch("verify_add_norm_kernel",
+                                    gs == 32 ? verify_add_norm_kernel<32> : verify_add_norm_kernel<128>,
+                                    dim3(kImageCols), dim3(kNormThreads), 0, s, H, D, nw, X, K, m.rms_eps, n, img,
+                                    fac_of(K));
+            if (r != ASDSL_OK) return r;
+            return preq2_batch_mfma_image(meta, quant, mimg, Y, M, K, gs, n, stream);
+        }
+        asdsl_status r = launch("verify_add_norm_kernel", verify_add_norm_kernel<0>, dim3(n), dim3(kNormThreads), 0, s,
+                                H, D, nw, X, K, m.rms_eps, n, static_cast<uint2*>(nullptr),
+                                static_cast<float2*>(nullptr));
+        if (r != ASDSL_OK) return r;
+        return preq2_fused_batch(meta, quant, X, Y, M, K, gs, n, stream, mfma, mimg, w.mimg_bytes);
+    };
     // H carries the residual stream of every column; O (attention output
     // projection) and S -> O (down projection) are added in by the next norm.
     const float* pending = nullptr;
     for (int l = 0; l < m.n_layers; ++l) {
         const asdsl_decode_layer& L = m.layers[l];
-        st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H, pending,
-                    L.rms_att, X, m.hidden, m.rms_eps);
-        if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.qkv_meta, L.qkv_quant, X, QKV, qkv_dim, m.hidden, m.gs_attn, n, stream, mfma, mimg,
-                           w.mimg_bytes);
+        st = norm_then_gemv(pending, L.rms_att, L.qkv_meta, L.qkv_quant, QKV, qkv_dim, m.gs_attn);
         if (st != ASDSL_OK) return st;
         const KvCache kv{L.k_cache, L.v_cache, L.k_scale, L.v_scale};
         st = launch("verify_rope_kv_kernel", q8 ? verify_rope_kv_kernel<true> : verify_rope_kv_kernel<false>,
@@ -1430,27 +1495,30 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
                     static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0);
         if (st != ASDSL_OK) return st;
         st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma, mimg,
-                           w.mimg_bytes);
+                               w.mimg_bytes);
         if (st != ASDSL_OK) return st;
-        st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H,
-                    static_cast<const float*>(O), L.rms_ffn, X, m.hidden, m.rms_eps);
+        st = norm_then_gemv(O, L.rms_ffn, L.gu_meta, L.gu_quant, GU, 2 * m.ffn, m.gs_ffn);
         if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.gu_meta, L.gu_quant, X, GU, 2 * m.ffn, m.hidden, m.gs_ffn, n, stream, mfma, mimg,
-                           w.mimg_bytes);
-        if (st != ASDSL_OK) return st;
-        st = launch("verify_swiglu_kernel", verify_swiglu_kernel, dim3((m.ffn + 1023) / 1024, n), dim3(256), 0, s,
-                    static_cast<const float*>(GU), S, m.ffn, L.fatrelu_threshold);
-        if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.down_meta, L.down_quant, S, O, m.hidden, m.ffn, m.gs_ffn, n, stream, mfma, mimg,
-                           w.mimg_bytes);
+        const bool down_img = preq2_batch_image_applies(L.down_meta, L.down_quant, m.hidden, m.ffn, m.gs_ffn, n, mfma);
+        const int sw_chunks = (m.ffn / 8 + 255) / 256;
+        if (down_img) {
+            st = launch("verify_swiglu_kernel", m.gs_ffn == 32 ? verify_swiglu_kernel<32> : verify_swiglu_kernel<128>,
+                        dim3(sw_chunks, kImageCols), dim3(256), 0, s, static_cast<const float*>(GU), S, m.ffn,
+                        L.fatrelu_threshold, n, img, fac_of(m.ffn));
+            if (st != ASDSL_OK) return st;
+            st = preq2_batch_mfma_image(L.down_meta, L.down_quant, mimg, O, m.hidden, m.ffn, m.gs_ffn, n, stream);
+        } else {
+            st = launch("verify_swiglu_kernel", verify_swiglu_kernel<0>, dim3(sw_chunks, n), dim3(256), 0, s,
+                        static_cast<const float*>(GU), S, m.ffn, L.fatrelu_threshold, n, static_cast<uint2*>(nullptr),
+                        static_cast<float2*>(nullptr));
+            if (st != ASDSL_OK) return st;
+            st = preq2_fused_batch(L.down_meta, L.down_quant, S, O, m.hidden, m.ffn, m.gs_ffn, n, stream, mfma, mimg,
+                                   w.mimg_bytes);
+        }
         if (st != ASDSL_OK) return st;
         pending = O;
     }
-    st = launch("verify_add_norm_kernel", verify_add_norm_kernel, dim3(n), dim3(kNormThreads), 0, s, H, pending,
-                m.rms_out, X, m.hidden, m.rms_eps);
-    if (st != ASDSL_OK) return st;
-    st = preq2_fused_batch(m.lm_meta, m.lm_quant, X, logits, m.vocab, m.hidden, m.gs_lm, n, stream, mfma, mimg,
-                           w.mimg_bytes);
+    st = norm_then_gemv(pending, m.rms_out, m.lm_meta, m.lm_quant, logits, m.vocab, m.gs_lm);
     if (st != ASDSL_OK) return st;
     st = launch("verify_argmax_kernel", verify_argmax_kernel, dim3(64, n), dim3(256), 0, s,
                 static_cast<const float*>(logits), m.vocab, keys);

@@ -284,6 +284,25 @@ struct ActStage {
     }
 };
 
+// The int8 activation image of the MFMA batched GEMV (16 columns): chunk c
+// (8 elements) of column n as split-order int8 at img[((c / 4) * 16 + n) * 4 +
+// c % 4], and per GS-group of column n (scale, integer sum * scale) at
+// fac[(c / (GS / 8)) * 16 + n].  The GS/8 lanes of a group are consecutive
+// lanes of one wave and all call this; `active` gates the stores.
+constexpr int kImageCols = 16;
+template <int GS>
+__device__ __forceinline__ void image_store8(const float (&v)[8], int c, int n, bool active, uint2* __restrict__ img,
+                                             float2* __restrict__ fac) {
+    constexpr int kLanes = GS / 8;
+    const QChunk q = quantize8<GS>(v);
+    const int gsum = kLanes == 4 ? q.usum : group_sum<kLanes>(sum4_i8(q.even) + sum4_i8(q.odd));
+    if (active) {
+        img[(static_cast<size_t>(c >> 2) * kImageCols + n) * 4 + (c & 3)] = make_uint2(q.even, q.odd);
+        if ((c & (kLanes - 1)) == 0)
+            fac[static_cast<size_t>(c / kLanes) * kImageCols + n] = make_float2(q.scale, static_cast<float>(gsum) * q.scale);
+    }
+}
+
 // Decode-step elementwise helpers shared by the fused GEMV prologues and the
 // batched verify pass, so both compute identical values.
 

@@ -183,10 +183,11 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_batch_kernel(const u
 // pass 2 instead was measured slower: every workgroup re-reads all of X.
 constexpr int kMfmaCols = 16;
 
+static_assert(kMfmaCols == kImageCols, "one image layout");
+
 template <int GS>
 __global__ __launch_bounds__(256) void batch_quantize_kernel(const float* __restrict__ X, uint2* __restrict__ img,
                                                              float2* __restrict__ fac, int K, int ncols) {
-    constexpr int kLanes = GS / 8;
     const int n = static_cast<int>(blockIdx.y);
     const int c = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
     const int nchunk = K >> 3;  // a multiple of 4: lanes past the end form whole groups
@@ -201,14 +202,7 @@ __global__ __launch_bounds__(256) void batch_quantize_kernel(const float* __rest
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     }
-    const QChunk q = quantize8<GS>(v);
-    const int gsum = kLanes == 4 ? q.usum : group_sum<kLanes>(sum4_i8(q.even) + sum4_i8(q.odd));
-    if (c < nchunk) {
-        img[(static_cast<size_t>(c >> 2) * kMfmaCols + n) * 4 + (c & 3)] = make_uint2(q.even, q.odd);
-        if ((c & (kLanes - 1)) == 0)
-            fac[static_cast<size_t>(c / kLanes) * kMfmaCols + n] =
-                make_float2(q.scale, static_cast<float>(gsum) * q.scale);
-    }
+    image_store8<GS>(v, c, n, c < nchunk, img, fac);
 }
 
 typedef int v4i32 __attribute__((ext_vector_type(4)));
@@ -658,6 +652,36 @@ extern "C" asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const 
 
 // The MFMA form's column image: per 32-group 16 columns x 32 int8 operands
 // and a (scale, scaled sum) pair.
+bool asdsl::preq2_batch_image_applies(const uint8_t* meta, const uint8_t* quant, int out_features, int in_features,
+                                      int group_size, int n_cols, bool allow_mfma) {
+    if (!allow_mfma || !meta || !quant || (group_size != 32 && group_size != 128) || out_features <= 0 ||
+        in_features <= 0 || in_features % group_size != 0 || in_features / 32 > 640 || n_cols < 1 ||
+        n_cols > kMfmaCols)
+        return false;
+    const int cus = cu_count_current();
+    if (cus < 0) return false;
+    static const int mfma_knob = env_knob("ASDSL_HIP_BATCH_MFMA_MIN_N");
+    const int mfma_min = mfma_knob > 0 ? mfma_knob : (in_features >= 4096 ? 3 : 4);
+    return n_cols >= mfma_min && plan_mfma(out_features, in_features, group_size, cus).ok &&
+           reinterpret_cast<uintptr_t>(meta) % 16 == 0 && reinterpret_cast<uintptr_t>(quant) % 4 == 0;
+}
+
+asdsl_status asdsl::preq2_batch_mfma_image(const uint8_t* meta, const uint8_t* quant, const void* image, float* Y,
+                                           int out_features, int in_features, int group_size, int n_cols,
+                                           asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(image && Y, "gemv_preq2_batch_image: null pointer");
+    ASDSL_CHECK_ARG(preq2_batch_image_applies(meta, quant, out_features, in_features, group_size, n_cols, true),
+                    "gemv_preq2_batch_image: the MFMA form does not apply to this call");
+    ASDSL_CU_COUNT(cus);
+    const int M = out_features, K = in_features;
+    const MfmaPlan mp = plan_mfma(M, K, group_size, cus);
+    const size_t img_bytes = static_cast<size_t>(K / 32) * kMfmaCols * 32;
+    const auto* img = static_cast<const uint2*>(image);
+    const auto* fac = reinterpret_cast<const float2*>(static_cast<const uint8_t*>(image) + img_bytes);
+    return launch_mfma(mp, group_size, reinterpret_cast<const uint32_t*>(meta), quant, img, fac, Y, M, K, n_cols,
+                       as_hip(stream));
+}
+
 extern "C" size_t asdsl_gemv_preq2_fused_batch_work_bytes(int in_features) {
     if (in_features <= 0 || in_features % 32 != 0) return 0;
     return static_cast<size_t>(in_features / 32) * kMfmaCols * (32 + sizeof(float2));
