@@ -424,22 +424,42 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 constexpr int kCombineGroups = 8;
 constexpr int kCombineThreads = kCombineGroups * kHeadDim;
 
+// IMG_GS (32 or 128): the head's 128 outputs of column c are also quantized
+// into the o_proj batched GEMV's int8 image (image_store8, 16 chunks per
+// head), and columns c >= ncols (the grid covers kImageCols columns) write
+// that image's zero columns.
+template <int IMG_GS>
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const float* __restrict__ part,
                                                                       const int* __restrict__ pos_ptr,
                                                                       float* __restrict__ out, int nsplit,
-                                                                      int max_seq, int fold) {
+                                                                      int max_seq, int fold, int ncols,
+                                                                      uint2* __restrict__ img,
+                                                                      float2* __restrict__ fac) {
     constexpr int kChunk = 16;
+    constexpr int kHeadChunks = kHeadDim / 8;
     __shared__ float gml[kCombineGroups][2];
     __shared__ float go[kCombineGroups][kHeadDim];
+    __shared__ float res_s[IMG_GS != 0 ? kHeadDim : 1];
     const int col = static_cast<int>(blockIdx.y);
     const int h = static_cast<int>(blockIdx.x);
-    const int d = static_cast<int>(threadIdx.x) % kHeadDim;
-    const int g = static_cast<int>(threadIdx.x) / kHeadDim;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int d = tid % kHeadDim;
+    const int g = tid / kHeadDim;
+    // the first kHeadChunks lanes quantize the head's outputs (8 each)
+    auto image_chunk = [&](const float (&v)[8]) {
+        if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, h * kHeadChunks + tid, col, true, img, fac);
+    };
+    const float zeros[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (IMG_GS != 0 && col >= ncols) {
+        if (tid < kHeadChunks) image_chunk(zeros);
+        return;
+    }
     const int pos = *pos_ptr + col;
     part += static_cast<size_t>(col) * gridDim.x * nsplit * kPartStride;
     out += static_cast<size_t>(col) * gridDim.x * kHeadDim;
     if (pos < 0 || pos >= max_seq) {  // outside the cache: no partials were written
         if (g == 0) out[static_cast<size_t>(h) * kHeadDim + d] = 0.0f;
+        if (IMG_GS != 0 && tid < kHeadChunks) image_chunk(zeros);
         return;
     }
     const int ns = pos / kSplit + 1;
@@ -479,28 +499,39 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
         M = cm;
     }
     ASDSL_TIMELINE_STAMP(tl_slot, h, 3);
-    if (ng == 1) {  // uniform: group 0 holds every split
-        if (g == 0) out[static_cast<size_t>(h) * kHeadDim + d] = o * (1.0f / L);
-        ASDSL_TIMELINE_STAMP(tl_slot, h, 4);
-        return;
-    }
-    go[g][d] = o;
-    if (d == 0) {
-        gml[g][0] = M;
-        gml[g][1] = L;
-    }
-    __syncthreads();
-    if (g == 0) {
-        float Mx = gml[0][0];
-        for (int q = 1; q < ng; ++q) Mx = fmaxf(Mx, gml[q][0]);
-        float sum = 0.0f, Ls = 0.0f;
-        for (int q = 0; q < ng; ++q) {
-            const float mq = gml[q][0];
-            const float e = mq == -INFINITY ? 0.0f : expf(mq - Mx);
-            sum = fmaf(e, go[q][d], sum);
-            Ls = fmaf(e, gml[q][1], Ls);
+    float res = 0.0f;  // group 0: the output of dimension d
+    if (ng == 1) {     // uniform: group 0 holds every split
+        res = o * (1.0f / L);
+    } else {
+        go[g][d] = o;
+        if (d == 0) {
+            gml[g][0] = M;
+            gml[g][1] = L;
         }
-        out[static_cast<size_t>(h) * kHeadDim + d] = sum * (1.0f / Ls);
+        __syncthreads();
+        if (g == 0) {
+            float Mx = gml[0][0];
+            for (int q = 1; q < ng; ++q) Mx = fmaxf(Mx, gml[q][0]);
+            float sum = 0.0f, Ls = 0.0f;
+            for (int q = 0; q < ng; ++q) {
+                const float mq = gml[q][0];
+                const float e = mq == -INFINITY ? 0.0f : expf(mq - Mx);
+                sum = fmaf(e, go[q][d], sum);
+                Ls = fmaf(e, gml[q][1], Ls);
+            }
+            res = sum * (1.0f / Ls);
+        }
+    }
+    if (g == 0) out[static_cast<size_t>(h) * kHeadDim + d] = res;
+    if constexpr (IMG_GS != 0) {
+        if (g == 0) res_s[d] = res;
+        __syncthreads();
+        if (tid < kHeadChunks) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = res_s[8 * tid + e];
+            image_chunk(v);
+        }
     }
     ASDSL_TIMELINE_STAMP(tl_slot, h, 4);
 }
@@ -828,8 +859,9 @@ asdsl_status launch_attention(const float* qkv, const KvCache& kv, bool q8, cons
                       n_heads, n_kv, max_seq, rot_half, nsplit);
     });
     if (st != ASDSL_OK) return st;
-    return launch("attn_combine_kernel", attn_combine_kernel, dim3(n_heads), dim3(kCombineThreads), 0, s,
-                  static_cast<const float*>(part), pos, att, nsplit, max_seq, fold);
+    return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
+                  static_cast<const float*>(part), pos, att, nsplit, max_seq, fold, 1, static_cast<uint2*>(nullptr),
+                  static_cast<float2*>(nullptr));
 }
 
 // Work buffer layout of one decode step (offsets in floats, 256-byte aligned).
@@ -1491,11 +1523,20 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
                           static_cast<const float*>(Q), kv, pos, part, m.n_heads, m.max_seq, nsplit);
         });
         if (st != ASDSL_OK) return st;
-        st = launch("attn_combine_kernel", attn_combine_kernel, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
-                    static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0);
-        if (st != ASDSL_OK) return st;
-        st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma, mimg,
-                               w.mimg_bytes);
+        if (preq2_batch_image_applies(L.o_meta, L.o_quant, m.hidden, q_dim, m.gs_attn, n, mfma)) {
+            st = launch("attn_combine_kernel", m.gs_attn == 32 ? attn_combine_kernel<32> : attn_combine_kernel<128>,
+                        dim3(m.n_heads, kImageCols), dim3(kCombineThreads), 0, s, static_cast<const float*>(part), pos,
+                        att, nsplit, m.max_seq, 0, n, img, fac_of(q_dim));
+            if (st != ASDSL_OK) return st;
+            st = preq2_batch_mfma_image(L.o_meta, L.o_quant, mimg, O, m.hidden, q_dim, m.gs_attn, n, stream);
+        } else {
+            st = launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
+                        static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0, n,
+                        static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
+            if (st != ASDSL_OK) return st;
+            st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma, mimg,
+                                   w.mimg_bytes);
+        }
         if (st != ASDSL_OK) return st;
         st = norm_then_gemv(O, L.rms_ffn, L.gu_meta, L.gu_quant, GU, 2 * m.ffn, m.gs_ffn);
         if (st != ASDSL_OK) return st;
