@@ -211,9 +211,10 @@ class DecodeEngine:
         return cls(cfg, layers, embed, norm_w(), lm_meta, lm_quant, fatrelu_threshold)
 
     # A step is shaped for the positions it serves (asdsl_decode_token_upto):
-    # below 256 the attention splits are merged in o_proj's prologue, beyond
-    # by the combine kernel.  One graph per range.
-    POS_LIMITS = (256,)
+    # below 512 the attention splits are merged in o_proj's prologue, beyond
+    # by the combine kernel, and the attention launch covers only the splits
+    # its range uses (4, 8, 16, 32).  One graph per range.
+    POS_LIMITS = (256, 512, 1024, 2048)
 
     def _pos_limit(self, pos: int) -> int:
         c = self.cfg

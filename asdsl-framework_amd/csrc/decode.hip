@@ -12,10 +12,10 @@
 //
 // Per layer: qkv GEMV with residual add + RMSNorm in its prologue (layer 0:
 // the embedding row itself), attention (RoPE, KV write, split partials),
-// o_proj GEMV (below 256 positions it merges the partials in its prologue;
+// o_proj GEMV (below 512 positions it merges the partials in its prologue;
 // beyond, a combine launch precedes it), gate_up GEMV with residual add +
-// RMSNorm in its prologue and SwiGLU in its epilogue, down GEMV.  Four
-// launches per layer at short context, five beyond; then lm_head with the
+// RMSNorm in its prologue and SwiGLU in its epilogue, down GEMV.  Five
+// launches per layer below 512 positions, six beyond; then lm_head with the
 // argmax and a one-thread finalize.  The token id and position live in
 // device memory, so a captured graph of one step replays token after token
 // with no host work.  The multi-token verify pass keeps a separate combine
@@ -433,6 +433,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
                                                                       const int* __restrict__ pos_ptr,
                                                                       float* __restrict__ out, int nsplit,
                                                                       int max_seq, int fold, int ncols,
+                                                                      int form_tile, int form_splits,
                                                                       uint2* __restrict__ img,
                                                                       float2* __restrict__ fac) {
     constexpr int kChunk = 16;
@@ -462,7 +463,11 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
         if (IMG_GS != 0 && tid < kHeadChunks) image_chunk(zeros);
         return;
     }
-    const int ns = pos / kSplit + 1;
+    // splits: form_splits > 0, the decode step's attention (pos / form_tile + 1
+    // tiles in at most form_splits splits); otherwise one per kSplit positions
+    const int nt = pos / (form_splits > 0 ? form_tile : kSplit) + 1;
+    const int tps = form_splits > 0 ? (nt + form_splits - 1) / form_splits : 1;
+    const int ns = (nt + tps - 1) / tps;
     if (ns <= fold) return;  // the consuming GEMV's prologue merges these splits itself
     const int tl_slot = col == 0 ? 6 : -1;
     ASDSL_TIMELINE_STAMP(tl_slot, h, 0);
@@ -537,28 +542,42 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
 }
 
 // ------------------------------------------------------------ decode attention
-// The short-context step's attention, whose split partials the o_proj
-// GEMV's prologue merges (no combine launch).  Workgroup (s, kvh) of WAVES
-// waves covers split s of the KV head's positions: tps consecutive tiles of
-// tile = 16 * WAVES positions (a wave takes 4 positions per step, 4 steps a
-// tile), at most max_splits splits, the next tile's K/V rows requested
-// before the current tile is used and a running (max, sum, P.V) per wave;
-// the waves merge in LDS and the partial (m, l, acc) of each query head is
-// stored.  Used below 256 positions: 4 waves, tiles of 64, at most 4 splits
-// of one tile.  Beyond, the partial kernel over 64-position splits and the
-// combine kernel: a folded form for long contexts (8 waves, tiles of 128,
-// at most 8 splits merged in the prologue) measured slower, 1436 against
-// 1275 us per 32-layer step at ctx 4096 and 1167 against 1150 at 1024, as
-// its 56-64 workgroups keep only two tiles each in flight.  The launch
-// covers only the splits of the positions it serves; a position outside the
-// cache gives zero output.
+// The decode step's attention.  Workgroup (s, kvh) of WAVES waves covers
+// split s of the KV head's positions: tps consecutive tiles of tile = 16 *
+// WAVES positions (a wave takes 4 positions per step, 4 steps a tile), at
+// most max_splits splits, the next tile's K/V rows requested before the
+// current tile is used and a running (max, sum, P.V) per lane; the lanes
+// merge in LDS and the partial (m, l, acc) of each query head is stored.
+// Two forms, both 4 waves and tiles of 64:
+//   short (positions below 512, at most 8 splits, one tile each): the o_proj
+//     GEMV's prologue merges the splits (no combine launch);
+//   long (beyond, at most 32 splits of ceil(tiles / 32) tiles): the combine
+//     kernel merges them.
+// Against 64-position splits over the whole cache with a combine (the
+// verify pass's form), the long form measured 1061 against 1097 us per
+// 32-layer step at ctx 1024 and 1213 against 1218 at 4096: the launch covers
+// only the splits its position range uses, and the combine folds at most 32
+// partials.  Capping at 8 or 16 splits (more tiles per workgroup) measured
+// slower (+56 / -3 us at 1024, +344 / +106 at 4096), as did 8 waves with
+// tiles of 128 or 16 waves with tiles of 256.  The launch covers only the
+// splits of the positions it serves; a position outside the cache gives
+// zero output.
 constexpr int kMaxSplits = 32;  // partial rows reserved per query head
-constexpr int kShortLimit = 256;
+constexpr int kShortLimit = 512;
 struct FoldForm {
     int waves, tile, max_splits;
 };
-constexpr FoldForm kShortForm{4, 64, 4};
+constexpr FoldForm kShortForm{4, 64, 8};
+constexpr FoldForm kLongForm{4, 64, kMaxSplits};
+// The int8 cache beyond this many positions takes the partial kernel over
+// 64-position splits of the whole cache instead of the long form: its
+// dequantization makes each tile's work longer, and one tile per workgroup
+// over every split measured 1197 against 1245 us per 32-layer step at ctx
+// 4096 (the long form's 3 tiles per workgroup), while at ctx 1024 the long
+// form is faster (1040 against 1072).
+constexpr int kPartialFrom = 2048;
 static_assert(kShortForm.max_splits <= 8, "o_proj's prologue folds at most 8 splits");
+static_assert(kShortForm.waves == kLongForm.waves && kShortForm.tile == kLongForm.tile, "one kernel instance");
 
 __host__ __device__ inline int attn_fold_tps(int pos, int tile, int max_splits) {
     const int nt = pos / tile + 1;
@@ -571,7 +590,7 @@ __host__ __device__ inline int attn_fold_splits(int pos, int tile, int max_split
     return (nt + tps - 1) / tps;
 }
 
-// Positions below pos_limit take the folded form when pos_limit <= 256.
+// Positions below pos_limit take the short form when pos_limit <= 512.
 bool attn_fold(int pos_limit) { return pos_limit <= kShortLimit; }
 
 // Most splits any position below pos_limit uses (the launch's grid.x).
@@ -781,25 +800,19 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
 }
 
 int attn_splits(int max_seq);
-asdsl_status launch_attention(const float* qkv, const KvCache& kv, bool q8, const float* rc, const float* rs,
-                              const int* pos, float* att, float* part, int n_heads, int n_kv, int rot_half,
-                              int max_seq, hipStream_t s, int fold);
 
 // Floats of the decode attention's work area: kMaxSplits partial rows per
-// query head for the folded forms, then the partial rows of the unfolded
-// form (one per 64 positions of max_seq).
+// query head (the short and long forms), then one partial row per 64
+// positions of max_seq (the int8 cache's long-context form).
 size_t attn_decode_work_floats(int n_heads, int max_seq) {
     return static_cast<size_t>(n_heads) * kMaxSplits * kPartStride +
            static_cast<size_t>(n_heads) * attn_splits(max_seq) * kPartStride;
 }
 
-// The unfolded form (the standalone attention entries, the verify pass and
-// ASDSL_HIP_NO_COMBINE_FOLD=1): the partial kernel over 64-position splits
-// and the combine kernel (up to eight groups of threads folding runs of
-// splits in parallel).  Merging in the attention kernel's last workgroup
-// instead (device-coherent partial stores, an atomic count, device-coherent
-// loads) measured slower than the combine launch: 13.2 us per layer at ctx
-// 1024 against 8.0 + 4.0.
+// Merging in the attention kernel's last-arriving workgroup instead of the
+// combine launch (device-coherent partial stores, an atomic count,
+// device-coherent loads) measured slower: 13.2 us per layer at ctx 1024
+// against 8.0 + 4.0.
 // The kernel instance for G query heads per KV head (1..4) and the cache
 // form: f(kernel) is called with the matching instantiation.
 template <template <int, bool> class K, typename F>
@@ -827,42 +840,42 @@ struct PartialAttnK {
     static auto fn() { return attn_partial_kernel<G, Q8>; }
 };
 
-// work: attn_decode_work_floats.  fold: the folded form for positions below
-// pos_limit <= 256 (partials at work, kMaxSplits rows per head, for the
-// o_proj prologue); otherwise the unfolded form, att receiving the merged
-// output.
+// work: attn_decode_work_floats.  fold: the short form, partials at work
+// (kMaxSplits rows per head) for the o_proj prologue; otherwise the long form
+// and the combine kernel, att receiving the merged output.
 asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q8, const float* rc, const float* rs,
                                      const int* pos, float* att, float* work, int n_heads, int n_kv, int rot_half,
                                      int max_seq, int pos_limit, bool fold, hipStream_t s) {
-    if (!fold)
-        return launch_attention(qkv, kv, q8, rc, rs, pos, att, work + static_cast<size_t>(n_heads) * kMaxSplits *
-                                kPartStride, n_heads, n_kv, rot_half, max_seq, s, 0);
     const int limit = pos_limit < max_seq ? pos_limit : max_seq;
-    const dim3 grid(attn_max_splits(limit, kShortForm), n_kv);
-    const dim3 block(kShortForm.waves * kWave);
-    const int max_splits = kShortForm.max_splits;
-    return with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, [&](auto kern) {
+    if (!fold && q8 && limit > kPartialFrom) {
+        // int8 cache beyond 2048 positions: one workgroup per 64 positions of
+        // the whole cache (partial rows after the forms' kMaxSplits rows)
+        float* part = work + static_cast<size_t>(n_heads) * kMaxSplits * kPartStride;
+        const int nsplit = attn_splits(max_seq);
+        const asdsl_status st = with_attn_kernel<PartialAttnK>(n_heads / n_kv, q8, [&](auto kern) {
+            return launch("attn_partial_kernel", kern, dim3(nsplit, n_kv), dim3(kAttnThreads), 0, s, qkv, kv, rc, rs,
+                          pos, part, n_heads, n_kv, max_seq, rot_half, nsplit);
+        });
+        if (st != ASDSL_OK) return st;
+        return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
+                      static_cast<const float*>(part), pos, att, nsplit, max_seq, 0, 1, 0, 0,
+                      static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
+    }
+    const FoldForm& f = fold ? kShortForm : kLongForm;
+    const dim3 grid(attn_max_splits(limit, f), n_kv);
+    const dim3 block(f.waves * kWave);
+    const int max_splits = f.max_splits;
+    const asdsl_status st = with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, [&](auto kern) {
         return launch("attn_decode_kernel", kern, grid, block, 0, s, qkv, kv, rc, rs, pos, work, att, n_heads, n_kv,
                       max_seq, rot_half, max_splits);
     });
+    if (st != ASDSL_OK || fold) return st;
+    return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
+                  static_cast<const float*>(work), pos, att, kMaxSplits, max_seq, 0, 1, f.tile, f.max_splits,
+                  static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
 }
 
 int attn_splits(int max_seq) { return (max_seq + kSplit - 1) / kSplit; }
-
-asdsl_status launch_attention(const float* qkv, const KvCache& kv, bool q8, const float* rc, const float* rs,
-                              const int* pos, float* att, float* part, int n_heads, int n_kv, int rot_half,
-                              int max_seq, hipStream_t s, int fold) {
-    const int nsplit = attn_splits(max_seq);
-    const dim3 grid(nsplit, n_kv);
-    const asdsl_status st = with_attn_kernel<PartialAttnK>(n_heads / n_kv, q8, [&](auto kern) {
-        return launch("attn_partial_kernel", kern, grid, dim3(kAttnThreads), 0, s, qkv, kv, rc, rs, pos, part,
-                      n_heads, n_kv, max_seq, rot_half, nsplit);
-    });
-    if (st != ASDSL_OK) return st;
-    return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
-                  static_cast<const float*>(part), pos, att, nsplit, max_seq, fold, 1, static_cast<uint2*>(nullptr),
-                  static_cast<float2*>(nullptr));
-}
 
 // Work buffer layout of one decode step (offsets in floats, 256-byte aligned).
 struct DecodeWork {
@@ -1368,7 +1381,7 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
     static const int no_fold = env_knob("ASDSL_HIP_NO_COMBINE_FOLD");
     const int limit = pos_limit < m.max_seq ? pos_limit : m.max_seq;
     const bool fold = no_fold == 0 && attn_fold(limit);
-    const FoldForm& form = kShortForm;
+    const FoldForm& form = kShortForm;  // o_proj's prologue merge (fold only)
     const bool q8 = m.kv_format == ASDSL_KV_INT8;
 
     // Layer 0's qkv GEMV reads the embedding row itself (and stores it to hA,
@@ -1526,12 +1539,12 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         if (preq2_batch_image_applies(L.o_meta, L.o_quant, m.hidden, q_dim, m.gs_attn, n, mfma)) {
             st = launch("attn_combine_kernel", m.gs_attn == 32 ? attn_combine_kernel<32> : attn_combine_kernel<128>,
                         dim3(m.n_heads, kImageCols), dim3(kCombineThreads), 0, s, static_cast<const float*>(part), pos,
-                        att, nsplit, m.max_seq, 0, n, img, fac_of(q_dim));
+                        att, nsplit, m.max_seq, 0, n, 0, 0, img, fac_of(q_dim));
             if (st != ASDSL_OK) return st;
             st = preq2_batch_mfma_image(L.o_meta, L.o_quant, mimg, O, m.hidden, q_dim, m.gs_attn, n, stream);
         } else {
             st = launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
-                        static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0, n,
+                        static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0, n, 0, 0,
                         static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
             if (st != ASDSL_OK) return st;
             st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma, mimg,

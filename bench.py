@@ -1125,7 +1125,7 @@ def pmc_probe(mode: str) -> int:
 # step stamp a 100 MHz wall clock at fixed points of every workgroup
 # (slots and stamp points: csrc/device_common.hpp, ASDSL_TIMELINE_STAMP).
 TIMELINE_KERNELS = {0: "o_proj (split merge)", 1: "gate_up (SwiGLU)", 2: "qkv (norm)", 3: "down",
-                    4: "attention (short form)", 5: "attention partials", 6: "attention combine", 7: "o_proj"}
+                    4: "attention", 5: "attention partials (int8 cache, long)", 6: "attention combine", 7: "o_proj"}
 _GEMV_PHASES = ((0, 1, "prologue"), (1, 2, "staging barrier"), (2, 3, "first tile"), (3, 4, "tail"))
 TIMELINE_PHASES = {0: _GEMV_PHASES, 1: _GEMV_PHASES, 2: _GEMV_PHASES, 3: _GEMV_PHASES, 7: _GEMV_PHASES,
                    4: ((0, 1, "loads and RoPE"), (1, 2, "barrier and K/V store"), (2, 3, "scores, softmax, P.V"),
@@ -1171,7 +1171,7 @@ def decode_timeline(ctx: int, n_layers: int = 32, steps: int = 8, seed: int = 11
     _hip.check(setter(None), "asdsl_timeline_set_buffer")
     t = buf.cpu().numpy().reshape(8, 1024, 8).astype(np.float64)
     rows = []
-    for slot in range(8):
+    for slot in TIMELINE_KERNELS:
         a = t[slot]
         a = a[(a[:, 0] > 0) & (a[:, 4] > 0)]  # workgroups that ran to the end
         if len(a):

@@ -500,10 +500,10 @@ asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int
 
 /* The same step for a position *pos < pos_limit (the caller guarantees it;
  * asdsl_decode_token is pos_limit = max_seq).  The launch is shaped for that
- * range: below 256 the attention grid covers only the (at most 4) splits
- * such positions use and the o_proj GEMV merges them in its prologue, with
- * no combine launch (same bits as the combine kernel).  A HIP graph of one call then
- * replays for every position below pos_limit.  No reference counterpart (the
+ * range: the attention grid covers only the splits such positions use (one
+ * per 64 positions, at most 32), and below 512 the o_proj GEMV merges them
+ * in its prologue, with no combine launch (same bits as the combine kernel).
+ * A HIP graph of one call then replays for every position below pos_limit.  No reference counterpart (the
  * reference passes the position by value, unified_engine.cpp:1339). */
 asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model, int* token, int* pos, int pos_limit,
                                      float* logits, void* work, asdsl_stream_t stream);

@@ -246,7 +246,7 @@ def test_decode_long_context_matches_oracle(gpu, ctx):
 @pytest.mark.parametrize("max_seq,ctx", [(300, 150), (1600, 1400), (3000, 2500)])
 def test_graph_replay_matches_eager_steps(gpu, max_seq, ctx):
     """Eager steps, each queued for its position's range as the engine
-    captures it (below 256 the splits merged in o_proj's prologue, beyond the
+    captures it (below 512 the splits merged in o_proj's prologue, beyond the
     combine kernel), against a captured graph replayed three times: bitwise
     equal."""
     import torch
@@ -278,8 +278,9 @@ def test_graph_replay_matches_eager_steps(gpu, max_seq, ctx):
 def test_short_form_gives_the_general_steps_bits(gpu, ctx):
     """A position below 256 through the step queued for positions below 256
     (attention splits merged in o_proj's prologue) and through the general
-    step (queued for any position: the partial and combine kernels), two
-    layers: the same logits, token and K/V rows bit for bit."""
+    step (queued for any position of a 600-position cache: the long form and
+    the combine kernel), two layers: the same logits, token and K/V rows bit
+    for bit."""
     import torch
 
     eng = _small_engine(n_layers=2, vocab=4096, max_seq=600, seed=ctx + 1)
@@ -334,12 +335,11 @@ np.save(OUT, np.stack(out))
 
 
 def test_combine_fold_gives_the_combine_kernels_bits(gpu, tmp_path):
-    """Positions 250..257: up to 255 (at most 4 splits of 64) a step shaped
-    for short contexts lets the o_proj GEMV's prologue merge the attention
-    splits; from 256 the combine kernel merges them.  A run that leaves the
-    merge to the combine kernel everywhere (ASDSL_HIP_NO_COMBINE_FOLD=1, read
-    once per process, so in a second process) gives the same logits bit for
-    bit at every position."""
+    """Positions 250..257 (4 splits of 64, then 5; steps shaped for
+    positions below 256, then below 512): the o_proj GEMV's prologue merges
+    the attention splits.  A run that leaves the merge to the combine kernel
+    everywhere (ASDSL_HIP_NO_COMBINE_FOLD=1, read once per process, so in a
+    second process) gives the same logits bit for bit at every position."""
     import os
     import subprocess
     import sys

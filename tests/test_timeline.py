@@ -48,14 +48,14 @@ def _timeline(contexts, layers=2):
 @needs_timing_build
 def test_timeline_orders_the_layer_kernels():
     """ctx 100: the short form (qkv, attention, o_proj merging the splits,
-    gate_up, down); ctx 300: partials and combine before a plain o_proj.
-    Kernels follow each other without overlap, every phase is non-negative,
-    and the workgroup counts are the launches' (Phi-4 shape)."""
-    short, long_ = _timeline([100, 300])
+    gate_up, down); ctx 600: the long form, whose combine runs before a plain
+    o_proj.  Kernels follow each other without overlap, every phase is
+    non-negative, and the workgroup counts are the launches' (Phi-4 shape)."""
+    short, long_ = _timeline([100, 600])
     assert [k["kernel"] for k in short["kernels"]] == [
-        "qkv (norm)", "attention (short form)", "o_proj (split merge)", "gate_up (SwiGLU)", "down"]
+        "qkv (norm)", "attention", "o_proj (split merge)", "gate_up (SwiGLU)", "down"]
     assert [k["kernel"] for k in long_["kernels"]] == [
-        "qkv (norm)", "attention partials", "attention combine", "o_proj", "gate_up (SwiGLU)", "down"]
+        "qkv (norm)", "attention", "attention combine", "o_proj", "gate_up (SwiGLU)", "down"]
     for tl in (short, long_):
         ks = tl["kernels"]
         assert ks[0]["first_start_us"] == 0.0
@@ -68,6 +68,6 @@ def test_timeline_orders_the_layer_kernels():
                     assert 0.0 <= v[0] <= v[1], (k["kernel"], name, v)
     wgs = {k["kernel"]: k["workgroups"] for k in short["kernels"]}
     assert wgs["qkv (norm)"] == 160 and wgs["gate_up (SwiGLU)"] == 256 and wgs["down"] == 192
-    assert wgs["attention (short form)"] == 2 * 8  # positions 0..100: two splits of 64, eight KV heads
+    assert wgs["attention"] == 2 * 8  # position 108: two splits of 64, eight KV heads
     wgs = {k["kernel"]: k["workgroups"] for k in long_["kernels"]}
-    assert wgs["attention partials"] == 5 * 8 and wgs["attention combine"] == 24
+    assert wgs["attention"] == 10 * 8 and wgs["attention combine"] == 24  # position 608: ten splits
