@@ -290,130 +290,6 @@ __device__ __forceinline__ void kv_quantize_new(float (*kv_new)[kHeadDim], const
     }
 }
 
-// Attention partials of one KV head over positions [s*kSplit, min((s+1)*kSplit, pos+1)).
-// G = query heads per KV head.  Lane l of a wave reads dims 8*(l%16).. of
-// position 4*step + l/16, so every K/V load instruction moves 1 KiB of
-// consecutive positions.  Writes per query head (m, l, acc[128]) with
-// acc = sum_p exp(s_p - m) v_p.  The split holding `pos` also applies RoPE to
-// the new K, rounds K and V to fp16 and stores them in the cache.
-// Each wave keeps its 32 positions' scores in registers and forms its own
-// (max, sum, P.V); the four waves are merged in LDS behind one barrier (a
-// block-wide softmax through LDS took two more barriers and ~2 us longer).
-
-template <int G, bool Q8>
-__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
-    const float* __restrict__ qkv, KvCache kv,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
-    float* __restrict__ part, int n_heads, int n_kv, int max_seq, int rot_half, int nsplit) {
-    __shared__ float q_s[G][kHeadDim];
-    __shared__ float kv_new[2][kHeadDim];
-    __shared__ float gml[kAttnThreads / 16][G][2];
-    __shared__ __align__(16) float gacc[kAttnThreads / 16][G][kHeadDim];
-    __shared__ float ge[G][kAttnThreads / 16];
-    const int s = static_cast<int>(blockIdx.x);
-    const int kvh = static_cast<int>(blockIdx.y);
-    const int pos = *pos_ptr;
-    const int p0 = s * kSplit;
-    // whole workgroup: this split is past the sequence, or the position is
-    // outside the cache (the combine then writes zeros)
-    if (p0 > pos || pos < 0 || pos >= max_seq) return;
-    const int p1 = min(p0 + kSplit, pos + 1);
-    const int tl_wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
-    ASDSL_TIMELINE_STAMP(5, tl_wg, 0);
-    const int tid = static_cast<int>(threadIdx.x);
-    const int lane = tid & (kWave - 1);
-    const int wave = tid >> 6;
-    const int pg = lane >> 4;   // position within the wave's four
-    const int dc = lane & 15;   // 8-dim chunk
-    const size_t row0 = static_cast<size_t>(kvh) * max_seq;  // cache row of position 0
-
-    // RoPE inputs first (small, from L2), then every K and V row this lane
-    // will use (they depend on nothing but pos): loads complete in issue
-    // order, so the rotation waits only for its own inputs and the kernel
-    // waits on HBM once.  Rows of positions 4*wave + pg + 16*it of the split;
-    // `pos` itself comes from LDS.
-    const float* cp = rope_cos + static_cast<size_t>(pos) * rot_half;
-    const float* sp = rope_sin + static_cast<size_t>(pos) * rot_half;
-    constexpr int kRope = ((G + 1) * kHeadDim + kAttnThreads - 1) / kAttnThreads;
-    float rx[kRope][4];
-#pragma unroll
-    for (int r = 0; r < kRope; ++r) {
-        const int e = tid + r * kAttnThreads;
-        const int hh = e / kHeadDim;
-        const int d = e % kHeadDim;
-        if (hh <= G) {
-            const float* src = hh < G ? qkv + static_cast<size_t>(kvh * G + hh) * kHeadDim
-                                      : qkv + static_cast<size_t>(n_heads + kvh) * kHeadDim;
-            if (d < 2 * rot_half) {
-                const int i = d < rot_half ? d : d - rot_half;
-                rx[r][0] = src[i];
-                rx[r][1] = src[i + rot_half];
-                rx[r][2] = cp[i];
-                rx[r][3] = sp[i];
-            } else {
-                rx[r][0] = src[d];
-            }
-        }
-    }
-    const float* vsrc = qkv + static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim;
-    const float vnew = tid < kHeadDim ? vsrc[tid] : 0.0f;
-    constexpr int kIt = kSplit / 16;
-    uint4 kraw[kIt], vraw[kIt];
-#pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-        const int p = p0 + wave * 4 + pg + 16 * it;
-        if (p < p1 && p != pos) {
-            kraw[it] = kv_load8<Q8>(kv.k, kv.ks, row0 + p, dc);
-            vraw[it] = kv_load8<Q8>(kv.v, kv.vs, row0 + p, dc);
-        } else {
-            kraw[it] = make_uint4(0u, 0u, 0u, 0u);
-            vraw[it] = kraw[it];
-        }
-    }
-
-    // RoPE (half split over the first 2*rot_half dims) on the G query heads
-    // and the KV head's new key; the new value as is.
-#pragma unroll
-    for (int r = 0; r < kRope; ++r) {
-        const int e = tid + r * kAttnThreads;
-        const int hh = e / kHeadDim;
-        const int d = e % kHeadDim;
-        if (hh <= G) {
-            float val;
-            if (d < 2 * rot_half) {
-                const float xf = rx[r][0], xs = rx[r][1], c = rx[r][2], sn = rx[r][3];
-                val = d < rot_half ? fmaf(xf, c, -(xs * sn)) : fmaf(xf, sn, xs * c);
-            } else {
-                val = rx[r][0];
-            }
-            if (hh < G) q_s[hh][d] = val;
-            else kv_new[0][d] = Q8 ? val : h2f(f2h(val));
-        }
-    }
-    if (tid < kHeadDim) kv_new[1][tid] = Q8 ? vnew : h2f(f2h(vnew));
-    ASDSL_TIMELINE_STAMP(5, tl_wg, 1);
-    __syncthreads();
-    if constexpr (Q8) {
-        kv_quantize_new(kv_new, kv, row0 + pos, pos < p1);
-        __syncthreads();
-    } else if (pos < p1 && tid < kHeadDim) {
-        static_cast<uint16_t*>(kv.k)[(row0 + pos) * kHeadDim + tid] = f2h(kv_new[0][tid]);
-        static_cast<uint16_t*>(kv.v)[(row0 + pos) * kHeadDim + tid] = f2h(kv_new[1][tid]);
-    }
-
-    float qr[G][8];
-#pragma unroll
-    for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qr[hh][e] = q_s[hh][8 * dc + e];
-
-    ASDSL_TIMELINE_STAMP(5, tl_wg, 2);
-    attn_split_core<G, true, Q8>(kraw, vraw, qr, p0, p1, pos, kv_new, gml, gacc, ge,
-                             part + (static_cast<size_t>(kvh * G) * nsplit + s) * kPartStride,
-                             static_cast<size_t>(nsplit) * kPartStride);
-    ASDSL_TIMELINE_STAMP(5, tl_wg, 4);
-}
-
 // out[h][d] = sum_s e_s acc_s[d] / sum_s e_s l_s, e_s = exp(m_s - max m).
 // Up to kCombineGroups groups of 128 threads each fold a contiguous run of
 // splits (chunks of kChunk loads issued together, a running (max, sum,
@@ -543,24 +419,24 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
 
 // ------------------------------------------------------------ decode attention
 // The decode step's attention.  Workgroup (s, kvh) of WAVES waves covers
-// split s of the KV head's positions: tps consecutive tiles of tile = 16 *
-// WAVES positions (a wave takes 4 positions per step, 4 steps a tile), at
-// most max_splits splits, the next tile's K/V rows requested before the
-// current tile is used and a running (max, sum, P.V) per lane; the lanes
-// merge in LDS and the partial (m, l, acc) of each query head is stored.
-// Two forms, both 4 waves and tiles of 64:
-//   short (positions below 512, at most 8 splits, one tile each): the o_proj
-//     GEMV's prologue merges the splits (no combine launch);
-//   long (beyond, at most 32 splits of ceil(tiles / 32) tiles): the combine
-//     kernel merges them.
+// split s of the KV head's positions: tps consecutive tiles of tile = 4 *
+// WAVES * KIT positions (a wave takes 4 positions per step, KIT steps a
+// tile), at most max_splits splits, the next tile's K/V rows requested
+// before the current tile is used and a running (max, sum, P.V) per lane;
+// the lanes merge in LDS and the partial (m, l, acc) of each query head is
+// stored.  Three forms, all with tiles of 64:
+//   short (positions below 512; 4 waves, at most 8 splits of one tile): the
+//     o_proj GEMV's prologue merges the splits (no combine launch);
+//   long (up to 2048; 4 waves, at most 32 splits of one tile) and deep
+//     (beyond; 8 waves, at most 32 splits of ceil(tiles / 32) tiles): the
+//     combine kernel merges them.
 // Against 64-position splits over the whole cache with a combine (the
-// verify pass's form), the long form measured 1061 against 1097 us per
-// 32-layer step at ctx 1024 and 1213 against 1218 at 4096: the launch covers
-// only the splits its position range uses, and the combine folds at most 32
-// partials.  Capping at 8 or 16 splits (more tiles per workgroup) measured
-// slower (+56 / -3 us at 1024, +344 / +106 at 4096), as did 8 waves with
-// tiles of 128 or 16 waves with tiles of 256.  The launch covers only the
-// splits of the positions it serves; a position outside the cache gives
+// verify pass's form), these measured 1040 against 1081 us per 32-layer
+// step at ctx 1024 and 1194 against 1218 at 4096 (fp16; int8 1039 against
+// 1073 and 1203 against 1195): the launch covers only the splits its
+// position range uses, and the combine folds at most 32 partials.  Capping
+// at 8, 16, 48, 64 or 80 splits measured slower, as did 8 waves with tiles
+// of 128 or 16 waves with tiles of 256.  A position outside the cache gives
 // zero output.
 constexpr int kMaxSplits = 32;  // partial rows reserved per query head
 constexpr int kShortLimit = 512;
@@ -569,15 +445,16 @@ struct FoldForm {
 };
 constexpr FoldForm kShortForm{4, 64, 8};
 constexpr FoldForm kLongForm{4, 64, kMaxSplits};
-// The int8 cache beyond this many positions takes the partial kernel over
-// 64-position splits of the whole cache instead of the long form: its
-// dequantization makes each tile's work longer, and one tile per workgroup
-// over every split measured 1197 against 1245 us per 32-layer step at ctx
-// 4096 (the long form's 3 tiles per workgroup), while at ctx 1024 the long
-// form is faster (1040 against 1072).
-constexpr int kPartialFrom = 2048;
+// Beyond 2048 positions a split holds several tiles: 8 waves per tile of 64
+// (two steps each) shorten each wave's dependent chain and measured 1194
+// against 1216 us per 32-layer step at ctx 4096 (int8 1203 against 1209 with
+// 4 waves); with one tile per split (up to 2048) they measured slower (1048
+// against 1043 at 1024), and 16 waves slower still.
+constexpr FoldForm kDeepForm{8, 64, kMaxSplits};
+constexpr int kDeepFrom = 2048;
 static_assert(kShortForm.max_splits <= 8, "o_proj's prologue folds at most 8 splits");
-static_assert(kShortForm.waves == kLongForm.waves && kShortForm.tile == kLongForm.tile, "one kernel instance");
+static_assert(kShortForm.waves == kLongForm.waves && kShortForm.tile == kLongForm.tile &&
+                  kDeepForm.tile == kLongForm.tile, "one tile size for the forms and the combine");
 
 __host__ __device__ inline int attn_fold_tps(int pos, int tile, int max_splits) {
     const int nt = pos / tile + 1;
@@ -604,16 +481,16 @@ int attn_max_splits(int pos_limit, const FoldForm& f) {
     return best;
 }
 
-template <int G, bool Q8, int WAVES>
+template <int G, bool Q8, int WAVES, int KIT>
 __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
     const float* __restrict__ qkv, KvCache kv,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
     float* __restrict__ part, float* __restrict__ att, int n_heads, int n_kv, int max_seq, int rot_half,
     int max_splits) {
     constexpr int kThreads = WAVES * kWave;
-    constexpr int kTile = 16 * WAVES;  // positions per tile
     constexpr int kStep = 4 * WAVES;   // positions per step of all waves
-    constexpr int kIt = kTile / kStep;
+    constexpr int kIt = KIT;           // steps per tile
+    constexpr int kTile = kStep * kIt; // positions per tile
     __shared__ float q_s[G][kHeadDim];
     __shared__ float kv_new[2][kHeadDim];
     __shared__ float gml[kThreads / 16][G][2];
@@ -802,11 +679,10 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
 int attn_splits(int max_seq);
 
 // Floats of the decode attention's work area: kMaxSplits partial rows per
-// query head (the short and long forms), then one partial row per 64
-// positions of max_seq (the int8 cache's long-context form).
+// query head (every form; at most kMaxSplits splits whatever max_seq).
 size_t attn_decode_work_floats(int n_heads, int max_seq) {
-    return static_cast<size_t>(n_heads) * kMaxSplits * kPartStride +
-           static_cast<size_t>(n_heads) * attn_splits(max_seq) * kPartStride;
+    (void)max_seq;
+    return static_cast<size_t>(n_heads) * kMaxSplits * kPartStride;
 }
 
 // Merging in the attention kernel's last-arriving workgroup instead of the
@@ -833,11 +709,11 @@ asdsl_status with_attn_kernel(int G, bool q8, F&& f) {
 }
 template <int G, bool Q8>
 struct DecodeAttnK {
-    static auto fn() { return attn_decode_kernel<G, Q8, kShortForm.waves>; }
+    static auto fn() { return attn_decode_kernel<G, Q8, kShortForm.waves, kShortForm.tile / (4 * kShortForm.waves)>; }
 };
 template <int G, bool Q8>
-struct PartialAttnK {
-    static auto fn() { return attn_partial_kernel<G, Q8>; }
+struct DeepAttnK {
+    static auto fn() { return attn_decode_kernel<G, Q8, kDeepForm.waves, kDeepForm.tile / (4 * kDeepForm.waves)>; }
 };
 
 // work: attn_decode_work_floats.  fold: the short form, partials at work
@@ -847,28 +723,17 @@ asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q
                                      const int* pos, float* att, float* work, int n_heads, int n_kv, int rot_half,
                                      int max_seq, int pos_limit, bool fold, hipStream_t s) {
     const int limit = pos_limit < max_seq ? pos_limit : max_seq;
-    if (!fold && q8 && limit > kPartialFrom) {
-        // int8 cache beyond 2048 positions: one workgroup per 64 positions of
-        // the whole cache (partial rows after the forms' kMaxSplits rows)
-        float* part = work + static_cast<size_t>(n_heads) * kMaxSplits * kPartStride;
-        const int nsplit = attn_splits(max_seq);
-        const asdsl_status st = with_attn_kernel<PartialAttnK>(n_heads / n_kv, q8, [&](auto kern) {
-            return launch("attn_partial_kernel", kern, dim3(nsplit, n_kv), dim3(kAttnThreads), 0, s, qkv, kv, rc, rs,
-                          pos, part, n_heads, n_kv, max_seq, rot_half, nsplit);
-        });
-        if (st != ASDSL_OK) return st;
-        return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
-                      static_cast<const float*>(part), pos, att, nsplit, max_seq, 0, 1, 0, 0,
-                      static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
-    }
-    const FoldForm& f = fold ? kShortForm : kLongForm;
+    const bool deep = !fold && limit > kDeepFrom;
+    const FoldForm& f = fold ? kShortForm : deep ? kDeepForm : kLongForm;
     const dim3 grid(attn_max_splits(limit, f), n_kv);
     const dim3 block(f.waves * kWave);
     const int max_splits = f.max_splits;
-    const asdsl_status st = with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, [&](auto kern) {
+    auto go = [&](auto kern) {
         return launch("attn_decode_kernel", kern, grid, block, 0, s, qkv, kv, rc, rs, pos, work, att, n_heads, n_kv,
                       max_seq, rot_half, max_splits);
-    });
+    };
+    const asdsl_status st = deep ? with_attn_kernel<DeepAttnK>(n_heads / n_kv, q8, go)
+                                 : with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, go);
     if (st != ASDSL_OK || fold) return st;
     return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
                   static_cast<const float*>(work), pos, att, kMaxSplits, max_seq, 0, 1, f.tile, f.max_splits,

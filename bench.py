@@ -1125,12 +1125,11 @@ def pmc_probe(mode: str) -> int:
 # step stamp a 100 MHz wall clock at fixed points of every workgroup
 # (slots and stamp points: csrc/device_common.hpp, ASDSL_TIMELINE_STAMP).
 TIMELINE_KERNELS = {0: "o_proj (split merge)", 1: "gate_up (SwiGLU)", 2: "qkv (norm)", 3: "down",
-                    4: "attention", 5: "attention partials (int8 cache, long)", 6: "attention combine", 7: "o_proj"}
+                    4: "attention", 6: "attention combine", 7: "o_proj"}
 _GEMV_PHASES = ((0, 1, "prologue"), (1, 2, "staging barrier"), (2, 3, "first tile"), (3, 4, "tail"))
 TIMELINE_PHASES = {0: _GEMV_PHASES, 1: _GEMV_PHASES, 2: _GEMV_PHASES, 3: _GEMV_PHASES, 7: _GEMV_PHASES,
                    4: ((0, 1, "loads and RoPE"), (1, 2, "barrier and K/V store"), (2, 3, "scores, softmax, P.V"),
                        (3, 4, "merge")),
-                   5: ((0, 1, "loads and RoPE"), (1, 2, "barrier and K/V store"), (2, 4, "split")),
                    6: ((0, 3, "fold"), (3, 4, "merge and store"))}
 
 
