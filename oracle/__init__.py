@@ -20,13 +20,15 @@ from __future__ import annotations
 import ctypes
 import importlib.machinery
 import importlib.util
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 ORACLE_DIR = Path(__file__).resolve().parent
-LIB_PATH = ORACLE_DIR / "lib" / "liboracle.so"
+# ASDSL_ORACLE_LIB names another build of asdsl_oracle.c (the sanitized one).
+LIB_PATH = Path(os.environ.get("ASDSL_ORACLE_LIB") or ORACLE_DIR / "lib" / "liboracle.so")
 REF_DIR = ORACLE_DIR / "_ref"
 REFERENCE_TREE = Path("/root/reference")
 
