@@ -35,6 +35,8 @@ SIGNATURES: dict[str, list] = {
     "asdsl_last_error": [],
     "asdsl_device_cu_count": [],
     "asdsl_profile_next_launch": [_P, _P],
+    "asdsl_profile_stages_begin": [_I],
+    "asdsl_profile_stages_end": [_I, _P, _P, _P, _P],
     "asdsl_stream_read": [_P, ctypes.c_size_t, _P, _I, _P],
     "asdsl_grid_sync_probe_work_bytes": [_I],
     "asdsl_grid_sync_probe": [_I, _I, _I, _P, ctypes.c_size_t, _I, _P],
@@ -108,6 +110,16 @@ def _load() -> ctypes.CDLL:
             f"{LIB_PATH} is not built; run `python asdsl-framework_amd/build_hip.py` "
             "(or __graft_entry__.build()). The HIP library is the only compute path."
         )
+    # torch's HIP runtime must be the process's only one.  torch links its
+    # bundled runtime by the name libamdhip64.so, this library by the soname
+    # libamdhip64.so.7, which that runtime carries: loaded after torch, the
+    # library binds to torch's runtime.  Loaded first, it pulls in the system
+    # runtime and torch then loads its own beside it; with torch's initialised
+    # first, this library's calls fail with hipErrorNoDevice.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(LIB_PATH))
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name, None)
@@ -213,3 +225,20 @@ def cu_count() -> int:
     if n < 0:
         raise RuntimeError(last_error())
     return n
+
+
+def profile_stages(run, max_launches: int = 4096) -> tuple[list[tuple[str, float]], float]:
+    """Runs ``run()``, which queues this library's launches on the calling
+    thread, with the stage recorder armed (asdsl_profile_stages_begin/_end):
+    returns each launch's (stage label, ms) in launch order and the ms from the
+    first launch's start to the last one's end.  Waits for the launches."""
+    check(LIB.asdsl_profile_stages_begin(max_launches), "asdsl_profile_stages_begin")
+    labels = (ctypes.c_char_p * max_launches)()
+    ms = (ctypes.c_float * max_launches)()
+    count, span = ctypes.c_int(0), ctypes.c_float(0.0)
+    try:
+        run()
+    finally:
+        status = LIB.asdsl_profile_stages_end(max_launches, labels, ms, ctypes.byref(count), ctypes.byref(span))
+    check(status, "asdsl_profile_stages_end")
+    return [(labels[i].decode(), float(ms[i])) for i in range(count.value)], float(span.value)

@@ -19,6 +19,8 @@ preq blocks of the reference's preq cache (asdsl.quantization.preq_cache).
 from __future__ import annotations
 
 import ctypes
+import os
+import sys
 from dataclasses import dataclass
 
 import numpy as np
@@ -181,6 +183,15 @@ class DecodeEngine:
         self.kv_seq_len = 0
         self._kv_snapshots: list[int] = []
         self._verify = None  # work, token, logits and next-token buffers of the verify pass
+        # ASDSL_ENGINE_PROFILE / ASDSL_ENGINE_PROFILE_TOKEN, read like the
+        # reference's engine_profile_enabled/_target_token
+        # (asdsl/kernels/native/unified_engine.cpp:71-87): the target decode
+        # step (counted from 1) runs eagerly with per-stage timing.
+        flag = os.environ.get("ASDSL_ENGINE_PROFILE", "")
+        self._profile_token = int(os.environ.get("ASDSL_ENGINE_PROFILE_TOKEN", "3")) if flag[:1] not in ("", "0") \
+            else None
+        self._decode_idx = 0
+        self.last_profile: dict | None = None
 
     # ------------------------------------------------------------ building
     @classmethod
@@ -269,7 +280,11 @@ class DecodeEngine:
             raise ValueError("forward_token: pos out of kv-cache range")
         self.token.fill_(token_id)
         self.pos.fill_(pos)
-        self._queue_step(_hip.stream_handle(), self._pos_limit(pos))
+        limit = self._pos_limit(pos)
+        if self._profile_due():
+            self._report(self.profile_step(limit))
+        else:
+            self._queue_step(_hip.stream_handle(), limit)
         self._host_pos = pos + 1
         self.kv_seq_len = max(self.kv_seq_len, pos + 1)
         return self.logits
@@ -317,10 +332,63 @@ class DecodeEngine:
         prefill, forward_token, the verify pass and the KV bookkeeping, read
         back by capture()); a position set by writing self.pos directly needs
         a capture() before the next step."""
+        if self._profile_due():
+            self._report(self.profile_step())
+            return
         if self._graph is None:
             self.capture()
         self._graph.replay()
         self._host_pos += 1
+
+    # ------------------------------------------------------------ profiling
+    STAGES = ("embed", "qkv", "attention", "attention_combine", "o_proj", "gate_up", "down", "lm_head", "finalize")
+
+    def profile_step(self, pos_limit: int | None = None) -> dict:
+        """One step queued eagerly (the same launches a captured step
+        replays; token and position advance on the device) with each launch
+        timed by its own dispatch events (asdsl_profile_stages_begin/_end).
+        Consumes self.token at the device position like step().  Returns ms
+        per stage summed over layers, the launch count, and the span from the
+        first launch's start to the last one's end; eager launches sit
+        further apart than a graph's, so the span exceeds a replayed step's
+        time."""
+        limit = self._pos_limit(self._host_pos) if pos_limit is None else int(pos_limit)
+        stages, span = _hip.profile_stages(lambda: self._queue_step(_hip.stream_handle(), limit),
+                                           max_launches=16 * self.cfg.n_layers + 16)
+        self._host_pos += 1
+        per: dict[str, float] = {}
+        for label, ms in stages:
+            per[label] = per.get(label, 0.0) + ms
+        return {"stages_ms": per, "launches": len(stages), "span_ms": span}
+
+    def _profile_due(self) -> bool:
+        if self._profile_token is None:
+            return False
+        self._decode_idx += 1
+        return self._decode_idx == self._profile_token
+
+    def _report(self, prof: dict) -> None:
+        """The reference's ASDSL_ENGINE_PROFILE report
+        (asdsl/kernels/native/unified_engine.cpp:1668-1687) on stderr: its
+        keys (activation quantization and the norms run inside the GEMV
+        prologues here, so those rows are 0), then what "other" holds."""
+        st = prof["stages_ms"]
+        gemv = {k: st.get(s, 0.0) for k, s in (("gate_up_gemv", "gate_up"), ("down_gemv", "down"),
+                                                 ("qkv_gemv", "qkv"), ("o_gemv", "o_proj"))}
+        lm = st.get("lm_head", 0.0)
+        total = prof["span_ms"]
+        other = max(0.0, total - sum(gemv.values()) - lm)
+        prof = dict(prof, token=self._decode_idx, other_ms=other)
+        self.last_profile = prof
+        lines = [f"[ASDSL_ENGINE_PROFILE] decode token {self._decode_idx} (ms, {self.cfg.n_layers} layers):"]
+        lines += [f"  {k} {v:.4f}" for k, v in gemv.items()]
+        lines += ["  activation_q8 0 (in the GEMV prologues)", "  prep_fused 0 (in the GEMV prologues)",
+                  f"  lm_head {lm:.4f}"]
+        parts = ", ".join(f"{k} {st[k]:.4f}" for k in ("attention", "attention_combine", "finalize", "embed")
+                          if k in st)
+        lines += [f"  other {other:.4f} ({parts}; the rest is time between launches)",
+                  f"  total {total:.4f} (eager launches, {prof['launches']} kernels)"]
+        print("\n".join(lines), file=sys.stderr, flush=True)
 
     # ------------------------------------------------------------ verify
     MAX_VERIFY_TOKENS = 16

@@ -4,14 +4,33 @@
 #include <stdlib.h>
 
 #include <mutex>
+#include <vector>
 
 #include "abi_util.hpp"
 
 namespace asdsl {
 
+thread_local const char* g_stage = nullptr;
+
 namespace {
 thread_local char g_error[512] = "";
 thread_local LaunchEvents g_events;
+
+// The stage recorder of asdsl_profile_stages_begin/_end: one event pair per
+// launch from a pool that is created at begin and kept for later sessions.
+constexpr int kMaxStageLaunches = 65536;
+struct StageRecord {
+    const char* label;
+    LaunchEvents ev;
+};
+struct StageRecorder {
+    bool armed = false;
+    int max = 0;
+    int launches = 0;  // launches while armed, recorded or not
+    std::vector<StageRecord> recs;
+    std::vector<hipEvent_t> pool;
+};
+thread_local StageRecorder g_rec;
 
 struct DeviceShape {
     int cus = -1;
@@ -36,10 +55,23 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() { g_error[0] = '\0'; }
 
-LaunchEvents take_launch_events() {
-    const LaunchEvents ev = g_events;
+asdsl_status take_launch_events(const char* what, hipStream_t stream, LaunchEvents* ev) {
+    *ev = g_events;
     g_events = LaunchEvents{};
-    return ev;
+    if (!g_rec.armed) return ASDSL_OK;
+    ++g_rec.launches;
+    if (ev->start != nullptr || ev->stop != nullptr) return ASDSL_OK;  // explicit pair wins (end reports it)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        set_error("%s: stage recording is armed on a stream under graph capture", what);
+        return ASDSL_ERR_UNSUPPORTED;
+    }
+    const size_t i = g_rec.recs.size();
+    if (static_cast<int>(i) >= g_rec.max) return ASDSL_OK;  // past the limit: end reports it
+    ev->start = g_rec.pool[2 * i];
+    ev->stop = g_rec.pool[2 * i + 1];
+    g_rec.recs.push_back(StageRecord{g_stage != nullptr ? g_stage : what, *ev});
+    return ASDSL_OK;
 }
 
 int cu_count_current() {
@@ -141,5 +173,56 @@ extern "C" int asdsl_device_cu_count(void) { return asdsl::cu_count_current(); }
 extern "C" asdsl_status asdsl_profile_next_launch(void* start_event, void* stop_event) {
     asdsl::g_events.start = static_cast<hipEvent_t>(start_event);
     asdsl::g_events.stop = static_cast<hipEvent_t>(stop_event);
+    return ASDSL_OK;
+}
+
+extern "C" asdsl_status asdsl_profile_stages_begin(int max_launches) {
+    using asdsl::g_rec;
+    ASDSL_CHECK_ARG(!g_rec.armed, "profile_stages_begin: already armed on this thread");
+    ASDSL_CHECK_ARG(max_launches >= 1 && max_launches <= asdsl::kMaxStageLaunches,
+                    "profile_stages_begin: max_launches must be in [1, 65536]");
+    while (g_rec.pool.size() < 2 * static_cast<size_t>(max_launches)) {
+        hipEvent_t e = nullptr;
+        const hipError_t err = hipEventCreate(&e);
+        if (err != hipSuccess) {
+            asdsl::set_error("profile_stages_begin: hipEventCreate failed: %s", hipGetErrorString(err));
+            return ASDSL_ERR_HIP;
+        }
+        g_rec.pool.push_back(e);
+    }
+    g_rec.recs.clear();
+    g_rec.recs.reserve(max_launches);
+    g_rec.max = max_launches;
+    g_rec.launches = 0;
+    g_rec.armed = true;
+    return ASDSL_OK;
+}
+
+extern "C" asdsl_status asdsl_profile_stages_end(int capacity, const char** labels, float* ms, int* count,
+                                                 float* span_ms) {
+    using asdsl::g_rec;
+    ASDSL_CHECK_ARG(g_rec.armed, "profile_stages_end: not armed on this thread");
+    g_rec.armed = false;
+    ASDSL_CHECK_ARG(labels && ms && count && span_ms, "profile_stages_end: null pointer");
+    const int n = static_cast<int>(g_rec.recs.size());
+    if (g_rec.launches != n) {
+        asdsl::set_error("profile_stages_end: %d launches, %d recorded (limit %d, or a launch armed by "
+                         "asdsl_profile_next_launch)", g_rec.launches, n, g_rec.max);
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    }
+    ASDSL_CHECK_ARG(capacity >= n, "profile_stages_end: capacity below the launch count");
+    *count = n;
+    *span_ms = 0.0f;
+    if (n == 0) return ASDSL_OK;
+    hipError_t err = hipEventSynchronize(g_rec.recs.back().ev.stop);
+    for (int i = 0; i < n && err == hipSuccess; ++i) {
+        labels[i] = g_rec.recs[i].label;
+        err = hipEventElapsedTime(&ms[i], g_rec.recs[i].ev.start, g_rec.recs[i].ev.stop);
+    }
+    if (err == hipSuccess) err = hipEventElapsedTime(span_ms, g_rec.recs.front().ev.start, g_rec.recs.back().ev.stop);
+    if (err != hipSuccess) {
+        asdsl::set_error("profile_stages_end: %s", hipGetErrorString(err));
+        return ASDSL_ERR_HIP;
+    }
     return ASDSL_OK;
 }

@@ -23,15 +23,32 @@ asdsl_status launch_status(const char* what);
 
 inline hipStream_t as_hip(asdsl_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Events armed by asdsl_profile_next_launch for the calling thread's next
-// kernel launch; returned and cleared.
+// Timing events of one launch.
 struct LaunchEvents {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
 };
-LaunchEvents take_launch_events();
 
-// Launches `kernel` on `stream`.  With armed events the launch goes through
+// Stage label of the calling thread's launches (a string literal), kept by the
+// stage recorder (asdsl_profile_stages_begin/_end) beside each launch's
+// events; a launch outside any StageScope is recorded under its kernel name.
+extern thread_local const char* g_stage;
+struct StageScope {
+    const char* prev;
+    explicit StageScope(const char* label) : prev(g_stage) { g_stage = label; }
+    ~StageScope() { g_stage = prev; }
+    StageScope(const StageScope&) = delete;
+    StageScope& operator=(const StageScope&) = delete;
+};
+
+// Events for the calling thread's next launch: the pair armed by
+// asdsl_profile_next_launch (returned and cleared), else, while the stage
+// recorder is armed, a pair of its own recorded under the current stage label
+// (ASDSL_ERR_UNSUPPORTED on a stream under graph capture, ASDSL_ERR_INVALID_ARGUMENT
+// past its launch limit), else none.
+asdsl_status take_launch_events(const char* what, hipStream_t stream, LaunchEvents* ev);
+
+// Launches `kernel` on `stream`.  With events the launch goes through
 // hipExtLaunchKernel, which records them as part of the kernel's own dispatch
 // (start and end of its execution, no extra packets on the stream).
 // Returns ASDSL_OK or ASDSL_ERR_HIP with the error text set.
@@ -39,7 +56,9 @@ template <typename... P, typename... A>
 asdsl_status launch(const char* what, void (*kernel)(P...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
                     A... args) {
     static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
-    const LaunchEvents ev = take_launch_events();
+    LaunchEvents ev;
+    const asdsl_status es = take_launch_events(what, stream, &ev);
+    if (es != ASDSL_OK) return es;
     if (ev.start == nullptr && ev.stop == nullptr) {
         kernel<<<grid, block, lds, stream>>>(args...);
         return launch_status(what);

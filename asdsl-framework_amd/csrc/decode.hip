@@ -735,6 +735,7 @@ asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q
     const asdsl_status st = deep ? with_attn_kernel<DeepAttnK>(n_heads / n_kv, q8, go)
                                  : with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, go);
     if (st != ASDSL_OK || fold) return st;
+    const StageScope stage("attention_combine");
     return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
                   static_cast<const float*>(work), pos, att, kMaxSplits, max_seq, 0, 1, f.tile, f.max_splits,
                   static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
@@ -1240,8 +1241,8 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
     hipStream_t s = as_hip(stream);
     const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
     const int q_dim = m.n_heads * m.head_dim;
-    // The attention form follows pos_limit (attn_fold): up to 256 o_proj's
-    // prologue merges the splits, beyond the combine kernel does.
+    // The attention form follows pos_limit (attn_fold): below 512 o_proj's
+    // prologue merges the splits, from there the combine kernel does.
     // ASDSL_HIP_NO_COMBINE_FOLD=1 always takes the combine kernel.
     static const int no_fold = env_knob("ASDSL_HIP_NO_COMBINE_FOLD");
     const int limit = pos_limit < m.max_seq ? pos_limit : m.max_seq;
@@ -1255,6 +1256,7 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
     const bool embed_fold = reinterpret_cast<uintptr_t>(m.embed) % 16 == 0;
     asdsl_status st = ASDSL_OK;
     if (!embed_fold) {
+        const StageScope stage("embed");
         st = launch("embed_kernel", embed_kernel, dim3((m.hidden + 1023) / 1024), dim3(256), 0, s, m.embed,
                     static_cast<const int*>(token), hA, m.hidden, m.vocab, amax);
         if (st != ASDSL_OK) return st;
@@ -1265,6 +1267,7 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
     float* nxt = hB;
     for (int l = 0; l < m.n_layers; ++l) {
         const asdsl_decode_layer& L = m.layers[l];
+        StageScope stage("qkv");
         if (l > 0) {
             st = asdsl_gemv_preq2_rmsnorm(L.qkv_meta, L.qkv_quant, cur, down, L.rms_att, nxt, qkv, qkv_dim,
                                           m.hidden, m.gs_attn, m.rms_eps, nullptr, stream);
@@ -1278,33 +1281,40 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
         }
         if (st != ASDSL_OK) return st;
         const KvCache kv{L.k_cache, L.v_cache, L.k_scale, L.v_scale};
+        g_stage = "attention";  // the combine labels itself
         st = launch_attention_decode(qkv, kv, q8, m.rope_cos, m.rope_sin, pos, att, part, m.n_heads,
                                      m.n_kv_heads, m.rotary_dim / 2, m.max_seq, limit, fold, s);
         if (st != ASDSL_OK) return st;
+        g_stage = "o_proj";
         st = fold ? preq2_fused_combine(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, part, pos, kMaxSplits,
                                         form.tile, form.max_splits, kPartStride, kHeadDim, m.max_seq, stream)
                   : asdsl_gemv_preq2_fused(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, stream);
         if (st != ASDSL_OK) return st;
         // gate_up with SwiGLU in its epilogue (gate and up rows in one
         // workgroup), down on the result; the SwiGLU prologue form otherwise
+        g_stage = "gate_up";
         st = asdsl_gemv_preq2_rmsnorm_swiglu(L.gu_meta, L.gu_quant, cur, o, L.rms_ffn, nxt, gu, m.ffn, m.hidden,
                                              m.gs_ffn, m.rms_eps, L.fatrelu_threshold, stream);
         if (st == ASDSL_OK) {
             std::swap(cur, nxt);
+            g_stage = "down";
             st = asdsl_gemv_preq2_fused(L.down_meta, L.down_quant, gu, down, m.hidden, m.ffn, m.gs_ffn, stream);
         } else if (st == ASDSL_ERR_UNSUPPORTED) {
             st = asdsl_gemv_preq2_rmsnorm(L.gu_meta, L.gu_quant, cur, o, L.rms_ffn, nxt, gu, 2 * m.ffn, m.hidden,
                                           m.gs_ffn, m.rms_eps, nullptr, stream);
             if (st != ASDSL_OK) return st;
             std::swap(cur, nxt);
+            g_stage = "down";
             st = asdsl_gemv_preq2_swiglu(L.down_meta, L.down_quant, gu, down, m.hidden, m.ffn, m.gs_ffn,
                                          L.fatrelu_threshold, stream);
         }
         if (st != ASDSL_OK) return st;
     }
+    StageScope stage("lm_head");
     st = asdsl_gemv_preq2_rmsnorm(m.lm_meta, m.lm_quant, cur, down, m.rms_out, nullptr, logits, m.vocab, m.hidden,
                                   m.gs_lm, m.rms_eps, amax, stream);
     if (st != ASDSL_OK) return st;
+    g_stage = "finalize";
     return launch("finalize_kernel", finalize_kernel, dim3(1), dim3(64), 0, s,
                   static_cast<const unsigned long long*>(amax), token, pos);
 }

@@ -451,6 +451,11 @@ def _decode_contexts(eng, contexts, steps: int) -> dict:
                          "bytes_per_token": bpt, "GB/s": round(bpt / (us * 1e-6) / 1e9, 1),
                          "roofline_tokens_per_s": round(ideal, 1), "frac_of_roofline": round(tps / ideal, 4),
                          "final_pos": int(eng.pos.item())}
+        # one more step queued eagerly with each launch timed (the engine's
+        # ASDSL_ENGINE_PROFILE breakdown): ms per stage over all layers
+        prof = eng.profile_step()
+        res[str(ctx)]["eager_stage_ms"] = {k: round(v, 4) for k, v in prof["stages_ms"].items()}
+        res[str(ctx)]["eager_span_ms"] = round(prof["span_ms"], 4)
         eng._graphs.clear()
     return res
 

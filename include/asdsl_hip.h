@@ -71,6 +71,26 @@ int asdsl_device_cu_count(void);
  * alone, with no extra commands on the stream. */
 asdsl_status asdsl_profile_next_launch(void* start_event, void* stop_event);
 
+/* Per-stage timing of a decode step, replacing the reference's
+ * ASDSL_ENGINE_PROFILE breakdown (asdsl/kernels/native/unified_engine.cpp:58-95,
+ * 1668-1687, which times each stage of UnifiedEngine::forward_token with a
+ * host clock).  Between begin and end, every kernel this library launches from
+ * the calling thread (at most max_launches, 1..65536) records two HIP events
+ * through its own dispatch, as asdsl_profile_next_launch does, under a stage
+ * label: the decode step's launches are labelled "embed", "qkv", "attention",
+ * "attention_combine", "o_proj", "gate_up", "down", "lm_head" and "finalize";
+ * any other launch carries its kernel's name.  begin creates the events it
+ * needs (kept for later sessions of the thread) and fails on a thread already
+ * armed; a launch while armed on a stream under graph capture fails with
+ * ASDSL_ERR_UNSUPPORTED.  end disarms, waits for the last recorded launch and
+ * writes launch i's label (a static string) and duration in ms to labels[i]
+ * and ms[i] in launch order, their number to *count (capacity at least that),
+ * and the time from the first launch's start to the last one's end to
+ * *span_ms; it fails when more launches than max_launches were made, or when
+ * one used events armed by asdsl_profile_next_launch instead. */
+asdsl_status asdsl_profile_stages_begin(int max_launches);
+asdsl_status asdsl_profile_stages_end(int capacity, const char** labels, float* ms, int* count, float* span_ms);
+
 /* Calibration, no reference counterpart: reads `bytes` (a multiple of 16)
  * from the 16-byte-aligned device buffer `data` with 16-byte non-temporal
  * loads over `grid` workgroups of 512 threads (<= 0: one per compute unit)
