@@ -35,6 +35,10 @@ SIGNATURES: dict[str, list] = {
     "asdsl_last_error": [],
     "asdsl_device_cu_count": [],
     "asdsl_profile_next_launch": [_P, _P],
+    "asdsl_dequant_gguf_q4k": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q6k": [_P, _P, _I, _I, _P],
+    "asdsl_repack_gguf_q4k_to_q4km": [_P, _P, _I, _I, _P],
+    "asdsl_quantize_q4_symmetric": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_profile_stages_begin": [_I],
     "asdsl_profile_stages_end": [_I, _P, _P, _P, _P],
     "asdsl_stream_read": [_P, ctypes.c_size_t, _P, _I, _P],
@@ -205,6 +209,8 @@ def to_device(a, np_dtype) -> "torch.Tensor":
             t = t.to(device())
         return t.contiguous()
     arr = np.ascontiguousarray(a, dtype=np_dtype)
+    if not arr.flags.writeable:  # a read-only memory map (a GGUF payload): torch needs writable memory
+        arr = arr.copy()
     if np_dtype == np.uint32:
         arr = arr.view(np.int32)
     return torch.from_numpy(arr).to(device(), non_blocking=False)

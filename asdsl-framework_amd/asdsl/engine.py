@@ -121,6 +121,116 @@ def layers_from_preq_blocks(cfg: "DecodeConfig", blocks: dict, norms: list) -> l
     return layers
 
 
+def config_from_gguf(metadata: dict, **overrides) -> DecodeConfig:
+    """DecodeConfig from a GGUF file's metadata (``{arch}.embedding_length``,
+    ``.feed_forward_length``, ``.block_count``, ``.attention.head_count``,
+    ``.attention.head_count_kv``, ``.rope.dimension_count``,
+    ``.context_length``, ``.attention.layer_norm_rms_epsilon``,
+    ``.rope.freq_base``, with arch = ``general.architecture``); the
+    vocabulary from the token list.  Keyword overrides win."""
+    arch = metadata.get("general.architecture", "phi3")
+
+    def get(key, default=None):
+        v = metadata.get(f"{arch}.{key}", default)
+        if v is None:
+            raise ValueError(f"GGUF metadata lacks {arch}.{key}")
+        return v
+
+    hidden, n_heads = int(get("embedding_length")), int(get("attention.head_count"))
+    tokens = metadata.get("tokenizer.ggml.tokens")
+    fields = dict(hidden=hidden, ffn=int(get("feed_forward_length")), n_layers=int(get("block_count")),
+                  n_heads=n_heads, n_kv_heads=int(get("attention.head_count_kv", n_heads)),
+                  head_dim=hidden // n_heads, rotary_dim=int(get("rope.dimension_count", hidden // n_heads)),
+                  max_seq=int(get("context_length")),
+                  rms_eps=float(get("attention.layer_norm_rms_epsilon", 1e-5)),
+                  rope_theta=float(get("rope.freq_base", 10000.0)))
+    if tokens is not None:
+        fields["vocab"] = len(tokens)
+    fields.update(overrides)
+    return DecodeConfig(**fields)
+
+
+def _gguf_projection(info: dict, rows: int, cols: int, gs: int, what: str):
+    """One GGUF weight -> preq2 (meta, quant) on the device: decoded to fp32
+    (asdsl_dequant_gguf_q4k / _q6k), requantized to symmetric Q4 at group
+    size gs (asdsl_quantize_q4_symmetric, the reference's load_from_gguf
+    rule, experiments/phi4_cpu_run.py:1437-1466) and packed as preq2
+    (asdsl_repack_asym_to_preq2, zero 7.5: the requantized weights exactly)."""
+    import torch
+
+    from asdsl.io.gguf_loader import dequant_tensor_device
+    from asdsl.quantization._device_repack import asym_to_preq2
+
+    got = tuple(info.get("logical_shape", ()))
+    if got != (rows, cols):
+        raise ValueError(f"GGUF {what}: shape {got}, expected {(rows, cols)}")
+    w = dequant_tensor_device(info).contiguous()
+    dev = w.device
+    packed = torch.empty(rows * cols // 2, dtype=torch.uint8, device=dev)
+    scales = torch.empty(rows * cols // gs, dtype=torch.float32, device=dev)
+    biases = torch.empty_like(scales)
+    _hip.call("asdsl_quantize_q4_symmetric", _hip.ptr(w), _hip.ptr(packed), _hip.ptr(scales), _hip.ptr(biases),
+              rows, cols, gs, _hip.stream_handle())
+    del w
+    return asym_to_preq2(packed, scales, biases, rows, cols, gs)
+
+
+def layers_from_gguf(cfg: DecodeConfig, tensors: dict) -> tuple[list[dict], dict]:
+    """Decode-step operands from the tensors of a GGUF file (read_gguf_tensors).
+
+    Per layer ``blk.{i}.``: attn_qkv, attn_output, the gate and up rows
+    (ffn_gate_up, or ffn_up holding both as in Phi-3/4 conversions, or
+    ffn_gate + ffn_up stacked), ffn_down -- Q4_K or Q6_K, decoded and
+    requantized on the GPU (_gguf_projection) -- and attn_norm / ffn_norm.
+    Model-wide: token_embd (decoded, stored fp16), output_norm, and output
+    (the embedding when absent: tied weights) as the lm_head at cfg.gs_lm.
+    Returns (layers, {"embed", "rms_out", "lm_meta", "lm_quant"})."""
+    import torch
+
+    from asdsl.io.gguf_loader import dequant_tensor_device
+
+    def need(name):
+        if name not in tensors:
+            raise ValueError(f"GGUF lacks {name}")
+        return tensors[name]
+
+    def norm(name):
+        v = dequant_tensor_device(need(name)).reshape(-1).float().contiguous()
+        if v.numel() != cfg.hidden:
+            raise ValueError(f"GGUF {name}: {v.numel()} values, expected {cfg.hidden}")
+        return v
+
+    mats = _layer_mats(cfg)
+    layers = []
+    for i in range(cfg.n_layers):
+        p = f"blk.{i}."
+        L = {}
+        for n, tname in (("qkv", "attn_qkv.weight"), ("o", "attn_output.weight"), ("down", "ffn_down.weight")):
+            rows, cols, gs = mats[n]
+            L[n] = _gguf_projection(need(p + tname), rows, cols, gs, p + tname)
+        rows, cols, gs = mats["gu"]
+        if p + "ffn_gate_up.weight" in tensors or (p + "ffn_up.weight" in tensors and p + "ffn_gate.weight" not in tensors):
+            name = p + ("ffn_gate_up.weight" if p + "ffn_gate_up.weight" in tensors else "ffn_up.weight")
+            L["gu"] = _gguf_projection(tensors[name], rows, cols, gs, name)
+        else:
+            g = dequant_tensor_device(need(p + "ffn_gate.weight"))
+            u = dequant_tensor_device(need(p + "ffn_up.weight"))
+            stacked = {"type": "f32", "shape": (cols, rows), "logical_shape": (rows, cols),
+                       "data": torch.cat([g, u]).cpu().numpy().view(np.uint8).reshape(-1)}
+            del g, u
+            L["gu"] = _gguf_projection(stacked, rows, cols, gs, p + "ffn_gate+ffn_up")
+        L["rms_att"], L["rms_ffn"] = norm(p + "attn_norm.weight"), norm(p + "ffn_norm.weight")
+        layers.append(L)
+    emb_info = need("token_embd.weight")
+    embed = dequant_tensor_device(emb_info)
+    if tuple(embed.shape) != (cfg.vocab, cfg.hidden):
+        raise ValueError(f"GGUF token_embd.weight: shape {tuple(embed.shape)}, expected {(cfg.vocab, cfg.hidden)}")
+    embed = embed.half().contiguous()
+    out_info = tensors.get("output.weight", emb_info)
+    lm_meta, lm_quant = _gguf_projection(out_info, cfg.vocab, cfg.hidden, cfg.gs_lm, "output.weight")
+    return layers, {"embed": embed, "rms_out": norm("output_norm.weight"), "lm_meta": lm_meta, "lm_quant": lm_quant}
+
+
 class DecodeEngine:
     """Holds the device weights, KV caches and step buffers of one model."""
 
@@ -220,6 +330,23 @@ class DecodeEngine:
         embed = torch.randn((cfg.vocab, cfg.hidden), generator=gen, device=dev, dtype=torch.float32).half()
         lm_meta, lm_quant = packed(cfg.vocab, cfg.hidden, cfg.gs_lm)
         return cls(cfg, layers, embed, norm_w(), lm_meta, lm_quant, fatrelu_threshold)
+
+    @classmethod
+    def from_gguf(cls, path, cfg: DecodeConfig | None = None, fatrelu_threshold: float = 0.0,
+                  **overrides) -> "DecodeEngine":
+        """A model from a GGUF file (its configuration from the file's
+        metadata unless cfg is given; overrides such as max_seq, gs_ffn or
+        kv_format apply to it).  The reference loads GGUF projections the
+        same way (experiments/phi4_cpu_run.py:1316-1466: K-quant decode,
+        symmetric Q4 requantization) but keeps the embeddings and norms of
+        its HF checkpoint; here they come from the file too."""
+        from asdsl.io.gguf_loader import GGUFFile, read_gguf_tensors
+
+        if cfg is None:
+            cfg = config_from_gguf(GGUFFile(path).metadata, **overrides)
+        layers, rest = layers_from_gguf(cfg, read_gguf_tensors(path))
+        return cls(cfg, layers, rest["embed"], rest["rms_out"], rest["lm_meta"], rest["lm_quant"],
+                   fatrelu_threshold)
 
     # A step is shaped for the positions it serves (asdsl_decode_token_upto):
     # below 512 the attention splits are merged in o_proj's prologue, beyond

@@ -1064,6 +1064,28 @@ def repack_rows(args, oracle) -> list:
         lambda: {"w": torch.randn(Mg * K, generator=gen, device="cuda") * 0.02}, {"blocks": Mg * G128 * 66},
         lambda c, o, h: lib.asdsl_repack_fp32_to_q4_128(P(c["w"]), P(o["blocks"]), Mg, K, 128, h),
         lambda hc, n: oracle.repack_fp32_to_q4_128(hc["w"][: n * K], n, K), 1024)
+
+    # GGUF loading (asdsl/io/gguf_loader.py, experiments/phi4_cpu_run.py:1316-1466)
+    G256 = K // 256
+    q4k_b, q6k_b = Mg * G256 * 144, Mg * G256 * 210
+    row("F4 GGUF Q4_K->fp32", "gate_up 16384x3072", Mg, K, q4k_b + 4 * Mg * K,
+        lambda: {"blocks": _dev_bytes(q4k_b, gen)}, {"w": 4 * Mg * K},
+        lambda c, o, h: lib.asdsl_dequant_gguf_q4k(P(c["blocks"]), P(o["w"]), Mg, K, h),
+        lambda hc, n: oracle.dequant_gguf_q4k(hc["blocks"][: n * G256 * 144], n * G256), 1024)
+    row("F4 GGUF Q6_K->fp32", "gate_up 16384x3072", Mg, K, q6k_b + 4 * Mg * K,
+        lambda: {"blocks": _dev_bytes(q6k_b, gen)}, {"w": 4 * Mg * K},
+        lambda c, o, h: lib.asdsl_dequant_gguf_q6k(P(c["blocks"]), P(o["w"]), Mg, K, h),
+        lambda hc, n: oracle.dequant_gguf_q6k(hc["blocks"][: n * G256 * 210], n * G256), 1024)
+    row("F4 GGUF Q4_K->ASDSL Q4_K", "gate_up 16384x3072", Mg, K, 2 * q4k_b,
+        lambda: {"blocks": _dev_bytes(q4k_b, gen)}, {"q4km": q4k_b},
+        lambda c, o, h: lib.asdsl_repack_gguf_q4k_to_q4km(P(c["blocks"]), P(o["q4km"]), Mg, K, h),
+        lambda hc, n: oracle.repack_gguf_q4k_to_q4km(hc["blocks"][: n * G256 * 144], n * G256), 1024)
+    row("F4 quantize fp32->Q4 symmetric g32", "gate_up 16384x3072", Mg, K, 4 * Mg * K + Mg * K // 2 + 8 * Mg * G32,
+        lambda: {"w": torch.randn(Mg * K, generator=gen, device="cuda") * 0.02},
+        {"packed": Mg * K // 2, "sc": 4 * Mg * G32, "bi": 4 * Mg * G32},
+        lambda c, o, h: lib.asdsl_quantize_q4_symmetric(P(c["w"]), P(o["packed"]), P(o["sc"]), P(o["bi"]), Mg, K, 32,
+                                                        h),
+        lambda hc, n: oracle.quantize_q4_symmetric(hc["w"][: n * K], 32), 1024)
     return out
 
 

@@ -633,6 +633,44 @@ asdsl_status asdsl_repack_asym_to_q4_128(const uint8_t* packed, const float* sca
 asdsl_status asdsl_repack_q4_128_to_preq2(const uint8_t* blocks, uint8_t* meta, uint8_t* quant, int rows, int cols,
                                           asdsl_stream_t stream);
 
+/* ------------------------------------------------------------- GGUF weights
+ * K-quant tensors of a GGUF file, in the file's row-major block order (rows =
+ * out_features, cols = in_features, a multiple of 256), on the device. */
+
+/* ggml Q4_K blocks[rows][cols/256][144] -> fp32 weights[rows][cols]:
+ * w = (d * sc) * q - (dmin * m) per 32-weight sub-block.  blocks and
+ * weights 16-byte aligned.  Replaces dequant_tensor for Q4_K
+ * (asdsl/io/gguf_loader.py:150-181, which calls gguf.quants.dequantize). */
+asdsl_status asdsl_dequant_gguf_q4k(const uint8_t* blocks, float* weights, int rows, int cols,
+                                   asdsl_stream_t stream);
+
+/* ggml Q6_K blocks[rows][cols/256][210] -> fp32 weights[rows][cols]:
+ * w = (d * scale) * (code - 32) per 16-weight group.  weights 16-byte
+ * aligned.  Replaces dequant_tensor for Q6_K (asdsl/io/gguf_loader.py:150-181). */
+asdsl_status asdsl_dequant_gguf_q6k(const uint8_t* blocks, float* weights, int rows, int cols,
+                                   asdsl_stream_t stream);
+
+/* ggml Q4_K blocks -> the ASDSL Q4_K variant blocks that asdsl_gemv_q4km_q8
+ * reads (6-bit scales and mins as one linear bitstream, each sub-block's
+ * codes in its own 16 bytes), losslessly, so that the GEMV computes ggml's
+ * weights.  Both 16-byte aligned.  The reference hands the GGUF bytes to its
+ * Q4_K GEMV unchanged (asdsl/io/gguf_loader.py:184-205 q4k_blocks_rowmajor,
+ * experiments/phi4_cpu_run.py:1480-1521), which reads ggml's fields in the
+ * variant's places; this entry point has no counterpart there. */
+asdsl_status asdsl_repack_gguf_q4k_to_q4km(const uint8_t* gguf_blocks, uint8_t* q4km_blocks, int rows, int cols,
+                                          asdsl_stream_t stream);
+
+/* fp32 weights[rows][cols] -> symmetric group-wise Q4: packed[rows*cols/2]
+ * (low nibble = even element), scales[groups] = f32(f16(max(amax, 1e-5) /
+ * 7.5)), biases[groups] = -7.5 * scale; q = clip(rne(w / max(scale, 1e-4) +
+ * 7.5), 0, 15).  group_size 32, 64 or 128 dividing cols; weights 16-byte,
+ * packed 2-byte, scales and biases 4-byte aligned.  Replaces
+ * quantize_weights(bits=4, symmetric=True) (asdsl/quantization/core.py:358-420)
+ * with the scale/bias form of load_from_gguf (experiments/phi4_cpu_run.py:1444-1459);
+ * asdsl_repack_asym_to_preq2 then builds the preq2 operands. */
+asdsl_status asdsl_quantize_q4_symmetric(const float* weights, uint8_t* packed, float* scales, float* biases,
+                                        int rows, int cols, int group_size, asdsl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

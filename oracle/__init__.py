@@ -359,3 +359,42 @@ def reference_q4_s256():
                             ctypes.c_int(K))
         return y
     return run
+
+
+# ------------------------------------------------------------------ GGUF
+def dequant_gguf_q4k(blocks, n_blocks: int) -> np.ndarray:
+    """ggml Q4_K blocks (144 bytes per 256 weights) -> float32 weights."""
+    b = _u8(blocks)
+    w = np.empty(n_blocks * 256, np.float32)
+    lib().oracle_dequant_gguf_q4k(_p(b, _c_u8p), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
+    return w
+
+
+def dequant_gguf_q6k(blocks, n_blocks: int) -> np.ndarray:
+    """ggml Q6_K blocks (210 bytes per 256 weights) -> float32 weights."""
+    b = _u8(blocks)
+    w = np.empty(n_blocks * 256, np.float32)
+    lib().oracle_dequant_gguf_q6k(_p(b, _c_u8p), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
+    return w
+
+
+def repack_gguf_q4k_to_q4km(blocks, n_blocks: int) -> np.ndarray:
+    """ggml Q4_K blocks -> the ASDSL Q4_K variant blocks gemv_q4km reads."""
+    b = _u8(blocks)
+    out = np.empty(n_blocks * 144, np.uint8)
+    lib().oracle_repack_gguf_q4k_to_q4km(_p(b, _c_u8p), _p(out, _c_u8p), ctypes.c_size_t(n_blocks))
+    return out
+
+
+def quantize_q4_symmetric(w, group_size: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """float32 weights (flat, a multiple of group_size) -> (packed codes,
+    f32 scales, f32 biases = -7.5 * scale): quantize_weights(bits=4,
+    symmetric=True) as the reference's GGUF requantization uses it."""
+    x = _f32(w).reshape(-1)
+    groups = x.size // group_size
+    packed = np.empty(x.size // 2, np.uint8)
+    scales = np.empty(groups, np.float32)
+    biases = np.empty(groups, np.float32)
+    lib().oracle_quantize_q4_symmetric(_p(x, _c_f32p), _p(packed, _c_u8p), _p(scales, _c_f32p),
+                                       _p(biases, _c_f32p), ctypes.c_size_t(groups), group_size)
+    return packed, scales, biases

@@ -636,3 +636,125 @@ EXPORT void oracle_gemv_q4_s256(const uint8_t* blocks, const int8_t* xq, const f
         y[r] = (float)acc;
     }
 }
+
+/* ------------------------------------------------------------------ GGUF
+ * ggml's Q4_K and Q6_K block decoders, as the reference reaches them through
+ * the gguf package (asdsl/io/gguf_loader.py:150-181, gguf.quants.dequantize;
+ * gguf-py from llama.cpp, no version pinned by the reference and absent
+ * here).  Restated from ggml's published block layouts; the float32 products
+ * and differences are formed in numpy's order, one rounding each.
+ * PARITY UNPINNED against the gguf package itself: the tests pin these by
+ * the layouts' invariants (each 6-bit field and nibble moves exactly the
+ * weights the layout assigns it) and by the lossless Q4_K -> ASDSL Q4_K
+ * rearrangement, whose decode through the pinned ASDSL GEMV must agree. */
+static void q4k_scale_min(const uint8_t* s, int j, int* sc, int* m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
+        *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+EXPORT void oracle_dequant_gguf_q4k(const uint8_t* blocks, float* w, size_t n_blocks) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* blk = blocks + b * 144;
+        const float d = half_to_float(rd16(blk));
+        const float dmin = half_to_float(rd16(blk + 2));
+        for (int j = 0; j < 8; ++j) {
+            int sc, m;
+            q4k_scale_min(blk + 4, j, &sc, &m);
+            volatile float d1 = d * (float)sc;
+            volatile float m1 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t byte = blk[16 + 32 * (j / 2) + l];
+                const int q = (j & 1) ? (byte >> 4) : (byte & 0x0F);
+                volatile float p = d1 * (float)q;
+                w[b * 256 + 32 * j + l] = p - m1;
+            }
+        }
+    }
+}
+
+EXPORT void oracle_dequant_gguf_q6k(const uint8_t* blocks, float* w, size_t n_blocks) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* blk = blocks + b * 210;
+        const float d = half_to_float(rd16(blk + 208));
+        for (int h = 0; h < 2; ++h) {
+            const uint8_t* ql = blk + 64 * h;
+            const uint8_t* qh = blk + 128 + 32 * h;
+            const int8_t* sc = (const int8_t*)(blk + 192 + 8 * h);
+            for (int k = 0; k < 4; ++k) {
+                for (int l = 0; l < 32; ++l) {
+                    const uint8_t lb = ql[l + 32 * (k & 1)];
+                    const int lo = k < 2 ? (lb & 0x0F) : (lb >> 4);
+                    const int hi = (qh[l] >> (2 * k)) & 3;
+                    volatile float ds = d * (float)sc[l / 16 + 2 * k];
+                    w[b * 256 + 128 * h + 32 * k + l] = ds * (float)((lo | (hi << 4)) - 32);
+                }
+            }
+        }
+    }
+}
+
+/* ggml Q4_K -> the ASDSL Q4_K variant read by oracle_gemv_q4km: the same d,
+ * dmin, 6-bit fields (linear LSB-first stream, scales then mins) and codes
+ * (sub-block j's 32 codes in bytes 16+16j.., low nibble first). */
+EXPORT void oracle_repack_gguf_q4k_to_q4km(const uint8_t* src, uint8_t* dst, size_t n_blocks) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* in = src + b * 144;
+        uint8_t* out = dst + b * 144;
+        memset(out, 0, 144);
+        memcpy(out, in, 4);
+        for (int idx = 0; idx < 16; ++idx) {
+            int sc, m;
+            q4k_scale_min(in + 4, idx % 8, &sc, &m);
+            const int v = idx < 8 ? sc : m;
+            for (int bit = 0; bit < 6; ++bit)
+                if (v & (1 << bit)) out[4 + (6 * idx + bit) / 8] |= (uint8_t)(1u << ((6 * idx + bit) % 8));
+        }
+        for (int j = 0; j < 8; ++j)
+            for (int k = 0; k < 32; ++k) {
+                const uint8_t byte = in[16 + 32 * (j / 2) + k];
+                const int q = (j & 1) ? (byte >> 4) : (byte & 0x0F);
+                out[16 + 16 * j + k / 2] |= (uint8_t)(q << (4 * (k & 1)));
+            }
+    }
+}
+
+/* Symmetric group-wise Q4 of fp32 weights (asdsl/quantization/core.py:358-420
+ * with symmetric=True, bits=4, compute_scale_zero at :63-86), as the
+ * reference requantizes GGUF projections (experiments/phi4_cpu_run.py:1444-1459):
+ * scale = f16(max(amax, 1e-5f) / 7.5), q = clip(rne(w / max(f32(scale),
+ * 1e-4f) + 7.5), 0, 15), packed low nibble first; scales out as f32(scale),
+ * biases as -7.5 * f32(scale). */
+EXPORT void oracle_quantize_q4_symmetric(const float* w, uint8_t* packed, float* scales, float* biases,
+                                         size_t groups, int gs) {
+    for (size_t g = 0; g < groups; ++g) {
+        const float* x = w + g * gs;
+        float amax = 0.0f;
+        for (int i = 0; i < gs; ++i) amax = fabsf(x[i]) > amax ? fabsf(x[i]) : amax;
+        if (amax < 1e-5f) amax = 1e-5f;
+        volatile float scale = amax / 7.5f;
+        double tmp = scale;
+        uint16_t bits;
+        oracle_double_to_half(&tmp, &bits, 1);
+        const float sf = half_to_float(bits);
+        const float denom = sf > 1e-4f ? sf : 1e-4f;
+        for (int i = 0; i < gs; i += 2) {
+            int q[2];
+            for (int e = 0; e < 2; ++e) {
+                volatile float r = x[i + e] / denom;
+                volatile float a = r + 7.5f;
+                float v = nearbyintf(a);
+                v = v < 0.0f ? 0.0f : (v > 15.0f ? 15.0f : v);
+                q[e] = (int)v;
+            }
+            packed[(g * gs + i) / 2] = (uint8_t)(q[0] | (q[1] << 4));
+        }
+        scales[g] = sf;
+        biases[g] = -7.5f * sf;
+    }
+}
+

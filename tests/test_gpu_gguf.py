@@ -1,0 +1,258 @@
+"""HIP parity for the GGUF path: ggml Q4_K / Q6_K decoding, the Q4_K ->
+ASDSL Q4_K rearrangement, the symmetric Q4 requantization (bit for bit
+against the oracle, up to the full Phi-4 projection shapes), the Q4_K GEMV
+on real-layout GGUF blocks, and a GGUF file loaded into the decode engine:
+every operand equal to the oracle pipeline's bytes and greedy steps within
+the decode bars of the oracle's step on them."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import decode as od
+from conftest import rel_l2
+from gguf_writer import ARRAY, FLOAT32, STRING, UINT32, write_gguf
+
+pytestmark = pytest.mark.gpu
+
+
+def _f16_bytes(v) -> np.ndarray:
+    return np.asarray(v, np.float16).view(np.uint8).reshape(-1, 2)
+
+
+def q4k_blocks(n, rng, scale=3e-5) -> np.ndarray:
+    b = rng.integers(0, 256, (n, 144), dtype=np.uint8)
+    b[:, 0:2] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    b[:, 2:4] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    return b.reshape(-1)
+
+
+def q6k_blocks(n, rng, scale=5e-6) -> np.ndarray:
+    b = rng.integers(0, 256, (n, 210), dtype=np.uint8)
+    b[:, 208:210] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    return b.reshape(-1)
+
+
+def _dev(a):
+    from asdsl import _hip
+
+    return _hip.to_device(np.ascontiguousarray(a), a.dtype)
+
+
+def _run(fn, *args):
+    from asdsl import _hip
+
+    _hip.call(fn, *args, _hip.stream_handle())
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (5, 512), (5120, 3072), (3072, 8192)])
+def test_dequant_q4k_bit_exact(gpu, rows, cols):
+    import torch
+
+    rng = np.random.default_rng(rows + cols)
+    n = rows * cols // 256
+    blocks = q4k_blocks(n, rng)
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    _run("asdsl_dequant_gguf_q4k", gpu.ptr(_dev(blocks)), gpu.ptr(out), rows, cols)
+    want = oracle.dequant_gguf_q4k(blocks, n).reshape(rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (7, 768), (3072, 8192), (200064 // 16, 3072)])
+def test_dequant_q6k_bit_exact(gpu, rows, cols):
+    import torch
+
+    rng = np.random.default_rng(rows * 3 + cols)
+    n = rows * cols // 256
+    blocks = q6k_blocks(n, rng)
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    _run("asdsl_dequant_gguf_q6k", gpu.ptr(_dev(blocks)), gpu.ptr(out), rows, cols)
+    want = oracle.dequant_gguf_q6k(blocks, n).reshape(rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_q6k_blocks_at_odd_offsets(gpu):
+    """Q6_K blocks are 210 bytes: a tensor may start 2-byte aligned."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    blocks = q6k_blocks(6, rng)
+    buf = _dev(np.concatenate([np.zeros(2, np.uint8), blocks]))
+    out = torch.empty((2, 768), dtype=torch.float32, device="cuda")
+    _run("asdsl_dequant_gguf_q6k", gpu.ptr(buf) + 2, gpu.ptr(out), 2, 768)
+    assert np.array_equal(out.cpu().numpy().reshape(-1), oracle.dequant_gguf_q6k(blocks, 6))
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 256), (16384, 3072)])
+def test_q4k_to_q4km_bit_exact_and_gemv(gpu, rows, cols):
+    import torch
+
+    rng = np.random.default_rng(rows)
+    n = rows * cols // 256
+    blocks = q4k_blocks(n, rng)
+    out = torch.empty(n * 144, dtype=torch.uint8, device="cuda")
+    _run("asdsl_repack_gguf_q4k_to_q4km", gpu.ptr(_dev(blocks)), gpu.ptr(out), rows, cols)
+    want = oracle.repack_gguf_q4k_to_q4km(blocks, n)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, want)
+    if rows > 3:
+        return
+    # the ASDSL Q4_K GEMV on the rearranged blocks computes ggml's weights
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    _run("asdsl_gemv_q4km_q8", gpu.ptr(out), gpu.ptr(_dev(x)), gpu.ptr(y), rows, cols)
+    xq, xs = oracle.quantize_activation_q4k(x)
+    xd = xq.astype(np.float64) * np.repeat(xs.astype(np.float64), 32)
+    w = oracle.dequant_gguf_q4k(blocks, n).reshape(rows, cols).astype(np.float64)
+    assert rel_l2(y.cpu().numpy(), w @ xd) < 1e-5
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("rows,cols", [(3, 256), (5120, 3072)])
+def test_quantize_q4_symmetric_bit_exact(gpu, gs, rows, cols):
+    import torch
+
+    rng = np.random.default_rng(gs + rows)
+    w = (rng.standard_normal((rows, cols)) * rng.uniform(1e-6, 0.1, (rows, 1))).astype(np.float32)
+    w[0, :gs] = 0.0
+    if rows > 3:
+        w[1, :gs] = ((rng.integers(0, 16, gs) - 7.5) * 0.25).astype(np.float32)  # ties and exact codes
+    groups = rows * cols // gs
+    packed = torch.empty(rows * cols // 2, dtype=torch.uint8, device="cuda")
+    scales = torch.empty(groups, dtype=torch.float32, device="cuda")
+    biases = torch.empty(groups, dtype=torch.float32, device="cuda")
+    _run("asdsl_quantize_q4_symmetric", gpu.ptr(_dev(w)), gpu.ptr(packed), gpu.ptr(scales), gpu.ptr(biases), rows,
+         cols, gs)
+    p, s, b = oracle.quantize_q4_symmetric(w, gs)
+    assert np.array_equal(packed.cpu().numpy(), p)
+    assert np.array_equal(scales.cpu().numpy(), s) and np.array_equal(biases.cpu().numpy(), b)
+
+
+def test_argument_errors(gpu):
+    from asdsl import _hip
+
+    with pytest.raises(ValueError, match="multiple of 256"):
+        _run("asdsl_dequant_gguf_q4k", 16, 16, 2, 100)
+    with pytest.raises(ValueError, match="group_size"):
+        _run("asdsl_quantize_q4_symmetric", 16, 16, 16, 16, 2, 96, 48)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        _run("asdsl_repack_gguf_q4k_to_q4km", 18, 32, 1, 256)
+    assert _hip.last_error()
+
+
+# ------------------------------------------------------------ whole model
+def _write_model(path, cfg, rng, gate_up_split=False):
+    """A Phi-4-shaped GGUF: qkv / o / gate_up Q4_K, down Q6_K, F32 norms,
+    Q6_K token_embd, Q4_K output, phi3 metadata."""
+    H, F, V = cfg.hidden, cfg.ffn, cfg.vocab
+    qkv_rows = cfg.qkv_dim
+    tensors = []
+
+    def add(name, rows, cols, kind):
+        if kind == "q4_k":
+            tensors.append((name, 12, (cols, rows), q4k_blocks(rows * cols // 256, rng)))
+        else:
+            tensors.append((name, 14, (cols, rows), q6k_blocks(rows * cols // 256, rng)))
+
+    for i in range(cfg.n_layers):
+        p = f"blk.{i}."
+        add(p + "attn_qkv.weight", qkv_rows, H, "q4_k")
+        add(p + "attn_output.weight", H, H, "q4_k")
+        if gate_up_split:
+            add(p + "ffn_gate.weight", F, H, "q4_k")
+            add(p + "ffn_up.weight", F, H, "q6_k")
+        else:
+            add(p + "ffn_up.weight", 2 * F, H, "q4_k")
+        add(p + "ffn_down.weight", H, F, "q6_k")
+        for n in ("attn_norm.weight", "ffn_norm.weight"):
+            tensors.append((p + n, 0, (H,), (1 + 0.1 * rng.standard_normal(H)).astype(np.float32).view(np.uint8)))
+    add("token_embd.weight", V, H, "q6_k")
+    tensors.append(("output_norm.weight", 0, (H,), (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+                    .view(np.uint8)))
+    add("output.weight", V, H, "q4_k")
+    meta = [("general.architecture", STRING, "phi3"), ("phi3.embedding_length", UINT32, H),
+            ("phi3.feed_forward_length", UINT32, F), ("phi3.block_count", UINT32, cfg.n_layers),
+            ("phi3.attention.head_count", UINT32, cfg.n_heads),
+            ("phi3.attention.head_count_kv", UINT32, cfg.n_kv_heads),
+            ("phi3.rope.dimension_count", UINT32, cfg.rotary_dim), ("phi3.context_length", UINT32, cfg.max_seq),
+            ("phi3.attention.layer_norm_rms_epsilon", FLOAT32, cfg.rms_eps),
+            ("phi3.rope.freq_base", FLOAT32, cfg.rope_theta),
+            ("tokenizer.ggml.tokens", ARRAY, (STRING, [f"t{i}" for i in range(V)]))]
+    write_gguf(path, tensors, meta)
+    return {name: (tid, raw) for name, tid, _, raw in tensors}
+
+
+def _oracle_preq2(tid, raw, rows, cols, gs):
+    n = rows * cols // 256
+    w = oracle.dequant_gguf_q4k(raw, n) if tid == 12 else oracle.dequant_gguf_q6k(raw, n)
+    p, s, b = oracle.quantize_q4_symmetric(w, gs)
+    return oracle.repack_asym_to_preq2(p, s, b, rows, cols, gs)
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_gguf_model_loads_and_decodes(gpu, tmp_path, split):
+    """2 Phi-4-shaped layers, vocab 4096, from a GGUF file: the config from
+    its metadata; every preq2 operand, norm and the fp16 embedding equal to
+    the oracle pipeline (decode, requantize, repack) bit for bit; three
+    greedy steps from a 100-position random KV prefix within 1e-3 of the
+    oracle's step with the same tokens."""
+    import torch
+
+    from asdsl.engine import DecodeConfig, DecodeEngine, _layer_mats
+
+    cfg0 = DecodeConfig(n_layers=2, vocab=4096, max_seq=512)
+    rng = np.random.default_rng(5 + split)
+    path = tmp_path / "m.gguf"
+    raw = _write_model(path, cfg0, rng, gate_up_split=split)
+    eng = DecodeEngine.from_gguf(path)
+    cfg = eng.cfg
+    assert (cfg.hidden, cfg.ffn, cfg.vocab, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.rotary_dim,
+            cfg.max_seq) == (3072, 8192, 4096, 2, 24, 8, 96, 512)
+
+    host = lambda t: t.cpu().numpy()  # noqa: E731
+    mats = _layer_mats(cfg)
+    names = {"qkv": "attn_qkv.weight", "o": "attn_output.weight", "down": "ffn_down.weight"}
+    layers = []
+    for i, L in enumerate(eng.layers):
+        ol = {}
+        for n, (rows, cols, gs) in mats.items():
+            if n == "gu" and split:
+                g = oracle.dequant_gguf_q4k(raw[f"blk.{i}.ffn_gate.weight"][1], rows // 2 * cols // 256)
+                u = oracle.dequant_gguf_q6k(raw[f"blk.{i}.ffn_up.weight"][1], rows // 2 * cols // 256)
+                p, s, b = oracle.quantize_q4_symmetric(np.concatenate([g, u]), gs)
+                want = oracle.repack_asym_to_preq2(p, s, b, rows, cols, gs)
+            else:
+                tid, r = raw[f"blk.{i}." + names.get(n, "ffn_up.weight")]
+                want = _oracle_preq2(tid, r, rows, cols, gs)
+            got = (host(L[n][0]).reshape(-1), host(L[n][1]).reshape(-1))
+            assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1]), (i, n)
+            ol[n] = want
+        for n, key in (("rms_att", "attn_norm.weight"), ("rms_ffn", "ffn_norm.weight")):
+            ol[n] = raw[f"blk.{i}.{key}"][1].view(np.float32)
+            assert np.array_equal(host(L[n]), ol[n])
+        layers.append(ol)
+    emb = oracle.dequant_gguf_q6k(raw["token_embd.weight"][1], cfg.vocab * cfg.hidden // 256)
+    emb16 = emb.astype(np.float16).reshape(cfg.vocab, cfg.hidden)
+    assert np.array_equal(host(eng.embed), emb16)
+    lm = _oracle_preq2(*raw["output.weight"], cfg.vocab, cfg.hidden, cfg.gs_lm)
+    assert np.array_equal(host(eng.lm_meta).reshape(-1), lm[0]) and np.array_equal(host(eng.lm_quant).reshape(-1), lm[1])
+    rms_out = raw["output_norm.weight"][1].view(np.float32)
+    assert np.array_equal(host(eng.rms_out), rms_out)
+
+    model = {"cfg": cfg, "layers": layers, "embed": emb16, "rms_out": rms_out, "lm_meta": lm[0],
+             "lm_quant": lm[1], "rope_cos": host(eng.rope_cos), "rope_sin": host(eng.rope_sin)}
+    ctx = 100
+    eng.prefill_kv_random(ctx, seed=4)
+    kc = [host(L["k_cache"]) for L in eng.layers]
+    vc = [host(L["v_cache"]) for L in eng.layers]
+    tok = 77
+    eng.token.fill_(tok)
+    for step in range(3):
+        want_logits, want_next = od.decode_step(model, tok, ctx + step, kc, vc)
+        eng._queue_step(int(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert rel_l2(host(eng.logits), want_logits) < 1e-3, step
+        assert eng.next_token() == want_next, step
+        tok = want_next

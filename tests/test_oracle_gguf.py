@@ -1,0 +1,178 @@
+"""The oracle's GGUF restatements on the CPU.
+
+ggml's Q4_K / Q6_K decoders reach the reference through the gguf package
+(asdsl/io/gguf_loader.py:150-181), which is absent here, so they are pinned
+by the layouts' invariants: each 6-bit field and each code moves exactly
+the weights the layout assigns it, with the value the formula gives.  The
+lossless Q4_K -> ASDSL Q4_K rearrangement is checked through the ASDSL GEMV
+(oracle_gemv_q4km, pinned against the reference's compiled kernel): a wrong
+field or nibble in either the decoder or the rearrangement changes the
+product.  The symmetric requantization is pinned by exact groups, ties,
+the floors, and the product package's numpy restatement of the reference's
+quantize_weights."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_l2
+
+
+def _f16(v) -> np.ndarray:
+    return np.frombuffer(np.float16(v).tobytes(), np.uint8)
+
+
+def _q4k_block(d=1.0, dmin=0.0, scales=(0,) * 8, mins=(0,) * 8, codes=None) -> np.ndarray:
+    """A ggml Q4_K block written field by field from the layout: byte j (j <
+    4) = scale j low 6 bits | top 2 bits of scale j+4; byte 4+j the same for
+    the mins; byte 8+j = low 4 bits of scale j+4 | low 4 bits of min j+4 << 4;
+    code l of sub-block j in byte 16 + 32*(j//2) + l, low nibble for even j."""
+    b = np.zeros(144, np.uint8)
+    b[0:2], b[2:4] = _f16(d), _f16(dmin)
+    for j in range(4):
+        b[4 + j] = (scales[j] & 63) | ((scales[j + 4] >> 4) << 6)
+        b[8 + j] = (mins[j] & 63) | ((mins[j + 4] >> 4) << 6)
+        b[12 + j] = (scales[j + 4] & 15) | ((mins[j + 4] & 15) << 4)
+    codes = np.zeros(256, np.int64) if codes is None else np.asarray(codes)
+    for j in range(8):
+        for l in range(32):
+            b[16 + 32 * (j // 2) + l] |= int(codes[32 * j + l]) << (4 * (j & 1))
+    return b
+
+
+@pytest.mark.parametrize("j", range(8))
+def test_q4k_each_scale_field_moves_its_sub_block(j):
+    rng = np.random.default_rng(j)
+    codes = rng.integers(0, 16, 256)
+    sc = [0] * 8
+    sc[j] = 37 + j  # exercises the top bits for j >= 4 (37..44 > 15)
+    w = oracle.dequant_gguf_q4k(_q4k_block(d=0.5, scales=sc, codes=codes), 1)
+    want = np.zeros(256, np.float32)
+    want[32 * j:32 * j + 32] = np.float32(0.5 * sc[j]) * codes[32 * j:32 * j + 32]
+    assert np.array_equal(w, want)
+
+
+@pytest.mark.parametrize("j", range(8))
+def test_q4k_each_min_field_moves_its_sub_block(j):
+    mins = [0] * 8
+    mins[j] = 63 - j
+    w = oracle.dequant_gguf_q4k(_q4k_block(d=2.0, dmin=0.25, mins=mins, codes=np.full(256, 9)), 1)
+    want = np.zeros(256, np.float32)
+    want[32 * j:32 * j + 32] = -np.float32(0.25 * mins[j])
+    assert np.array_equal(w, want)
+
+
+def test_q4k_formula_rounding_and_block_order():
+    """w = f32(d*sc)*q - f32(dmin*m), two fp32 roundings per weight, block b
+    at weights 256b.."""
+    rng = np.random.default_rng(7)
+    blocks, want = [], []
+    for _ in range(3):
+        d, dm = np.float16(rng.uniform(0.001, 0.02)), np.float16(rng.uniform(0.001, 0.02))
+        sc, mn, codes = rng.integers(0, 64, 8), rng.integers(0, 64, 8), rng.integers(0, 16, 256)
+        blocks.append(_q4k_block(float(d), float(dm), sc, mn, codes))
+        d1 = (np.float32(d) * sc.astype(np.float32)).repeat(32)
+        m1 = (np.float32(dm) * mn.astype(np.float32)).repeat(32)
+        want.append(d1 * codes.astype(np.float32) - m1)
+    assert np.array_equal(oracle.dequant_gguf_q4k(np.concatenate(blocks), 3), np.concatenate(want))
+
+
+def _q6k_block(d, scales, codes) -> np.ndarray:
+    """ggml Q6_K from the layout: per half h of 128, code 32k+l (k < 4, l <
+    32) keeps its low 4 bits in byte 64h + l + 32(k&1) (low nibble for k < 2)
+    and its high 2 bits at bits 2k of byte 128 + 32h + l; int8 scale g (per
+    16 weights) at byte 192 + g; fp16 d at 208."""
+    b = np.zeros(210, np.uint8)
+    for h in range(2):
+        for k in range(4):
+            for l in range(32):
+                c = int(codes[128 * h + 32 * k + l])
+                b[64 * h + l + 32 * (k & 1)] |= (c & 15) << (0 if k < 2 else 4)
+                b[128 + 32 * h + l] |= (c >> 4) << (2 * k)
+    b[192:208] = np.asarray(scales, np.int8).view(np.uint8)
+    b[208:210] = _f16(d)
+    return b
+
+
+@pytest.mark.parametrize("g", [0, 3, 5, 10, 15])
+def test_q6k_each_scale_moves_its_16_weights(g):
+    rng = np.random.default_rng(g)
+    codes = rng.integers(0, 64, 256)
+    scales = [0] * 16
+    scales[g] = -77 + g
+    w = oracle.dequant_gguf_q6k(_q6k_block(0.125, scales, codes), 1)
+    # scale g covers 16 weights: half g // 8, quarter (g % 8) // 2, l in 16*(g % 2)..
+    h, k, l0 = g // 8, (g % 8) // 2, 16 * (g % 2)
+    idx = 128 * h + 32 * k + l0 + np.arange(16)
+    want = np.zeros(256, np.float32)
+    want[idx] = np.float32(0.125 * scales[g]) * (codes[idx] - 32).astype(np.float32)
+    assert np.array_equal(w, want)
+
+
+def test_q6k_codes_span_six_bits():
+    codes = np.arange(256) % 64
+    w = oracle.dequant_gguf_q6k(_q6k_block(1.0, [1] * 16, codes), 1)
+    assert np.array_equal(w, (codes - 32).astype(np.float32))
+
+
+def test_q4k_rearrangement_through_the_asdsl_gemv():
+    """ggml Q4_K blocks -> ASDSL Q4_K -> oracle_gemv_q4km equals the ggml
+    decode times the same int8 activation: sum over sub-blocks of xs *
+    (d1 * sum q*xq - m1 * sum xq)."""
+    rng = np.random.default_rng(3)
+    M, K = 6, 512
+    nb = M * K // 256
+    blocks = rng.integers(0, 256, nb * 144).astype(np.uint8)
+    for b in range(nb):  # finite, moderate d and dmin
+        blocks[144 * b:144 * b + 2] = _f16(rng.uniform(0.001, 0.01))
+        blocks[144 * b + 2:144 * b + 4] = _f16(rng.uniform(0.001, 0.01))
+    q4km = oracle.repack_gguf_q4k_to_q4km(blocks, nb)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = oracle.gemv_q4km(q4km, x, M, K)
+    xq, xs = oracle.quantize_activation_q4k(x)
+    xd = xq.astype(np.float64) * np.repeat(xs.astype(np.float64), 32)
+    w = oracle.dequant_gguf_q4k(blocks, nb).reshape(M, K).astype(np.float64)
+    assert rel_l2(y, w @ xd) < 1e-6
+    # the rearrangement is a bijection on the fields: d, dmin kept; every
+    # byte of a block changes something the GEMV reads
+    assert np.array_equal(q4km.reshape(nb, 144)[:, :4], blocks.reshape(nb, 144)[:, :4])
+    y0 = y
+    for byte in (4, 9, 15, 16, 79, 143):
+        mod = blocks.copy()
+        mod[byte] ^= 0x11
+        assert not np.array_equal(oracle.gemv_q4km(oracle.repack_gguf_q4k_to_q4km(mod, nb), x, M, K), y0), byte
+
+
+def test_quantize_q4_symmetric_exact_groups_and_floors():
+    s = 0.25  # exact in fp16: amax = 7.5 * s gives scale s
+    codes = np.array([0, 15, 7, 8, 3, 12, 1, 14] * 4)
+    w = ((codes - 7.5) * s).astype(np.float32)
+    packed, scales, biases = oracle.quantize_q4_symmetric(w, 32)
+    assert scales[0] == np.float32(0.25) and biases[0] == np.float32(-1.875)
+    got = np.stack([packed & 15, packed >> 4], -1).reshape(-1)
+    assert np.array_equal(got, codes)
+    # zero group: amax floored at 1e-5, scale f16(1e-5 / 7.5), divisor
+    # floored at 1e-4, every code rint(7.5) = 8
+    p0, s0, _ = oracle.quantize_q4_symmetric(np.zeros(32, np.float32), 32)
+    assert np.all(p0 == 0x88) and s0[0] == np.float32(np.float16(np.float32(1e-5) / np.float32(7.5)))
+    # ties round half to even: w / s + 7.5 = 5.5 -> 6 and 6.5 -> 6; amax itself -> 15
+    t = np.array([(5.5 - 7.5) * s, (6.5 - 7.5) * s, 7.5 * s] + [0.0] * 29, np.float32)
+    pt, _, _ = oracle.quantize_q4_symmetric(t, 32)
+    q = np.stack([pt & 15, pt >> 4], -1).reshape(-1)
+    assert q[0] == 6 and q[1] == 6 and q[2] == 15
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_quantize_q4_symmetric_matches_the_numpy_restatement(gs):
+    from asdsl.quantization.core import quantize_weights
+
+    rng = np.random.default_rng(gs)
+    w = (rng.standard_normal((48, 256)) * rng.uniform(1e-4, 0.1, (48, 1))).astype(np.float32)
+    w[3] = 0.0
+    packed, scales, biases = oracle.quantize_q4_symmetric(w, gs)
+    qt = quantize_weights(w, bits=4, group_size=gs, symmetric=True)
+    assert np.array_equal(packed, qt.data)
+    assert np.array_equal(scales, qt.scales.astype(np.float32))
+    assert np.array_equal(biases, (-7.5 * qt.scales.astype(np.float32)).astype(np.float32))
