@@ -905,65 +905,71 @@ __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __
     }
 }
 
-// RoPE of column c's query and key heads at position pos + c (grid: heads x
-// columns, one thread per dimension): rotated q (fp32) to Q[c][head], the
-// key and value into the caches at that position as the decode step stores
-// them (fp16, or int8 codes and scales with one wave per 64-dim block).
-// Columns past the cache write nothing.
+// Dim d of a head row src rotated for position `pos` (rope_apply_inplace,
+// unified_engine.cpp:499-540: pairs (i, i + rot_half) for i < rot_half, the
+// rest passed through), fused as fmaf(x_i, c, -x_{i+h} * s).
+__device__ __forceinline__ float rope_dim(const float* __restrict__ src, int d, int pos, int rot_half,
+                                          const float* __restrict__ rope_cos, const float* __restrict__ rope_sin) {
+    if (d >= 2 * rot_half) return src[d];
+    const int i = d < rot_half ? d : d - rot_half;
+    const float xf = src[i], xs = src[i + rot_half];
+    const float cs = rope_cos[static_cast<size_t>(pos) * rot_half + i];
+    const float sn = rope_sin[static_cast<size_t>(pos) * rot_half + i];
+    return d < rot_half ? fmaf(xf, cs, -(xs * sn)) : fmaf(xf, sn, xs * cs);
+}
+
+// set_kv_cache's int8 rule (kv_q8_code) on a 64-dim block held 8 values a
+// lane by the 8 lanes of an aligned group: codes to q[8], the scale returned.
+__device__ __forceinline__ float kv_q8_codes8(const float (&x)[8], int (&q)[8]) {
+    float a = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(x[e]));
+#pragma unroll
+    for (int o = 4; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 8));
+    const float scale = a > 1e-12f ? a * kInv127 : 1e-12f;
+    const float inv = 1.0f / scale;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = static_cast<int>(fminf(fmaxf(__builtin_rintf(x[e] * inv), -127.0f), 127.0f));
+    return scale;
+}
+
+// Dims 8*dc..+8 of a new row (fp32) in kv_load8's form: fp16 bits, or the 8
+// codes and the block scale (the 8 lanes of the 64-dim block call together).
 template <bool Q8>
-__global__ __launch_bounds__(kHeadDim) void verify_rope_kv_kernel(const float* __restrict__ QKV,
-                                                                  float* __restrict__ Q, KvCache kv,
-                                                                  const float* __restrict__ rope_cos,
-                                                                  const float* __restrict__ rope_sin,
-                                                                  const int* __restrict__ pos_ptr, int n_heads,
-                                                                  int n_kv, int max_seq, int rot_half) {
-    const int c = static_cast<int>(blockIdx.y);
-    const int hh = static_cast<int>(blockIdx.x);  // query heads, then key heads
-    const int d = static_cast<int>(threadIdx.x);
-    const int pos = *pos_ptr + c;
-    if (pos < 0 || pos >= max_seq) return;
-    const float* row = QKV + static_cast<size_t>(c) * (n_heads + 2 * n_kv) * kHeadDim;
-    const float* src = row + static_cast<size_t>(hh) * kHeadDim;
-    float val;
-    if (d < 2 * rot_half) {
-        const int i = d < rot_half ? d : d - rot_half;
-        const float xf = src[i], xs = src[i + rot_half];
-        const float cs = rope_cos[static_cast<size_t>(pos) * rot_half + i];
-        const float sn = rope_sin[static_cast<size_t>(pos) * rot_half + i];
-        val = d < rot_half ? fmaf(xf, cs, -(xs * sn)) : fmaf(xf, sn, xs * cs);
-    } else {
-        val = src[d];
-    }
-    if (hh < n_heads) {
-        Q[(static_cast<size_t>(c) * n_heads + hh) * kHeadDim + d] = val;
-    } else {
-        const int kvh = hh - n_heads;
-        const size_t crow = static_cast<size_t>(kvh) * max_seq + pos;
-        const float vv = row[static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim + d];
-        if constexpr (Q8) {
-            float sk, sv;
-            const int qk = kv_q8_code(val, sk);
-            const int qv = kv_q8_code(vv, sv);
-            static_cast<int8_t*>(kv.k)[crow * kHeadDim + d] = static_cast<int8_t>(qk);
-            static_cast<int8_t*>(kv.v)[crow * kHeadDim + d] = static_cast<int8_t>(qv);
-            if ((d & (kWave - 1)) == 0) {
-                kv.ks[crow * 2 + d / kWave] = sk;
-                kv.vs[crow * 2 + d / kWave] = sv;
-            }
-        } else {
-            static_cast<uint16_t*>(kv.k)[crow * kHeadDim + d] = f2h(val);
-            static_cast<uint16_t*>(kv.v)[crow * kHeadDim + d] = f2h(vv);
+__device__ __forceinline__ uint4 kv_pack8(const float (&x)[8]) {
+    if constexpr (Q8) {
+        int q[8];
+        const float scale = kv_q8_codes8(x, q);
+        uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            lo |= (static_cast<uint32_t>(q[e]) & 0xFFu) << (8 * e);
+            hi |= (static_cast<uint32_t>(q[4 + e]) & 0xFFu) << (8 * e);
         }
+        return make_uint4(lo, hi, __float_as_uint(scale), 0u);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = static_cast<uint32_t>(f2h(x[2 * e])) | (static_cast<uint32_t>(f2h(x[2 * e + 1])) << 16);
+        return make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
 // Attention partials of column c (position pos + c) for one KV head and one
-// split, every K/V row from the cache (the pass's own rows are there).
+// split, with RoPE and the pass's own K/V rows done here: the column's G
+// query heads are rotated from its qkv row; rows of positions at or past the
+// pass's first (columns c' <= c) are rebuilt from column c''s qkv row
+// exactly as the cache holds them (rotated key and value, rounded to fp16 or
+// quantized to int8 codes and a scale per 64 dims), older rows come from the
+// cache.  The workgroup whose split holds column c's own position stores
+// that row into the cache; no other workgroup reads it there, so the pass
+// needs no ordering between workgroups.  Columns past the cache do nothing.
 template <int G, bool Q8>
-__global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const float* __restrict__ Q, KvCache kv,
-                                                                           const int* __restrict__ pos_ptr,
-                                                                           float* __restrict__ part, int n_heads,
-                                                                           int max_seq, int nsplit) {
+__global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(
+    const float* __restrict__ QKV, KvCache kv, const float* __restrict__ rope_cos,
+    const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr, float* __restrict__ part, int n_heads,
+    int n_kv, int max_seq, int nsplit, int rot_half) {
     __shared__ float q_s[G][kHeadDim];
     __shared__ float gml[kAttnThreads / 16][G][2];
     __shared__ __align__(16) float gacc[kAttnThreads / 16][G][kHeadDim];
@@ -971,7 +977,8 @@ __global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const
     const int s = static_cast<int>(blockIdx.x);
     const int kvh = static_cast<int>(blockIdx.y);
     const int c = static_cast<int>(blockIdx.z);
-    const int pos = *pos_ptr + c;
+    const int first = *pos_ptr;
+    const int pos = first + c;
     const int p0 = s * kSplit;
     if (p0 > pos || pos < 0 || pos >= max_seq) return;
     const int p1 = min(p0 + kSplit, pos + 1);
@@ -981,21 +988,52 @@ __global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(const
     const int pg = lane >> 4;
     const int dc = lane & 15;
     const size_t row0 = static_cast<size_t>(kvh) * max_seq;
+    const size_t qkv_row = static_cast<size_t>(n_heads + 2 * n_kv) * kHeadDim;
     constexpr int kIt = kSplit / 16;
     uint4 kraw[kIt], vraw[kIt];
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-        const int p = p0 + wave * 4 + pg + 16 * it;
-        if (p < p1) {
+        const int p = p0 + wave * 4 + pg + 16 * it;  // uniform over the 16 lanes of a position
+        if (p < p1 && p < first) {
             kraw[it] = kv_load8<Q8>(kv.k, kv.ks, row0 + p, dc);
             vraw[it] = kv_load8<Q8>(kv.v, kv.vs, row0 + p, dc);
+        } else if (p < p1) {
+            const float* row = QKV + static_cast<size_t>(p - first) * qkv_row;
+            const float* ksrc = row + static_cast<size_t>(n_heads + kvh) * kHeadDim;
+            const float* vsrc = row + static_cast<size_t>(n_heads + n_kv + kvh) * kHeadDim;
+            float k8[8], v8[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                k8[e] = rope_dim(ksrc, 8 * dc + e, p, rot_half, rope_cos, rope_sin);
+                v8[e] = vsrc[8 * dc + e];
+            }
+            kraw[it] = kv_pack8<Q8>(k8);
+            vraw[it] = kv_pack8<Q8>(v8);
+            if (p == pos) {  // this column's own row: into the cache
+                const size_t crow = row0 + p;
+                if constexpr (Q8) {
+                    *reinterpret_cast<uint2*>(static_cast<int8_t*>(kv.k) + crow * kHeadDim + 8 * dc) =
+                        make_uint2(kraw[it].x, kraw[it].y);
+                    *reinterpret_cast<uint2*>(static_cast<int8_t*>(kv.v) + crow * kHeadDim + 8 * dc) =
+                        make_uint2(vraw[it].x, vraw[it].y);
+                    if ((dc & 7) == 0) {
+                        kv.ks[crow * 2 + (dc >> 3)] = __uint_as_float(kraw[it].z);
+                        kv.vs[crow * 2 + (dc >> 3)] = __uint_as_float(vraw[it].z);
+                    }
+                } else {
+                    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(kv.k) + crow * kHeadDim + 8 * dc) = kraw[it];
+                    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(kv.v) + crow * kHeadDim + 8 * dc) = vraw[it];
+                }
+            }
         } else {
             kraw[it] = make_uint4(0u, 0u, 0u, 0u);
             vraw[it] = kraw[it];
         }
     }
-    const float* qsrc = Q + (static_cast<size_t>(c) * n_heads + kvh * G) * kHeadDim;
-    for (int e = tid; e < G * kHeadDim; e += kAttnThreads) q_s[e / kHeadDim][e % kHeadDim] = qsrc[e];
+    const float* qsrc = QKV + static_cast<size_t>(c) * qkv_row + static_cast<size_t>(kvh * G) * kHeadDim;
+    for (int e = tid; e < G * kHeadDim; e += kAttnThreads)
+        q_s[e / kHeadDim][e % kHeadDim] = rope_dim(qsrc + (e / kHeadDim) * kHeadDim, e % kHeadDim, pos, rot_half,
+                                                   rope_cos, rope_sin);
     __syncthreads();
     float qr[G][8];
 #pragma unroll
@@ -1116,7 +1154,7 @@ struct VerifyAttnK {
 
 // Work buffer layout of a verify pass of up to n tokens (offsets in floats).
 struct VerifyWork {
-    size_t H, X, QKV, Q, part, att, O, GU, S, keys, mimg, mimg_bytes, total;
+    size_t H, X, QKV, part, att, O, GU, S, keys, mimg, mimg_bytes, total;
 };
 
 VerifyWork verify_work(const asdsl_decode_model& m, int n) {
@@ -1132,7 +1170,6 @@ VerifyWork verify_work(const asdsl_decode_model& m, int n) {
     w.H = take(N * m.hidden);
     w.X = take(N * (m.hidden > m.ffn ? m.hidden : m.ffn));
     w.QKV = take(N * qkv_dim);
-    w.Q = take(N * m.n_heads * m.head_dim);
     w.part = take(N * m.n_heads * attn_splits(m.max_seq) * kPartStride);
     w.att = take(N * m.n_heads * m.head_dim);
     w.O = take(N * m.hidden);
@@ -1346,7 +1383,6 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     float* H = base + w.H;
     float* X = base + w.X;
     float* QKV = base + w.QKV;
-    float* Q = base + w.Q;
     float* part = base + w.part;
     float* att = base + w.att;
     float* O = base + w.O;
@@ -1401,14 +1437,11 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         st = norm_then_gemv(pending, L.rms_att, L.qkv_meta, L.qkv_quant, QKV, qkv_dim, m.gs_attn);
         if (st != ASDSL_OK) return st;
         const KvCache kv{L.k_cache, L.v_cache, L.k_scale, L.v_scale};
-        st = launch("verify_rope_kv_kernel", q8 ? verify_rope_kv_kernel<true> : verify_rope_kv_kernel<false>,
-                    dim3(m.n_heads + m.n_kv_heads, n), dim3(kHeadDim), 0, s, static_cast<const float*>(QKV), Q, kv,
-                    m.rope_cos, m.rope_sin, pos, m.n_heads, m.n_kv_heads, m.max_seq, m.rotary_dim / 2);
-        if (st != ASDSL_OK) return st;
         const dim3 pgrid(nsplit, m.n_kv_heads, n);
         st = with_attn_kernel<VerifyAttnK>(G, q8, [&](auto kern) {
             return launch("verify_attn_partial_kernel", kern, pgrid, dim3(kAttnThreads), 0, s,
-                          static_cast<const float*>(Q), kv, pos, part, m.n_heads, m.max_seq, nsplit);
+                          static_cast<const float*>(QKV), kv, m.rope_cos, m.rope_sin, pos, part, m.n_heads,
+                          m.n_kv_heads, m.max_seq, nsplit, m.rotary_dim / 2);
         });
         if (st != ASDSL_OK) return st;
         if (preq2_batch_image_applies(L.o_meta, L.o_quant, m.hidden, q_dim, m.gs_attn, n, mfma)) {
