@@ -22,7 +22,7 @@
 // for K=8192 reads more bytes than the workgroup's own weights when
 // workgroups are small; KS grows only while fewer than CUs/2 workgroups would
 // be launched.  o_proj 3072x3072 3.0 us (KS=2), gate_up 16384x3072 6.9 us
-// (KS=1), down 3072x8192 5.4 us (KS=4, 16 waves).
+// (KS=1), down 3072x8192 5.1 us (KS=4, 12 waves).
 //
 // The activation loads are issued before the weight loads (vmcnt retires in
 // order) and quantized while the weights are in flight; the next tile's loads
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     constexpr int kTl = PRO == Pro::kCombine                 ? 0
                         : SWIGLU_EPI                         ? 1
                         : (PRO == Pro::kNorm && !ARGMAX)     ? 2
-                        : (PRO == Pro::kPlain && !Q8)        ? (WAVES == 16 ? 3 : 7)
+                        : (PRO == Pro::kPlain && !Q8)        ? (WAVES > 8 ? 3 : 7)
                                                              : -1;
     const int tl_wg = static_cast<int>(blockIdx.x);
     ASDSL_TIMELINE_STAMP(kTl, tl_wg, 0);
@@ -279,7 +279,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     // slowest wave (down 3072x8192: 5.55 -> 5.24 us; at 8 waves it measured
     // ~1 % slower, so it is not done there).  The barrier waits on nothing
     // outstanding.
-    if constexpr (WAVES == 16) __syncthreads();
+    if constexpr (WAVES > 8) __syncthreads();
     load_tile(tile);           // grid <= ntiles, so this tile exists
     // kNorm: 1/rms is one positive factor of the whole input, so the int8
     // codes of (h * inv_rms) * nw are those of h * nw (each group's scale is
@@ -540,7 +540,8 @@ int check_preq2_args(const void* meta, const void* quant, const void* x, const v
 }
 
 // Launch plan.  waves: 8 per workgroup, 16 when K > 4096 (the activation is
-// then 32+ KB of fp32 per workgroup).  KS: the smallest power of two that
+// then 32+ KB of fp32 per workgroup), 12 where that fills the compute units
+// better (below).  KS: the smallest power of two that
 // leaves each lane at most 6 units (loads) per band; then doubled, while it
 // splits the band evenly, as long as fewer than CUs/2 workgroups would run.
 // ASDSL_HIP_KSPLIT forces KS (a power of two <= 8; raised where the forced
@@ -570,6 +571,13 @@ Plan plan_preq2(int M, int K, int cus) {
         while (p.lks < 3 && nu_of(p.lks) > 6) ++p.lks;
         while (p.lks < 3 && tiles_of(p.lks) < cus / 2 && upb % (kWave << (p.lks + 1)) == 0) ++p.lks;
     }
+    // K > 4096 at KS = 4: 12 waves (3 bands a tile) instead of 16 when that
+    // fills every compute unit with one workgroup where 16 would leave a
+    // quarter idle (down 3072x8192: 256 instead of 192 workgroups, 5.28 ->
+    // 5.11 us)
+    const int nb3 = nbands / 3;
+    if (forced == 0 && p.waves == 16 && p.lks == 2 && nbands % 3 == 0 && nbands / 4 < cus && nb3 <= cus)
+        p.waves = 12;
     p.nu = nu_of(p.lks);
     p.exact = p.nu * (kWave << p.lks) == upb;
     const int cap = cus * (32 / p.waves);  // at most 32 waves per compute unit
@@ -652,6 +660,10 @@ asdsl_status launch_preq2_fused(const uint8_t* meta, const uint8_t* quant, const
     const auto* m = reinterpret_cast<const uint32_t*>(meta);
     const auto* q = reinterpret_cast<const uint4*>(quant);
     if (p.waves == 8) return launch_waves<GS, 8, 1, false, PRO, ARGMAX>(p, m, q, x, nullptr, nullptr, y, M, K, stream, pa);
+    if constexpr (PRO != Pro::kCombine) {  // kCombine stages one chunk per thread
+        if (p.waves == 12)
+            return launch_waves<GS, 12, 2, false, PRO, ARGMAX>(p, m, q, x, nullptr, nullptr, y, M, K, stream, pa);
+    }
     return launch_waves<GS, 16, 1, false, PRO, ARGMAX>(p, m, q, x, nullptr, nullptr, y, M, K, stream, pa);
 }
 
@@ -663,6 +675,7 @@ asdsl_status launch_preq2(const uint8_t* meta, const uint8_t* quant, const float
     const auto* q = reinterpret_cast<const uint4*>(quant);
     // one 8-element activation chunk per thread and pass: NCH = ceil(K / (8 * threads))
     if (p.waves == 8) return launch_waves<GS, 8, 1, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);
+    if (p.waves == 12) return launch_waves<GS, 12, 2, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);
     if (K <= 8192) return launch_waves<GS, 16, 1, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);
     if (K <= 16384) return launch_waves<GS, 16, 2, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);
     return launch_waves<GS, 16, 3, Q8>(p, m, q, x, xq8, xsc, y, M, K, stream);

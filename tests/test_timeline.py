@@ -67,7 +67,7 @@ def test_timeline_orders_the_layer_kernels():
                 if name.endswith("_us") and isinstance(v, list):
                     assert 0.0 <= v[0] <= v[1], (k["kernel"], name, v)
     wgs = {k["kernel"]: k["workgroups"] for k in short["kernels"]}
-    assert wgs["qkv (norm)"] == 160 and wgs["gate_up (SwiGLU)"] == 256 and wgs["down"] == 192
+    assert wgs["qkv (norm)"] == 160 and wgs["gate_up (SwiGLU)"] == 256 and wgs["down"] == 256
     assert wgs["attention"] == 2 * 8  # position 108: two splits of 64, eight KV heads
     wgs = {k["kernel"]: k["workgroups"] for k in long_["kernels"]}
     assert wgs["attention"] == 10 * 8 and wgs["attention combine"] == 24  # position 608: ten splits
