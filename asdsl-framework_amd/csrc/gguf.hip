@@ -125,19 +125,20 @@ __global__ __launch_bounds__(kGgufThreads) void dequant_q6k_kernel(const uint8_t
 // ggml Q4_K -> ASDSL Q4_K variant (asdsl/kernels/native/gemv_q4_avx2.cpp:78-120,
 // 283-420: fp16 d | fp16 dmin | sixteen 6-bit entries LSB-first, scales then
 // mins | sub-block j's 32 nibbles in bytes 16+16j.., low nibble first).
-// Lossless: the same d, dmin, 6-bit scales, mins and 4-bit codes.  16 lanes
-// per block: lanes 0-7 write sub-block j's 16 nibble bytes, lane 8 the
-// 16-byte head; one 16-byte store each.
+// Lossless: the same d, dmin, 6-bit scales, mins and 4-bit codes.  One
+// thread per 16-byte piece of the output (9 a block: piece j < 8 is
+// sub-block j's codes, piece 8 the head), so consecutive threads store
+// consecutive bytes.
 __global__ __launch_bounds__(kGgufThreads) void q4k_to_q4km_kernel(const uint8_t* __restrict__ src,
                                                                    uint8_t* __restrict__ dst, size_t n_blocks) {
     const size_t t = static_cast<size_t>(blockIdx.x) * kGgufThreads + threadIdx.x;
-    const size_t b = t / 16;
-    const int lane = static_cast<int>(t % 16);
-    if (b >= n_blocks || lane > 8) return;
+    const size_t b = t / 9;
+    const int piece = static_cast<int>(t % 9);
+    if (b >= n_blocks) return;
     const uint8_t* blk = src + b * kQ4kBytes;
     uint8_t* out = dst + b * kQ4kBytes;
-    if (lane < 8) {
-        const int j = lane;
+    if (piece < 8) {
+        const int j = piece;
         const uint4* chunk = reinterpret_cast<const uint4*>(blk + 16 + 32 * (j / 2));
         const uint4 a = chunk[0], c = chunk[1];
         const uint32_t in[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
@@ -252,7 +253,7 @@ extern "C" asdsl_status asdsl_repack_gguf_q4k_to_q4km(const uint8_t* gguf_blocks
     ASDSL_CHECK_ARG(aligned(gguf_blocks, 16) && aligned(q4km_blocks, 16),
                     "repack_gguf_q4k_to_q4km: both block arrays must be 16-byte aligned");
     const size_t n = static_cast<size_t>(rows) * (cols / 256);
-    return launch("q4k_to_q4km_kernel", q4k_to_q4km_kernel, dim3(grid_for(n * 16)), dim3(kGgufThreads), 0,
+    return launch("q4k_to_q4km_kernel", q4k_to_q4km_kernel, dim3(grid_for(n * 9)), dim3(kGgufThreads), 0,
                   as_hip(stream), gguf_blocks, q4km_blocks, n);
 }
 
