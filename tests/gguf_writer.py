@@ -1,4 +1,4 @@
-"""A minimal GGUF (version 3) writer for test fixtures: typed metadata and
+"""A minimal GGUF (version 3, or 2: the same layout) writer for test fixtures: typed metadata and
 tensors given as raw bytes, laid out as the format defines it (magic,
 version, tensor and key/value counts, metadata, tensor infos with offsets
 relative to the data section, the data section aligned to
@@ -31,14 +31,14 @@ def _value(vtype: int, v) -> bytes:
     return struct.pack(_FMT[vtype], v)
 
 
-def write_gguf(path, tensors: list, metadata: list | None = None, alignment: int = 32) -> None:
+def write_gguf(path, tensors: list, metadata: list | None = None, alignment: int = 32, version: int = 3) -> None:
     """tensors: [(name, ggml type id, dims (ne0 first), raw bytes)];
     metadata: [(key, value type, value)] (ARRAY values as (element type,
     items)).  A ``general.alignment`` entry is added when alignment != 32."""
     meta = list(metadata or [])
     if alignment != 32:
         meta.append(("general.alignment", UINT32, alignment))
-    head = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(meta))
+    head = b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(meta))
     head += b"".join(_string(k) + struct.pack("<I", t) + _value(t, v) for k, t, v in meta)
     offset, infos, blobs = 0, b"", []
     for name, type_id, dims, raw in tensors:

@@ -130,3 +130,17 @@ def test_no_cpu_decode_of_k_quants(tmp_path):
     info = {"type": "q4_k", "shape": (256, 1), "logical_shape": (1, 256), "data": np.zeros(144, np.uint8)}
     with pytest.raises(Exception):
         gl.dequant_tensor(info)
+
+
+def test_version_2_reads_like_version_3(tmp_path):
+    """Versions 2 and 3 share the layout (64-bit counts and lengths); 3
+    only adds big-endian files, which the reader does not take."""
+    raw = np.arange(32, dtype=np.float32)
+    for version in (2, 3):
+        path = tmp_path / f"v{version}.gguf"
+        write_gguf(path, [("t", 0, (8, 4), raw.view(np.uint8))], [("k", STRING, "v")], version=version)
+        f = gl.GGUFFile(path)
+        assert f.version == version and f.metadata == {"k": "v"}
+        t = gl.read_gguf_tensors(path)["t"]
+        assert t["logical_shape"] == (4, 8)
+        assert np.array_equal(gl.dequant_tensor(t), raw.reshape(4, 8))
