@@ -153,17 +153,20 @@ def test_graph_replay_matches_eager_steps(gpu):
     assert np.array_equal(ka, kb) and np.array_equal(sa, sb)
 
 
-def test_verify_matches_serial_oracle(gpu):
-    """Four tokens through the multi-token pass over an int8 cache: every
-    column has the oracle's greedy token, logits within 1e-3 in three
-    columns of four and all within 5e-2 (the fp16 cache's verify bar), and
-    the codes written for the four positions as the decode step's."""
+@pytest.mark.parametrize("n", [4, 9])
+def test_verify_matches_serial_oracle(gpu, n):
+    """n tokens through the multi-token pass over an int8 cache (124 + 9
+    crosses the 128-position split boundary, so two splits rebuild the
+    pass's rows): every column has the oracle's greedy token, logits within
+    1e-3 in three columns of four and all within 5e-2 (the fp16 cache's
+    verify bar), and the codes written for the n positions as the decode
+    step's."""
     eng = _engine(n_layers=1, max_seq=512, seed=5)
     ctx = 124
     eng.prefill_kv_random(ctx, seed=3)
     model = od.host_model(eng)
     kc, vc = _caches(eng)
-    toks = [int(t) for t in np.random.default_rng(4).integers(0, eng.cfg.vocab, 4)]
+    toks = [int(t) for t in np.random.default_rng(4).integers(0, eng.cfg.vocab, n)]
     logits = _host(eng.forward_batch_all_logits(toks, ctx))
     nxt = eng.verify_next_tokens()
     errs = []
@@ -173,8 +176,8 @@ def test_verify_matches_serial_oracle(gpu):
         assert nxt[c] == want_next, c
     errs = np.asarray(errs)
     assert np.all(errs < 5e-2) and np.mean(errs < 1e-3) >= 0.75, errs
-    got = _host(eng.layers[0]["k_cache"][:, ctx:ctx + 4]).astype(np.int32)
-    diff = np.abs(got - kc[0][0][:, ctx:ctx + 4].astype(np.int32))
+    got = _host(eng.layers[0]["k_cache"][:, ctx:ctx + n]).astype(np.int32)
+    diff = np.abs(got - kc[0][0][:, ctx:ctx + n].astype(np.int32))
     assert diff.max() <= 1 and np.mean(diff == 0) >= 0.99
 
 
