@@ -336,14 +336,15 @@ class DecodeEngine:
                   **overrides) -> "DecodeEngine":
         """A model from a GGUF file (its configuration from the file's
         metadata unless cfg is given; overrides such as max_seq, gs_ffn or
-        kv_format apply to it).  The reference loads GGUF projections the
+        kv_format apply to either).  The reference loads GGUF projections the
         same way (experiments/phi4_cpu_run.py:1316-1466: K-quant decode,
         symmetric Q4 requantization) but keeps the embeddings and norms of
         its HF checkpoint; here they come from the file too."""
+        from dataclasses import replace
+
         from asdsl.io.gguf_loader import GGUFFile, read_gguf_tensors
 
-        if cfg is None:
-            cfg = config_from_gguf(GGUFFile(path).metadata, **overrides)
+        cfg = config_from_gguf(GGUFFile(path).metadata, **overrides) if cfg is None else replace(cfg, **overrides)
         layers, rest = layers_from_gguf(cfg, read_gguf_tensors(path))
         return cls(cfg, layers, rest["embed"], rest["rms_out"], rest["lm_meta"], rest["lm_quant"],
                    fatrelu_threshold)
