@@ -118,3 +118,28 @@ def test_library_imported_before_torch(gpu):
     res = subprocess.run([sys.executable, "-c", _LOAD_ORDER.format(pkg=str(REPO / "asdsl-framework_amd"))],
                          capture_output=True, text=True, timeout=300)
     assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stderr[-2000:]
+
+
+@pytest.mark.gpu
+def test_explicit_launch_events_while_recording_are_reported(gpu, monkeypatch):
+    """A launch that takes the pair armed by asdsl_profile_next_launch is
+    not recorded by the stage recorder; end says so instead of returning a
+    partial profile, and the explicit events still time that launch."""
+    import torch
+
+    eng = _engine(50, monkeypatch, token=0)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()  # torch creates the HIP events at their first record
+    stop.record()
+    torch.cuda.synchronize()
+    assert start.cuda_event and stop.cuda_event
+
+    def run():
+        _hip.check(_hip.LIB.asdsl_profile_next_launch(ctypes.c_void_p(start.cuda_event),
+                                                      ctypes.c_void_p(stop.cuda_event)), "next_launch")
+        eng._queue_step(_hip.stream_handle(), 256)
+
+    with pytest.raises(ValueError, match="asdsl_profile_next_launch"):
+        _hip.profile_stages(run, max_launches=64)
+    torch.cuda.synchronize()
+    assert start.elapsed_time(stop) > 0.0
