@@ -145,6 +145,38 @@ def argmax_first(x: np.ndarray) -> int:
     return int(np.argmax(x))
 
 
+def quantize_lm_head_q4_128(w: np.ndarray) -> np.ndarray:
+    """The engine's load-time Q4_128 quantization of the output projection
+    (UnifiedEngine constructor, unified_engine.cpp:413-461, lm_head_group_size
+    128) on float32 rows [rows][cols] (cols a multiple of 128), as built with
+    -ffast-math: per 128-group amax; amax < 1e-12 -> scale 0 and nibbles 0x88;
+    else scale = amax * f32(1/7) (the constant division becomes a reciprocal
+    multiply) stored as fp16 (round to nearest even), inv = 7.0f / amax (a
+    true float32 division), q = round-half-away(x * inv) + 8 clamped to
+    [0, 15] (std::round).  Differs from repack_q4_128.py's quantizer in the
+    rounding of ties (half away, not half even) and in forming the scale in
+    float32.  Returns flat 66-byte blocks (uint8)."""
+    x = np.ascontiguousarray(w, F32)
+    rows, cols = x.shape
+    g = x.reshape(rows * (cols // 128), 128)
+    amax = np.abs(g).max(axis=1)
+    tiny = amax < F32(1e-12)
+    safe = np.where(tiny, F32(1.0), amax).astype(F32)
+    scale = (safe * F32(1.0 / 7.0)).astype(F32)
+    inv = (F32(7.0) / safe).astype(F32)
+    v = (g * inv[:, None]).astype(F32)
+    t = np.trunc(v)
+    r = t + np.where(np.abs(v - t) >= F32(0.5), np.sign(v), F32(0.0))  # half away from zero, exact in float32
+    q = np.clip(r + F32(8.0), 0, 15).astype(np.uint8)
+    q[tiny] = 8
+    s16 = np.where(tiny, F32(0.0), scale).astype(np.float16).view(np.uint16)
+    blocks = np.empty((g.shape[0], 66), np.uint8)
+    blocks[:, 0] = (s16 & 0xFF).astype(np.uint8)
+    blocks[:, 1] = (s16 >> 8).astype(np.uint8)
+    blocks[:, 2:] = q[:, 0::2] | (q[:, 1::2] << 4)
+    return blocks.reshape(-1)
+
+
 def layer_forward(model: dict, li: int, h: np.ndarray, pos: int, k_cache: list, v_cache: list,
                   trace: dict | None = None, gemv=None) -> np.ndarray:
     """Decoder layer li at position pos on the residual stream h (float32
@@ -194,14 +226,16 @@ def lm_head_forward(model: dict, h: np.ndarray, gemv=None) -> np.ndarray:
 
 
 def decode_step(model: dict, token: int, pos: int, k_cache: list, v_cache: list, trace: list | None = None,
-                gemv=None) -> tuple[np.ndarray, int]:
+                gemv=None, lm_head: bool = True) -> tuple[np.ndarray, int]:
     """One greedy step.  model: host copies of the engine's weights
     (host_model); k_cache/v_cache: per layer either an fp16 array
     [n_kv][max_seq][128] or, for the int8 cache, a pair (int8
     [n_kv][max_seq][128], float32 scales [n_kv][max_seq][2]); updated at
     `pos` in place.  trace (a list), when given, receives per layer a dict
     with the layer's input stream "h" and the values layer_forward traces,
-    then {"h": final stream}.  gemv replaces oracle.gemv_preq2_fused."""
+    then {"h": final stream}.  gemv replaces oracle.gemv_preq2_fused.
+    lm_head=False stops after the layers (the K/V rows written, no logits:
+    the reference's forward_token_prefill) and returns (None, None)."""
     h = model["embed"][token].astype(F32)
     for li in range(len(model["layers"])):
         t = {"h": h} if trace is not None else None
@@ -210,6 +244,8 @@ def decode_step(model: dict, token: int, pos: int, k_cache: list, v_cache: list,
             trace.append(t)
     if trace is not None:
         trace.append({"h": h})
+    if not lm_head:
+        return None, None
     logits = lm_head_forward(model, h, gemv)
     return logits, argmax_first(logits)
 
