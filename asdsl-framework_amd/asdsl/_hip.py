@@ -34,14 +34,18 @@ SIGNATURES: dict[str, list] = {
     "asdsl_abi_version": [],
     "asdsl_last_error": [],
     "asdsl_device_cu_count": [],
+    "asdsl_reserve_workspace": [ctypes.c_size_t],
     "asdsl_profile_next_launch": [_P, _P],
     "asdsl_dequant_gguf_q4k": [_P, _P, _I, _I, _P],
     "asdsl_dequant_gguf_q6k": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q5k": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q8_0": [_P, _P, _I, _I, _P],
     "asdsl_repack_gguf_q4k_to_q4km": [_P, _P, _I, _I, _P],
     "asdsl_quantize_q4_symmetric": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_profile_stages_begin": [_I],
     "asdsl_profile_stages_end": [_I, _P, _P, _P, _P],
     "asdsl_stream_read": [_P, ctypes.c_size_t, _P, _I, _P],
+    "asdsl_stream_read_ex": [_P, ctypes.c_size_t, _P, _I, _I, _I, _I, _P],
     "asdsl_grid_sync_probe_work_bytes": [_I],
     "asdsl_grid_sync_probe": [_I, _I, _I, _P, ctypes.c_size_t, _I, _P],
     "asdsl_quantize_activation": [_P, _P, _P, _I, _I, _P],
@@ -84,6 +88,7 @@ SIGNATURES: dict[str, list] = {
     "asdsl_attention_f16kv": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "asdsl_attention_q8kv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "asdsl_decode_work_bytes": [_P],
+    "asdsl_decode_flags_offset": [_P],
     "asdsl_decode_token": [_P, _P, _P, _P, _P, _P],
     "asdsl_decode_token_upto": [_P, _P, _P, _I, _P, _P, _P],
     "asdsl_decode_verify_work_bytes": [_P, _I],
@@ -99,6 +104,7 @@ SIGNATURES: dict[str, list] = {
 }
 _RESTYPE = {"asdsl_last_error": ctypes.c_char_p, "asdsl_attention_work_floats": ctypes.c_size_t,
             "asdsl_decode_work_bytes": ctypes.c_size_t, "asdsl_decode_verify_work_bytes": ctypes.c_size_t,
+            "asdsl_decode_flags_offset": ctypes.c_size_t,
             "asdsl_sparse_down_work_bytes": ctypes.c_size_t, "asdsl_grid_sync_probe_work_bytes": ctypes.c_size_t,
             "asdsl_gemv_preq2_fused_batch_work_bytes": ctypes.c_size_t,
             "asdsl_affine_batch_work_bytes": ctypes.c_size_t}

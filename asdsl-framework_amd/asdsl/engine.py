@@ -121,13 +121,20 @@ def layers_from_preq_blocks(cfg: "DecodeConfig", blocks: dict, norms: list) -> l
     return layers
 
 
+GGUF_DEFAULT_MAX_SEQ = 4096  # KV positions a GGUF model gets unless max_seq is given
+
+
 def config_from_gguf(metadata: dict, **overrides) -> DecodeConfig:
     """DecodeConfig from a GGUF file's metadata (``{arch}.embedding_length``,
     ``.feed_forward_length``, ``.block_count``, ``.attention.head_count``,
     ``.attention.head_count_kv``, ``.rope.dimension_count``,
     ``.context_length``, ``.attention.layer_norm_rms_epsilon``,
     ``.rope.freq_base``, with arch = ``general.architecture``); the
-    vocabulary from the token list.  Keyword overrides win."""
+    vocabulary from the token list.  The KV cache holds
+    min(context_length, GGUF_DEFAULT_MAX_SEQ = 4096) positions unless the
+    caller passes max_seq: a file's trained context (131072 for Phi-4-mini)
+    would otherwise allocate ~17 GB of fp16 cache and RoPE tables of that
+    many rows.  Keyword overrides win."""
     arch = metadata.get("general.architecture", "phi3")
 
     def get(key, default=None):
@@ -141,7 +148,7 @@ def config_from_gguf(metadata: dict, **overrides) -> DecodeConfig:
     fields = dict(hidden=hidden, ffn=int(get("feed_forward_length")), n_layers=int(get("block_count")),
                   n_heads=n_heads, n_kv_heads=int(get("attention.head_count_kv", n_heads)),
                   head_dim=hidden // n_heads, rotary_dim=int(get("rope.dimension_count", hidden // n_heads)),
-                  max_seq=int(get("context_length")),
+                  max_seq=min(int(get("context_length")), GGUF_DEFAULT_MAX_SEQ),
                   rms_eps=float(get("attention.layer_norm_rms_epsilon", 1e-5)),
                   rope_theta=float(get("rope.freq_base", 10000.0)))
     if tokens is not None:
@@ -152,7 +159,7 @@ def config_from_gguf(metadata: dict, **overrides) -> DecodeConfig:
 
 def _gguf_projection(info: dict, rows: int, cols: int, gs: int, what: str):
     """One GGUF weight -> preq2 (meta, quant) on the device: decoded to fp32
-    (asdsl_dequant_gguf_q4k / _q6k), requantized to symmetric Q4 at group
+    (asdsl_dequant_gguf_q4k / _q5k / _q6k / _q8_0), requantized to symmetric Q4 at group
     size gs (asdsl_quantize_q4_symmetric, the reference's load_from_gguf
     rule, experiments/phi4_cpu_run.py:1437-1466) and packed as preq2
     (asdsl_repack_asym_to_preq2, zero 7.5: the requantized weights exactly)."""
@@ -180,8 +187,9 @@ def layers_from_gguf(cfg: DecodeConfig, tensors: dict) -> tuple[list[dict], dict
 
     Per layer ``blk.{i}.``: attn_qkv, attn_output, the gate and up rows
     (ffn_gate_up, or ffn_up holding both as in Phi-3/4 conversions, or
-    ffn_gate + ffn_up stacked), ffn_down -- Q4_K or Q6_K, decoded and
-    requantized on the GPU (_gguf_projection) -- and attn_norm / ffn_norm.
+    ffn_gate + ffn_up stacked), ffn_down -- Q4_K, Q5_K, Q6_K, Q8_0 or a
+    float type, decoded and requantized on the GPU (_gguf_projection) -- and
+    attn_norm / ffn_norm.
     Model-wide: token_embd (decoded, stored fp16), output_norm, and output
     (the embedding when absent: tied weights) as the lm_head at cfg.gs_lm.
     Returns (layers, {"embed", "rms_out", "lm_meta", "lm_quant"})."""
@@ -282,7 +290,10 @@ class DecodeEngine:
         nbytes = _hip.LIB.asdsl_decode_work_bytes(ctypes.byref(m))
         if nbytes == 0:
             raise ValueError(f"invalid decode model: {_hip.last_error()}")
-        self.work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        # zeroed: the step's flags word lives in it (asdsl_decode_flags_offset)
+        self.work = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        off = _hip.LIB.asdsl_decode_flags_offset(ctypes.byref(m))
+        self._flags = self.work[off:off + 4].view(torch.int32)
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.logits = torch.empty(cfg.vocab, dtype=torch.float32, device=dev)
@@ -417,8 +428,39 @@ class DecodeEngine:
         self.kv_seq_len = max(self.kv_seq_len, pos + 1)
         return self.logits
 
+    # bits of the step's device flags word (include/asdsl_hip.h)
+    FLAG_POS_LIMIT, FLAG_POS_RANGE = 1, 2
+
+    def device_flags(self) -> int:
+        """The flags the steps raised on the device since they were last
+        cleared (0: none); reading waits for the queued steps."""
+        return int(self._flags.item())
+
+    def check_device_flags(self) -> None:
+        """Raise RuntimeError (and clear the word) if a step ran at a
+        position its launch did not cover: a captured graph replayed at or
+        past the position range it was shaped for (FLAG_POS_LIMIT), or a
+        position outside the KV cache (FLAG_POS_RANGE).  Such a step computed
+        zero attention and wrote no K/V row, so its logits and token are not
+        the model's.  Called at the engine's sync points (next_token,
+        capture)."""
+        f = self.device_flags()
+        if f:
+            self._flags.zero_()
+            why = []
+            if f & self.FLAG_POS_LIMIT:
+                why.append("a step ran at a position past the range its graph was captured for")
+            if f & self.FLAG_POS_RANGE:
+                why.append("a step ran at a position outside the KV cache")
+            raise RuntimeError("decode step: " + "; ".join(why) + f" (device flags 0x{f:x})")
+
     def next_token(self) -> int:
-        return int(self.token.item())
+        import torch
+
+        tok, flags = torch.stack((self.token[0], self._flags[0])).tolist()  # one device read
+        if flags:
+            self.check_device_flags()
+        return int(tok)
 
     def capture(self) -> None:
         """HIP graph of one step (token and position advance on the device)
@@ -426,6 +468,7 @@ class DecodeEngine:
         host's copy of the position is read back from the device here."""
         import torch
 
+        self.check_device_flags()
         self._host_pos = int(self.pos.item())
         limit = self._pos_limit(self._host_pos)
         side = torch.cuda.Stream()

@@ -10,8 +10,9 @@ typed key/value metadata, tensor infos, a data section aligned to
 ``general.alignment``, default 32).  Tensor payloads are views of the map,
 never copies.
 
-K-quant tensors decode on the GPU (``asdsl_dequant_gguf_q4k`` /
-``_q6k``); there is no CPU decode path.  Deviations from the reference,
+Block-quantized tensors decode on the GPU (``asdsl_dequant_gguf_q4k``,
+``_q5k``, ``_q6k``, ``_q8_0``); there is no CPU decode path, and other
+types are refused.  Deviations from the reference,
 each a fix:
 
 * ``data`` is the tensor's raw bytes for every type.  The reference converts
@@ -53,6 +54,11 @@ GGML_BLOCK: dict[str, tuple[int, int]] = {
 
 # K-quant block sizes (bytes per 256 weights along the input axis)
 _K_BLOCK_BYTES: dict[str, int] = {t: GGML_BLOCK[t][1] for t in ("q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "q8_k")}
+# legacy 32-weight block types whose rows are whole blocks
+_ROW_BLOCK_TYPES = ("q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q8_1")
+# types decoded on the GPU: ggml type -> C-ABI decoder
+_DEVICE_DECODERS = {"q4_k": "asdsl_dequant_gguf_q4k", "q5_k": "asdsl_dequant_gguf_q5k",
+                    "q6_k": "asdsl_dequant_gguf_q6k", "q8_0": "asdsl_dequant_gguf_q8_0"}
 
 # GGUF tensor suffix -> (ASDSL projection, module), the reference's map
 GGUF_TO_ASDSL: dict[str, tuple[str, str]] = {
@@ -80,18 +86,23 @@ def ggml_type_name(type_id: int) -> str:
 
 
 def row_bytes_for_type(type_name: str, in_features: int) -> int:
-    """Bytes per GGUF storage row (K axis = in_features for logical W @ x)."""
+    """Size in bytes of one stored row of `in_features` weights (one output
+    feature) of a block-quantized ggml type: whole blocks of the type's
+    weights-per-block."""
     t = type_name.lower()
     if t in _K_BLOCK_BYTES:
         return (in_features // 256) * _K_BLOCK_BYTES[t]
-    raise ValueError(f"row_bytes_for_type: unsupported type {type_name}")
+    if t in _ROW_BLOCK_TYPES:
+        per, nbytes = GGML_BLOCK[t]
+        return (in_features // per) * nbytes
+    raise ValueError(f"no stored-row size for ggml type {type_name!r}")
 
 
 def logical_shape(file_shape: tuple[int, ...], type_name: str) -> tuple[int, int]:
-    """On-disk GGUF dims (ne0 = in_features, the contiguous axis, then ne1 =
-    out_features) -> logical (out_features, in_features)."""
+    """A GGUF weight's dims as stored (ne0, the contiguous input axis, first)
+    turned into the (out_features, in_features) of W in y = W x."""
     if len(file_shape) != 2:
-        raise ValueError(f"Expected rank-2 weight, got {file_shape}")
+        raise ValueError(f"logical_shape: a weight has two dims, this one {tuple(file_shape)}")
     return int(file_shape[1]), int(file_shape[0])
 
 
@@ -190,7 +201,7 @@ def read_gguf_tensors(path: str | Path, *, name_filter: str | None = None) -> di
 
     Returns name -> {type, type_id, shape, file_shape, data (raw bytes, a
     uint8 view of the file), n_bytes, and for rank-2 tensors logical_shape
-    (out, in) and, for K-quants, row_bytes}."""
+    (out, in) and, for block-quantized types, row_bytes}."""
     f = GGUFFile(path)
     out: dict[str, dict[str, Any]] = {}
     for name, (type_id, dims, _, size) in f.tensors.items():
@@ -201,38 +212,45 @@ def read_gguf_tensors(path: str | Path, *, name_filter: str | None = None) -> di
                                 "data": f.tensor_bytes(name), "n_bytes": size}
         if len(dims) == 2:
             info["logical_shape"] = logical_shape(dims, tname)
-            if tname in _K_BLOCK_BYTES:
+            if tname in _K_BLOCK_BYTES or tname in _ROW_BLOCK_TYPES:
                 info["row_bytes"] = row_bytes_for_type(tname, info["logical_shape"][1])
         out[name] = info
     return out
 
 
-def k_blocks_rowmajor(info: dict[str, Any], type_name: str | None = None) -> np.ndarray:
-    """A K-quant tensor's bytes as row-major [out rows x (in/256 blocks)]."""
-    tname = (type_name or str(info.get("type", ""))).lower()
-    if tname not in _K_BLOCK_BYTES:
-        raise ValueError(f"k_blocks_rowmajor: unsupported type {tname}")
+def _blocks_rowmajor(info: dict[str, Any], tname: str, fn: str) -> np.ndarray:
+    """The tensor's raw bytes, checked to be exactly rows x row_bytes: GGUF
+    stores a weight one output row after another, each a run of blocks."""
     rows, cols = info["logical_shape"]
     flat = np.asarray(info["data"], dtype=np.uint8).reshape(-1)
-    expected = rows * (cols // 256) * _K_BLOCK_BYTES[tname]
-    if flat.size != expected:
-        raise ValueError(f"k_blocks_rowmajor({tname}): byte count {flat.size} != expected {expected} "
-                         f"for logical {rows}x{cols}")
+    want = rows * row_bytes_for_type(tname, cols)
+    if flat.size != want:
+        raise ValueError(f"{fn}: {rows} x {cols} {tname} weights take {want} bytes, the tensor has {flat.size}")
     return flat
 
 
+def k_blocks_rowmajor(info: dict[str, Any], type_name: str | None = None) -> np.ndarray:
+    """A K-quant weight's bytes: per output row, in_features/256 blocks."""
+    tname = (type_name or str(info.get("type", ""))).lower()
+    if tname not in _K_BLOCK_BYTES:
+        raise ValueError(f"k_blocks_rowmajor: {tname!r} is not a K-quant type")
+    return _blocks_rowmajor(info, tname, "k_blocks_rowmajor")
+
+
 def q4k_blocks_rowmajor(info: dict[str, Any]) -> np.ndarray:
-    """ggml Q4_K bytes [rows x (cols/256 x 144)], as the reference hands them
-    to its Q4_K GEMV.  ``asdsl_repack_gguf_q4k_to_q4km`` (``q4km_from_gguf``)
-    rearranges them into the layout that GEMV decodes."""
+    """A ggml Q4_K weight's bytes, 144 per 256 weights of a row -- what the
+    reference gives its Q4_K GEMV.  ``q4km_from_gguf`` rearranges them into
+    the ASDSL Q4_K variant that GEMV decodes."""
     return k_blocks_rowmajor(info, "q4_k")
 
 
 def q5k_blocks_rowmajor(info: dict[str, Any]) -> np.ndarray:
+    """A ggml Q5_K weight's bytes, 176 per 256 weights of a row."""
     return k_blocks_rowmajor(info, "q5_k")
 
 
 def q6k_blocks_rowmajor(info: dict[str, Any]) -> np.ndarray:
+    """A ggml Q6_K weight's bytes, 210 per 256 weights of a row."""
     return k_blocks_rowmajor(info, "q6_k")
 
 
@@ -250,8 +268,8 @@ def _dense(info: dict[str, Any]) -> np.ndarray:
 
 def dequant_tensor_device(info: dict[str, Any]):
     """A tensor decoded to float32 on the GPU: shape (out, in) for rank-2
-    tensors (1-D otherwise).  Q4_K and Q6_K decode in the HIP kernels;
-    F32/F16/BF16 are converted from their bytes and uploaded."""
+    tensors (1-D otherwise).  Q4_K, Q5_K, Q6_K and Q8_0 decode in the HIP
+    kernels; F32/F16/BF16 are converted from their bytes and uploaded."""
     from asdsl import _hip
 
     torch = _hip._torch()
@@ -260,12 +278,12 @@ def dequant_tensor_device(info: dict[str, Any]):
     shape = info.get("logical_shape", dims if len(dims) != 1 else (dims[0],))
     if t in ("f32", "f16", "bf16"):
         return torch.from_numpy(np.ascontiguousarray(_dense(info)).reshape(shape)).to(_hip.device())
-    fn = {"q4_k": "asdsl_dequant_gguf_q4k", "q6_k": "asdsl_dequant_gguf_q6k"}.get(t)
+    fn = _DEVICE_DECODERS.get(t)
     if fn is None or len(dims) != 2:
         raise ValueError(f"dequant_tensor: type {info.get('type')} (rank {len(dims)}) is not decoded here "
-                         "(Q4_K, Q6_K, F32, F16, BF16)")
+                         f"({', '.join(k.upper() for k in _DEVICE_DECODERS)}, F32, F16, BF16)")
     rows, cols = shape
-    blocks = _hip.to_device(k_blocks_rowmajor(info, t), np.uint8)
+    blocks = _hip.to_device(_blocks_rowmajor(info, t, "dequant_tensor"), np.uint8)
     out = torch.empty((rows, cols), dtype=torch.float32, device=_hip.device())
     _hip.call(fn, _hip.ptr(blocks), _hip.ptr(out), rows, cols, _hip.stream_handle())
     return out

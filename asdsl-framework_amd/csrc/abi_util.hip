@@ -41,6 +41,7 @@ DeviceShape g_shape[64];
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
+    bool fixed = false;  // asdsl_reserve_workspace: never grown again
 };
 std::mutex g_ws_mu;
 Workspace g_ws[64];
@@ -103,6 +104,11 @@ asdsl_status device_workspace(hipStream_t stream, size_t bytes, void** out, cons
     }
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace& ws = g_ws[dev];
+    if (ws.bytes < bytes && ws.fixed) {
+        set_error("%s: needs a %zu-byte work buffer; %zu bytes were reserved by asdsl_reserve_workspace "
+                  "(reserve more, or pass a work buffer)", what, bytes, ws.bytes);
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    }
     if (ws.bytes < bytes) {
         hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
         e = hipStreamIsCapturing(stream, &cap);
@@ -128,6 +134,34 @@ asdsl_status device_workspace(hipStream_t stream, size_t bytes, void** out, cons
         ws.bytes = grown;
     }
     *out = ws.ptr;
+    return ASDSL_OK;
+}
+
+asdsl_status reserve_workspace(size_t bytes) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("reserve_workspace: no usable HIP device: %s", hipGetErrorString(e));
+        return ASDSL_ERR_HIP;
+    }
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace& ws = g_ws[dev];
+    if (bytes == 0) {
+        ws.fixed = false;
+        return ASDSL_OK;
+    }
+    if (ws.bytes < bytes) {
+        const size_t grown = (bytes + 255) & ~static_cast<size_t>(255);  // what was asked, not the growth step
+        void* fresh = nullptr;
+        e = hipMalloc(&fresh, grown);
+        if (e != hipSuccess) {
+            set_error("reserve_workspace: hipMalloc(%zu) failed: %s", grown, hipGetErrorString(e));
+            return ASDSL_ERR_HIP;
+        }
+        ws.ptr = fresh;  // a smaller earlier buffer is kept (queued work or a graph may use it)
+        ws.bytes = grown;
+    }
+    ws.fixed = true;
     return ASDSL_OK;
 }
 
@@ -226,3 +260,5 @@ extern "C" asdsl_status asdsl_profile_stages_end(int capacity, const char** labe
     }
     return ASDSL_OK;
 }
+
+extern "C" asdsl_status asdsl_reserve_workspace(size_t bytes) { return asdsl::reserve_workspace(bytes); }

@@ -84,8 +84,14 @@ asdsl_status launch(const char* what, void (*kernel)(P...), dim3 grid, dim3 bloc
 // between them) race on it; calls ordered by a stream or by events do not.
 // Growing calls hipMalloc, which a stream under graph capture does not allow:
 // an earlier call of at least the same size sizes it first
-// (ASDSL_ERR_UNSUPPORTED otherwise).
+// (ASDSL_ERR_UNSUPPORTED otherwise).  After reserve_workspace(n > 0) on the
+// device it is never grown: a request beyond it is ASDSL_ERR_INVALID_ARGUMENT.
 asdsl_status device_workspace(hipStream_t stream, size_t bytes, void** out, const char* what);
+
+// asdsl_reserve_workspace: allocate the current device's library buffer to
+// at least `bytes` now and fix it (no later call allocates); 0 returns to
+// growth on demand.
+asdsl_status reserve_workspace(size_t bytes);
 
 // The work buffer of one call: the caller's (`work`, `work_bytes`; at least
 // `need` bytes, 256-byte aligned, else ASDSL_ERR_INVALID_ARGUMENT) when
@@ -110,6 +116,26 @@ asdsl_status preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const 
                                int out_features, int in_features, int group_size, int n_cols, asdsl_stream_t stream,
                                bool allow_mfma, void* work = nullptr, size_t work_bytes = 0);
 
+// Whether the norm-fed preq2 GEMVs take the factored form (quantize h * nw,
+// scale the reduced outputs by 1/rms) instead of the reference's order
+// (quantize (h * inv_rms) * nw): ASDSL_HIP_NORM_FACTORED=1, read per call.
+bool preq2_norm_factored();
+
+// The launch shape of the single-column preq2 GEMV for M x K (K split
+// 1 << lks, nu units per lane, waves per workgroup, exact = the split covers
+// a band with no masked unit): the per-row fp32 order of its result.
+void preq2_plan_shape(int M, int K, int cus, int* lks, int* nu, int* waves, bool* exact);
+
+// The batched dot4 GEMV in the single-column GEMV's launch shape, so column
+// n of Y is bit for bit what that GEMV gives on column n of X (same units
+// per lane, same row reduction, same K-split sum); inv (per column, may be
+// null) scales each partial row after its reduction and before the K-split
+// sum, as the norm-fed single-column GEMVs apply 1/rms.  Returns
+// ASDSL_ERR_UNSUPPORTED (nothing launched) where that shape leaves masked
+// units or K > 8192.  1 <= n_cols <= 64.
+asdsl_status preq2_batch_exact(const uint8_t* meta, const uint8_t* quant, const float* X, const float* inv, float* Y,
+                               int out_features, int in_features, int group_size, int n_cols, asdsl_stream_t stream);
+
 // The MFMA form of preq2_fused_batch (up to 16 columns) on an activation
 // image another kernel already wrote at `image` (image_store8 layout: img,
 // then fac at image + in_features * 16 bytes; columns past n_cols zero).
@@ -125,13 +151,13 @@ asdsl_status preq2_batch_mfma_image(const uint8_t* meta, const uint8_t* quant, c
 // The decode step's o_proj: gemv_preq2_fused of the attention output, which
 // the GEMV's prologue merges itself from the split partials (part: per head
 // nsplit rows of part_stride floats, m, l, acc[head_dim]) of a position
-// *pos in [0, max_seq): nt = pos / tile + 1 tiles in splits of
-// ceil(nt / max_splits) tiles (max_splits <= 8).  A position outside the
-// cache reads `att` (the attention kernel zeroed it).
+// *pos in [0, min(max_seq, pos_limit)): nt = pos / tile + 1 tiles in splits
+// of ceil(nt / max_splits) tiles (max_splits <= 8).  A position outside that
+// range reads `att` (the attention kernel zeroed it).
 asdsl_status preq2_fused_combine(const uint8_t* meta, const uint8_t* quant, const float* att, float* y,
                                  int out_features, int in_features, int group_size, const float* part, const int* pos,
                                  int nsplit, int tile, int max_splits, int part_stride, int head_dim, int max_seq,
-                                 asdsl_stream_t stream);
+                                 int pos_limit, asdsl_stream_t stream);
 
 // The decode step's first qkv GEMV: the RMSNorm prologue reads h as the fp16
 // embedding row of *token (row 0 for a token outside [0, vocab)), workgroup 0

@@ -308,7 +308,7 @@ template <int IMG_GS>
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const float* __restrict__ part,
                                                                       const int* __restrict__ pos_ptr,
                                                                       float* __restrict__ out, int nsplit,
-                                                                      int max_seq, int fold, int ncols,
+                                                                      int max_seq, int pos_limit, int fold, int ncols,
                                                                       int form_tile, int form_splits,
                                                                       uint2* __restrict__ img,
                                                                       float2* __restrict__ fac) {
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
     const int pos = *pos_ptr + col;
     part += static_cast<size_t>(col) * gridDim.x * nsplit * kPartStride;
     out += static_cast<size_t>(col) * gridDim.x * kHeadDim;
-    if (pos < 0 || pos >= max_seq) {  // outside the cache: no partials were written
+    if (pos < 0 || pos >= max_seq || pos >= pos_limit) {  // no partials were written (see attn_decode_kernel)
         if (g == 0) out[static_cast<size_t>(h) * kHeadDim + d] = 0.0f;
         if (IMG_GS != 0 && tid < kHeadChunks) image_chunk(zeros);
         return;
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
     const float* __restrict__ qkv, KvCache kv,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, const int* __restrict__ pos_ptr,
     float* __restrict__ part, float* __restrict__ att, int n_heads, int n_kv, int max_seq, int rot_half,
-    int max_splits) {
+    int max_splits, int pos_limit, uint32_t* __restrict__ flags) {
     constexpr int kThreads = WAVES * kWave;
     constexpr int kStep = 4 * WAVES;   // positions per step of all waves
     constexpr int kIt = KIT;           // steps per tile
@@ -502,9 +502,14 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
     const int tl_wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
     ASDSL_TIMELINE_STAMP(4, tl_wg, 0);
     const int pos = *pos_ptr;
-    if (pos < 0 || pos >= max_seq) {  // outside the cache: zero output, nothing written to the cache
+    // Outside the cache, or at or past the range the launch was shaped for
+    // (its grid would not cover the position's splits): zero output, nothing
+    // written to the cache, and the reason raised in *flags for the host.
+    if (pos < 0 || pos >= max_seq || pos >= pos_limit) {
         if (s == 0)
             for (int e = tid; e < G * kHeadDim; e += kThreads) att[static_cast<size_t>(kvh * G) * kHeadDim + e] = 0.0f;
+        if (flags && s == 0 && kvh == 0 && tid == 0)
+            *flags |= pos < 0 || pos >= max_seq ? ASDSL_DECODE_FLAG_POS_RANGE : ASDSL_DECODE_FLAG_POS_LIMIT;
         return;
     }
     const int tps = attn_fold_tps(pos, kTile, max_splits);
@@ -721,7 +726,7 @@ struct DeepAttnK {
 // and the combine kernel, att receiving the merged output.
 asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q8, const float* rc, const float* rs,
                                      const int* pos, float* att, float* work, int n_heads, int n_kv, int rot_half,
-                                     int max_seq, int pos_limit, bool fold, hipStream_t s) {
+                                     int max_seq, int pos_limit, bool fold, uint32_t* flags, hipStream_t s) {
     const int limit = pos_limit < max_seq ? pos_limit : max_seq;
     const bool deep = !fold && limit > kDeepFrom;
     const FoldForm& f = fold ? kShortForm : deep ? kDeepForm : kLongForm;
@@ -730,14 +735,14 @@ asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q
     const int max_splits = f.max_splits;
     auto go = [&](auto kern) {
         return launch("attn_decode_kernel", kern, grid, block, 0, s, qkv, kv, rc, rs, pos, work, att, n_heads, n_kv,
-                      max_seq, rot_half, max_splits);
+                      max_seq, rot_half, max_splits, limit, flags);
     };
     const asdsl_status st = deep ? with_attn_kernel<DeepAttnK>(n_heads / n_kv, q8, go)
                                  : with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, go);
     if (st != ASDSL_OK || fold) return st;
     const StageScope stage("attention_combine");
     return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
-                  static_cast<const float*>(work), pos, att, kMaxSplits, max_seq, 0, 1, f.tile, f.max_splits,
+                  static_cast<const float*>(work), pos, att, kMaxSplits, max_seq, limit, 0, 1, f.tile, f.max_splits,
                   static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
 }
 
@@ -745,7 +750,7 @@ int attn_splits(int max_seq) { return (max_seq + kSplit - 1) / kSplit; }
 
 // Work buffer layout of one decode step (offsets in floats, 256-byte aligned).
 struct DecodeWork {
-    size_t hA, hB, qkv, att, o, gu, down, part, amax, total;
+    size_t hA, hB, qkv, att, o, gu, down, part, amax, flags, total;
 };
 
 size_t align64(size_t f) { return (f + 63) & ~static_cast<size_t>(63); }
@@ -768,6 +773,7 @@ DecodeWork decode_work(const asdsl_decode_model& m) {
     w.down = take(m.hidden);
     w.part = take(attn_decode_work_floats(m.n_heads, m.max_seq));
     w.amax = take(2);
+    w.flags = take(1);  // ASDSL_DECODE_FLAG_* bits, set by the attention kernel, cleared by the host
     w.total = at;
     return w;
 }
@@ -839,13 +845,18 @@ __global__ __launch_bounds__(256) void verify_embed_kernel(const uint16_t* __res
 // int8 image (image_store8, the values batch_quantize_kernel would form from
 // X), and workgroups c >= ncols (the grid covers kImageCols columns) write
 // that image's zero columns, so the GEMV needs no quantize launch of its own.
+// inv_out (IMG_GS = 0 only): the single-token GEMV's factored form instead,
+// X[c] = h * w and inv_out[c] = inv_rms, which the batched GEMV applies to
+// its reduced rows (preq2_batch_exact), as the norm-fed GEMV's prologue and
+// epilogue do.
 template <int IMG_GS>
 __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __restrict__ H,
                                                                        const float* __restrict__ D,
                                                                        const float* __restrict__ w,
                                                                        float* __restrict__ X, int K, float eps,
                                                                        int ncols, uint2* __restrict__ img,
-                                                                       float2* __restrict__ fac) {
+                                                                       float2* __restrict__ fac,
+                                                                       float* __restrict__ inv_out) {
     __shared__ float red[kNormThreads / kWave];
     const int col = static_cast<int>(blockIdx.x);
     const int tid = static_cast<int>(threadIdx.x);
@@ -886,6 +897,16 @@ __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __
 #pragma unroll
     for (int q = 1; q < kNormThreads / kWave; ++q) tot += red[q];
     const float inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+    if (IMG_GS == 0 && inv_out) {
+        if (tid == 0) inv_out[col] = inv_rms;
+        for (int ch = tid; ch < nchunk; ch += kNormThreads) {
+            const float4 a = h[2 * ch], b = h[2 * ch + 1];
+            const float4 wa = w4[2 * ch], wb = w4[2 * ch + 1];
+            x[2 * ch] = make_float4(a.x * wa.x, a.y * wa.y, a.z * wa.z, a.w * wa.w);
+            x[2 * ch + 1] = make_float4(b.x * wb.x, b.y * wb.y, b.z * wb.z, b.w * wb.w);
+        }
+        return;
+    }
     // the loop is uniform per workgroup (every lane of a quantization group
     // takes part); chunks past the end quantize a copy of the last chunk and
     // store nothing
@@ -1154,7 +1175,7 @@ struct VerifyAttnK {
 
 // Work buffer layout of a verify pass of up to n tokens (offsets in floats).
 struct VerifyWork {
-    size_t H, X, QKV, part, att, O, GU, S, keys, mimg, mimg_bytes, total;
+    size_t H, X, QKV, part, att, O, GU, S, keys, inv, mimg, mimg_bytes, total;
 };
 
 VerifyWork verify_work(const asdsl_decode_model& m, int n) {
@@ -1176,6 +1197,7 @@ VerifyWork verify_work(const asdsl_decode_model& m, int n) {
     w.GU = take(N * 2 * m.ffn);
     w.S = take(N * m.ffn);
     w.keys = take(2 * N);
+    w.inv = take(N);
     // the MFMA batched GEMV's column image (the widest input, K = max(hidden, ffn))
     w.mimg_bytes = asdsl_gemv_preq2_fused_batch_work_bytes(m.hidden > m.ffn ? m.hidden : m.ffn);
     w.mimg = take((w.mimg_bytes + sizeof(float) - 1) / sizeof(float));
@@ -1235,7 +1257,7 @@ extern "C" asdsl_status asdsl_attention_f16kv(const float* qkv, uint16_t* k_cach
     if (cs != ASDSL_OK) return cs;
     const KvCache kv{k_cache, v_cache, nullptr, nullptr};
     return launch_attention_decode(qkv, kv, false, rope_cos, rope_sin, pos, att_out, work, n_heads, n_kv_heads,
-                                   rotary_dim / 2, max_seq, max_seq, false, as_hip(stream));
+                                   rotary_dim / 2, max_seq, max_seq, false, nullptr, as_hip(stream));
 }
 
 extern "C" asdsl_status asdsl_attention_q8kv(const float* qkv, int8_t* k_cache, int8_t* v_cache, float* k_scale,
@@ -1248,12 +1270,17 @@ extern "C" asdsl_status asdsl_attention_q8kv(const float* qkv, int8_t* k_cache, 
     ASDSL_CHECK_ARG(k_scale && v_scale, "attention_q8kv: null scale array");
     const KvCache kv{k_cache, v_cache, k_scale, v_scale};
     return launch_attention_decode(qkv, kv, true, rope_cos, rope_sin, pos, att_out, work, n_heads, n_kv_heads,
-                                   rotary_dim / 2, max_seq, max_seq, false, as_hip(stream));
+                                   rotary_dim / 2, max_seq, max_seq, false, nullptr, as_hip(stream));
 }
 
 extern "C" size_t asdsl_decode_work_bytes(const asdsl_decode_model* model) {
     if (check_model(model) != ASDSL_OK) return 0;
     return decode_work(*model).total * sizeof(float);
+}
+
+extern "C" size_t asdsl_decode_flags_offset(const asdsl_decode_model* model) {
+    if (check_model(model) != ASDSL_OK) return 0;
+    return decode_work(*model).flags * sizeof(float);
 }
 
 extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model, int* token, int* pos, int pos_limit,
@@ -1275,6 +1302,7 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
     float* down = base + w.down;
     float* part = base + w.part;
     auto* amax = reinterpret_cast<unsigned long long*>(base + w.amax);
+    auto* flags = reinterpret_cast<uint32_t*>(base + w.flags);
     hipStream_t s = as_hip(stream);
     const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
     const int q_dim = m.n_heads * m.head_dim;
@@ -1320,11 +1348,11 @@ extern "C" asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model,
         const KvCache kv{L.k_cache, L.v_cache, L.k_scale, L.v_scale};
         g_stage = "attention";  // the combine labels itself
         st = launch_attention_decode(qkv, kv, q8, m.rope_cos, m.rope_sin, pos, att, part, m.n_heads,
-                                     m.n_kv_heads, m.rotary_dim / 2, m.max_seq, limit, fold, s);
+                                     m.n_kv_heads, m.rotary_dim / 2, m.max_seq, limit, fold, flags, s);
         if (st != ASDSL_OK) return st;
         g_stage = "o_proj";
         st = fold ? preq2_fused_combine(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, part, pos, kMaxSplits,
-                                        form.tile, form.max_splits, kPartStride, kHeadDim, m.max_seq, stream)
+                                        form.tile, form.max_splits, kPartStride, kHeadDim, m.max_seq, limit, stream)
                   : asdsl_gemv_preq2_fused(L.o_meta, L.o_quant, att, o, m.hidden, q_dim, m.gs_attn, stream);
         if (st != ASDSL_OK) return st;
         // gate_up with SwiGLU in its epilogue (gate and up rows in one
@@ -1389,6 +1417,7 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     float* GU = base + w.GU;
     float* S = base + w.S;
     auto* keys = reinterpret_cast<unsigned long long*>(base + w.keys);
+    float* INV = base + w.inv;
     void* mimg = base + w.mimg;
     hipStream_t s = as_hip(stream);
     const int qkv_dim = (m.n_heads + 2 * m.n_kv_heads) * m.head_dim;
@@ -1396,13 +1425,26 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     const int nsplit = attn_splits(m.max_seq);
     const int G = m.n_heads / m.n_kv_heads;
     const bool q8 = m.kv_format == ASDSL_KV_INT8;
-    // The projections take the MFMA batched GEMV (16 columns per launch, so
-    // each weight byte streams once per pass; from 4 columns on, 3 once
-    // K >= 4096).  Its fp32 summation order differs from the single-token
-    // step's GEMVs, so a column's downstream int8 activations can round
-    // differently.  ASDSL_HIP_VERIFY_DOT4=1 (read per call) keeps the dot4
-    // forms, whose per-column arithmetic follows the single-token step.
-    const bool mfma = env_knob("ASDSL_HIP_VERIFY_DOT4") <= 0;
+    // The projections take the dot4 batched GEMV in each single-token GEMV's
+    // own launch shape (preq2_batch_exact), the norm-fed ones in the
+    // single-token step's norm form (the normed input, or with
+    // ASDSL_HIP_NORM_FACTORED h * w quantized and 1/rms applied to the
+    // reduced rows): below 2048 positions, where the attention splits
+    // coincide too, every column then gives the single-token step's logits,
+    // K/V rows and token bit for bit, as lossless speculative decoding needs.  ASDSL_HIP_VERIFY_MFMA=1 (read
+    // per call) takes the MFMA batched GEMV instead (16 columns per launch,
+    // from 4 columns on, 3 once K >= 4096): faster at many columns, but its
+    // fp32 summation order differs, so a column's int8 activations can round
+    // differently from the single-token step's.
+    const bool mfma = env_knob("ASDSL_HIP_VERIFY_MFMA") > 0;
+    // dot4 in the single-token launch shape, else (a shape whose split masks
+    // units) the batched GEMV's own dot4 plan
+    auto gemv_exact = [&](const uint8_t* meta, const uint8_t* quant, const float* Xin, const float* inv, float* Y,
+                          int M, int K, int gs) -> asdsl_status {
+        const asdsl_status r = preq2_batch_exact(meta, quant, Xin, inv, Y, M, K, gs, n, stream);
+        if (r != ASDSL_ERR_UNSUPPORTED || inv) return r;
+        return preq2_fused_batch(meta, quant, Xin, Y, M, K, gs, n, stream, false, mimg, w.mimg_bytes);
+    };
 
     asdsl_status st = launch("verify_embed_kernel", verify_embed_kernel, dim3((m.hidden + 1023) / 1024, n), dim3(256),
                              0, s, m.embed, tokens, H, m.hidden, m.vocab, keys);
@@ -1419,15 +1461,30 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
             asdsl_status r = launch("verify_add_norm_kernel",
                                     gs == 32 ? verify_add_norm_kernel<32> : verify_add_norm_kernel<128>,
                                     dim3(kImageCols), dim3(kNormThreads), 0, s, H, D, nw, X, K, m.rms_eps, n, img,
-                                    fac_of(K));
+                                    fac_of(K), static_cast<float*>(nullptr));
             if (r != ASDSL_OK) return r;
             return preq2_batch_mfma_image(meta, quant, mimg, Y, M, K, gs, n, stream);
         }
+        // the single-token GEMVs' norm form: the reference's order (normed
+        // X, below) or the factored one; the factored form's 1/rms sum
+        // follows the 8-wave prologue of the norm-fed GEMVs, which covers
+        // K <= 4096 (the only plan they take there)
+        const bool factored = !mfma && K <= 4096 && K % 8 == 0 && preq2_norm_factored();
         asdsl_status r = launch("verify_add_norm_kernel", verify_add_norm_kernel<0>, dim3(n), dim3(kNormThreads), 0, s,
                                 H, D, nw, X, K, m.rms_eps, n, static_cast<uint2*>(nullptr),
-                                static_cast<float2*>(nullptr));
+                                static_cast<float2*>(nullptr), factored ? INV : nullptr);
         if (r != ASDSL_OK) return r;
-        return preq2_fused_batch(meta, quant, X, Y, M, K, gs, n, stream, mfma, mimg, w.mimg_bytes);
+        if (factored) {
+            r = preq2_batch_exact(meta, quant, X, INV, Y, M, K, gs, n, stream);
+            if (r != ASDSL_ERR_UNSUPPORTED) return r;
+            // no exact shape: normalize in place and take the plain batched form
+            r = launch("verify_add_norm_kernel", verify_add_norm_kernel<0>, dim3(n), dim3(kNormThreads), 0, s, H,
+                       static_cast<const float*>(nullptr), nw, X, K, m.rms_eps, n, static_cast<uint2*>(nullptr),
+                       static_cast<float2*>(nullptr), static_cast<float*>(nullptr));
+            if (r != ASDSL_OK) return r;
+        }
+        return mfma ? preq2_fused_batch(meta, quant, X, Y, M, K, gs, n, stream, true, mimg, w.mimg_bytes)
+                    : gemv_exact(meta, quant, X, nullptr, Y, M, K, gs);
     };
     // H carries the residual stream of every column; O (attention output
     // projection) and S -> O (down projection) are added in by the next norm.
@@ -1447,16 +1504,17 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         if (preq2_batch_image_applies(L.o_meta, L.o_quant, m.hidden, q_dim, m.gs_attn, n, mfma)) {
             st = launch("attn_combine_kernel", m.gs_attn == 32 ? attn_combine_kernel<32> : attn_combine_kernel<128>,
                         dim3(m.n_heads, kImageCols), dim3(kCombineThreads), 0, s, static_cast<const float*>(part), pos,
-                        att, nsplit, m.max_seq, 0, n, 0, 0, img, fac_of(q_dim));
+                        att, nsplit, m.max_seq, m.max_seq, 0, n, 0, 0, img, fac_of(q_dim));
             if (st != ASDSL_OK) return st;
             st = preq2_batch_mfma_image(L.o_meta, L.o_quant, mimg, O, m.hidden, q_dim, m.gs_attn, n, stream);
         } else {
             st = launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
-                        static_cast<const float*>(part), pos, att, nsplit, m.max_seq, 0, n, 0, 0,
+                        static_cast<const float*>(part), pos, att, nsplit, m.max_seq, m.max_seq, 0, n, 0, 0,
                         static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
             if (st != ASDSL_OK) return st;
-            st = preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, mfma, mimg,
-                                   w.mimg_bytes);
+            st = mfma ? preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, true,
+                                          mimg, w.mimg_bytes)
+                      : gemv_exact(L.o_meta, L.o_quant, att, nullptr, O, m.hidden, q_dim, m.gs_attn);
         }
         if (st != ASDSL_OK) return st;
         st = norm_then_gemv(O, L.rms_ffn, L.gu_meta, L.gu_quant, GU, 2 * m.ffn, m.gs_ffn);
@@ -1474,8 +1532,9 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
                         static_cast<const float*>(GU), S, m.ffn, L.fatrelu_threshold, n, static_cast<uint2*>(nullptr),
                         static_cast<float2*>(nullptr));
             if (st != ASDSL_OK) return st;
-            st = preq2_fused_batch(L.down_meta, L.down_quant, S, O, m.hidden, m.ffn, m.gs_ffn, n, stream, mfma, mimg,
-                                   w.mimg_bytes);
+            st = mfma ? preq2_fused_batch(L.down_meta, L.down_quant, S, O, m.hidden, m.ffn, m.gs_ffn, n, stream,
+                                          true, mimg, w.mimg_bytes)
+                      : gemv_exact(L.down_meta, L.down_quant, S, nullptr, O, m.hidden, m.ffn, m.gs_ffn);
         }
         if (st != ASDSL_OK) return st;
         pending = O;

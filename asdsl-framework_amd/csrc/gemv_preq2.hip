@@ -78,6 +78,10 @@ struct ProArgs {
     unsigned long long* amax = nullptr;
     float eps = 0.0f;
     float thr = 0.0f;
+    // kNorm / kNormEmbed: quantize (h * inv_rms) * nw, the reference's
+    // order (0), or h * nw with the outputs scaled by inv_rms (1: the
+    // factored form, preq2_norm_factored())
+    int norm_factored = 0;
     // kCombine: partials [head][split][m, l, acc[head_dim]] (part_stride
     // floats each, nsplit rows per head), the position and the split policy:
     // nt = pos / tile + 1 tiles, tps = ceil(nt / max_splits) tiles per split,
@@ -85,6 +89,7 @@ struct ProArgs {
     const float* part = nullptr;
     const int* pos = nullptr;
     int nsplit = 0, tile = 0, max_splits = 0, part_stride = 0, head_dim = 0, max_seq = 0;
+    int pos_limit = 0x7FFFFFFF;  // positions at or past it had no partials written
     // SWIGLU_EPI: the output rows are [gate F | up F] with F = 4 * fbands;
     // y receives swiglu(gate, up) (F values, pa.thr applies)
     int fbands = 0;
@@ -93,6 +98,14 @@ struct ProArgs {
     const int* token = nullptr;
     int vocab = 0;
 };
+
+// Units of a lane's first tile requested before the activation is staged,
+// by split code: 0 all of them, 1 a third, 2 a half, 3 two thirds (rounded
+// up); the rest are requested once the activation is staged.
+template <int NU, int SPLIT>
+constexpr int pre_units() {
+    return SPLIT == 0 ? NU : SPLIT == 1 ? (NU + 2) / 3 : SPLIT == 2 ? (NU + 1) / 2 : (2 * NU + 2) / 3;
+}
 
 // Block sum in fixed order, in two halves around a barrier the caller
 // already has: each wave's butterfly sum to s_red[wave], then, after the
@@ -112,7 +125,7 @@ __device__ __forceinline__ float sum_waves(const float* s_red) {
 }
 
 template <int GS, int NU, int WAVES, int NCH, bool Q8, bool EXACT, bool XREG, Pro PRO = Pro::kPlain,
-          bool ARGMAX = false, bool SWIGLU_EPI = false>
+          bool ARGMAX = false, bool SWIGLU_EPI = false, int SPLIT = 0>
 __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_t* __restrict__ meta,
                                                                   const uint4* __restrict__ quant,
                                                                   const float* __restrict__ x,
@@ -172,7 +185,8 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     uint32_t mt[NU];
     // Loads are unconditional at in-bounds indices; values of rows >= M
     // (tail band) are never stored.
-    auto load_tile = [&](int tile) {
+    // units lo .. hi-1 of a tile (uniform bounds)
+    auto load_tile = [&](int tile, int lo, int hi) {
         const int band = min(band_of(tile), nbands - 1);
         const uint4* qb = quant + static_cast<size_t>(band) * upb;
         const int row = min(band * 4 + slot, M - 1);
@@ -181,14 +195,18 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
             const uint4* qp = qb + c0;
             const uint32_t* mp = mrow + c0 / UPG4;
 #pragma unroll
-            for (int j = 0; j < NU; ++j) w[j] = load_stream16(qp + j * kWave);
+            for (int j = 0; j < NU; ++j)
+                if (j >= lo && j < hi) w[j] = load_stream16(qp + j * kWave);
 #pragma unroll
-            for (int j = 0; j < NU; ++j) mt[j] = mp[j * (kWave / UPG4)];
+            for (int j = 0; j < NU; ++j)
+                if (j >= lo && j < hi) mt[j] = mp[j * (kWave / UPG4)];
         } else {
 #pragma unroll
-            for (int j = 0; j < NU; ++j) w[j] = load_stream16(qb + cu[j]);
+            for (int j = 0; j < NU; ++j)
+                if (j >= lo && j < hi) w[j] = load_stream16(qb + cu[j]);
 #pragma unroll
-            for (int j = 0; j < NU; ++j) mt[j] = mrow[cu[j] / UPG4];
+            for (int j = 0; j < NU; ++j)
+                if (j >= lo && j < hi) mt[j] = mrow[cu[j] / UPG4];
         }
     };
 
@@ -204,7 +222,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     int fns = 0;       // kCombine: splits merged here (0: x holds the merged output)
     if constexpr (PRO == Pro::kCombine) {
         const int p = *pa.pos;
-        if (p >= 0 && p < pa.max_seq) {
+        if (p >= 0 && p < pa.max_seq && p < pa.pos_limit) {
             const int nt = p / pa.tile + 1;
             const int tps = (nt + pa.max_splits - 1) / pa.max_splits;
             fns = (nt + tps - 1) / tps;  // <= max_splits <= kMaxFold
@@ -280,16 +298,21 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
     // ~1 % slower, so it is not done there).  The barrier waits on nothing
     // outstanding.
     if constexpr (WAVES > 8) __syncthreads();
-    load_tile(tile);           // grid <= ntiles, so this tile exists
-    // kNorm: 1/rms is one positive factor of the whole input, so the int8
-    // codes of (h * inv_rms) * nw are those of h * nw (each group's scale is
-    // amax / 127 and takes the factor once) and the output of the GEMV on
-    // h * nw is inv_rms times that of the GEMV on the normed input.  The GEMV
-    // therefore quantizes h * nw right away and scales its outputs by
-    // inv_rms: the sum of squares is reduced behind the staging barrier and
-    // the norm adds no barrier or dependent step before the dot products.
-    // (Equal to the normed form up to fp32 rounding; an element whose
-    // quotient lies within rounding of a .5 boundary can take the other code.)
+    // grid <= ntiles, so this tile exists.  SPLIT: only the first units go
+    // out now, the rest once the activation is staged (below), so that the
+    // activation is not queued behind the launch's whole weight stream.
+    constexpr int kPre = pre_units<NU, SPLIT>();
+    load_tile(tile, 0, kPre);
+    // kNorm: the GEMV input is rmsnorm(h) = (h * inv_rms) * nw, quantized
+    // per group as the reference's rmsnorm + quantize_activation form it;
+    // the block sum of squares (fixed order) is reduced behind an extra
+    // barrier before the quantization.  The factored form
+    // (pa.norm_factored) skips that barrier: 1/rms is one positive factor of
+    // the whole input, so the codes of h * nw are those of the normed input
+    // up to fp32 rounding (a quotient within rounding of a .5 boundary can
+    // take the other code) and the GEMV of h * nw scaled by inv_rms is the
+    // GEMV of the normed input; it quantizes h * nw at once and scales its
+    // reduced outputs by inv_rms.
     __shared__ float s_red[kNormed ? WAVES : 1];
     if constexpr (kNormed) {
         float ss = 0.0f;
@@ -308,10 +331,21 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
                         make_float4(act.v[i][4], act.v[i][5], act.v[i][6], act.v[i][7]);
                 }
             }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) act.v[i][e] *= ew[i][e];
         }
         wave_sum_to_lds(ss, s_red);
+        if (pa.norm_factored) {  // uniform per launch
+#pragma unroll
+            for (int i = 0; i < NCH; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) act.v[i][e] *= ew[i][e];
+        } else {
+            __syncthreads();
+            const float inv = 1.0f / sqrtf(sum_waves<WAVES>(s_red) / static_cast<float>(K) + pa.eps);
+#pragma unroll
+            for (int i = 0; i < NCH; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) act.v[i][e] = (act.v[i][e] * inv) * ew[i][e];
+        }
     } else if constexpr (PRO == Pro::kSwiglu) {
 #pragma unroll
         for (int i = 0; i < NCH; ++i)
@@ -342,11 +376,17 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
         }
     }
     act.process(K, im);        // quantize while the weights are in flight
+    if constexpr (kPre < NU) {
+        __builtin_amdgcn_sched_barrier(0);  // keep these requests behind the staging
+        load_tile(tile, kPre, NU);
+    }
     ASDSL_TIMELINE_STAMP(kTl, tl_wg, 1);
     __syncthreads();
     ASDSL_TIMELINE_STAMP(kTl, tl_wg, 2);
-    float inv_rms = 1.0f;
-    if constexpr (kNormed) inv_rms = 1.0f / sqrtf(sum_waves<WAVES>(s_red) / static_cast<float>(K) + pa.eps);
+    float inv_rms = 1.0f;  // the factored form's output scale (1 otherwise: an exact multiply)
+    if constexpr (kNormed) {
+        if (pa.norm_factored) inv_rms = 1.0f / sqrtf(sum_waves<WAVES>(s_red) / static_cast<float>(K) + pa.eps);
+    }
 
     // XREG: this lane's activation units are copied from LDS into registers
     // once and reused for every tile; otherwise they are read per tile.
@@ -391,7 +431,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
         if constexpr (kNormed) acc *= inv_rms;
         // next tile's loads after the reduction: issuing them before it keeps
         // ~20 more VGPRs live (measured), costing a workgroup per CU at NU=6
-        if (tile + tile_step < ntiles) load_tile(tile + tile_step);
+        if (tile + tile_step < ntiles) load_tile(tile + tile_step, 0, NU);
         const int row = band * 4 + slot;
         if constexpr (SWIGLU_EPI) {
             // the up waves hand their rows to the gate waves through LDS (two
@@ -550,12 +590,13 @@ int check_preq2_args(const void* meta, const void* quant, const void* x, const v
 struct Plan {
     int lks, nu, waves, grid;
     bool exact;
+    int split;  // pre_units split code of the first tile's weight requests
 };
 
-Plan plan_preq2(int M, int K, int cus) {
+Plan plan_preq2(int M, int K, int cus, int gs) {
     const int upb = K / 8;
     const int nbands = (M + 3) / 4;
-    Plan p{0, 0, K > 4096 ? 16 : 8, 0, false};
+    Plan p{0, 0, K > 4096 ? 16 : 8, 0, false, 0};
     auto nu_of = [&](int lks) { return (upb + (kWave << lks) - 1) / (kWave << lks); };
     auto tiles_of = [&](int lks) {
         const int bpt = p.waves >> lks;
@@ -583,6 +624,19 @@ Plan plan_preq2(int M, int K, int cus) {
     const int cap = cus * (32 / p.waves);  // at most 32 waves per compute unit
     const int tiles = tiles_of(p.lks);
     p.grid = tiles < cap ? tiles : cap;
+    // The activation waits in the memory queues behind the weight requests
+    // issued before it, so its arrival grows with the bytes a launch
+    // requests up front (1.3 us at 5.9 MB, 3-6 us at 31.5 MB).  From 8 MB of
+    // weights the first tile's requests are split around the staging: half
+    // of them first below 16 MB, a third from 16 MB (measured: qkv 9.9 MB
+    // 4.25 -> 3.87 us, down 15.8 MB 5.08 -> 4.76, gate_up 31.5 MB 7.03 ->
+    // 6.81; o_proj 5.9 MB is slower split).  ASDSL_HIP_PRE_SPLIT (read per
+    // call) sets the code instead: 1 a third, 2 a half, 4 none.
+    const double bytes = static_cast<double>(M) * K * (0.5 + 4.0 / gs);
+    p.split = bytes < 8e6 ? 0 : bytes < 16e6 ? 2 : 1;
+    const int forced_split = env_knob("ASDSL_HIP_PRE_SPLIT");
+    if (forced_split == 1 || forced_split == 2) p.split = forced_split;
+    if (forced_split == 4) p.split = 0;
     return p;
 }
 
@@ -590,21 +644,32 @@ template <int GS, int WAVES, int NCH, bool Q8, bool EXACT, Pro PRO = Pro::kPlain
           bool SWI = false>
 asdsl_status launch_exact(const Plan& p, const uint32_t* m, const uint4* q, const float* x, const int8_t* xq8,
                           const float* xsc, float* y, int M, int K, hipStream_t stream, const ProArgs& pa = ProArgs{}) {
-    constexpr bool XREG = true;
     const size_t lds = x_image_bytes(K, GS);
     const dim3 block(WAVES * kWave);
-#define ASDSL_PREQ2_NU(N)                                                                                         \
+    constexpr bool XREG = true;
+#define ASDSL_PREQ2_NU(N, SPLIT)                                                                                 \
     case N:                                                                                                       \
-        return launch("preq2_gemv_kernel", preq2_gemv_kernel<GS, N, WAVES, NCH, Q8, EXACT, XREG, PRO, ARGMAX, SWI>, \
-                      dim3(p.grid), block, lds, stream, m, q, x, xq8, xsc, y, M, K, p.lks, pa);
-    switch (p.nu) {
-        ASDSL_PREQ2_NU(1)
-        ASDSL_PREQ2_NU(2)
-        ASDSL_PREQ2_NU(3)
-        ASDSL_PREQ2_NU(4)
-        ASDSL_PREQ2_NU(5)
-        default: ASDSL_PREQ2_NU(6)
+        return launch("preq2_gemv_kernel",                                                                        \
+                      preq2_gemv_kernel<GS, N, WAVES, NCH, Q8, EXACT, XREG, PRO, ARGMAX, SWI, SPLIT>, dim3(p.grid), \
+                      block, lds, stream, m, q, x, xq8, xsc, y, M, K, p.lks, pa);
+#define ASDSL_PREQ2_NUS(SPLIT)      \
+    switch (p.nu) {                 \
+        ASDSL_PREQ2_NU(1, SPLIT)    \
+        ASDSL_PREQ2_NU(2, SPLIT)    \
+        ASDSL_PREQ2_NU(3, SPLIT)    \
+        ASDSL_PREQ2_NU(4, SPLIT)    \
+        ASDSL_PREQ2_NU(5, SPLIT)    \
+        default: ASDSL_PREQ2_NU(6, SPLIT) \
     }
+    if constexpr (EXACT && !Q8) {  // the split forms are built for the fp32-input shapes K tiles exactly
+        switch (p.split) {
+            case 1: ASDSL_PREQ2_NUS(1)
+            case 2: ASDSL_PREQ2_NUS(2)
+            default: break;
+        }
+    }
+    ASDSL_PREQ2_NUS(0)
+#undef ASDSL_PREQ2_NUS
 #undef ASDSL_PREQ2_NU
 }
 
@@ -622,7 +687,7 @@ asdsl_status launch_waves(const Plan& p, const uint32_t* m, const uint4* q, cons
 template <int GS>
 asdsl_status launch_gateup_swiglu(const uint8_t* meta, const uint8_t* quant, const float* x, float* y, int F, int K,
                                   ProArgs pa, hipStream_t stream, int cus) {
-    Plan p = plan_preq2(2 * F, K, cus);
+    Plan p = plan_preq2(2 * F, K, cus, GS);
     const int hpt = (p.waves >> p.lks) / 2;
     if (p.lks != 0 || hpt < 1 || F % 4 != 0 || (F / 4) % hpt != 0) return ASDSL_ERR_UNSUPPORTED;
     pa.fbands = F / 4;
@@ -656,7 +721,7 @@ asdsl_status launch_gateup_swiglu(const uint8_t* meta, const uint8_t* quant, con
 template <int GS, Pro PRO, bool ARGMAX>
 asdsl_status launch_preq2_fused(const uint8_t* meta, const uint8_t* quant, const float* x, float* y, int M, int K,
                                 const ProArgs& pa, hipStream_t stream, int cus) {
-    const Plan p = plan_preq2(M, K, cus);
+    const Plan p = plan_preq2(M, K, cus, GS);
     const auto* m = reinterpret_cast<const uint32_t*>(meta);
     const auto* q = reinterpret_cast<const uint4*>(quant);
     if (p.waves == 8) return launch_waves<GS, 8, 1, false, PRO, ARGMAX>(p, m, q, x, nullptr, nullptr, y, M, K, stream, pa);
@@ -670,7 +735,7 @@ asdsl_status launch_preq2_fused(const uint8_t* meta, const uint8_t* quant, const
 template <int GS, bool Q8>
 asdsl_status launch_preq2(const uint8_t* meta, const uint8_t* quant, const float* x, const int8_t* xq8,
                           const float* xsc, float* y, int M, int K, hipStream_t stream, int cus) {
-    const Plan p = plan_preq2(M, K, cus);
+    const Plan p = plan_preq2(M, K, cus, GS);
     const auto* m = reinterpret_cast<const uint32_t*>(meta);
     const auto* q = reinterpret_cast<const uint4*>(quant);
     // one 8-element activation chunk per thread and pass: NCH = ceil(K / (8 * threads))
@@ -682,6 +747,16 @@ asdsl_status launch_preq2(const uint8_t* meta, const uint8_t* quant, const float
 }
 
 }  // namespace
+
+bool preq2_norm_factored() { return env_knob("ASDSL_HIP_NORM_FACTORED") > 0; }
+
+void preq2_plan_shape(int M, int K, int cus, int* lks, int* nu, int* waves, bool* exact) {
+    const Plan p = plan_preq2(M, K, cus, 32);  // the split code does not change the shape
+    *lks = p.lks;
+    *nu = p.nu;
+    *waves = p.waves;
+    *exact = p.exact;
+}
 
 #ifdef ASDSL_WG_TIMELINE
 asdsl_status timeline_set_preq2(void* buf) {
@@ -723,6 +798,7 @@ extern "C" asdsl_status asdsl_gemv_preq2_rmsnorm(const uint8_t* meta, const uint
     ProArgs pa;
     pa.delta = delta;
     pa.nw = norm_w;
+    pa.norm_factored = preq2_norm_factored() ? 1 : 0;
     pa.h_out = h_out;
     pa.eps = eps;
     pa.amax = argmax_key;
@@ -747,6 +823,7 @@ asdsl_status asdsl::preq2_embed_rmsnorm(const uint8_t* meta, const uint8_t* quan
     ASDSL_CU_COUNT(cus);
     ProArgs pa;
     pa.nw = norm_w;
+    pa.norm_factored = preq2_norm_factored() ? 1 : 0;
     pa.h_out = h_out;
     pa.eps = eps;
     pa.amax = clear_key;
@@ -763,7 +840,7 @@ asdsl_status asdsl::preq2_embed_rmsnorm(const uint8_t* meta, const uint8_t* quan
 asdsl_status asdsl::preq2_fused_combine(const uint8_t* meta, const uint8_t* quant, const float* att, float* y,
                                         int out_features, int in_features, int group_size, const float* part,
                                         const int* pos, int nsplit, int tile, int max_splits, int part_stride,
-                                        int head_dim, int max_seq, asdsl_stream_t stream) {
+                                        int head_dim, int max_seq, int pos_limit, asdsl_stream_t stream) {
     if (check_preq2_args(meta, quant, att, y, out_features, in_features, group_size, "gemv_preq2_combine"))
         return ASDSL_ERR_INVALID_ARGUMENT;
     ASDSL_CHECK_ARG(in_features <= 8192, "gemv_preq2_combine: in_features must be <= 8192");
@@ -781,6 +858,7 @@ asdsl_status asdsl::preq2_fused_combine(const uint8_t* meta, const uint8_t* quan
     pa.part_stride = part_stride;
     pa.head_dim = head_dim;
     pa.max_seq = max_seq;
+    pa.pos_limit = pos_limit;
     hipStream_t s = as_hip(stream);
     if (group_size == 32)
         return launch_preq2_fused<32, Pro::kCombine, false>(meta, quant, att, y, out_features, in_features, pa, s, cus);
@@ -802,6 +880,7 @@ extern "C" asdsl_status asdsl_gemv_preq2_rmsnorm_swiglu(const uint8_t* meta, con
     ProArgs pa;
     pa.delta = delta;
     pa.nw = norm_w;
+    pa.norm_factored = preq2_norm_factored() ? 1 : 0;
     pa.h_out = h_out;
     pa.eps = eps;
     pa.thr = threshold;

@@ -27,6 +27,7 @@ template <int GS, int NU, int WAVES, int NB>
 __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_batch_kernel(const uint32_t* __restrict__ meta,
                                                                         const uint4* __restrict__ quant,
                                                                         const float* __restrict__ X,
+                                                                        const float* __restrict__ inv,
                                                                         float* __restrict__ Y, int M, int K,
                                                                         int ncols, int lks) {
     extern __shared__ __align__(16) uint32_t lds[];
@@ -68,8 +69,11 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_batch_kernel(const u
     // tile's weights are requested right after the first columns' loads.
     int tile = static_cast<int>(blockIdx.x);
     const int tile_step = static_cast<int>(gridDim.x);
+    // 8-element chunks per thread: K <= 4096 at 8 waves, <= 8192 at 16, and
+    // 12 waves (K <= 8192) need two
+    constexpr int NCHB = WAVES == 12 ? 2 : 1;
     for (int n0 = 0; n0 < NB; n0 += 4) {
-        ActStage<GS, WAVES * kWave, 1, false> act[4];
+        ActStage<GS, WAVES * kWave, NCHB, false> act[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             if (n0 + q < ncols) act[q].load(X + static_cast<size_t>(n0 + q) * K, nullptr, nullptr, K);
@@ -129,6 +133,11 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_batch_kernel(const u
         const int band = tile * bpt + bl;
 #pragma unroll
         for (int n = 0; n < NB; ++n) acc[n] = slot_sum<SB>(acc[n]);
+        if (inv) {  // the norm-fed single-column GEMV's 1/rms, before the K-split sum
+#pragma unroll
+            for (int n = 0; n < NB; ++n)
+                if (n < ncols) acc[n] *= inv[n];
+        }
         if (tile + tile_step < ntiles) load_tile(tile + tile_step);
         const int row = band * 4 + slot;
         if (lks == 0) {
@@ -527,15 +536,15 @@ int resident_grid(Kern kern, const BatchPlan& p, int threads, size_t lds) {
 }
 
 template <int GS, int WAVES, int NB>
-asdsl_status launch_batch_nb(const BatchPlan& p, const uint32_t* m, const uint4* q, const float* X, float* Y, int M,
-                             int K, int ncols, hipStream_t stream) {
+asdsl_status launch_batch_nb(const BatchPlan& p, const uint32_t* m, const uint4* q, const float* X, const float* inv,
+                             float* Y, int M, int K, int ncols, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(NB) * batch_image_bytes(K, GS);
     const dim3 block(WAVES * kWave);
 #define ASDSL_BATCH_NU(N)                                                                                        \
     case N: {                                                                                                    \
         auto* kern = preq2_gemv_batch_kernel<GS, N, WAVES, NB>;                                                 \
         return launch("preq2_gemv_batch_kernel", kern, dim3(resident_grid(kern, p, WAVES * kWave, lds)), block, \
-                      lds, stream, m, q, X, Y, M, K, ncols, p.lks);                                             \
+                      lds, stream, m, q, X, inv, Y, M, K, ncols, p.lks);                                        \
     }
     switch (p.nu) {
         ASDSL_BATCH_NU(1)
@@ -550,11 +559,29 @@ asdsl_status launch_batch_nb(const BatchPlan& p, const uint32_t* m, const uint4*
 
 template <int GS, int WAVES>
 asdsl_status launch_batch_waves(const BatchPlan& p, const uint32_t* m, const uint4* q, const float* X, float* Y,
-                                int M, int K, int ncols, hipStream_t stream) {
-    if (ncols <= 2) return launch_batch_nb<GS, WAVES, 2>(p, m, q, X, Y, M, K, ncols, stream);
-    if (ncols <= 4) return launch_batch_nb<GS, WAVES, 4>(p, m, q, X, Y, M, K, ncols, stream);
-    if (ncols <= 8) return launch_batch_nb<GS, WAVES, 8>(p, m, q, X, Y, M, K, ncols, stream);
-    return launch_batch_nb<GS, WAVES, 16>(p, m, q, X, Y, M, K, ncols, stream);
+                                int M, int K, int ncols, hipStream_t stream, const float* inv = nullptr) {
+    if (ncols <= 2) return launch_batch_nb<GS, WAVES, 2>(p, m, q, X, inv, Y, M, K, ncols, stream);
+    if (ncols <= 4) return launch_batch_nb<GS, WAVES, 4>(p, m, q, X, inv, Y, M, K, ncols, stream);
+    if (ncols <= 8) return launch_batch_nb<GS, WAVES, 8>(p, m, q, X, inv, Y, M, K, ncols, stream);
+    return launch_batch_nb<GS, WAVES, 16>(p, m, q, X, inv, Y, M, K, ncols, stream);
+}
+
+// plan_batch's column count and grid on the single-column GEMV's launch
+// shape (preq2_plan_shape): K split, units per lane and waves (8, 12 or 16).
+BatchPlan plan_batch_single(int M, int K, int gs, int cus) {
+    BatchPlan p{0, 0, 8, 0, 16, false, cus};
+    preq2_plan_shape(M, K, cus, &p.lks, &p.nu, &p.waves, &p.exact);
+    if (!p.exact || K > 8192) {
+        p.exact = false;
+        return p;
+    }
+    const int bpt = p.waves >> p.lks;
+    p.grid = ((M + 3) / 4 + bpt - 1) / bpt;
+    if (p.waves == 8) p.nb = p.nu <= 2 ? 16 : 8;
+    else p.nb = p.nu <= 4 ? 8 : 4;
+    const size_t img = batch_image_bytes(K, gs);
+    while (p.nb > 2 && static_cast<size_t>(p.nb) * img > 96 * 1024) p.nb >>= 1;
+    return p;
 }
 
 }  // namespace
@@ -638,6 +665,45 @@ asdsl_status asdsl::preq2_fused_batch(const uint8_t* meta, const uint8_t* quant,
         } else {
             st = p.waves == 8 ? launch_batch_waves<128, 8>(p, m, q, Xc, Yc, M, K, nc, s)
                               : launch_batch_waves<128, 16>(p, m, q, Xc, Yc, M, K, nc, s);
+        }
+        if (st != ASDSL_OK) return st;
+    }
+    return ASDSL_OK;
+}
+
+asdsl_status asdsl::preq2_batch_exact(const uint8_t* meta, const uint8_t* quant, const float* X, const float* inv,
+                                      float* Y, int out_features, int in_features, int group_size, int n_cols,
+                                      asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(meta && quant && X && Y, "gemv_preq2_batch_exact: null pointer");
+    ASDSL_CHECK_ARG(group_size == 32 || group_size == 128, "gemv_preq2_batch_exact: group_size must be 32 or 128");
+    ASDSL_CHECK_ARG(out_features > 0 && in_features > 0 && in_features % group_size == 0 && in_features / 32 <= 640,
+                    "gemv_preq2_batch_exact: invalid dimensions");
+    ASDSL_CHECK_ARG(n_cols >= 1 && n_cols <= 64, "gemv_preq2_batch_exact: n_cols must be in [1, 64]");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(X) % 16 == 0, "gemv_preq2_batch_exact: X must be 16-byte aligned");
+    ASDSL_CU_COUNT(cus);
+    const int M = out_features, K = in_features;
+    const BatchPlan p = plan_batch_single(M, K, group_size, cus);
+    if (!p.exact) {
+        set_error("gemv_preq2_batch_exact: the single-column launch shape of %dx%d leaves masked units", M, K);
+        return ASDSL_ERR_UNSUPPORTED;
+    }
+    const auto* m = reinterpret_cast<const uint32_t*>(meta);
+    const auto* q = reinterpret_cast<const uint4*>(quant);
+    hipStream_t s = as_hip(stream);
+    for (int n0 = 0; n0 < n_cols; n0 += p.nb) {
+        const int nc = n_cols - n0 < p.nb ? n_cols - n0 : p.nb;
+        const float* Xc = X + static_cast<size_t>(n0) * K;
+        float* Yc = Y + static_cast<size_t>(n0) * M;
+        const float* ic = inv ? inv + n0 : nullptr;
+        asdsl_status st;
+        if (group_size == 32) {
+            st = p.waves == 8    ? launch_batch_waves<32, 8>(p, m, q, Xc, Yc, M, K, nc, s, ic)
+                 : p.waves == 12 ? launch_batch_waves<32, 12>(p, m, q, Xc, Yc, M, K, nc, s, ic)
+                                 : launch_batch_waves<32, 16>(p, m, q, Xc, Yc, M, K, nc, s, ic);
+        } else {
+            st = p.waves == 8    ? launch_batch_waves<128, 8>(p, m, q, Xc, Yc, M, K, nc, s, ic)
+                 : p.waves == 12 ? launch_batch_waves<128, 12>(p, m, q, Xc, Yc, M, K, nc, s, ic)
+                                 : launch_batch_waves<128, 16>(p, m, q, Xc, Yc, M, K, nc, s, ic);
         }
         if (st != ASDSL_OK) return st;
     }

@@ -1,4 +1,4 @@
-// GGUF weights on the GPU: ggml's Q4_K and Q6_K blocks decoded to fp32, Q4_K
+// GGUF weights on the GPU: ggml's Q4_K, Q5_K, Q6_K and Q8_0 blocks decoded to fp32, Q4_K
 // blocks rearranged into the ASDSL Q4_K variant that asdsl_gemv_q4km_q8 reads,
 // and fp32 weights quantized to symmetric group-wise Q4 the way the
 // reference requantizes GGUF projections (experiments/phi4_cpu_run.py:1437-1466:
@@ -34,6 +34,8 @@ namespace {
 constexpr int kGgufThreads = 256;
 constexpr int kQ4kBytes = 144;
 constexpr int kQ6kBytes = 210;
+constexpr int kQ5kBytes = 176;
+constexpr int kQ80Bytes = 34;
 
 __device__ __forceinline__ float half_bits(uint32_t bits) {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xFFFFu)));
@@ -118,6 +120,63 @@ __global__ __launch_bounds__(kGgufThreads) void dequant_q6k_kernel(const uint8_t
         const int hi = (qh[i] >> (2 * k)) & 3;
         v[i] = __fmul_rn(ds, static_cast<float>((lo | (hi << 4)) - 32));
     }
+    out[t * 2] = make_float4(v[0], v[1], v[2], v[3]);
+    out[t * 2 + 1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// ggml Q5_K -> fp32: 32 lanes per block, lane l writes weights 8l..8l+7 of
+// sub-block j = l/4.  A block is 176 bytes (16-byte aligned blocks keep
+// every field's offset a multiple of 4): fp16 d | fp16 dmin | the Q4_K
+// 12-byte scale/min field | 32 bytes of high bits | 128 bytes of low
+// nibbles.  Weight 32j + i (i < 32) takes the low (even j) or high (odd j)
+// nibble of byte 48 + 32*(j/2) + i and bit j of byte 16 + i as its fifth
+// bit: w = (d*sc)*q - (dmin*m), q in 0..31.
+__global__ __launch_bounds__(kGgufThreads) void dequant_q5k_kernel(const uint8_t* __restrict__ blocks,
+                                                                   float4* __restrict__ out, size_t n_blocks) {
+    const size_t t = static_cast<size_t>(blockIdx.x) * kGgufThreads + threadIdx.x;
+    const size_t b = t / 32;
+    if (b >= n_blocks) return;
+    const int l = static_cast<int>(t % 32);
+    const uint8_t* blk = blocks + b * kQ5kBytes;
+    float d, dmin;
+    uint8_t s[12];
+    load_q4k_head(blk, d, dmin, s);
+    const int j = l / 4;
+    int sc, m;
+    q4k_scale_min(s, j, sc, m);
+    const float d1 = __fmul_rn(d, static_cast<float>(sc));
+    const float m1 = __fmul_rn(dmin, static_cast<float>(m));
+    const int i0 = 8 * (l % 4);
+    const uint2 lo = *reinterpret_cast<const uint2*>(blk + 48 + 32 * (j / 2) + i0);
+    const uint2 hi = *reinterpret_cast<const uint2*>(blk + 16 + i0);
+    const int shift = (j & 1) * 4;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t lw = i < 4 ? lo.x : lo.y;
+        const uint32_t hw = i < 4 ? hi.x : hi.y;
+        const int q = static_cast<int>(((lw >> (8 * (i % 4) + shift)) & 0x0Fu) |
+                                       (((hw >> (8 * (i % 4) + j)) & 1u) << 4));
+        v[i] = __fsub_rn(__fmul_rn(d1, static_cast<float>(q)), m1);
+    }
+    out[t * 2] = make_float4(v[0], v[1], v[2], v[3]);
+    out[t * 2 + 1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// ggml Q8_0 -> fp32: 34 bytes per 32 weights, fp16 d then 32 int8 codes;
+// w = code * d.  One thread per 8 weights, bytes read one at a time (the
+// blocks are 2-byte aligned).
+__global__ __launch_bounds__(kGgufThreads) void dequant_q8_0_kernel(const uint8_t* __restrict__ blocks,
+                                                                    float4* __restrict__ out, size_t n_blocks) {
+    const size_t t = static_cast<size_t>(blockIdx.x) * kGgufThreads + threadIdx.x;
+    const size_t b = t / 4;
+    if (b >= n_blocks) return;
+    const uint8_t* blk = blocks + b * kQ80Bytes;
+    const float d = half_bits(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
+    const uint8_t* q = blk + 2 + 8 * (t % 4);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(static_cast<float>(static_cast<int8_t>(q[i])), d);
     out[t * 2] = make_float4(v[0], v[1], v[2], v[3]);
     out[t * 2 + 1] = make_float4(v[4], v[5], v[6], v[7]);
 }
@@ -242,6 +301,33 @@ extern "C" asdsl_status asdsl_dequant_gguf_q6k(const uint8_t* blocks, float* wei
     ASDSL_CHECK_ARG(aligned(weights, 16), "dequant_gguf_q6k: weights must be 16-byte aligned");
     const size_t n = static_cast<size_t>(rows) * (cols / 256);
     return launch("dequant_q6k_kernel", dequant_q6k_kernel, dim3(grid_for(n * 32)), dim3(kGgufThreads), 0,
+                  as_hip(stream), blocks, reinterpret_cast<float4*>(weights), n);
+}
+
+extern "C" asdsl_status asdsl_dequant_gguf_q5k(const uint8_t* blocks, float* weights, int rows, int cols,
+                                               asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(blocks && weights, "dequant_gguf_q5k: null pointer");
+    const asdsl_status cs = check_k_blocks("dequant_gguf_q5k", rows, cols);
+    if (cs != ASDSL_OK) return cs;
+    ASDSL_CHECK_ARG(aligned(blocks, 16) && aligned(weights, 16),
+                    "dequant_gguf_q5k: blocks and weights must be 16-byte aligned");
+    const size_t n = static_cast<size_t>(rows) * (cols / 256);
+    return launch("dequant_q5k_kernel", dequant_q5k_kernel, dim3(grid_for(n * 32)), dim3(kGgufThreads), 0,
+                  as_hip(stream), blocks, reinterpret_cast<float4*>(weights), n);
+}
+
+extern "C" asdsl_status asdsl_dequant_gguf_q8_0(const uint8_t* blocks, float* weights, int rows, int cols,
+                                                asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(blocks && weights, "dequant_gguf_q8_0: null pointer");
+    if (rows <= 0 || cols <= 0 || cols % 32 != 0) {
+        set_error("dequant_gguf_q8_0: rows must be positive and cols a positive multiple of 32 (got %d x %d)", rows,
+                  cols);
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    }
+    ASDSL_CHECK_ARG(aligned(blocks, 2) && aligned(weights, 16),
+                    "dequant_gguf_q8_0: blocks must be 2-byte and weights 16-byte aligned");
+    const size_t n = static_cast<size_t>(rows) * (cols / 32);
+    return launch("dequant_q8_0_kernel", dequant_q8_0_kernel, dim3(grid_for(n * 4)), dim3(kGgufThreads), 0,
                   as_hip(stream), blocks, reinterpret_cast<float4*>(weights), n);
 }
 

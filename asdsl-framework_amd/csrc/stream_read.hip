@@ -35,10 +35,136 @@ __global__ __launch_bounds__(kReadThreads) void stream_read_kernel(const u32x4* 
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// The calibration read in the shapes a launch can take: THREADS threads per
+// workgroup, LIF 16-byte loads in flight per lane, and either SLAB = false
+// (grid-stride: each load instruction of the grid covers consecutive
+// 16-byte units, the kernel above) or SLAB = true (workgroup w reads one
+// contiguous slab of ceil(units / grid) units, as a GEMV workgroup reads its
+// bands).
+template <int THREADS, int LIF, bool SLAB>
+__global__ __launch_bounds__(THREADS) void stream_read_sweep_kernel(const u32x4* __restrict__ p, size_t n16,
+                                                                     uint32_t* __restrict__ sink) {
+    uint32_t acc = 0;
+    size_t i, end, stride;
+    if (SLAB) {
+        const size_t slab = (n16 + gridDim.x - 1) / gridDim.x;
+        const size_t begin = static_cast<size_t>(blockIdx.x) * slab;
+        end = begin + slab < n16 ? begin + slab : n16;
+        i = begin + threadIdx.x;
+        stride = THREADS;
+    } else {
+        end = n16;
+        stride = static_cast<size_t>(gridDim.x) * THREADS;
+        i = static_cast<size_t>(blockIdx.x) * THREADS + threadIdx.x;
+    }
+    for (; i + (LIF - 1) * stride < end; i += LIF * stride) {
+        u32x4 v[LIF];
+#pragma unroll
+        for (int j = 0; j < LIF; ++j) v[j] = __builtin_nontemporal_load(p + i + j * stride);
+#pragma unroll
+        for (int j = 0; j < LIF; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    for (; i < end; i += stride) {
+        const u32x4 a = __builtin_nontemporal_load(p + i);
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+// The read a GEMV makes: workgroup w reads slab w of THREADS * L consecutive
+// 16-byte units, every one of its L loads per lane requested before any is
+// used (a GEMV tile's weights are requested at once), slabs taken grid-stride
+// when the grid is smaller than the slab count.  With one slab per
+// workgroup and every workgroup resident, the whole buffer is requested at
+// the start, as a GEMV launch does; the launch shape (THREADS, L, grid) sets
+// how many waves per compute unit hold those requests.
+template <int THREADS, int L>
+__global__ __launch_bounds__(THREADS) void stream_read_oneshot_kernel(const u32x4* __restrict__ p, size_t n16,
+                                                                       uint32_t* __restrict__ sink) {
+    constexpr size_t kSlab = static_cast<size_t>(THREADS) * L;
+    const size_t nslabs = (n16 + kSlab - 1) / kSlab;
+    uint32_t acc = 0;
+    for (size_t sl = blockIdx.x; sl < nslabs; sl += gridDim.x) {
+        const size_t base = sl * kSlab + threadIdx.x;
+        u32x4 v[L];
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            const size_t i = base + static_cast<size_t>(j) * THREADS;
+            v[j] = __builtin_nontemporal_load(p + (i < n16 ? i : n16 - 1));
+        }
+#pragma unroll
+        for (int j = 0; j < L; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+template <int THREADS>
+asdsl_status launch_oneshot(int l, int grid, const u32x4* p, size_t n16, uint32_t* sink, hipStream_t s) {
+#define ASDSL_ONESHOT(N)                                                                                   \
+    case N:                                                                                                \
+        return launch("stream_read_oneshot_kernel", stream_read_oneshot_kernel<THREADS, N>, dim3(grid),   \
+                      dim3(THREADS), 0, s, p, n16, sink);
+    switch (l) {
+        ASDSL_ONESHOT(2)
+        ASDSL_ONESHOT(3)
+        ASDSL_ONESHOT(4)
+        ASDSL_ONESHOT(6)
+        ASDSL_ONESHOT(8)
+        default: ASDSL_ONESHOT(12)
+    }
+#undef ASDSL_ONESHOT
+}
+
+template <int THREADS, int LIF>
+asdsl_status launch_sweep(bool slab, int grid, const u32x4* p, size_t n16, uint32_t* sink, hipStream_t s) {
+    return slab ? launch("stream_read_sweep_kernel", stream_read_sweep_kernel<THREADS, LIF, true>, dim3(grid),
+                         dim3(THREADS), 0, s, p, n16, sink)
+                : launch("stream_read_sweep_kernel", stream_read_sweep_kernel<THREADS, LIF, false>, dim3(grid),
+                         dim3(THREADS), 0, s, p, n16, sink);
+}
+
+template <int THREADS>
+asdsl_status launch_sweep_lif(int lif, bool slab, int grid, const u32x4* p, size_t n16, uint32_t* sink,
+                              hipStream_t s) {
+    switch (lif) {
+        case 4: return launch_sweep<THREADS, 4>(slab, grid, p, n16, sink, s);
+        case 8: return launch_sweep<THREADS, 8>(slab, grid, p, n16, sink, s);
+        default: return launch_sweep<THREADS, 16>(slab, grid, p, n16, sink, s);
+    }
+}
+
 }  // namespace
 }  // namespace asdsl
 
 using namespace asdsl;
+
+extern "C" asdsl_status asdsl_stream_read_ex(const void* data, size_t bytes, uint32_t* sink, int grid, int threads,
+                                             int inflight, int slab, asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(data && sink, "stream_read_ex: null pointer");
+    ASDSL_CHECK_ARG(bytes >= 16 && bytes % 16 == 0, "stream_read_ex: bytes must be a positive multiple of 16");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(data) % 16 == 0, "stream_read_ex: data must be 16-byte aligned");
+    ASDSL_CHECK_ARG(grid > 0 && grid <= 65536, "stream_read_ex: grid must be in [1, 65536]");
+    ASDSL_CHECK_ARG(threads == 256 || threads == 512 || threads == 1024, "stream_read_ex: threads must be 256, 512 "
+                    "or 1024");
+    ASDSL_CHECK_ARG(slab == 0 || slab == 1 || slab == 2, "stream_read_ex: slab must be 0, 1 or 2");
+    const u32x4* p = static_cast<const u32x4*>(data);
+    hipStream_t s = as_hip(stream);
+    const size_t n16 = bytes / 16;
+    if (slab == 2) {
+        ASDSL_CHECK_ARG(threads == 256 || threads == 512, "stream_read_ex: the one-shot read takes 256 or 512 threads");
+        ASDSL_CHECK_ARG(inflight == 2 || inflight == 3 || inflight == 4 || inflight == 6 || inflight == 8 ||
+                            inflight == 12,
+                        "stream_read_ex: the one-shot read takes 2, 3, 4, 6, 8 or 12 loads per lane");
+        return threads == 256 ? launch_oneshot<256>(inflight, grid, p, n16, sink, s)
+                              : launch_oneshot<512>(inflight, grid, p, n16, sink, s);
+    }
+    ASDSL_CHECK_ARG(inflight == 4 || inflight == 8 || inflight == 16, "stream_read_ex: inflight must be 4, 8 or 16");
+    switch (threads) {
+        case 256: return launch_sweep_lif<256>(inflight, slab != 0, grid, p, n16, sink, s);
+        case 512: return launch_sweep_lif<512>(inflight, slab != 0, grid, p, n16, sink, s);
+        default: return launch_sweep_lif<1024>(inflight, slab != 0, grid, p, n16, sink, s);
+    }
+}
 
 extern "C" asdsl_status asdsl_stream_read(const void* data, size_t bytes, uint32_t* sink, int grid,
                                           asdsl_stream_t stream) {

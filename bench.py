@@ -60,6 +60,7 @@ LM_HEAD = (200064, 3072, 128)
 # profiles/hbm_traffic_gemv_decode_sparse_down.md.  A property of the
 # kernel's access pattern: re-measure when the kernel's loads change.
 GATE_UP_TRAFFIC_BYTES = 31_680_680
+GATE_UP_BYTES = 31_535_104  # gemv_bytes(16384, 3072): the gate_up GEMV's algorithmic bytes
 
 
 def gemv_bytes(M: int, K: int, gs: int = GS) -> int:
@@ -352,6 +353,68 @@ def lm_head_kernel(lib, capture, timed_replays):
             "frac_of_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def shape_sweep(args) -> int:
+    """Each layer GEMV (the headline's four shapes, preq2 g32) timed like the
+    headline's per-GEMV figure (a graph of 4*L launches over L rotated weight
+    sets) under every launch shape the tuning switches give: the K split
+    (ASDSL_HIP_KSPLIT: the plan's, 1, 2, 4) times the activation source
+    (ASDSL_HIP_XLDS: registers or LDS) or the first tile's weight requests
+    split around the activation staging (ASDSL_HIP_PRE_SPLIT 1..3).  The
+    switches are read per call, so each graph is captured under its own
+    setting.  Outputs are compared with the plan's launch (relative L2; the
+    K split changes the fp32 summation order only)."""
+    import numpy as np
+    import torch
+
+    from asdsl import _hip
+
+    layers, xs, ys = build_layers(args.layers, seed=42)
+    lib = _hip.LIB
+    ptrs = [{n: (_hip.ptr(m), _hip.ptr(q)) for n, (m, q) in L.items()} for L in layers]
+    L = len(layers)
+    knobs = ("ASDSL_HIP_KSPLIT", "ASDSL_HIP_XLDS", "ASDSL_HIP_PRE_SPLIT")
+    saved = {k: os.environ.get(k) for k in knobs}
+    try:
+        for n, M, K in LAYER:
+            rows, want = [], None
+            for ks in ("", "1", "2", "4"):
+                for xl, sp in (("", ""), ("1", ""), ("", "1"), ("", "2"), ("", "3")):
+                    for k, v in zip(knobs, (ks, xl, sp)):
+                        os.environ[k] = v
+                    y = ys[n]
+
+                    def calls(h, n=n, M=M, K=K):
+                        for i in range(4 * L):
+                            p = ptrs[i % L]
+                            if lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], _hip.ptr(xs[n]), _hip.ptr(y), M, K, GS,
+                                                          h):
+                                raise RuntimeError(_hip.last_error())
+                    g = capture(calls)
+                    reps = 25
+                    us = 1e3 * timed_replays(g, reps) / (reps * 4 * L)
+                    del g
+                    p0 = ptrs[0][n]
+                    if lib.asdsl_gemv_preq2_fused(p0[0], p0[1], _hip.ptr(xs[n]), _hip.ptr(y), M, K, GS,
+                                                  int(torch.cuda.current_stream().cuda_stream)):
+                        raise RuntimeError(_hip.last_error())
+                    got = y.cpu().numpy().astype(np.float64)
+                    if want is None:
+                        want = got
+                    rel = float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+                    rows.append({"ksplit": ks or "plan", "x_from": "lds" if xl else "regs", "pre_split": int(sp or 0),
+                                 "us": round(us, 3),
+                                 "GB/s": round(gemv_bytes(M, K) / (us * 1e-6) / 1e9, 1), "rel_l2_vs_plan": rel})
+            print(json.dumps({"shape_sweep": n, "shape": [M, K], "bytes": gemv_bytes(M, K), "rows": rows}),
+                  flush=True)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    return 0
+
+
 def stream_floor_us(lib, nbytes: int, launches: int = 64) -> dict:
     """The practical ceiling for one launch that streams `nbytes`: the library's
     calibration read kernel (asdsl_stream_read), a graph of back-to-back
@@ -380,6 +443,79 @@ def stream_floor_us(lib, nbytes: int, launches: int = 64) -> dict:
     del bufs
     torch.cuda.empty_cache()
     return {"us": round(best[0], 3), "GB/s": round(nbytes / (best[0] * 1e-6) / 1e9, 1), "grid": best[1]}
+
+
+def ceiling_configs(nbytes: int, oneshot_only: bool = False) -> list[tuple[int, int, int, int]]:
+    """(slab, threads, inflight, grid) of the ceiling sweep: the grid-stride
+    and slab reads over grids 256..2048, 256/512/1024 threads, 4/8/16 loads in
+    flight per lane; and the one-shot read a GEMV tile makes (slab 2: 256 or
+    512 threads, 2..12 loads per lane, one slab per workgroup, so the grid is
+    bytes / (threads * loads * 16))."""
+    out = []
+    if not oneshot_only:
+        out = [(slab, threads, lif, grid) for slab in (0, 1) for threads in (256, 512, 1024) for lif in (4, 8, 16)
+               for grid in (256, 512, 1024, 2048)]
+    for threads in (256, 512):
+        for lif in (2, 3, 4, 6, 8, 12):
+            grid = -(-nbytes // (16 * threads * lif))
+            if grid <= 65536:
+                out.append((2, threads, lif, grid))
+    return out
+
+
+def ceiling_sweep(lib, sizes=None, launches: int = 64, oneshot_only: bool = False) -> list[dict]:
+    """The single-launch read ceiling against byte count: asdsl_stream_read_ex
+    in every launch shape of ceiling_configs, each a graph of `launches`
+    back-to-back launches over rotated buffers (~1 GB), timed like the GEMVs
+    (per-launch average, dispatch gaps included); beside it torch's own
+    reductions over the same bytes (fp32 and uint8 sums, eager, per call).
+    One JSON row per byte count: every configuration's us and the best."""
+    import torch
+
+    from asdsl import _hip
+
+    sizes = sizes or [("o_proj", 5922816), ("qkv", 9863168), ("down_g32", 15773696), ("gate_up", GATE_UP_BYTES),
+                      ("2x_gate_up", 2 * GATE_UP_BYTES), ("lm_head_g128", 327316992)]
+    rows = []
+    for name, nbytes in sizes:
+        nbytes = (nbytes + 255) // 256 * 256
+        ncopies = max(2, min(16, (1 << 30) // nbytes))
+        bufs = [torch.ones(nbytes, dtype=torch.uint8, device="cuda") for _ in range(ncopies)]
+        sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+        res = []
+        for slab, threads, lif, grid in ceiling_configs(nbytes, oneshot_only):
+            def calls(h, grid=grid, threads=threads, lif=lif, slab=slab):
+                for i in range(launches):
+                    if lib.asdsl_stream_read_ex(_hip.ptr(bufs[i % ncopies]), nbytes, _hip.ptr(sink), grid,
+                                                threads, lif, slab, h):
+                        raise RuntimeError(_hip.last_error())
+            g = capture(calls)
+            us = 1e3 * timed_replays(g, 6) / (6 * launches)
+            del g
+            res.append({"slab": slab, "threads": threads, "inflight": lif, "grid": grid, "us": round(us, 3)})
+        best = min(res, key=lambda r: r["us"])
+        torch_rows = {}
+        for label, view in (("torch_sum_fp32", lambda b: b.view(torch.float32)), ("torch_sum_u8", lambda b: b)):
+            for i in range(4):
+                view(bufs[i % ncopies]).sum()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            n = 48
+            e0.record()
+            for i in range(n):
+                view(bufs[i % ncopies]).sum()
+            e1.record()
+            torch.cuda.synchronize()
+            torch_rows[label] = round(1e3 * e0.elapsed_time(e1) / n, 3)
+        row = {"ceiling": name, "bytes": nbytes, "best": best,
+               "best_GB/s": round(nbytes / (best["us"] * 1e-6) / 1e9, 1),
+               "best_frac_of_8TB/s": round(nbytes / (best["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+               "torch_eager_us_per_call": torch_rows, "configs": res}
+        rows.append(row)
+        print(json.dumps({k: v for k, v in row.items() if k != "configs"}), flush=True)
+        del bufs
+        torch.cuda.empty_cache()
+    return rows
 
 
 # --------------------------------------------------------------------------- decode
@@ -464,12 +600,25 @@ def verify_pass_us(eng, ctx: int, per_token_us, counts=(4, 8, 16), reps: int = 2
     """Multi-token verify pass (asdsl_decode_verify) of N tokens at position
     ctx, captured in a HIP graph (the token ids and the position already on
     the device) and replayed: microseconds per pass against N single-token
-    steps at the same context."""
+    steps at the same context; the default form (dot4 in the single-token
+    GEMVs' launch shapes, bit for bit the single-token step) at the top level,
+    the MFMA form (ASDSL_HIP_VERIFY_MFMA=1) under "mfma"."""
+    res = {"ctx": ctx, **_verify_pass_rows(eng, ctx, per_token_us, counts, reps)}
+    os.environ["ASDSL_HIP_VERIFY_MFMA"] = "1"
+    try:
+        res["mfma"] = _verify_pass_rows(eng, ctx, per_token_us, counts, reps)
+    finally:
+        del os.environ["ASDSL_HIP_VERIFY_MFMA"]
+    res["mfma_vs_dot4"] = verify_flip_rate(eng, ctx, max(counts))
+    return res
+
+
+def _verify_pass_rows(eng, ctx: int, per_token_us, counts, reps) -> dict:
     import torch
 
     from asdsl import _hip
 
-    res = {"ctx": ctx}
+    res = {}
     eng.prefill_kv_random(ctx, seed=ctx)
     for n in counts:
         eng.forward_batch_all_logits(list(range(1, n + 1)), ctx)  # allocates and warms the pass
@@ -498,7 +647,6 @@ def verify_pass_us(eng, ctx: int, per_token_us, counts=(4, 8, 16), reps: int = 2
             row["speedup_vs_serial"] = round(n * per_token_us / us, 2)
         res[str(n)] = row
         del g
-    res["mfma_vs_dot4"] = verify_flip_rate(eng, ctx, max(counts))
     return res
 
 
@@ -552,25 +700,26 @@ def pld_tokens_per_s(eng, new_tokens: int = 96, max_draft_k: int = 8) -> dict:
 
 
 def verify_flip_rate(eng, ctx: int, n: int) -> dict:
-    """The verify pass of tokens 1..n at ctx with the projections as MFMA
-    batched GEMVs (the default) and as the dot4 forms
-    (ASDSL_HIP_VERIFY_DOT4=1, whose per-column arithmetic follows the
-    single-token step): how often the greedy tokens agree and the logits'
-    relative L2 distance, plus the dot4 pass's time (eager, one pass)."""
+    """The verify pass of tokens 1..n at ctx with the projections as the
+    dot4 forms in the single-token launch shapes (the default, bit for bit
+    the single-token step) and as MFMA batched GEMVs
+    (ASDSL_HIP_VERIFY_MFMA=1): how often the greedy tokens agree and the
+    logits' relative L2 distance, plus the dot4 pass's time (eager, one
+    pass)."""
     import torch
 
     toks = list(range(1, n + 1))
-    mf = eng.forward_batch_all_logits(toks, ctx).float().cpu().numpy()
-    mt = eng.verify_next_tokens()
-    os.environ["ASDSL_HIP_VERIFY_DOT4"] = "1"
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    d4 = eng.forward_batch_all_logits(toks, ctx).float().cpu().numpy()
+    dot4_ms = 1e3 * (time.perf_counter() - t0)
+    dt = eng.verify_next_tokens()
+    os.environ["ASDSL_HIP_VERIFY_MFMA"] = "1"
     try:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        d4 = eng.forward_batch_all_logits(toks, ctx).float().cpu().numpy()
-        dot4_ms = 1e3 * (time.perf_counter() - t0)
-        dt = eng.verify_next_tokens()
+        mf = eng.forward_batch_all_logits(toks, ctx).float().cpu().numpy()
+        mt = eng.verify_next_tokens()
     finally:
-        del os.environ["ASDSL_HIP_VERIFY_DOT4"]
+        del os.environ["ASDSL_HIP_VERIFY_MFMA"]
     errs = [float(np.linalg.norm(mf[c] - d4[c]) / np.linalg.norm(d4[c])) for c in range(n)]
     return {"columns": n, "same_token_share": sum(a == b for a, b in zip(mt, dt)) / n,
             "rel_l2_median": float(np.median(errs)), "rel_l2_max": float(max(errs)),
@@ -1220,6 +1369,61 @@ def decode_timeline(ctx: int, n_layers: int = 32, steps: int = 8, seed: int = 11
             "kernels": kernels}
 
 
+def gemv_timeline(name: str, launches: int = 16) -> dict:
+    """Per-workgroup timeline of one layer GEMV (preq2 g32, one of the
+    headline's four shapes) in the last of `launches` graph-replayed launches
+    over rotated weights.  Needs the timing build, like --decode-timeline.
+    Stamps per workgroup (thread 0): start, activation staged, staging
+    barrier passed, first tile's dot products done, end; reported as
+    percentiles over workgroups of each stamp's time from the first start."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from asdsl import _hip
+
+    try:
+        setter = _hip.LIB.asdsl_timeline_set_buffer
+    except AttributeError:
+        raise SystemExit("--gemv-timeline needs the timing build: "
+                         "ASDSL_HIP_LIB=asdsl-framework_amd/lib/libasdsl_hip_timeline.so") from None
+    setter.argtypes = [ctypes.c_void_p]
+    setter.restype = ctypes.c_int
+    (n, M, K), = [row for row in LAYER if row[0] == name]
+    layers, xs, ys = build_layers(8, seed=42)
+    lib = _hip.LIB
+    ptrs = [L[n] for L in layers]
+
+    def calls(h):
+        for i in range(launches):
+            m, q = ptrs[i % len(ptrs)]
+            if lib.asdsl_gemv_preq2_fused(_hip.ptr(m), _hip.ptr(q), _hip.ptr(xs[n]), _hip.ptr(ys[n]), M, K, GS, h):
+                raise RuntimeError(_hip.last_error())
+    g = capture(calls)
+    g.replay()
+    torch.cuda.synchronize()
+    buf = torch.zeros(8 * 1024 * 8, dtype=torch.int64, device="cuda")
+    _hip.check(setter(ctypes.c_void_p(buf.data_ptr())), "asdsl_timeline_set_buffer")
+    g.replay()
+    torch.cuda.synchronize()
+    _hip.check(setter(None), "asdsl_timeline_set_buffer")
+    t = buf.cpu().numpy().reshape(8, 1024, 8).astype(np.float64)
+    out = {"gemv": n, "shape": [M, K], "bytes": gemv_bytes(M, K), "launches": launches}
+    for slot in (3, 7):
+        a = t[slot]
+        a = a[(a[:, 0] > 0) & (a[:, 4] > 0)]
+        if not len(a):
+            continue
+        us = (a[:, :5] - a[:, 0].min()) * 0.01  # 100 MHz ticks -> us from the first start
+        pct = {}
+        for i, label in enumerate(("start", "staged", "barrier", "first_tile", "end")):
+            pct[label] = [round(float(np.percentile(us[:, i], q)), 2) for q in (0, 10, 50, 90, 100)]
+        out["workgroups"] = int(len(a))
+        out["stamps_us_p0_p10_p50_p90_p100"] = pct
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1238,6 +1442,15 @@ def main() -> int:
                     help="per-workgroup timeline of one decode layer at these contexts (needs the timing "
                          "build: ASDSL_HIP_LIB=asdsl-framework_amd/lib/libasdsl_hip_timeline.so)")
     ap.add_argument("--timeline-layers", type=int, default=32, help="--decode-timeline: layers of the model")
+    ap.add_argument("--gemv-timeline", nargs="+", default=None, choices=[n for n, _, _ in LAYER],
+                    help="per-workgroup timeline of these layer GEMVs (the timing build, as --decode-timeline)")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="only the single-launch read ceiling sweep (asdsl_stream_read_ex) against byte count")
+    ap.add_argument("--ceiling-out", default="", help="--ceiling: also write every configuration to this JSON file")
+    ap.add_argument("--ceiling-oneshot", action="store_true", help="--ceiling: only the one-shot (slab 2) reads")
+    ap.add_argument("--shape-sweep", action="store_true",
+                    help="only the layer GEMVs under each launch shape the tuning switches select "
+                         "(ASDSL_HIP_KSPLIT x ASDSL_HIP_XLDS), one JSON line per GEMV")
     ap.add_argument("--suite", action="store_true",
                     help="one JSON line per hot-path row: kernel at its workload vs the HBM roofline, "
                          "with the reference's compiled CPU kernel timed on the same inputs")
@@ -1258,6 +1471,19 @@ def main() -> int:
 
     if args.suite:
         return run_suite(args)
+    if args.shape_sweep:
+        return shape_sweep(args)
+    if args.ceiling:
+        from asdsl import _hip
+
+        rows = ceiling_sweep(_hip.LIB, oneshot_only=args.ceiling_oneshot)
+        if args.ceiling_out:
+            Path(args.ceiling_out).write_text(json.dumps(rows, indent=1))
+        return 0
+    if args.gemv_timeline:
+        for name in args.gemv_timeline:
+            print(json.dumps({"gemv_timeline": gemv_timeline(name)}), flush=True)
+        return 0
     if args.decode_timeline:
         for ctx in args.decode_timeline:
             print(json.dumps({"decode_timeline": decode_timeline(ctx, n_layers=args.timeline_layers)}), flush=True)

@@ -12,7 +12,10 @@
  * (size from the matching *_work_bytes query) and allocates nothing; the
  * plain forms use one buffer per device that the library grows on first use
  * and keeps (calls that overlap on one device on unordered streams race on
- * it; growing is refused under graph capture).
+ * it; growing is refused under graph capture).  A caller that must not see
+ * hipMalloc on the call path reserves that buffer once at load,
+ * asdsl_reserve_workspace(bytes): the plain forms then never allocate, and
+ * one that needs more than was reserved returns ASDSL_ERR_INVALID_ARGUMENT.
  * Buffers are owned by the
  * caller, exactly as in the reference kernels, which take caller-owned
  * host buffers (asdsl/kernels/native/gemv_q4_kernel.h:25-121).
@@ -63,6 +66,16 @@ const char* asdsl_last_error(void);
  * get_num_threads/has_openmp (asdsl/kernels/native/gemv_q4_avx2.cpp:1490-1505). */
 int asdsl_device_cu_count(void);
 
+/* Allocates the current device's library work buffer (the one the plain
+ * forms of the work-buffer calls use) to at least `bytes` now and fixes it:
+ * from then on no call on this device allocates, and a plain-form call that
+ * needs more than `bytes` returns ASDSL_ERR_INVALID_ARGUMENT (the matching
+ * *_work_bytes query gives each call's need).  bytes = 0 returns to growth on
+ * demand.  Call it once per device at load, outside graph capture.  No
+ * reference counterpart: the reference kernels allocate only thread-local
+ * host scratch (gemv_q4_preq_restored.cpp:483-484, gemv_preq2_avx2.cpp:315-316). */
+asdsl_status asdsl_reserve_workspace(size_t bytes);
+
 /* Instrumentation, no reference counterpart: arms two HIP events (hipEvent_t,
  * created by the caller; either may be NULL) for the calling thread's next
  * kernel launch by this library.  The launch records them as part of the
@@ -98,6 +111,18 @@ asdsl_status asdsl_profile_stages_end(int capacity, const char** labels, float* 
  * if the loaded words fold to a fixed sentinel).  Timed like a GEMV it gives
  * the practical ceiling for streaming that many bytes in one launch. */
 asdsl_status asdsl_stream_read(const void* data, size_t bytes, uint32_t* sink, int grid, asdsl_stream_t stream);
+
+/* The same read in the launch shapes a sweep of the single-launch ceiling
+ * covers: `threads` (256, 512 or 1024) per workgroup, `inflight` (4, 8 or
+ * 16) 16-byte loads in flight per lane, grid-stride units (slab = 0) or one
+ * contiguous slab of bytes/grid per workgroup (slab = 1, a GEMV
+ * workgroup's access).  slab = 2 is the one-shot read a GEMV tile makes:
+ * workgroup w reads slabs of threads * inflight consecutive 16-byte units
+ * (threads 256 or 512, inflight 2, 3, 4, 6, 8 or 12 loads per lane, all
+ * requested before any is used), slabs w, w + grid, ...  No reference
+ * counterpart (calibration). */
+asdsl_status asdsl_stream_read_ex(const void* data, size_t bytes, uint32_t* sink, int grid, int threads,
+                                  int inflight, int slab, asdsl_stream_t stream);
 
 /* Calibration, no reference counterpart: the cost of a grid-wide handoff
  * inside one kernel.  One cooperative launch of `grid` workgroups (256
@@ -507,24 +532,43 @@ typedef struct asdsl_decode_model {
 /* Bytes of device work buffer asdsl_decode_token needs (0 for an invalid model). */
 size_t asdsl_decode_work_bytes(const asdsl_decode_model* model);
 
+/* Bits of the decode step's flags word (a uint32 in the work buffer at
+ * asdsl_decode_flags_offset(model) bytes).  The step only sets them; the
+ * caller zeroes the word before the first step (with the whole buffer) and
+ * after reading a raised bit.  A step that raises one computed its attention
+ * as zero and wrote no K/V row, so its logits are not the model's. */
+#define ASDSL_DECODE_FLAG_POS_LIMIT 1u /* *pos was at or past asdsl_decode_token_upto's pos_limit */
+#define ASDSL_DECODE_FLAG_POS_RANGE 2u /* *pos was outside [0, max_seq) */
+
+/* Byte offset of the flags word in the decode work buffer (0 for an invalid
+ * model; a valid model's word is never at offset 0).  No reference
+ * counterpart (the reference throws std::out_of_range on the host,
+ * unified_engine.cpp:1352-1354). */
+size_t asdsl_decode_flags_offset(const asdsl_decode_model* model);
+
 /* Queues one greedy decode step on `stream`: embeds *token (device int),
  * runs every layer at position *pos (device int), writes logits[vocab], then
  * sets *token to the argmax and increments *pos.  Nothing else changes on
  * the host side between steps, so a HIP graph of one call replays step after
- * step.  work: asdsl_decode_work_bytes() bytes, 256-byte aligned, scratch
- * whose contents after a call are unspecified.
+ * step.  work: asdsl_decode_work_bytes() bytes, 256-byte aligned, zeroed
+ * before the first step; apart from the flags word its contents after a call
+ * are unspecified.  A position outside [0, max_seq) raises
+ * ASDSL_DECODE_FLAG_POS_RANGE.
  * Replaces UnifiedEngine::forward_token + greedy argmax
  * (asdsl/kernels/native/unified_engine.cpp:1339-1688,207-233). */
 asdsl_status asdsl_decode_token(const asdsl_decode_model* model, int* token, int* pos, float* logits,
                                 void* work, asdsl_stream_t stream);
 
-/* The same step for a position *pos < pos_limit (the caller guarantees it;
- * asdsl_decode_token is pos_limit = max_seq).  The launch is shaped for that
- * range: the attention grid covers only the splits such positions use (one
- * per 64 positions, at most 32), and below 512 the o_proj GEMV merges them
- * in its prologue, with no combine launch (same bits as the combine kernel).
- * A HIP graph of one call then replays for every position below pos_limit.  No reference counterpart (the
- * reference passes the position by value, unified_engine.cpp:1339). */
+/* The same step for a position *pos < pos_limit (asdsl_decode_token is
+ * pos_limit = max_seq).  The launch is shaped for that range: the attention
+ * grid covers only the splits such positions use (one per 64 positions, at
+ * most 32), and below 512 the o_proj GEMV merges them in its prologue, with
+ * no combine launch (same bits as the combine kernel).  A HIP graph of one
+ * call then replays for every position below pos_limit.  A replay at a
+ * position at or past pos_limit is detected on the device: its attention is
+ * zero, no K/V row is written, ASDSL_DECODE_FLAG_POS_LIMIT is raised, and
+ * *token and *pos still advance.  No reference counterpart (the reference
+ * passes the position by value, unified_engine.cpp:1339). */
 asdsl_status asdsl_decode_token_upto(const asdsl_decode_model* model, int* token, int* pos, int pos_limit,
                                      float* logits, void* work, asdsl_stream_t stream);
 
@@ -649,6 +693,20 @@ asdsl_status asdsl_dequant_gguf_q4k(const uint8_t* blocks, float* weights, int r
  * aligned.  Replaces dequant_tensor for Q6_K (asdsl/io/gguf_loader.py:150-181). */
 asdsl_status asdsl_dequant_gguf_q6k(const uint8_t* blocks, float* weights, int rows, int cols,
                                    asdsl_stream_t stream);
+
+/* ggml Q5_K blocks[rows][cols/256][176] -> fp32 weights[rows][cols]:
+ * w = (d * sc) * q - (dmin * m) per 32-weight sub-block, q = the 4-bit code
+ * with its fifth bit from the 32 high-bit bytes.  blocks and weights 16-byte
+ * aligned.  Replaces dequant_tensor for Q5_K (asdsl/io/gguf_loader.py:150-181). */
+asdsl_status asdsl_dequant_gguf_q5k(const uint8_t* blocks, float* weights, int rows, int cols,
+                                   asdsl_stream_t stream);
+
+/* ggml Q8_0 blocks[rows][cols/32][34] -> fp32 weights[rows][cols] (cols a
+ * multiple of 32): w = code * d, one fp16 d per 32 int8 codes.  blocks 2-byte
+ * and weights 16-byte aligned.  Replaces dequant_tensor for Q8_0
+ * (asdsl/io/gguf_loader.py:150-181). */
+asdsl_status asdsl_dequant_gguf_q8_0(const uint8_t* blocks, float* weights, int rows, int cols,
+                                    asdsl_stream_t stream);
 
 /* ggml Q4_K blocks -> the ASDSL Q4_K variant blocks that asdsl_gemv_q4km_q8
  * reads (6-bit scales and mins as one linear bitstream, each sub-block's

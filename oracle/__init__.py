@@ -362,9 +362,18 @@ def reference_q4_s256():
 
 
 # ------------------------------------------------------------------ GGUF
+def _blocks_in(blocks, n_blocks: int, block_bytes: int) -> np.ndarray:
+    """The block bytes as uint8, refusing a buffer shorter than n_blocks blocks
+    (the C routines read n_blocks * block_bytes bytes)."""
+    b = _u8(blocks)
+    if n_blocks < 0 or b.size < n_blocks * block_bytes:
+        raise ValueError(f"{n_blocks} blocks of {block_bytes} bytes need {n_blocks * block_bytes} bytes, got {b.size}")
+    return b
+
+
 def dequant_gguf_q4k(blocks, n_blocks: int) -> np.ndarray:
     """ggml Q4_K blocks (144 bytes per 256 weights) -> float32 weights."""
-    b = _u8(blocks)
+    b = _blocks_in(blocks, n_blocks, 144)
     w = np.empty(n_blocks * 256, np.float32)
     lib().oracle_dequant_gguf_q4k(_p(b, _c_u8p), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
     return w
@@ -372,15 +381,31 @@ def dequant_gguf_q4k(blocks, n_blocks: int) -> np.ndarray:
 
 def dequant_gguf_q6k(blocks, n_blocks: int) -> np.ndarray:
     """ggml Q6_K blocks (210 bytes per 256 weights) -> float32 weights."""
-    b = _u8(blocks)
+    b = _blocks_in(blocks, n_blocks, 210)
     w = np.empty(n_blocks * 256, np.float32)
     lib().oracle_dequant_gguf_q6k(_p(b, _c_u8p), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
     return w
 
 
+def dequant_gguf_q5k(blocks, n_blocks: int) -> np.ndarray:
+    """ggml Q5_K blocks (176 bytes per 256 weights) -> float32 weights."""
+    b = _blocks_in(blocks, n_blocks, 176)
+    w = np.empty(n_blocks * 256, np.float32)
+    lib().oracle_dequant_gguf_q5k(_p(b, _c_u8p), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
+    return w
+
+
+def dequant_gguf_q8_0(blocks, n_blocks: int) -> np.ndarray:
+    """ggml Q8_0 blocks (34 bytes per 32 weights) -> float32 weights."""
+    b = _blocks_in(blocks, n_blocks, 34)
+    w = np.empty(n_blocks * 32, np.float32)
+    lib().oracle_dequant_gguf_q8_0(_p(b, _c_u8p), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
+    return w
+
+
 def repack_gguf_q4k_to_q4km(blocks, n_blocks: int) -> np.ndarray:
     """ggml Q4_K blocks -> the ASDSL Q4_K variant blocks gemv_q4km reads."""
-    b = _u8(blocks)
+    b = _blocks_in(blocks, n_blocks, 144)
     out = np.empty(n_blocks * 144, np.uint8)
     lib().oracle_repack_gguf_q4k_to_q4km(_p(b, _c_u8p), _p(out, _c_u8p), ctypes.c_size_t(n_blocks))
     return out

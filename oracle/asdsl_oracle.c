@@ -638,7 +638,7 @@ EXPORT void oracle_gemv_q4_s256(const uint8_t* blocks, const int8_t* xq, const f
 }
 
 /* ------------------------------------------------------------------ GGUF
- * ggml's Q4_K and Q6_K block decoders, as the reference reaches them through
+ * ggml's Q4_K and Q6_K block decoders (Q5_K and Q8_0 below), as the reference reaches them through
  * the gguf package (asdsl/io/gguf_loader.py:150-181, gguf.quants.dequantize;
  * gguf-py from llama.cpp, no version pinned by the reference and absent
  * here).  Restated from ggml's published block layouts; the float32 products
@@ -695,6 +695,44 @@ EXPORT void oracle_dequant_gguf_q6k(const uint8_t* blocks, float* w, size_t n_bl
                 }
             }
         }
+    }
+}
+
+/* ggml Q5_K (176 bytes per 256 weights: fp16 d, fp16 dmin, Q4_K's 12-byte
+ * scale/min field, 32 high-bit bytes qh, 128 low-nibble bytes qs): weight
+ * 32j + l of sub-block j takes nibble (j & 1) of qs[32*(j/2) + l] and bit j
+ * of qh[l] as its fifth bit, w = (d*sc_j)*q - (dmin*m_j) (ggml's
+ * dequantize_row_q5_K; gguf-py's Q5_K.dequantize_blocks forms the same
+ * float32 products).  Same parity status as the Q4_K/Q6_K decoders above. */
+EXPORT void oracle_dequant_gguf_q5k(const uint8_t* blocks, float* w, size_t n_blocks) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* blk = blocks + b * 176;
+        const float d = half_to_float(rd16(blk));
+        const float dmin = half_to_float(rd16(blk + 2));
+        const uint8_t* qh = blk + 16;
+        const uint8_t* qs = blk + 48;
+        for (int j = 0; j < 8; ++j) {
+            int sc, m;
+            q4k_scale_min(blk + 4, j, &sc, &m);
+            volatile float d1 = d * (float)sc;
+            volatile float m1 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t byte = qs[32 * (j / 2) + l];
+                const int q = ((j & 1) ? (byte >> 4) : (byte & 0x0F)) | (((qh[l] >> j) & 1) << 4);
+                volatile float p = d1 * (float)q;
+                w[b * 256 + 32 * j + l] = p - m1;
+            }
+        }
+    }
+}
+
+/* ggml Q8_0 (34 bytes per 32 weights: fp16 d, 32 int8 codes): w = code * d
+ * (dequantize_row_q8_0; gguf-py's Q8_0.dequantize_blocks, x * d in float32). */
+EXPORT void oracle_dequant_gguf_q8_0(const uint8_t* blocks, float* w, size_t n_blocks) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* blk = blocks + b * 34;
+        const float d = half_to_float(rd16(blk));
+        for (int l = 0; l < 32; ++l) w[b * 32 + l] = (float)(int8_t)blk[2 + l] * d;
     }
 }
 

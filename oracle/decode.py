@@ -145,6 +145,27 @@ def argmax_first(x: np.ndarray) -> int:
     return int(np.argmax(x))
 
 
+def _lm_head_levels(w: np.ndarray, gs: int):
+    """The engine's symmetric load-time rule per gs-group (see
+    quantize_lm_head_q4_128): returns (q uint8 [rows][G][gs] in 0..15,
+    fp16 scale bits [rows][G]) with q = 8 and scale 0 for amax < 1e-12."""
+    x = np.ascontiguousarray(w, F32)
+    rows, cols = x.shape
+    g = x.reshape(rows, cols // gs, gs)
+    amax = np.abs(g).max(axis=2)
+    tiny = amax < F32(1e-12)
+    safe = np.where(tiny, F32(1.0), amax).astype(F32)
+    scale = (safe * F32(1.0 / 7.0)).astype(F32)
+    inv = (F32(7.0) / safe).astype(F32)
+    v = (g * inv[:, :, None]).astype(F32)
+    t = np.trunc(v)
+    r = t + np.where(np.abs(v - t) >= F32(0.5), np.sign(v), F32(0.0))  # half away from zero, exact in float32
+    q = np.clip(r + F32(8.0), 0, 15).astype(np.uint8)
+    q[tiny] = 8
+    s16 = np.where(tiny, F32(0.0), scale).astype(np.float16).view(np.uint16)
+    return q, s16
+
+
 def quantize_lm_head_q4_128(w: np.ndarray) -> np.ndarray:
     """The engine's load-time Q4_128 quantization of the output projection
     (UnifiedEngine constructor, unified_engine.cpp:413-461, lm_head_group_size
@@ -156,25 +177,54 @@ def quantize_lm_head_q4_128(w: np.ndarray) -> np.ndarray:
     [0, 15] (std::round).  Differs from repack_q4_128.py's quantizer in the
     rounding of ties (half away, not half even) and in forming the scale in
     float32.  Returns flat 66-byte blocks (uint8)."""
-    x = np.ascontiguousarray(w, F32)
-    rows, cols = x.shape
-    g = x.reshape(rows * (cols // 128), 128)
-    amax = np.abs(g).max(axis=1)
-    tiny = amax < F32(1e-12)
-    safe = np.where(tiny, F32(1.0), amax).astype(F32)
-    scale = (safe * F32(1.0 / 7.0)).astype(F32)
-    inv = (F32(7.0) / safe).astype(F32)
-    v = (g * inv[:, None]).astype(F32)
-    t = np.trunc(v)
-    r = t + np.where(np.abs(v - t) >= F32(0.5), np.sign(v), F32(0.0))  # half away from zero, exact in float32
-    q = np.clip(r + F32(8.0), 0, 15).astype(np.uint8)
-    q[tiny] = 8
-    s16 = np.where(tiny, F32(0.0), scale).astype(np.float16).view(np.uint16)
-    blocks = np.empty((g.shape[0], 66), np.uint8)
-    blocks[:, 0] = (s16 & 0xFF).astype(np.uint8)
-    blocks[:, 1] = (s16 >> 8).astype(np.uint8)
+    q, s16 = _lm_head_levels(w, 128)
+    n = q.shape[0] * q.shape[1]
+    q = q.reshape(n, 128)
+    blocks = np.empty((n, 66), np.uint8)
+    blocks[:, 0] = (s16.reshape(n) & 0xFF).astype(np.uint8)
+    blocks[:, 1] = (s16.reshape(n) >> 8).astype(np.uint8)
     blocks[:, 2:] = q[:, 0::2] | (q[:, 1::2] << 4)
     return blocks.reshape(-1)
+
+
+def quantize_lm_head_preq_g32(w: np.ndarray) -> np.ndarray:
+    """The engine's load-time quantization of the output projection at
+    lm_head_group_size 32 (unified_engine.cpp:320-372): the same symmetric
+    rule per 32-group, stored as 20-byte preq blocks with zero-point fp16 8.0
+    (0x4800): [fp16 scale | fp16 8.0 | 16 B nibbles]; an all-zero group is
+    scale 0, zero 8.0, nibbles 0x88.  The engine then copies them into its
+    preq2 lm_head byte for byte (unified_engine.cpp:374-398).  Returns flat
+    blocks (uint8)."""
+    q, s16 = _lm_head_levels(w, 32)
+    n = q.shape[0] * q.shape[1]
+    q = q.reshape(n, 32)
+    blocks = np.empty((n, 20), np.uint8)
+    blocks[:, 0] = (s16.reshape(n) & 0xFF).astype(np.uint8)
+    blocks[:, 1] = (s16.reshape(n) >> 8).astype(np.uint8)
+    blocks[:, 2] = 0x00
+    blocks[:, 3] = 0x48
+    blocks[:, 4:] = q[:, 0::2] | (q[:, 1::2] << 4)
+    return blocks.reshape(-1)
+
+
+def rmsnorm_factored(x: np.ndarray, w: np.ndarray, eps: float) -> tuple[np.ndarray, np.float32]:
+    """The factored form of rmsnorm_f32 that the GPU's norm-fed GEMVs take
+    on request: (x * w, inv_rms) -- the GEMV quantizes x * w and its outputs
+    are scaled by inv_rms afterwards (1/rms is one positive factor of the
+    whole input)."""
+    x = x.astype(F32)
+    ss = F32(np.dot(x.astype(np.float64), x.astype(np.float64)))
+    inv = F32(1.0) / np.sqrt(ss / F32(x.size) + F32(eps), dtype=F32)
+    return (x * w.astype(F32)).astype(F32), inv
+
+
+def _norm_gemv(gemv, meta, quant, h, w, eps, M, K, gs, factored):
+    """gemv(rmsnorm(h, w)), or in the factored form gemv(h * w) * inv_rms."""
+    if not factored:
+        x = rmsnorm(h, w, eps)
+        return x, gemv(meta, quant, x, M, K, gs)
+    x, inv = rmsnorm_factored(h, w, eps)
+    return x, (gemv(meta, quant, x, M, K, gs) * inv).astype(F32)
 
 
 def layer_forward(model: dict, li: int, h: np.ndarray, pos: int, k_cache: list, v_cache: list,
@@ -188,11 +238,11 @@ def layer_forward(model: dict, li: int, h: np.ndarray, pos: int, k_cache: list, 
     oracle.gemv_preq2_fused (same signature)."""
     c = model["cfg"]
     gemv = gemv or oracle.gemv_preq2_fused
+    fact = bool(model.get("factored_norm", False))
     hd, nh, nkv = c.head_dim, c.n_heads, c.n_kv_heads
     cos_row, sin_row = model["rope_cos"][pos], model["rope_sin"][pos]
     L = model["layers"][li]
-    x = rmsnorm(h, L["rms_att"], c.rms_eps)
-    qkv = gemv(*L["qkv"], x, c.qkv_dim, c.hidden, c.gs_attn)
+    x, qkv = _norm_gemv(gemv, *L["qkv"], h, L["rms_att"], c.rms_eps, c.qkv_dim, c.hidden, c.gs_attn, fact)
     q = rope(qkv[: nh * hd].reshape(nh, hd), cos_row, sin_row)
     k = rope(qkv[nh * hd:(nh + nkv) * hd].reshape(nkv, hd), cos_row, sin_row)
     v = qkv[(nh + nkv) * hd:].reshape(nkv, hd)
@@ -208,8 +258,7 @@ def layer_forward(model: dict, li: int, h: np.ndarray, pos: int, k_cache: list, 
         att = attention(q, k_cache[li][:, :pos + 1], v_cache[li][:, :pos + 1], nkv)
     o = gemv(*L["o"], att.reshape(-1), c.hidden, nh * hd, c.gs_attn)
     h_mid = (h + o).astype(F32)
-    x_ffn = rmsnorm(h_mid, L["rms_ffn"], c.rms_eps)
-    gu = gemv(*L["gu"], x_ffn, 2 * c.ffn, c.hidden, c.gs_ffn)
+    x_ffn, gu = _norm_gemv(gemv, *L["gu"], h_mid, L["rms_ffn"], c.rms_eps, 2 * c.ffn, c.hidden, c.gs_ffn, fact)
     sw = swiglu(gu[: c.ffn], gu[c.ffn:], model.get("fatrelu_threshold", 0.0))
     down = gemv(*L["down"], sw, c.hidden, c.ffn, c.gs_ffn)
     if trace is not None:
@@ -221,14 +270,15 @@ def lm_head_forward(model: dict, h: np.ndarray, gemv=None) -> np.ndarray:
     """logits = lm_head(rmsnorm(h, rms_out)) (unified_engine.cpp:1634-1648)."""
     c = model["cfg"]
     gemv = gemv or oracle.gemv_preq2_fused
-    return gemv(model["lm_meta"], model["lm_quant"], rmsnorm(h, model["rms_out"], c.rms_eps), c.vocab, c.hidden,
-                c.gs_lm)
+    return _norm_gemv(gemv, model["lm_meta"], model["lm_quant"], h, model["rms_out"], c.rms_eps, c.vocab, c.hidden,
+                      c.gs_lm, bool(model.get("factored_norm", False)))[1]
 
 
 def decode_step(model: dict, token: int, pos: int, k_cache: list, v_cache: list, trace: list | None = None,
                 gemv=None, lm_head: bool = True) -> tuple[np.ndarray, int]:
     """One greedy step.  model: host copies of the engine's weights
-    (host_model); k_cache/v_cache: per layer either an fp16 array
+    (host_model; model["factored_norm"] = True takes the norm-fed GEMVs'
+    factored form, rmsnorm_factored); k_cache/v_cache: per layer either an fp16 array
     [n_kv][max_seq][128] or, for the int8 cache, a pair (int8
     [n_kv][max_seq][128], float32 scales [n_kv][max_seq][2]); updated at
     `pos` in place.  trace (a list), when given, receives per layer a dict

@@ -55,6 +55,12 @@ def test_invalid_arguments_rejected_without_gpu():
     assert "exceeds" in _hip.last_error()
     assert lib.asdsl_gemv_q4_32_preq_fused(one, one, one, 0, 64, 32, None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
     assert lib.asdsl_quantize_activation(one, one, one, 100, 32, None) == _hip.ASDSL_ERR_INVALID_ARGUMENT
+    # the calibration read's launch shapes
+    u32 = ctypes.c_void_p(16)
+    for grid, threads, inflight, slab in ((1, 1024, 4, 2), (1, 256, 5, 2), (1, 256, 2, 0), (1, 256, 4, 3),
+                                          (0, 256, 4, 0)):
+        assert lib.asdsl_stream_read_ex(one, 4096, u32, grid, threads, inflight, slab, None) == \
+            _hip.ASDSL_ERR_INVALID_ARGUMENT, (grid, threads, inflight, slab)
 
 
 def test_python_wrapper_validates_sizes():

@@ -86,14 +86,15 @@ def test_tensor_types_and_alignment(tmp_path, alignment):
 
 def test_reference_helpers():
     assert gl.row_bytes_for_type("Q4_K", 3072) == 12 * 144 and gl.row_bytes_for_type("q6_k", 8192) == 32 * 210
+    assert gl.row_bytes_for_type("q5_k", 512) == 2 * 176 and gl.row_bytes_for_type("Q8_0", 256) == 8 * 34
     with pytest.raises(ValueError):
-        gl.row_bytes_for_type("q8_0", 256)
+        gl.row_bytes_for_type("iq2_xs", 256)
     assert gl.logical_shape((3072, 5120), "q4_k") == (5120, 3072) == gl.logical_shape((3072, 5120), "f16")
     with pytest.raises(ValueError):
         gl.logical_shape((4,), "f32")
     assert gl.ggml_type_name(12) == "q4_k" and gl.ggml_type_name(30) == "bf16" and gl.ggml_type_name(99) == "unknown_99"
     info = {"type": "q4_k", "logical_shape": (2, 256), "data": np.zeros(200, np.uint8)}
-    with pytest.raises(ValueError, match="byte count 200"):
+    with pytest.raises(ValueError, match="take 288 bytes, the tensor has 200"):
         gl.q4k_blocks_rowmajor(info)
     with pytest.raises(ValueError):
         gl.k_blocks_rowmajor({"type": "f32", "logical_shape": (1, 1), "data": np.zeros(4, np.uint8)})
@@ -144,3 +145,21 @@ def test_version_2_reads_like_version_3(tmp_path):
         t = gl.read_gguf_tensors(path)["t"]
         assert t["logical_shape"] == (4, 8)
         assert np.array_equal(gl.dequant_tensor(t), raw.reshape(4, 8))
+
+
+def test_config_from_gguf_caps_the_kv_length():
+    """A file's trained context sizes the KV cache only up to 4096 positions
+    unless max_seq is passed; every other field comes from the metadata."""
+    from asdsl.engine import GGUF_DEFAULT_MAX_SEQ, config_from_gguf
+
+    meta = {"general.architecture": "phi3", "phi3.embedding_length": 3072, "phi3.feed_forward_length": 8192,
+            "phi3.block_count": 32, "phi3.attention.head_count": 24, "phi3.attention.head_count_kv": 8,
+            "phi3.rope.dimension_count": 96, "phi3.context_length": 131072,
+            "phi3.attention.layer_norm_rms_epsilon": 1e-5, "phi3.rope.freq_base": 10000.0,
+            "tokenizer.ggml.tokens": [f"t{i}" for i in range(200064)]}
+    c = config_from_gguf(meta)
+    assert GGUF_DEFAULT_MAX_SEQ == 4096 and c.max_seq == 4096
+    assert (c.hidden, c.ffn, c.n_layers, c.n_heads, c.n_kv_heads, c.rotary_dim, c.vocab) == \
+        (3072, 8192, 32, 24, 8, 96, 200064)
+    assert config_from_gguf(meta, max_seq=131072).max_seq == 131072
+    assert config_from_gguf({**meta, "phi3.context_length": 512}).max_seq == 512

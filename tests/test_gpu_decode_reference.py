@@ -18,8 +18,8 @@ Q4_128 blocks of N(0, 0.02) weights, which the reference runs as they are
 and the GPU and the oracle run as preq2-g128 (the lossless Q4_128 repack);
 the output projection is an fp16 matrix that the reference quantizes at
 load and that the GPU and the oracle get quantized by the same rule
-(decode_c01.quantize_lm_head_q4_128_torch, a slice of it checked here
-against oracle.decode.quantize_lm_head_q4_128).
+(asdsl.quantization.lm_head.quantize_output_projection on the device, a
+slice of it checked here against oracle.decode.quantize_lm_head_q4_128).
 
 Each side prefills positions 0..ctx-1 with the same seeded tokens (the
 reference with forward_token_prefill; the oracle with the reference's
@@ -50,7 +50,7 @@ import pytest
 
 import oracle
 from conftest import rel_l2
-from decode_c01 import quantize_lm_head_q4_128_torch, tie_rows_torch
+from decode_c01 import tie_rows_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -79,6 +79,7 @@ def c01(gpu):
     import torch
     from asdsl import _hip
     from asdsl.engine import DecodeConfig, DecodeEngine, _layer_mats
+    from asdsl.quantization.lm_head import quantize_output_projection
     from asdsl.quantization.repack import repack_q4_128_blocks_to_preq2
     from asdsl.quantization.synthetic import preq2_from_weights_torch, q4_128_from_weights_torch
     from oracle import decode as od
@@ -123,10 +124,11 @@ def c01(gpu):
         ref_layers[li] = R
     embed = torch.randn((cfg.vocab, cfg.hidden), generator=gen, device=dev, dtype=torch.float32).half()
     lm_w = tie_rows_torch(cfg.vocab, cfg.hidden, gen, dev)
-    lm_blocks = quantize_lm_head_q4_128_torch(lm_w)
-    nb = 4096 * (cfg.hidden // 128) * 66
-    assert np.array_equal(host(lm_blocks[:nb]), od.quantize_lm_head_q4_128(host(lm_w[:4096].float())))
-    lm_meta, lm_quant = repack_q4_128_blocks_to_preq2(lm_blocks, cfg.vocab, cfg.hidden)
+    lm_meta, lm_quant = quantize_output_projection(lm_w, 128)
+    G = cfg.hidden // 128
+    want = repack_q4_128_blocks_to_preq2(od.quantize_lm_head_q4_128(host(lm_w[:4096].float())), 4096, cfg.hidden)
+    assert np.array_equal(host(lm_meta[:4096 * G * 4]), np.ravel(want[0]))
+    assert np.array_equal(host(lm_quant[:1024 * G * 256]), np.ravel(want[1]))
     rms_out = norm_w()
     eng = DecodeEngine(cfg, layers, embed, rms_out, lm_meta, lm_quant)
 
@@ -135,8 +137,6 @@ def c01(gpu):
     s.model = {"cfg": cfg, "layers": host_layers, "embed": host(embed), "rms_out": host(rms_out),
                "lm_meta": host(lm_meta), "lm_quant": host(lm_quant), "rope_cos": host(eng.rope_cos),
                "rope_sin": host(eng.rope_sin)}
-    q4[id(s.model["lm_quant"])] = host(lm_blocks)
-    del lm_blocks
 
     ue = oracle.load_reference("_native_unified")
     ec = ue.EngineConfig()

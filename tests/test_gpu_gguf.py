@@ -1,4 +1,5 @@
-"""HIP parity for the GGUF path: ggml Q4_K / Q6_K decoding, the Q4_K ->
+"""HIP parity for the GGUF path: ggml Q4_K / Q5_K / Q6_K / Q8_0 decoding
+(random blocks against the oracle, the hand-worked known-answer blocks), the Q4_K ->
 ASDSL Q4_K rearrangement, the symmetric Q4 requantization (bit for bit
 against the oracle, up to the full Phi-4 projection shapes), the Q4_K GEMV
 on real-layout GGUF blocks, and a GGUF file loaded into the decode engine:
@@ -33,6 +34,30 @@ def q6k_blocks(n, rng, scale=5e-6) -> np.ndarray:
     b = rng.integers(0, 256, (n, 210), dtype=np.uint8)
     b[:, 208:210] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
     return b.reshape(-1)
+
+
+def q5k_blocks(n, rng, scale=3e-5) -> np.ndarray:
+    b = rng.integers(0, 256, (n, 176), dtype=np.uint8)
+    b[:, 0:2] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    b[:, 2:4] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    return b.reshape(-1)
+
+
+def q8_0_blocks(n, rng, scale=2e-4) -> np.ndarray:
+    b = rng.integers(0, 256, (n, 34), dtype=np.uint8)
+    b[:, 0:2] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    return b.reshape(-1)
+
+
+# ggml type id -> (weights per block, block maker, oracle decoder)
+KINDS = {12: (256, q4k_blocks, oracle.dequant_gguf_q4k), 13: (256, q5k_blocks, oracle.dequant_gguf_q5k),
+         14: (256, q6k_blocks, oracle.dequant_gguf_q6k), 8: (32, q8_0_blocks, oracle.dequant_gguf_q8_0)}
+TYPE_ID = {"q4_k": 12, "q5_k": 13, "q6_k": 14, "q8_0": 8}
+
+
+def _decode(tid, raw, n_weights):
+    per, _, dec = KINDS[tid]
+    return dec(raw, n_weights // per)
 
 
 def _dev(a):
@@ -71,6 +96,57 @@ def test_dequant_q6k_bit_exact(gpu, rows, cols):
     _run("asdsl_dequant_gguf_q6k", gpu.ptr(_dev(blocks)), gpu.ptr(out), rows, cols)
     want = oracle.dequant_gguf_q6k(blocks, n).reshape(rows, cols)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (5, 512), (3072, 8192)])
+def test_dequant_q5k_bit_exact(gpu, rows, cols):
+    import torch
+
+    rng = np.random.default_rng(rows * 5 + cols)
+    n = rows * cols // 256
+    blocks = q5k_blocks(n, rng)
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    _run("asdsl_dequant_gguf_q5k", gpu.ptr(_dev(blocks)), gpu.ptr(out), rows, cols)
+    want = oracle.dequant_gguf_q5k(blocks, n).reshape(rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (7, 96), (3072, 3072)])
+def test_dequant_q8_0_bit_exact(gpu, rows, cols):
+    import torch
+
+    rng = np.random.default_rng(rows * 7 + cols)
+    n = rows * cols // 32
+    blocks = q8_0_blocks(n, rng)
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    _run("asdsl_dequant_gguf_q8_0", gpu.ptr(_dev(blocks)), gpu.ptr(out), rows, cols)
+    want = oracle.dequant_gguf_q8_0(blocks, n).reshape(rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    # 34-byte blocks: a tensor may start 2-byte aligned
+    seven = q8_0_blocks(7, rng)
+    buf = _dev(np.concatenate([np.zeros(2, np.uint8), seven]))
+    out2 = torch.empty((7, 32), dtype=torch.float32, device="cuda")
+    _run("asdsl_dequant_gguf_q8_0", gpu.ptr(buf) + 2, gpu.ptr(out2), 7, 32)
+    assert np.array_equal(out2.cpu().numpy().reshape(-1).view(np.uint32),
+                          oracle.dequant_gguf_q8_0(seven, 7).view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["q4k", "q5k", "q6k", "q8_0"])
+def test_known_answer_blocks_on_the_gpu(gpu, kind):
+    """The hand-worked blocks of test_oracle_gguf.py through the kernels."""
+    import torch
+
+    from test_oracle_gguf import KNOWN
+
+    make, _, n = KNOWN[kind]
+    blk, want = make()
+    out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    fn = {"q4k": "asdsl_dequant_gguf_q4k", "q5k": "asdsl_dequant_gguf_q5k", "q6k": "asdsl_dequant_gguf_q6k",
+          "q8_0": "asdsl_dequant_gguf_q8_0"}[kind]
+    _run(fn, gpu.ptr(_dev(blk.copy())), gpu.ptr(out), 1, n)
+    w = out.cpu().numpy().reshape(-1)
+    for i, v in want.items():
+        assert w[i] == np.float32(v), (kind, i, w[i], v)
 
 
 def test_dequant_q6k_blocks_at_odd_offsets(gpu):
@@ -143,35 +219,43 @@ def test_argument_errors(gpu):
 
 
 # ------------------------------------------------------------ whole model
-def _write_model(path, cfg, rng, gate_up_split=False):
-    """A Phi-4-shaped GGUF: qkv / o / gate_up Q4_K, down Q6_K, F32 norms,
-    Q6_K token_embd, Q4_K output, phi3 metadata."""
+# tensor -> ggml type of the two mixes: "q4" (Q4_K with Q6_K down and
+# embedding, as a Q4_K_M file) and "q5" (Q5_K and Q8_0 beside Q6_K)
+MIXES = {"q4": {"qkv": "q4_k", "o": "q4_k", "gu": "q4_k", "gate": "q4_k", "up": "q6_k", "down": "q6_k",
+                "embd": "q6_k", "out": "q4_k"},
+         "q5": {"qkv": "q5_k", "o": "q8_0", "gu": "q5_k", "gate": "q8_0", "up": "q5_k", "down": "q6_k",
+                "embd": "q8_0", "out": "q5_k"}}
+
+
+def _write_model(path, cfg, rng, gate_up_split=False, mix="q4"):
+    """A Phi-4-shaped GGUF with the projections, token_embd and output in
+    the types of MIXES[mix], F32 norms, phi3 metadata."""
     H, F, V = cfg.hidden, cfg.ffn, cfg.vocab
     qkv_rows = cfg.qkv_dim
     tensors = []
+    kinds = MIXES[mix]
 
-    def add(name, rows, cols, kind):
-        if kind == "q4_k":
-            tensors.append((name, 12, (cols, rows), q4k_blocks(rows * cols // 256, rng)))
-        else:
-            tensors.append((name, 14, (cols, rows), q6k_blocks(rows * cols // 256, rng)))
+    def add(name, rows, cols, what):
+        tid = TYPE_ID[kinds[what]]
+        per, make, _ = KINDS[tid]
+        tensors.append((name, tid, (cols, rows), make(rows * cols // per, rng)))
 
     for i in range(cfg.n_layers):
         p = f"blk.{i}."
-        add(p + "attn_qkv.weight", qkv_rows, H, "q4_k")
-        add(p + "attn_output.weight", H, H, "q4_k")
+        add(p + "attn_qkv.weight", qkv_rows, H, "qkv")
+        add(p + "attn_output.weight", H, H, "o")
         if gate_up_split:
-            add(p + "ffn_gate.weight", F, H, "q4_k")
-            add(p + "ffn_up.weight", F, H, "q6_k")
+            add(p + "ffn_gate.weight", F, H, "gate")
+            add(p + "ffn_up.weight", F, H, "up")
         else:
-            add(p + "ffn_up.weight", 2 * F, H, "q4_k")
-        add(p + "ffn_down.weight", H, F, "q6_k")
+            add(p + "ffn_up.weight", 2 * F, H, "gu")
+        add(p + "ffn_down.weight", H, F, "down")
         for n in ("attn_norm.weight", "ffn_norm.weight"):
             tensors.append((p + n, 0, (H,), (1 + 0.1 * rng.standard_normal(H)).astype(np.float32).view(np.uint8)))
-    add("token_embd.weight", V, H, "q6_k")
+    add("token_embd.weight", V, H, "embd")
     tensors.append(("output_norm.weight", 0, (H,), (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
                     .view(np.uint8)))
-    add("output.weight", V, H, "q4_k")
+    add("output.weight", V, H, "out")
     meta = [("general.architecture", STRING, "phi3"), ("phi3.embedding_length", UINT32, H),
             ("phi3.feed_forward_length", UINT32, F), ("phi3.block_count", UINT32, cfg.n_layers),
             ("phi3.attention.head_count", UINT32, cfg.n_heads),
@@ -185,14 +269,13 @@ def _write_model(path, cfg, rng, gate_up_split=False):
 
 
 def _oracle_preq2(tid, raw, rows, cols, gs):
-    n = rows * cols // 256
-    w = oracle.dequant_gguf_q4k(raw, n) if tid == 12 else oracle.dequant_gguf_q6k(raw, n)
+    w = _decode(tid, raw, rows * cols)
     p, s, b = oracle.quantize_q4_symmetric(w, gs)
     return oracle.repack_asym_to_preq2(p, s, b, rows, cols, gs)
 
 
-@pytest.mark.parametrize("split", [False, True])
-def test_gguf_model_loads_and_decodes(gpu, tmp_path, split):
+@pytest.mark.parametrize("split,mix", [(False, "q4"), (True, "q4"), (False, "q5"), (True, "q5")])
+def test_gguf_model_loads_and_decodes(gpu, tmp_path, split, mix):
     """2 Phi-4-shaped layers, vocab 4096, from a GGUF file: the config from
     its metadata; every preq2 operand, norm and the fp16 embedding equal to
     the oracle pipeline (decode, requantize, repack) bit for bit; three
@@ -205,7 +288,7 @@ def test_gguf_model_loads_and_decodes(gpu, tmp_path, split):
     cfg0 = DecodeConfig(n_layers=2, vocab=4096, max_seq=512)
     rng = np.random.default_rng(5 + split)
     path = tmp_path / "m.gguf"
-    raw = _write_model(path, cfg0, rng, gate_up_split=split)
+    raw = _write_model(path, cfg0, rng, gate_up_split=split, mix=mix)
     eng = DecodeEngine.from_gguf(path)
     cfg = eng.cfg
     assert (cfg.hidden, cfg.ffn, cfg.vocab, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.rotary_dim,
@@ -219,8 +302,8 @@ def test_gguf_model_loads_and_decodes(gpu, tmp_path, split):
         ol = {}
         for n, (rows, cols, gs) in mats.items():
             if n == "gu" and split:
-                g = oracle.dequant_gguf_q4k(raw[f"blk.{i}.ffn_gate.weight"][1], rows // 2 * cols // 256)
-                u = oracle.dequant_gguf_q6k(raw[f"blk.{i}.ffn_up.weight"][1], rows // 2 * cols // 256)
+                g = _decode(*raw[f"blk.{i}.ffn_gate.weight"], rows // 2 * cols)
+                u = _decode(*raw[f"blk.{i}.ffn_up.weight"], rows // 2 * cols)
                 p, s, b = oracle.quantize_q4_symmetric(np.concatenate([g, u]), gs)
                 want = oracle.repack_asym_to_preq2(p, s, b, rows, cols, gs)
             else:
@@ -233,7 +316,7 @@ def test_gguf_model_loads_and_decodes(gpu, tmp_path, split):
             ol[n] = raw[f"blk.{i}.{key}"][1].view(np.float32)
             assert np.array_equal(host(L[n]), ol[n])
         layers.append(ol)
-    emb = oracle.dequant_gguf_q6k(raw["token_embd.weight"][1], cfg.vocab * cfg.hidden // 256)
+    emb = _decode(*raw["token_embd.weight"], cfg.vocab * cfg.hidden)
     emb16 = emb.astype(np.float16).reshape(cfg.vocab, cfg.hidden)
     assert np.array_equal(host(eng.embed), emb16)
     lm = _oracle_preq2(*raw["output.weight"], cfg.vocab, cfg.hidden, cfg.gs_lm)

@@ -92,14 +92,14 @@ def test_verify_matches_serial_oracle(gpu, ctx, n):
         assert np.array_equal(gk[:, :ctx], kc[li][:, :ctx]) and not gk[:, ctx + n:].any()
 
 
-@pytest.mark.parametrize("form", ["mfma", "dot4"])
+@pytest.mark.parametrize("form", ["mfma"])
 def test_verify_matches_single_token_steps(gpu, form, monkeypatch):
-    """The batched pass against the engine's own single-token step at the
-    same positions (K/V rolled back in between): 1e-5, same tokens, with the
-    projections as MFMA batched GEMVs (the default) and as the dot4 forms
-    (ASDSL_HIP_VERIFY_DOT4=1)."""
-    if form == "dot4":
-        monkeypatch.setenv("ASDSL_HIP_VERIFY_DOT4", "1")
+    """The batched pass with the projections as MFMA batched GEMVs
+    (ASDSL_HIP_VERIFY_MFMA=1) against the engine's own single-token step at
+    the same positions (K/V rolled back in between): 1e-5, same tokens.  The
+    default form is bit for bit the single-token step
+    (test_verify_is_the_single_token_step_bit_for_bit)."""
+    monkeypatch.setenv("ASDSL_HIP_VERIFY_MFMA", "1")
     eng = _engine(seed=7)
     eng.prefill_kv_random(200, seed=1)
     toks = [11, 22, 33, 44, 55, 66, 77, 88]
@@ -304,3 +304,61 @@ def test_columns_past_the_cache_write_nothing(gpu):
         k1, v1 = _host(L["k_cache"]), _host(L["v_cache"])
         assert np.array_equal(k1[:, :126], k0[:, :126]) and np.array_equal(v1[:, :126], v0[:, :126])
         assert k1[:, 126:].any() and v1[:, 126:].any()  # rows 126, 127 written by the in-cache columns
+
+
+def _bits_case(eng, ctx, toks):
+    """The verify pass of toks at ctx, then (K/V rolled back) the engine's
+    single-token steps at the same positions: logits, greedy tokens and the
+    K/V rows each writes, bit for bit."""
+    import torch
+
+    n = len(toks)
+    eng.snapshot_kv()
+    batched = eng.forward_batch_all_logits(toks, ctx).clone()
+    bnext = eng.verify_next_tokens()
+    kv_b = [(L["k_cache"][:, ctx:ctx + n].clone(), L["v_cache"][:, ctx:ctx + n].clone()) for L in eng.layers]
+    if eng.kv_int8:
+        sc_b = [(L["k_scale"][:, ctx:ctx + n].clone(), L["v_scale"][:, ctx:ctx + n].clone()) for L in eng.layers]
+    eng.restore_kv()
+    for c, t in enumerate(toks):
+        single = eng.forward_token(t, ctx + c)
+        assert torch.equal(batched[c], single), (ctx, c, rel_l2(_host(batched[c]), _host(single)))
+        assert bnext[c] == eng.next_token(), (ctx, c)
+    for li, L in enumerate(eng.layers):
+        assert torch.equal(L["k_cache"][:, ctx:ctx + n], kv_b[li][0]) and \
+            torch.equal(L["v_cache"][:, ctx:ctx + n], kv_b[li][1]), li
+        if eng.kv_int8:
+            assert torch.equal(L["k_scale"][:, ctx:ctx + n], sc_b[li][0]) and \
+                torch.equal(L["v_scale"][:, ctx:ctx + n], sc_b[li][1]), li
+
+
+@pytest.mark.parametrize("kv", ["fp16", "int8"])
+@pytest.mark.parametrize("ctx,n", [(0, 3), (200, 8), (500, 16), (1000, 5)])
+def test_verify_is_the_single_token_step_bit_for_bit(gpu, kv, ctx, n):
+    """The default verify pass (dot4 GEMVs in the single-token launch
+    shapes, factored norms, the attention's one-tile splits) on a 2-layer
+    model: every column equals the single-token step at its position bit for
+    bit, across the short form (below 512: o_proj merges the splits) and the
+    long form (combine kernel), 500 + 16 crossing between them."""
+    from asdsl.engine import DecodeConfig, DecodeEngine
+
+    eng = DecodeEngine.synthetic(DecodeConfig(n_layers=2, vocab=4096, max_seq=1100, kv_format=kv), seed=ctx + n)
+    eng.prefill_kv_random(ctx, seed=5)
+    toks = [int(t) for t in np.random.default_rng(ctx).integers(0, eng.cfg.vocab, n)]
+    _bits_case(eng, ctx, toks)
+
+
+@pytest.fixture(scope="module")
+def full32(gpu):
+    from asdsl.engine import DecodeConfig, DecodeEngine
+
+    return DecodeEngine.synthetic(DecodeConfig(max_seq=1100, kv_format="int8"), seed=77)
+
+
+@pytest.mark.parametrize("ctx,n", [(128, 8), (1000, 16)])
+def test_verify_is_the_single_token_step_bit_for_bit_full_size(full32, ctx, n):
+    """The same on the 32-layer, vocab-200064 Phi-4-shaped model (qkv/o
+    preq2 g32, gate_up/down/lm_head preq2-g128, int8 KV cache)."""
+    full32.prefill_kv_random(ctx, seed=ctx)
+    toks = [int(t) for t in np.random.default_rng(ctx + 1).integers(0, full32.cfg.vocab, n)]
+    _bits_case(full32, ctx, toks)

@@ -127,3 +127,99 @@ def test_gemm_q4_128_ws_equals_library_buffer(gpu):
     _hip.call("asdsl_gemm_q4_128_ws", P(blocks), P(X), P(Y2), M, K, 128, B, P(work), nbytes, s)
     torch.cuda.synchronize()
     assert _same(Y1, Y2)
+
+
+_RESERVE_CHILD = r'''
+import sys
+import numpy as np
+import torch
+from asdsl import _hip
+
+s, P = _hip.stream_handle(), _hip.ptr
+LIB = _hip.LIB
+
+
+def case(IN, OUT, gs, n_active, seed):
+    rng = np.random.default_rng(seed)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    wT = dev(rng.integers(0, 256, IN * OUT // 2, dtype=np.uint8))
+    sT = dev((rng.random(IN * OUT // gs) * 0.01 + 1e-3).astype(np.float32))
+    bT = -8.0 * sT
+    x = np.zeros(IN, np.float32)
+    rows = np.sort(rng.choice(IN, n_active, replace=False)).astype(np.int32)
+    x[rows] = rng.random(n_active).astype(np.float32) + 0.1
+    return wT, sT, bT, dev(x), dev(rows)
+
+
+def plain(args, n_active, y, IN, OUT, gs, stream=None):
+    wT, sT, bT, x, rows = args
+    return LIB.asdsl_sparse_down_proj_T(P(wT), P(sT), P(bT), P(x), P(rows), n_active, P(y), IN, OUT, gs,
+                                        s if stream is None else stream)
+
+
+def same(a, b):
+    return np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
+
+
+small = (2048, 1024, 32, 1500)
+big = (2048, 16384, 32, 2048)
+need_small = LIB.asdsl_sparse_down_work_bytes(small[1])
+assert LIB.asdsl_reserve_workspace(need_small) == 0, _hip.last_error()
+
+# within the reservation: the plain form runs and gives the _ws form's bits
+a = case(*small, seed=1)
+y1 = torch.empty(small[1], device="cuda")
+y2 = torch.full((small[1],), float("nan"), device="cuda")
+work = torch.empty(need_small, dtype=torch.uint8, device="cuda")
+assert plain(a, small[3], y1, *small[:3]) == 0, _hip.last_error()
+wT, sT, bT, x, rows = a
+assert LIB.asdsl_sparse_down_proj_T_ws(P(wT), P(sT), P(bT), P(x), P(rows), small[3], P(y2), small[0], small[1],
+                                       small[2], P(work), need_small, s) == 0
+torch.cuda.synchronize()
+assert same(y1, y2)
+
+# and under graph capture, replayed three times with eager work between
+yg = torch.full((small[1],), float("nan"), device="cuda")
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    st = plain(a, small[3], yg, *small[:3], stream=int(torch.cuda.current_stream().cuda_stream))
+assert st == 0, _hip.last_error()
+for _ in range(3):
+    yg.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert same(yg, y1)
+
+# beyond it: refused, nothing allocated
+b = case(*big, seed=2)
+yb = torch.empty(big[1], device="cuda")
+st = plain(b, big[3], yb, *big[:3])
+assert st == _hip.ASDSL_ERR_INVALID_ARGUMENT, st
+assert "reserved" in _hip.last_error(), _hip.last_error()
+
+# 0 returns to growth on demand
+assert LIB.asdsl_reserve_workspace(0) == 0
+assert plain(b, big[3], yb, *big[:3]) == 0, _hip.last_error()
+torch.cuda.synchronize()
+print("RESERVE_OK")
+'''
+
+
+def test_reserved_workspace_never_grows(gpu):
+    """asdsl_reserve_workspace, in a fresh process (the library buffer is
+    per process and earlier tests grow it): after reserving the sparse
+    down-projection's need at 1024 outputs, the plain form runs within it
+    with the _ws form's bits, also captured in a graph and replayed; the
+    same call at 16384 outputs, which needs more, is refused with
+    ASDSL_ERR_INVALID_ARGUMENT instead of allocating; reserving 0 returns to
+    growth on demand."""
+    import os
+    import subprocess
+    import sys
+
+    from conftest import REPO
+
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([str(REPO), str(REPO / "asdsl-framework_amd")]))
+    r = subprocess.run([sys.executable, "-c", _RESERVE_CHILD], capture_output=True, text=True, timeout=240, env=env)
+    assert r.returncode == 0 and "RESERVE_OK" in r.stdout, (r.stdout[-2000:], r.stderr[-4000:])

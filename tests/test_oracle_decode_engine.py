@@ -366,3 +366,78 @@ def test_kv_q8_rule_known_blocks():
     assert s[2, 0] == np.float32(1.0) and q[2, 1] == 0 and q[2, 2] == 2 and q[2, 3] == -2
     deq = od.kv_dequant_q8(q, s)
     assert np.all(np.abs(deq - x) <= 0.5 * np.repeat(s, 64, axis=1) * (1 + 1e-6))
+
+
+def test_lm_head_g32_quantizer_is_the_engines():
+    """At lm_head_group_size 32 the engine quantizes an fp16 output
+    projection itself (unified_engine.cpp:320-398: symmetric levels in preq
+    blocks with zero 8.0, copied into its preq2 lm_head).  The preq2 lm_head
+    it exports (export_lm_head_preq2) equals the oracle's restatement
+    (quantize_lm_head_preq_g32, repacked) byte for byte, tie rows included,
+    and none of its tie nibbles is the round-half-even one."""
+    import torch
+
+    from asdsl.quantization.repack import repack_preq_blocks_to_preq2
+    from decode_c01 import tie_rows_torch
+
+    n_layers, n_heads, n_kv, vocab = 1, 6, 2, 2048
+    model, _ = _model(n_layers, n_heads, n_kv, 2048, vocab, 96, seed=21)
+    c = model["cfg"]
+    lm_w = tie_rows_torch(vocab, c.hidden, torch.Generator().manual_seed(21), "cpu").numpy()
+    ue = oracle.load_reference("_native_unified")
+    ec = ue.EngineConfig()
+    ec.num_layers, ec.hidden_size, ec.num_heads, ec.num_kv_heads = n_layers, c.hidden, n_heads, n_kv
+    ec.head_dim, ec.intermediate_size, ec.vocab_size, ec.rms_norm_eps = 128, 2048, vocab, c.rms_eps
+    ec.group_size, ec.lm_head_group_size, ec.max_seq_len, ec.rotary_dim, ec.weight_format = 32, 32, 96, 96, 0
+    ref_layers = {}
+    for li, L in enumerate(model["layers"]):
+        R = {"rms_att": L["rms_att"], "rms_ffn": L["rms_ffn"]}
+        for n, name in (("qkv", "qkv_proj"), ("o", "o_proj"), ("gu", "gate_up_proj"), ("down", "down_proj")):
+            R[name + "_meta"], R[name + "_quant"] = L[n]
+            R[name] = np.zeros(len(L[n][0]) // 4 * 20, np.uint8)
+        ref_layers[li] = R
+    engine = ue.UnifiedEngine(ec, model["embed"], model["rms_out"], lm_w, model["rope_cos"], model["rope_sin"],
+                              ref_layers)
+    meta, quant = engine.export_lm_head_preq2()
+    blocks = od.quantize_lm_head_preq_g32(lm_w.astype(np.float32))
+    want = repack_preq_blocks_to_preq2(blocks, vocab, c.hidden, 32)
+    assert np.array_equal(meta, np.ravel(want[0])) and np.array_equal(quant, np.ravel(want[1]))
+    w = lm_w[0::4].astype(np.float32).reshape(-1, 32)  # tie rows: amax 7 in the group of each +-7
+    v = w * (np.float32(7.0) / np.abs(w).max(axis=1, keepdims=True))
+    ties = np.abs(v - np.trunc(v)) == 0.5
+    b = blocks.reshape(vocab, -1, 20)[0::4].reshape(-1, 20)[:, 4:]
+    lv = np.empty((b.shape[0], 32), np.int64)
+    lv[:, 0::2], lv[:, 1::2] = b & 0xF, b >> 4
+    assert ties.sum() > 1000 and np.all(lv[ties] - 8 == (np.trunc(v) + np.sign(v))[ties])
+
+
+def test_factored_norm_form_is_the_same_map_up_to_rounding():
+    """The oracle's factored norm form (the GEMV quantizes x * w and scales
+    its outputs by 1/rms) computes the same step as the reference order up
+    to int8 rounding flips: with the activation scale's 1/rms factored out
+    the two forms quantize the same vector to the same levels except where
+    a value sits on a rounding boundary.  The norm factor is 1/rms; a step's
+    logits agree within 5e-3 (one int8 level flip moves a 2-layer model's
+    logits by ~3e-3) and their median within 1e-5 (measured: 1.1e-7 to
+    1.5e-7, no flips in these four steps)."""
+    from oracle import decode as od
+
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(3072).astype(np.float32) * 3
+    w = (1 + 0.1 * rng.standard_normal(3072)).astype(np.float32)
+    xw, inv = od.rmsnorm_factored(x, w, 1e-5)
+    ref = od.rmsnorm(x, w, 1e-5)
+    assert np.array_equal(xw, (x * w).astype(np.float32))
+    assert abs(float(inv) * np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5) - 1) < 1e-6
+    assert rel_l2(xw * inv, ref) < 1e-6
+
+    model, _, _ = model_c01(2, 8, 2, 1024, 1024, 64, seed=9)
+    fmodel = dict(model, factored_norm=True)
+    shape = (2, 64, model["cfg"].head_dim)
+    caches = [[np.zeros(shape, np.float16) for _ in range(2)] for _ in range(4)]
+    errs = []
+    for pos, t in enumerate([5, 77, 300, 12]):
+        a, _ = od.decode_step(model, t, pos, caches[0], caches[1])
+        b, _ = od.decode_step(fmodel, t, pos, caches[2], caches[3])
+        errs.append(rel_l2(b, a))
+    assert max(errs) < 5e-3 and np.median(errs) < 1e-5, errs

@@ -176,3 +176,95 @@ def test_quantize_q4_symmetric_matches_the_numpy_restatement(gs):
     assert np.array_equal(packed, qt.data)
     assert np.array_equal(scales, qt.scales.astype(np.float32))
     assert np.array_equal(biases, (-7.5 * qt.scales.astype(np.float32)).astype(np.float32))
+
+
+# ----------------------------------------------------------- known answers
+# Blocks written byte by byte from ggml's layouts (block_q4_K, block_q5_K,
+# block_q6_K, block_q8_0) with the expected weights worked out by hand, so
+# that nothing here comes from the code under test.  The 12-byte scale/min
+# field of Q4_K and Q5_K encodes scales (1, 2, 3, 4, 50, 20, 63, 5) and mins
+# (0, 1, 0, 0, 33, 0, 7, 60): bytes 0-3 hold scale j's low 6 bits and, in
+# bits 6-7, the top 2 bits of scale j+4; bytes 4-7 the same for the mins;
+# bytes 8-11 the low 4 bits of scale j+4 (low nibble) and min j+4 (high).
+KA_SCALES = bytes([0xC1, 0x42, 0xC3, 0x04, 0x80, 0x01, 0x00, 0xC0, 0x12, 0x04, 0x7F, 0xC5])
+
+
+def known_q4k() -> tuple[np.ndarray, dict]:
+    """d = 1.0, dmin = 0.5; byte 83 = 0x97 puts codes 7 (sub-block 4) and
+    9 (sub-block 5) at position 3; byte 143 = 0x1F codes 15 (sub-block 6) and
+    1 (sub-block 7) at position 31; every other code 0."""
+    b = bytearray(144)
+    b[0:2], b[2:4] = b"\x00\x3c", b"\x00\x38"
+    b[4:16] = KA_SCALES
+    b[83], b[143] = 0x97, 0x1F
+    return np.frombuffer(bytes(b), np.uint8), {
+        0: 0.0, 32: -0.5, 131: 333.5, 163: 180.0, 223: 941.5, 255: -25.0, 128: -16.5, 224: -30.0}
+
+
+def known_q5k() -> tuple[np.ndarray, dict]:
+    """d = 1.0, dmin = 1.0; high-bit byte 16 = 0x01 (bit 0: sub-block 0,
+    position 0), byte 23 = 0x10 (bit 4: sub-block 4, position 7), byte 47 =
+    0xC0 (bits 6, 7: sub-blocks 6, 7, position 31); low-nibble byte 119 =
+    0xA3 (sub-blocks 4/5, position 7: 3 and 10), byte 175 = 0xFF (sub-blocks
+    6/7, position 31: 15 and 15)."""
+    b = bytearray(176)
+    b[0:2], b[2:4] = b"\x00\x3c", b"\x00\x3c"
+    b[4:16] = KA_SCALES
+    b[16], b[23], b[47] = 0x01, 0x10, 0xC0
+    b[119], b[175] = 0xA3, 0xFF
+    return np.frombuffer(bytes(b), np.uint8), {
+        0: 16.0, 32: -1.0, 135: 917.0, 167: 200.0, 223: 1946.0, 255: 95.0, 63: -1.0, 31: 0.0, 128: -33.0}
+
+
+def known_q6k() -> tuple[np.ndarray, dict]:
+    """d = 0.5 (bytes 208-209); scales 2, -3, 7, -1 at bytes 192, 194, 196,
+    198, every other scale 1; at position 5 of the first half the four
+    quarters' codes 63, 0, 33, 20: low-nibble byte 5 = 0x1F (quarters 0 and
+    2), byte 37 = 0x40 (quarters 1 and 3), high-bit byte 133 = 0x63 (2-bit
+    fields 3, 0, 2, 1); every other code 0, i.e. -32 after the offset."""
+    b = bytearray(210)
+    b[5], b[37], b[133] = 0x1F, 0x40, 0x63
+    b[192:208] = bytes([1] * 16)
+    b[192], b[194], b[196], b[198] = 2, 0xFD, 7, 0xFF
+    b[208:210] = b"\x00\x38"
+    return np.frombuffer(bytes(b), np.uint8), {
+        5: 31.0, 37: 48.0, 69: 3.5, 101: 6.0, 0: -32.0, 16: -16.0, 32: 48.0, 128: -16.0, 255: -16.0}
+
+
+def known_q8_0() -> tuple[np.ndarray, dict]:
+    """d = 0.25, codes -128, -1, 0, 1, 127, then zeros."""
+    b = bytearray(34)
+    b[0:2] = b"\x00\x34"
+    b[2:7] = bytes([0x80, 0xFF, 0x00, 0x01, 0x7F])
+    return np.frombuffer(bytes(b), np.uint8), {0: -32.0, 1: -0.25, 2: 0.0, 3: 0.25, 4: 31.75, 31: 0.0}
+
+
+KNOWN = {"q4k": (known_q4k, oracle.dequant_gguf_q4k, 256), "q5k": (known_q5k, oracle.dequant_gguf_q5k, 256),
+         "q6k": (known_q6k, oracle.dequant_gguf_q6k, 256), "q8_0": (known_q8_0, oracle.dequant_gguf_q8_0, 32)}
+
+
+@pytest.mark.parametrize("kind", sorted(KNOWN))
+def test_known_answer_blocks(kind):
+    make, decode, n = KNOWN[kind]
+    blk, want = make()
+    w = decode(blk, 1)
+    assert w.shape == (n,)
+    for i, v in want.items():
+        assert w[i] == np.float32(v), (kind, i, w[i], v)
+
+
+@pytest.mark.parametrize("j", range(8))
+def test_q5k_each_high_bit_moves_its_weight(j):
+    """Bit j of high-bit byte l is the fifth bit of weight 32j + l and of no
+    other weight (d = 1, scales 1, mins 0, all low nibbles 0)."""
+    b = np.zeros(176, np.uint8)
+    b[0:2] = _f16(1.0)
+    b[4:8] = 1  # scales 0-3 = 1 (and the top bits of scales 4-7 zero)
+    b[12:16] = 1  # scales 4-7 = 1, mins 4-7 = 0
+    for l in (0, 13, 31):
+        blk = b.copy()
+        blk[16 + l] = 1 << j
+        w = oracle.dequant_gguf_q5k(blk, 1)
+        want = np.zeros(256, np.float32)
+        want[32 * j + l] = 16.0
+        assert np.array_equal(w, want), (j, l)
