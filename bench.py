@@ -54,12 +54,13 @@ LAYER = [("qkv", 5120, 3072), ("o_proj", 3072, 3072), ("gate_up", 16384, 3072), 
 GS = 32
 LM_HEAD = (200064, 3072, 128)
 # HBM bytes per gate_up launch measured by rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on `bench.py --pmc-probe gate_up` at commit 343f414 (median of
-# 50 dispatches: 31,615,144 fetched + 65,536 written), each scaled by the same
-# counter on a 64 MiB device copy (fetch x1.9993, write x1.0); see
-# profiles/hbm_traffic_gemv_decode_sparse_down.md.  A property of the
-# kernel's access pattern: re-measure when the kernel's loads change.
-GATE_UP_TRAFFIC_BYTES = 31_680_680
+# WRITE_SIZE on `bench.py --pmc-probe gate_up` with the first tile's weight
+# requests split around the activation staging (median of 50 dispatches:
+# 15,442 KiB fetched, 64 KiB written), each scaled by the same counter on a
+# 64 MiB device copy (fetch x1.9993, write x1.0): 31,614,121 + 65,536 bytes;
+# see profiles/preq2_gemv_phi4_layer_g32.md.  A property of the kernel's
+# access pattern: re-measure when the kernel's loads change.
+GATE_UP_TRAFFIC_BYTES = 31_679_657
 GATE_UP_BYTES = 31_535_104  # gemv_bytes(16384, 3072): the gate_up GEMV's algorithmic bytes
 
 
@@ -357,12 +358,12 @@ def shape_sweep(args) -> int:
     """Each layer GEMV (the headline's four shapes, preq2 g32) timed like the
     headline's per-GEMV figure (a graph of 4*L launches over L rotated weight
     sets) under every launch shape the tuning switches give: the K split
-    (ASDSL_HIP_KSPLIT: the plan's, 1, 2, 4) times the activation source
-    (ASDSL_HIP_XLDS: registers or LDS) or the first tile's weight requests
-    split around the activation staging (ASDSL_HIP_PRE_SPLIT 1..3).  The
-    switches are read per call, so each graph is captured under its own
-    setting.  Outputs are compared with the plan's launch (relative L2; the
-    K split changes the fp32 summation order only)."""
+    (ASDSL_HIP_KSPLIT: the plan's, 1, 2, 4) times the first tile's weight
+    requests split around the activation staging (ASDSL_HIP_PRE_SPLIT: the
+    plan's, 1 a third up front, 2 a half, 4 all).  The switches are read per
+    call, so each graph is captured under its own setting.  Outputs are
+    compared with the plan's launch (relative L2; the K split changes the
+    fp32 summation order only, the request split nothing)."""
     import numpy as np
     import torch
 
@@ -372,14 +373,14 @@ def shape_sweep(args) -> int:
     lib = _hip.LIB
     ptrs = [{n: (_hip.ptr(m), _hip.ptr(q)) for n, (m, q) in L.items()} for L in layers]
     L = len(layers)
-    knobs = ("ASDSL_HIP_KSPLIT", "ASDSL_HIP_XLDS", "ASDSL_HIP_PRE_SPLIT")
+    knobs = ("ASDSL_HIP_KSPLIT", "ASDSL_HIP_PRE_SPLIT")
     saved = {k: os.environ.get(k) for k in knobs}
     try:
         for n, M, K in LAYER:
             rows, want = [], None
             for ks in ("", "1", "2", "4"):
-                for xl, sp in (("", ""), ("1", ""), ("", "1"), ("", "2"), ("", "3")):
-                    for k, v in zip(knobs, (ks, xl, sp)):
+                for sp in ("", "1", "2", "4"):
+                    for k, v in zip(knobs, (ks, sp)):
                         os.environ[k] = v
                     y = ys[n]
 
@@ -401,8 +402,7 @@ def shape_sweep(args) -> int:
                     if want is None:
                         want = got
                     rel = float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
-                    rows.append({"ksplit": ks or "plan", "x_from": "lds" if xl else "regs", "pre_split": int(sp or 0),
-                                 "us": round(us, 3),
+                    rows.append({"ksplit": ks or "plan", "pre_split": sp or "plan", "us": round(us, 3),
                                  "GB/s": round(gemv_bytes(M, K) / (us * 1e-6) / 1e9, 1), "rel_l2_vs_plan": rel})
             print(json.dumps({"shape_sweep": n, "shape": [M, K], "bytes": gemv_bytes(M, K), "rows": rows}),
                   flush=True)
@@ -415,11 +415,18 @@ def shape_sweep(args) -> int:
     return 0
 
 
+# Read shapes that reach the single-launch ceiling in the ceiling sweep
+# (31.5 MB: grid-stride 256 threads x 8 loads x 2048 workgroups 5.78 us,
+# 512 x 16 x 1024 5.83; one-shot 256 x 4 and 512 x 2, 5.97): the floor is the
+# best of them at each byte count.
+FLOOR_CONFIGS = ((0, 256, 8, 2048), (0, 512, 16, 1024), (0, 1024, 16, 512), (2, 256, 4, 0), (2, 512, 2, 0))
+
+
 def stream_floor_us(lib, nbytes: int, launches: int = 64) -> dict:
     """The practical ceiling for one launch that streams `nbytes`: the library's
-    calibration read kernel (asdsl_stream_read), a graph of back-to-back
-    launches over rotated buffers (~1 GB in all, at least two), timed exactly
-    like the GEMVs; the faster of 256 and 1024 workgroups."""
+    calibration read (asdsl_stream_read_ex) in each of FLOOR_CONFIGS, a graph
+    of back-to-back launches over rotated buffers (~1 GB in all, at least
+    two), timed exactly like the GEMVs; the fastest."""
     import torch
 
     from asdsl import _hip
@@ -429,20 +436,24 @@ def stream_floor_us(lib, nbytes: int, launches: int = 64) -> dict:
     bufs = [torch.ones(nbytes, dtype=torch.uint8, device="cuda") for _ in range(ncopies)]
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
     best = None
-    for grid in (256, 1024):
-        def calls(h, grid=grid):
+    for slab, threads, lif, grid in FLOOR_CONFIGS:
+        if slab == 2:
+            grid = -(-nbytes // (16 * threads * lif))
+
+        def calls(h, slab=slab, threads=threads, lif=lif, grid=grid):
             for i in range(launches):
-                if lib.asdsl_stream_read(_hip.ptr(bufs[i % ncopies]), nbytes, _hip.ptr(sink), grid, h):
+                if lib.asdsl_stream_read_ex(_hip.ptr(bufs[i % ncopies]), nbytes, _hip.ptr(sink), grid, threads, lif,
+                                            slab, h):
                     raise RuntimeError(_hip.last_error())
         g = capture(calls)
         reps = 10
         us = 1e3 * timed_replays(g, reps) / (reps * launches)
         del g
         if best is None or us < best[0]:
-            best = (us, grid)
+            best = (us, {"slab": slab, "threads": threads, "inflight": lif, "grid": grid})
     del bufs
     torch.cuda.empty_cache()
-    return {"us": round(best[0], 3), "GB/s": round(nbytes / (best[0] * 1e-6) / 1e9, 1), "grid": best[1]}
+    return {"us": round(best[0], 3), "GB/s": round(nbytes / (best[0] * 1e-6) / 1e9, 1), "config": best[1]}
 
 
 def ceiling_configs(nbytes: int, oneshot_only: bool = False) -> list[tuple[int, int, int, int]]:
@@ -1450,7 +1461,7 @@ def main() -> int:
     ap.add_argument("--ceiling-oneshot", action="store_true", help="--ceiling: only the one-shot (slab 2) reads")
     ap.add_argument("--shape-sweep", action="store_true",
                     help="only the layer GEMVs under each launch shape the tuning switches select "
-                         "(ASDSL_HIP_KSPLIT x ASDSL_HIP_XLDS), one JSON line per GEMV")
+                         "(ASDSL_HIP_KSPLIT x ASDSL_HIP_PRE_SPLIT), one JSON line per GEMV")
     ap.add_argument("--suite", action="store_true",
                     help="one JSON line per hot-path row: kernel at its workload vs the HBM roofline, "
                          "with the reference's compiled CPU kernel timed on the same inputs")
@@ -1536,8 +1547,13 @@ def main() -> int:
     cycle = capture(lambda h: [step(i, h) for i in range(L)])
     rem = args.steps % L
     tail = capture(lambda h: [step(i, h) for i in range(rem)]) if rem else None
-    for _ in range(max(1, args.warmup // L)):
+    # exactly --warmup untimed steps: whole rotation cycles, then the rest
+    for _ in range(args.warmup // L):
         cycle.replay()
+    if args.warmup % L:
+        warm_tail = capture(lambda h: [step(i, h) for i in range(args.warmup % L)])
+        warm_tail.replay()
+        del warm_tail
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -1640,8 +1656,10 @@ def main() -> int:
             "stream_floor_us": floors["gate_up"]["us"],
             "stream_floor_GB/s": floors["gate_up"]["GB/s"],
             "frac_of_stream_floor": round(floors["gate_up"]["us"] / gu_us, 4),
-            "stream_floor": "asdsl_stream_read over the same byte count, same graph timing: the practical "
-                            "ceiling for one launch of this size",
+            "stream_floor_config": floors["gate_up"]["config"],
+            "stream_floor": "asdsl_stream_read_ex over the same byte count in the read shapes that reach the "
+                            "single-launch ceiling (FLOOR_CONFIGS), same graph timing: the practical ceiling "
+                            "for one launch of this size",
         },
         "per_gemv": per,
         "extra": extra,
