@@ -26,14 +26,16 @@ PHI4_NO_LMHEAD_PREQ2_CACHE, ASDSL_IGNORE_EOS.
 
 pld_generate verifies a draft in one multi-token pass (the verify columns'
 greedy tokens come from the GPU), then, like the reference, rolls the KV
-cache back and re-runs the committed tokens one at a time.  The batched pass
-follows the single-token step's arithmetic only to fp32 rounding, and int8
-activation quantization can turn such a difference into a different argmax
-where two logits are close; so each re-run step's own argmax is checked
-against the next committed token, and the commit stops at the first
-disagreement (the serial token then comes next).  The returned tokens are
-therefore exactly those of serial greedy decoding.  rerun=False instead
-keeps the verify pass's K/V and argmax (no serial re-run).
+cache back and re-runs the committed tokens one at a time.  Each re-run
+step's own argmax is checked against the next committed token, and the
+commit stops at the first disagreement (the serial token then comes next),
+so the returned tokens are exactly those of serial greedy decoding whatever
+the pass computes.  rerun=False instead keeps the verify pass's K/V and
+argmax (no serial re-run).  The default pass is the single-token step bit
+for bit below 2048 positions, so that is lossless too; with the MFMA form
+(ASDSL_HIP_VERIFY_MFMA=1) the pass follows the step only to fp32 rounding,
+which int8 activation quantization can turn into a different argmax where
+two logits are close.
 """
 
 from __future__ import annotations

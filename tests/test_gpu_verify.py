@@ -1,14 +1,15 @@
 """HIP parity for the multi-token verify pass (asdsl_decode_verify), the KV
 snapshot / restore / truncate semantics and Prompt Lookup Decoding.
 
-Bars (the decode step's, from the task statement: logits within 1e-3
-relative L2 with top-1 agreement): every verify column has the oracle's
-greedy token (the oracle's serial decode step at that position is the
-reference's serial fallback, unified_engine.cpp:1774-1789) and logits
-within 1e-3 relative L2 of it in at least half of the columns, all within
-5e-2; the K/V rows it writes equal the oracle's to one fp16 ulp.  Against
-the single-token step on the GPU the same with 1e-5.  PLD returns exactly
-the greedy tokens.  (The stage-by-stage bars hold at full size in
+Bars (the decode step's: logits within 1e-3 relative L2 with top-1
+agreement): every verify column has the oracle's greedy token (the oracle's
+serial decode step at that position is the reference's serial fallback,
+unified_engine.cpp:1774-1789) and logits within 1e-3 relative L2 of it in
+at least three columns of four, all within 5e-2; the K/V rows it writes
+equal the oracle's to one fp16 ulp (layers after one whose input rounded an
+activation level the other way: 5e-2).  The default pass equals the
+single-token step bit for bit; the MFMA form is held to 1e-5 in three
+columns of four against it.  PLD returns exactly the greedy tokens.  (The stage-by-stage bars hold at full size in
 test_gpu_decode_full.py: every kernel within 1e-3 of the oracle fed the
 oracle's own input.)
 
@@ -31,12 +32,22 @@ from conftest import rel_l2
 
 pytestmark = pytest.mark.gpu
 
-TIGHT_SHARE = 0.5  # measured: 2 of 4 columns flip in a 2-layer model at ctx 100
+# measured: 29 of 30 columns at 2e-7; one at 8.3e-3 (ctx 300, 16 columns: the
+# single-token step's own int8 flip, which the pass reproduces bit for bit)
+TIGHT_SHARE = 0.75
 LOOSE = 5e-2
 
 
-def _check_columns(errs, tight):
-    """errs: per-column relative L2 errors."""
+def _check_columns(errs, tight, label=None):
+    """errs: per-column relative L2 errors (one JSON line of them, with
+    label, to the file ASDSL_DECODE_PARITY_LOG names, if set)."""
+    import json
+    import os
+
+    path = os.environ.get("ASDSL_DECODE_PARITY_LOG")
+    if path and label is not None:
+        with open(path, "a") as f:
+            f.write(json.dumps({"test": "verify_columns", **label, "errs": [float(e) for e in errs]}) + "\n")
     errs = np.asarray(errs)
     assert np.all(errs < LOOSE), errs
     assert np.mean(errs < tight) >= TIGHT_SHARE, errs
@@ -79,15 +90,15 @@ def test_verify_matches_serial_oracle(gpu, ctx, n):
         want, want_next = od.decode_step(model, t, ctx + c, kc, vc)
         errs.append(rel_l2(logits[c], want))
         assert nxt[c] == want_next == od.argmax_first(logits[c]), c
-    _check_columns(errs, 1e-3)
+    _check_columns(errs, 1e-3, {"vs": "oracle", "ctx": ctx, "n": n})
     for li, L in enumerate(eng.layers):
         gk, gv = _host(L["k_cache"]), _host(L["v_cache"])
         sl = slice(ctx, ctx + n)
         for got, want in ((gk, kc[li]), (gv, vc[li])):
             g32, w32 = got[:, sl].astype(np.float32), want[:, sl].astype(np.float32)
-            if li == 0:  # fp16 of GEMV outputs that differ from the oracle's in the last fp32 bits: one fp16 ulp
+            if li == 0 or max(errs) < 1e-3:  # fp16 of GEMV outputs that differ in the last fp32 bits: one ulp
                 np.testing.assert_allclose(g32, w32, rtol=1e-3, atol=1e-3)
-            else:  # fed by layer 0's output, which carries any activation level rounded the other way
+            else:  # fed by a layer whose input had an activation level rounded the other way
                 assert rel_l2(g32.ravel(), w32.ravel()) < 5e-2, li
         assert np.array_equal(gk[:, :ctx], kc[li][:, :ctx]) and not gk[:, ctx + n:].any()
 
@@ -112,7 +123,7 @@ def test_verify_matches_single_token_steps(gpu, form, monkeypatch):
         single = _host(eng.forward_token(t, 200 + c))
         errs.append(rel_l2(batched[c], single))
         assert bnext[c] == eng.next_token(), c
-    _check_columns(errs, 1e-5)
+    _check_columns(errs, 1e-5, {"vs": "single_token_" + form, "ctx": 200, "n": len(toks)})
 
 
 def test_snapshot_restore_truncate(gpu):
@@ -336,7 +347,7 @@ def _bits_case(eng, ctx, toks):
 @pytest.mark.parametrize("ctx,n", [(0, 3), (200, 8), (500, 16), (1000, 5)])
 def test_verify_is_the_single_token_step_bit_for_bit(gpu, kv, ctx, n):
     """The default verify pass (dot4 GEMVs in the single-token launch
-    shapes, factored norms, the attention's one-tile splits) on a 2-layer
+    shapes, norms in the step's order, the attention's one-tile splits) on a 2-layer
     model: every column equals the single-token step at its position bit for
     bit, across the short form (below 512: o_proj merges the splits) and the
     long form (combine kernel), 500 + 16 crossing between them."""
