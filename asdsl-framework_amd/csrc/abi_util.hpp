@@ -148,6 +148,18 @@ asdsl_status preq2_batch_mfma_image(const uint8_t* meta, const uint8_t* quant, c
                                     int out_features, int in_features, int group_size, int n_cols,
                                     asdsl_stream_t stream);
 
+// The MFMA batched GEMV in the single-column GEMV's fp32 order (up to 16
+// columns): column n of Y is bit for bit what that GEMV gives on column n
+// (same per-lane unit order, row reduction tree and K-split sum), the int32
+// dots from MFMA.  Reads an image with its per-slice sums (image_store8 with
+// `us`; image_fac_offset / image_us_offset).  preq2_batch_exact_mfma_applies
+// says whether the single-column shape of M x K allows it (exact split, K
+// split <= 4, K <= 8192, 1..16 columns).
+bool preq2_batch_exact_mfma_applies(int out_features, int in_features, int group_size, int n_cols);
+asdsl_status preq2_batch_exact_mfma_image(const uint8_t* meta, const uint8_t* quant, const void* image, float* Y,
+                                          int out_features, int in_features, int group_size, int n_cols,
+                                          asdsl_stream_t stream);
+
 // The decode step's o_proj: gemv_preq2_fused of the attention output, which
 // the GEMV's prologue merges itself from the split partials (part: per head
 // nsplit rows of part_stride floats, m, l, acc[head_dim]) of a position

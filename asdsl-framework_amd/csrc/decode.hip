@@ -311,7 +311,8 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
                                                                       int max_seq, int pos_limit, int fold, int ncols,
                                                                       int form_tile, int form_splits,
                                                                       uint2* __restrict__ img,
-                                                                      float2* __restrict__ fac) {
+                                                                      float2* __restrict__ fac,
+                                                                      float* __restrict__ us) {
     constexpr int kChunk = 16;
     constexpr int kHeadChunks = kHeadDim / 8;
     __shared__ float gml[kCombineGroups][2];
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
     const int g = tid / kHeadDim;
     // the first kHeadChunks lanes quantize the head's outputs (8 each)
     auto image_chunk = [&](const float (&v)[8]) {
-        if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, h * kHeadChunks + tid, col, true, img, fac);
+        if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, h * kHeadChunks + tid, col, true, img, fac, us);
     };
     const float zeros[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     if (IMG_GS != 0 && col >= ncols) {
@@ -743,7 +744,7 @@ asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q
     const StageScope stage("attention_combine");
     return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
                   static_cast<const float*>(work), pos, att, kMaxSplits, max_seq, limit, 0, 1, f.tile, f.max_splits,
-                  static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
+                  static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr), static_cast<float*>(nullptr));
 }
 
 int attn_splits(int max_seq) { return (max_seq + kSplit - 1) / kSplit; }
@@ -856,6 +857,7 @@ __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __
                                                                        float* __restrict__ X, int K, float eps,
                                                                        int ncols, uint2* __restrict__ img,
                                                                        float2* __restrict__ fac,
+                                                                       float* __restrict__ us,
                                                                        float* __restrict__ inv_out) {
     __shared__ float red[kNormThreads / kWave];
     const int col = static_cast<int>(blockIdx.x);
@@ -865,7 +867,7 @@ __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __
         if (col >= ncols) {
             const float z[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
             for (int base = 0; base < nchunk; base += kNormThreads)  // uniform per workgroup
-                image_store8<IMG_GS>(z, base + tid, col, base + tid < nchunk, img, fac);
+                image_store8<IMG_GS>(z, base + tid, col, base + tid < nchunk, img, fac, us);
             return;
         }
     }
@@ -922,7 +924,7 @@ __global__ __launch_bounds__(kNormThreads) void verify_add_norm_kernel(float* __
             x[2 * ch] = make_float4(v[0], v[1], v[2], v[3]);
             x[2 * ch + 1] = make_float4(v[4], v[5], v[6], v[7]);
         }
-        if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, ch, col, ch < nchunk, img, fac);
+        if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, ch, col, ch < nchunk, img, fac, us);
     }
 }
 
@@ -1075,7 +1077,7 @@ __global__ __launch_bounds__(kAttnThreads) void verify_attn_partial_kernel(
 template <int IMG_GS>
 __global__ __launch_bounds__(256) void verify_swiglu_kernel(const float* __restrict__ GU, float* __restrict__ S,
                                                             int ffn, float thr, int ncols, uint2* __restrict__ img,
-                                                            float2* __restrict__ fac) {
+                                                            float2* __restrict__ fac, float* __restrict__ us) {
     const int col = static_cast<int>(blockIdx.y);
     const size_t c = static_cast<size_t>(col);
     const int nchunk = ffn >> 3;
@@ -1095,7 +1097,7 @@ __global__ __launch_bounds__(256) void verify_swiglu_kernel(const float* __restr
             sp[1] = make_float4(v[4], v[5], v[6], v[7]);
         }
     }
-    if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, ch, col, ch < nchunk, img, fac);
+    if constexpr (IMG_GS != 0) image_store8<IMG_GS>(v, ch, col, ch < nchunk, img, fac, us);
 }
 
 // keys[c] = max over rows of argmax_key(logits[c][row], row): the largest
@@ -1425,18 +1427,29 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     const int nsplit = attn_splits(m.max_seq);
     const int G = m.n_heads / m.n_kv_heads;
     const bool q8 = m.kv_format == ASDSL_KV_INT8;
-    // The projections take the dot4 batched GEMV in each single-token GEMV's
-    // own launch shape (preq2_batch_exact), the norm-fed ones in the
-    // single-token step's norm form (the normed input, or with
+    // Every projection repeats the single-token GEMV's arithmetic on each
+    // column, and the norm-fed ones its norm form (the normed input, or with
     // ASDSL_HIP_NORM_FACTORED h * w quantized and 1/rms applied to the
     // reduced rows): below 2048 positions, where the attention splits
     // coincide too, every column then gives the single-token step's logits,
-    // K/V rows and token bit for bit, as lossless speculative decoding needs.  ASDSL_HIP_VERIFY_MFMA=1 (read
-    // per call) takes the MFMA batched GEMV instead (16 columns per launch,
-    // from 4 columns on, 3 once K >= 4096): faster at many columns, but its
-    // fp32 summation order differs, so a column's int8 activations can round
+    // K/V rows and token bit for bit, as lossless speculative decoding needs.
+    // From 5 columns (ASDSL_HIP_VERIFY_EXACT_MFMA_MIN_N, read per call), where
+    // the single-token shape allows (preq2_batch_exact_mfma_applies), the
+    // projection is the exact MFMA form on an activation image that the
+    // kernel before it writes (the norm, the combine, the SwiGLU): the weights
+    // stream once for up to 16 columns (32-layer pass at ctx 1024: 2.23 ms
+    // against 2.70 for the dot4 form at 8 columns, 2.52 against 4.81 at 16;
+    // at 4 columns dot4 measured 2.01 against 2.15).  Otherwise, with the
+    // factored norm or ASDSL_HIP_VERIFY_DOT4=1 (read per call), the dot4
+    // batched GEMV in the single-token launch shape (preq2_batch_exact).
+    // ASDSL_HIP_VERIFY_MFMA=1 (read per call) takes the MFMA batched GEMV in
+    // its own order instead: a column's int8 activations can then round
     // differently from the single-token step's.
     const bool mfma = env_knob("ASDSL_HIP_VERIFY_MFMA") > 0;
+    const bool factored_norm = !mfma && preq2_norm_factored();
+    const int exact_min_n = env_knob("ASDSL_HIP_VERIFY_EXACT_MFMA_MIN_N");
+    const bool exact_mfma = !mfma && !factored_norm && env_knob("ASDSL_HIP_VERIFY_DOT4") == 0 &&
+                            n >= (exact_min_n > 0 ? exact_min_n : 5);
     // dot4 in the single-token launch shape, else (a shape whose split masks
     // units) the batched GEMV's own dot4 plan
     auto gemv_exact = [&](const uint8_t* meta, const uint8_t* quant, const float* Xin, const float* inv, float* Y,
@@ -1449,30 +1462,42 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     asdsl_status st = launch("verify_embed_kernel", verify_embed_kernel, dim3((m.hidden + 1023) / 1024, n), dim3(256),
                              0, s, m.embed, tokens, H, m.hidden, m.vocab, keys);
     if (st != ASDSL_OK) return st;
-    // The norm and SwiGLU kernels write the next projection's int8 image
-    // themselves when that projection takes the MFMA form, which then runs
-    // without its quantize launch.
+    // The norm, combine and SwiGLU kernels write the next projection's int8
+    // image themselves when that projection takes an image-fed form (1: the
+    // MFMA form, 2: the exact MFMA form), which then runs without a quantize
+    // launch of its own.
     auto* img = static_cast<uint2*>(mimg);
-    auto fac_of = [&](int K) { return reinterpret_cast<float2*>(static_cast<uint8_t*>(mimg) + static_cast<size_t>(K) * 16); };
+    auto fac_of = [&](int K) { return reinterpret_cast<float2*>(static_cast<uint8_t*>(mimg) + image_fac_offset(K)); };
+    auto us_of = [&](int K) { return reinterpret_cast<float*>(static_cast<uint8_t*>(mimg) + image_us_offset(K)); };
+    auto image_form = [&](const uint8_t* meta, const uint8_t* quant, int M, int K, int gs) -> int {
+        if (mfma) return preq2_batch_image_applies(meta, quant, M, K, gs, n, true) ? 1 : 0;
+        return exact_mfma && preq2_batch_exact_mfma_applies(M, K, gs, n) ? 2 : 0;
+    };
+    auto image_gemv = [&](int form, const uint8_t* meta, const uint8_t* quant, float* Y, int M, int K,
+                          int gs) -> asdsl_status {
+        return form == 1 ? preq2_batch_mfma_image(meta, quant, mimg, Y, M, K, gs, n, stream)
+                         : preq2_batch_exact_mfma_image(meta, quant, mimg, Y, M, K, gs, n, stream);
+    };
     auto norm_then_gemv = [&](const float* D, const float* nw, const uint8_t* meta, const uint8_t* quant, float* Y,
                               int M, int gs) -> asdsl_status {
         const int K = m.hidden;
-        if (preq2_batch_image_applies(meta, quant, M, K, gs, n, mfma)) {
+        const int form = image_form(meta, quant, M, K, gs);
+        if (form != 0) {
             asdsl_status r = launch("verify_add_norm_kernel",
                                     gs == 32 ? verify_add_norm_kernel<32> : verify_add_norm_kernel<128>,
                                     dim3(kImageCols), dim3(kNormThreads), 0, s, H, D, nw, X, K, m.rms_eps, n, img,
-                                    fac_of(K), static_cast<float*>(nullptr));
+                                    fac_of(K), us_of(K), static_cast<float*>(nullptr));
             if (r != ASDSL_OK) return r;
-            return preq2_batch_mfma_image(meta, quant, mimg, Y, M, K, gs, n, stream);
+            return image_gemv(form, meta, quant, Y, M, K, gs);
         }
         // the single-token GEMVs' norm form: the reference's order (normed
         // X, below) or the factored one; the factored form's 1/rms sum
         // follows the 8-wave prologue of the norm-fed GEMVs, which covers
         // K <= 4096 (the only plan they take there)
-        const bool factored = !mfma && K <= 4096 && K % 8 == 0 && preq2_norm_factored();
+        const bool factored = factored_norm && K <= 4096 && K % 8 == 0;
         asdsl_status r = launch("verify_add_norm_kernel", verify_add_norm_kernel<0>, dim3(n), dim3(kNormThreads), 0, s,
                                 H, D, nw, X, K, m.rms_eps, n, static_cast<uint2*>(nullptr),
-                                static_cast<float2*>(nullptr), factored ? INV : nullptr);
+                                static_cast<float2*>(nullptr), static_cast<float*>(nullptr), factored ? INV : nullptr);
         if (r != ASDSL_OK) return r;
         if (factored) {
             r = preq2_batch_exact(meta, quant, X, INV, Y, M, K, gs, n, stream);
@@ -1480,7 +1505,7 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
             // no exact shape: normalize in place and take the plain batched form
             r = launch("verify_add_norm_kernel", verify_add_norm_kernel<0>, dim3(n), dim3(kNormThreads), 0, s, H,
                        static_cast<const float*>(nullptr), nw, X, K, m.rms_eps, n, static_cast<uint2*>(nullptr),
-                       static_cast<float2*>(nullptr), static_cast<float*>(nullptr));
+                       static_cast<float2*>(nullptr), static_cast<float*>(nullptr), static_cast<float*>(nullptr));
             if (r != ASDSL_OK) return r;
         }
         return mfma ? preq2_fused_batch(meta, quant, X, Y, M, K, gs, n, stream, true, mimg, w.mimg_bytes)
@@ -1501,16 +1526,17 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
                           m.n_kv_heads, m.max_seq, nsplit, m.rotary_dim / 2);
         });
         if (st != ASDSL_OK) return st;
-        if (preq2_batch_image_applies(L.o_meta, L.o_quant, m.hidden, q_dim, m.gs_attn, n, mfma)) {
+        const int o_form = image_form(L.o_meta, L.o_quant, m.hidden, q_dim, m.gs_attn);
+        if (o_form != 0) {
             st = launch("attn_combine_kernel", m.gs_attn == 32 ? attn_combine_kernel<32> : attn_combine_kernel<128>,
                         dim3(m.n_heads, kImageCols), dim3(kCombineThreads), 0, s, static_cast<const float*>(part), pos,
-                        att, nsplit, m.max_seq, m.max_seq, 0, n, 0, 0, img, fac_of(q_dim));
+                        att, nsplit, m.max_seq, m.max_seq, 0, n, 0, 0, img, fac_of(q_dim), us_of(q_dim));
             if (st != ASDSL_OK) return st;
-            st = preq2_batch_mfma_image(L.o_meta, L.o_quant, mimg, O, m.hidden, q_dim, m.gs_attn, n, stream);
+            st = image_gemv(o_form, L.o_meta, L.o_quant, O, m.hidden, q_dim, m.gs_attn);
         } else {
             st = launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
                         static_cast<const float*>(part), pos, att, nsplit, m.max_seq, m.max_seq, 0, n, 0, 0,
-                        static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr));
+                        static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr), static_cast<float*>(nullptr));
             if (st != ASDSL_OK) return st;
             st = mfma ? preq2_fused_batch(L.o_meta, L.o_quant, att, O, m.hidden, q_dim, m.gs_attn, n, stream, true,
                                           mimg, w.mimg_bytes)
@@ -1519,18 +1545,18 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         if (st != ASDSL_OK) return st;
         st = norm_then_gemv(O, L.rms_ffn, L.gu_meta, L.gu_quant, GU, 2 * m.ffn, m.gs_ffn);
         if (st != ASDSL_OK) return st;
-        const bool down_img = preq2_batch_image_applies(L.down_meta, L.down_quant, m.hidden, m.ffn, m.gs_ffn, n, mfma);
+        const int down_form = image_form(L.down_meta, L.down_quant, m.hidden, m.ffn, m.gs_ffn);
         const int sw_chunks = (m.ffn / 8 + 255) / 256;
-        if (down_img) {
+        if (down_form != 0) {
             st = launch("verify_swiglu_kernel", m.gs_ffn == 32 ? verify_swiglu_kernel<32> : verify_swiglu_kernel<128>,
                         dim3(sw_chunks, kImageCols), dim3(256), 0, s, static_cast<const float*>(GU), S, m.ffn,
-                        L.fatrelu_threshold, n, img, fac_of(m.ffn));
+                        L.fatrelu_threshold, n, img, fac_of(m.ffn), us_of(m.ffn));
             if (st != ASDSL_OK) return st;
-            st = preq2_batch_mfma_image(L.down_meta, L.down_quant, mimg, O, m.hidden, m.ffn, m.gs_ffn, n, stream);
+            st = image_gemv(down_form, L.down_meta, L.down_quant, O, m.hidden, m.ffn, m.gs_ffn);
         } else {
             st = launch("verify_swiglu_kernel", verify_swiglu_kernel<0>, dim3(sw_chunks, n), dim3(256), 0, s,
                         static_cast<const float*>(GU), S, m.ffn, L.fatrelu_threshold, n, static_cast<uint2*>(nullptr),
-                        static_cast<float2*>(nullptr));
+                        static_cast<float2*>(nullptr), static_cast<float*>(nullptr));
             if (st != ASDSL_OK) return st;
             st = mfma ? preq2_fused_batch(L.down_meta, L.down_quant, S, O, m.hidden, m.ffn, m.gs_ffn, n, stream,
                                           true, mimg, w.mimg_bytes)

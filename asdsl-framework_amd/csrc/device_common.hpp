@@ -287,12 +287,14 @@ struct ActStage {
 // The int8 activation image of the MFMA batched GEMV (16 columns): chunk c
 // (8 elements) of column n as split-order int8 at img[((c / 4) * 16 + n) * 4 +
 // c % 4], and per GS-group of column n (scale, integer sum * scale) at
-// fac[(c / (GS / 8)) * 16 + n].  The GS/8 lanes of a group are consecutive
-// lanes of one wave and all call this; `active` gates the stores.
+// fac[(c / (GS / 8)) * 16 + n]; with `us`, per 32-element slice of column n
+// (integer sum * scale, the single-column GEMV's usum of that slice) at
+// us[(c / 4) * 16 + n].  The GS/8 lanes of a group are consecutive lanes of
+// one wave and all call this; `active` gates the stores.
 constexpr int kImageCols = 16;
 template <int GS>
 __device__ __forceinline__ void image_store8(const float (&v)[8], int c, int n, bool active, uint2* __restrict__ img,
-                                             float2* __restrict__ fac) {
+                                             float2* __restrict__ fac, float* __restrict__ us = nullptr) {
     constexpr int kLanes = GS / 8;
     const QChunk q = quantize8<GS>(v);
     const int gsum = kLanes == 4 ? q.usum : group_sum<kLanes>(sum4_i8(q.even) + sum4_i8(q.odd));
@@ -300,8 +302,16 @@ __device__ __forceinline__ void image_store8(const float (&v)[8], int c, int n, 
         img[(static_cast<size_t>(c >> 2) * kImageCols + n) * 4 + (c & 3)] = make_uint2(q.even, q.odd);
         if ((c & (kLanes - 1)) == 0)
             fac[static_cast<size_t>(c / kLanes) * kImageCols + n] = make_float2(q.scale, static_cast<float>(gsum) * q.scale);
+        if (us && (c & 3) == 0) us[static_cast<size_t>(c >> 2) * kImageCols + n] = static_cast<float>(q.usum) * q.scale;
     }
 }
+
+// Byte offsets of an image's parts for in_features K: img at 0 (K * 16 B),
+// fac at K * 16 (room for group size 32: K / 32 * 16 pairs), us at K * 20
+// (K / 32 * 16 floats); K * 22 bytes in all.
+__host__ __device__ constexpr size_t image_fac_offset(int K) { return static_cast<size_t>(K) * 16; }
+__host__ __device__ constexpr size_t image_us_offset(int K) { return static_cast<size_t>(K) * 20; }
+__host__ __device__ constexpr size_t image_bytes(int K) { return static_cast<size_t>(K) * 22; }
 
 // Decode-step elementwise helpers shared by the fused GEMV prologues and the
 // batched verify pass, so both compute identical values.

@@ -568,6 +568,236 @@ asdsl_status launch_batch_waves(const BatchPlan& p, const uint32_t* m, const uin
 
 // plan_batch's column count and grid on the single-column GEMV's launch
 // shape (preq2_plan_shape): K split, units per lane and waves (8, 12 or 16).
+// ------------------------------------------------------- exact MFMA form
+// The batched GEMV with the single-column GEMV's fp32 order (plan_preq2's
+// shape: K split KS = 1 << lks, NU units per lane), on an activation image
+// that carries the per-slice sums (image_store8 with `us`).  In the
+// single-column kernel the lane at virtual position v of a band's wave ks
+// accumulates, unit by unit in unit order, acc = fma(d, s*xs, acc);
+// acc = fma(-(z*s), xu, acc), where d is the exact int32 dot of the unit's 32
+// nibbles with 32 int8 activations; slot_sum then reduces the 16 lanes of a
+// row in a fixed tree and the KS partial rows are added in ks order.  Here
+// the int32 dots come from v_mfma_i32_16x16x32_i8 (16 rows x 16 columns per
+// 32-element slice, exact in any order) and the float steps are repeated in
+// the same order:
+//   GS 32:  the 16 accumulators of a row are the quads qd = g mod 16 (lane
+//           bits 2-5; in-row position qd & 3, DPP row qd >> 2).  Wave w of
+//           a K-range takes qd in [4w, 4w + 4): in every block of 16 groups
+//           its 4 consecutive groups, in block order.
+//   GS 128: the accumulators are (g mod 4, slice t) (lane bits 4-5 and 0-1).
+//           Wave w takes the groups with g mod 4 = w, in group order, all
+//           four slices of each.
+// The tree: each wave folds its four accumulators as slot_sum's in-row steps
+// do (GS 32: row_ror 4 then row_ror 8, so position 0 ends with (x0 + x3) +
+// (x2 + x1); GS 128: quad xor 1 then xor 2, (x0 + x1) + (x2 + x3)); the four
+// waves' values then pair as xor 16 and xor 32 do, (R0 + R1) + (R2 + R3); the
+// K-ranges add in order.  Workgroup = 4 * KS waves (wave 4 * ks + w) over
+// 16-row tiles (tile = blockIdx.x, += gridDim.x): the waves' activation
+// operands stay in registers and the columns' scales in LDS for every tile.
+// A tile step: 4 bands x 256 contiguous bytes, one 16-byte unit per lane,
+// staged in the wave's LDS area (bands 16 bytes apart against bank
+// conflicts), from which lane (r16, q) reads dword q of its row's unit for
+// each of the step's four MFMAs.  With PF each wave requests the next tile's
+// weights and (s, z) pairs before it computes the current one (two register
+// sets, used alternately).
+template <int GS, int NU, int KS, bool PF>
+__global__ __launch_bounds__(4 * KS * kWave) void preq2_batch_exact_mfma_kernel(
+    const uint32_t* __restrict__ meta, const uint8_t* __restrict__ quant, const uint2* __restrict__ img,
+    const float2* __restrict__ fac, const float* __restrict__ us, float* __restrict__ Y, int M, int K, int ncols) {
+#pragma clang fp contract(off)
+    constexpr int UPS = GS / 32;
+    constexpr int kGroupBytes = GS * 2;            // a band's group: 4 rows x UPS 16-byte slices
+    constexpr int kStepGroups = GS == 32 ? 4 : 1;  // groups of one wave step
+    constexpr int kRangeGroups = GS == 32 ? 16 * NU : 4 * NU;
+    extern __shared__ __align__(16) uint32_t lds_words[];
+    const int G = K / GS;
+    float2* sfac = reinterpret_cast<float2*>(lds_words);                                  // [G][16]
+    float* sus = reinterpret_cast<float*>(sfac + static_cast<size_t>(G) * kMfmaCols);    // [K/32][16] (GS 128)
+    float* red = sus + (GS == 128 ? static_cast<size_t>(K / 32) * kMfmaCols : 0);        // [2][KS][4][4][kWave]
+    uint8_t* stage_all = reinterpret_cast<uint8_t*>(red + 2 * static_cast<size_t>(KS) * 16 * kWave);
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWave - 1);
+    const int wave = tid >> 6;
+    const int ks = wave >> 2;
+    const int w = wave & 3;
+    const int r16 = lane & 15;
+    const int q = lane >> 4;
+    const int ntiles = (M + 15) >> 4;
+    const int nbands = (M + 3) >> 2;
+
+    auto first_group = [&](int st) {
+        return GS == 32 ? ks * kRangeGroups + 16 * st + 4 * w : ks * kRangeGroups + 4 * st + w;
+    };
+    // a tile's weights (lane e: unit e % 16 of band e / 16's 256-byte run)
+    // and (s, z) pairs for this wave's NU steps.  Rows past M read the last
+    // row and are never stored.
+    auto load_tile = [&](uint4 (&wq)[NU], uint32_t (&mt)[NU][kStepGroups], int tile) {
+        const int lband = min(tile * 4 + (lane >> 4), nbands - 1);
+        const int row = min(tile * 16 + r16, M - 1);
+#pragma unroll
+        for (int st = 0; st < NU; ++st)
+            wq[st] = load_stream16(
+                reinterpret_cast<const uint4*>(quant + (static_cast<size_t>(lband) * G + first_group(st)) * kGroupBytes) +
+                (lane & 15));
+#pragma unroll
+        for (int st = 0; st < NU; ++st) {
+            const uint32_t* mp = meta + static_cast<size_t>(row) * G + first_group(st);
+            if constexpr (kStepGroups == 4) {
+                const uint4 m4 = *reinterpret_cast<const uint4*>(mp);  // 4 consecutive groups: 16-byte aligned
+                mt[st][0] = m4.x;
+                mt[st][1 % kStepGroups] = m4.y;
+                mt[st][2 % kStepGroups] = m4.z;
+                mt[st][3 % kStepGroups] = m4.w;
+            } else {
+                mt[st][0] = mp[0];
+            }
+        }
+    };
+
+    // the wave's activation operands (column r16, chunk q of each slice) and,
+    // in LDS, the columns' (xs, X*xs) and slice sums for every group
+    long av[NU][4];
+#pragma unroll
+    for (int st = 0; st < NU; ++st)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            // MFMA k of the step: GS 32 group g0 + k; GS 128 slice k of group g0
+            const int slice = GS == 32 ? first_group(st) + k : first_group(st) * UPS + k;
+            const uint2 v = img[(static_cast<size_t>(slice) * kMfmaCols + r16) * 4 + q];
+            av[st][k] = static_cast<long>(static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32));
+        }
+    int tile = static_cast<int>(blockIdx.x);
+    const int step = static_cast<int>(gridDim.x);
+    uint4 wq0[NU], wq1[PF ? NU : 1];
+    constexpr int kBandStride = 256 + 16;
+    constexpr int kStepBytes = 4 * kBandStride;
+    uint8_t* stage = stage_all + static_cast<size_t>(wave) * NU * kStepBytes;
+    uint32_t mt0[NU][kStepGroups], mt1[PF ? NU : 1][kStepGroups];
+    load_tile(wq0, mt0, tile);  // the grid never exceeds the tile count
+    for (int e = tid; e < G * kMfmaCols; e += 4 * KS * kWave) sfac[e] = fac[e];
+    if constexpr (GS == 128)
+        for (int e = tid; e < (K / 32) * kMfmaCols; e += 4 * KS * kWave) sus[e] = us[e];
+    __syncthreads();
+
+    const v4i32 zero = {0, 0, 0, 0};
+    auto run_tile = [&](auto prefetch, uint4 (&wq)[NU], uint32_t (&mt)[NU][kStepGroups], auto& wn, auto& mn,
+                        int parity) {
+        // stage this tile's weights (the wave reads back only what it wrote;
+        // a wave's LDS operations complete in order)
+#pragma unroll
+        for (int st = 0; st < NU; ++st)
+            *reinterpret_cast<uint4*>(stage + st * kStepBytes + (lane >> 4) * kBandStride + (lane & 15) * 16) = wq[st];
+        float sf[NU][kStepGroups], zs[NU][kStepGroups];
+#pragma unroll
+        for (int st = 0; st < NU; ++st)
+#pragma unroll
+            for (int k = 0; k < kStepGroups; ++k) {
+                sf[st][k] = half_bits_to_float(mt[st][k]);
+                zs[st][k] = -(half_bits_to_float(mt[st][k] >> 16) * sf[st][k]);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(prefetch)::value) load_tile(wn, mn, tile + step);
+        __builtin_amdgcn_sched_barrier(0);
+        float acc[4][4];  // [column 4q + v][accumulator j of this wave]
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[v][j] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < NU; ++st) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // the 16-byte unit of MFMA k in a band's run: GS 32, group
+                // k's row r16 & 3 (unit 4k + r); GS 128, slice k of row r
+                // (unit 4r + k); its dword q holds elements 8q..8q+7 (low
+                // nibble even), split as the activation operand is
+                const int unit = GS == 32 ? 4 * k + (r16 & 3) : 4 * (r16 & 3) + k;
+                const uint32_t wsel = *reinterpret_cast<const uint32_t*>(
+                    stage + st * kStepBytes + (r16 >> 2) * kBandStride + unit * 16 + q * 4);
+                const uint64_t b = static_cast<uint64_t>(wsel & 0x0F0F0F0Fu) |
+                                   (static_cast<uint64_t>((wsel >> 4) & 0x0F0F0F0Fu) << 32);
+                const v4i32 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[st][k], static_cast<long>(b), zero, 0, 0, 0);
+                const int g = GS == 32 ? first_group(st) + k : first_group(st);
+                const int mk = GS == 32 ? k : 0;
+                const float4 f0 = reinterpret_cast<const float4*>(sfac + static_cast<size_t>(g) * kMfmaCols + 4 * q)[0];
+                const float4 f1 = reinterpret_cast<const float4*>(sfac + static_cast<size_t>(g) * kMfmaCols + 4 * q)[1];
+                const float xs[4] = {f0.x, f0.z, f1.x, f1.z};
+                float xu[4] = {f0.y, f0.w, f1.y, f1.w};
+                if constexpr (GS == 128) {
+                    const float4 u = reinterpret_cast<const float4*>(
+                        sus + static_cast<size_t>(g * UPS + k) * kMfmaCols + 4 * q)[0];
+                    xu[0] = u.x; xu[1] = u.y; xu[2] = u.z; xu[3] = u.w;
+                }
+                // accumulator: GS 32 in-row position g mod 4 = k; GS 128 slice k
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    acc[v][k] = fmaf(static_cast<float>(d[v]), sf[st][mk] * xs[v], acc[v][k]);
+                    acc[v][k] = fmaf(zs[st][mk], xu[v], acc[v][k]);
+                }
+            }
+        }
+        // the wave's in-row fold, then the four waves and the K-ranges in LDS
+        // (two buffers by tile parity: one barrier per tile suffices)
+        float* rb = red + static_cast<size_t>(parity) * KS * 16 * kWave;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float r = GS == 32 ? (acc[v][0] + acc[v][3]) + (acc[v][2] + acc[v][1])
+                                     : (acc[v][0] + acc[v][1]) + (acc[v][2] + acc[v][3]);
+            rb[((ks * 4 + w) * 4 + v) * kWave + lane] = r;
+        }
+        __syncthreads();
+        if (wave < 4) {  // wave w stores column 4q + w
+            const int v = w;
+            float sum = 0.0f;
+#pragma unroll
+            for (int k2 = 0; k2 < KS; ++k2) {
+                const float* rr = rb + static_cast<size_t>(k2) * 16 * kWave;
+                const float p = (rr[(0 * 4 + v) * kWave + lane] + rr[(1 * 4 + v) * kWave + lane]) +
+                                (rr[(2 * 4 + v) * kWave + lane] + rr[(3 * 4 + v) * kWave + lane]);
+                sum = k2 == 0 ? p : sum + p;
+            }
+            const int n = 4 * q + v;
+            const int orow = tile * 16 + r16;
+            if (n < ncols && orow < M) Y[static_cast<size_t>(n) * M + orow] = sum;
+        }
+    };
+    const std::true_type pf_on;
+    const std::false_type pf_off;
+    if constexpr (PF) {
+        while (true) {  // uniform per workgroup
+            if (tile + step >= ntiles) {
+                run_tile(pf_off, wq0, mt0, wq0, mt0, 0);
+                break;
+            }
+            run_tile(pf_on, wq0, mt0, wq1, mt1, 0);
+            tile += step;
+            if (tile + step >= ntiles) {
+                run_tile(pf_off, wq1, mt1, wq1, mt1, 1);
+                break;
+            }
+            run_tile(pf_on, wq1, mt1, wq0, mt0, 1);
+            tile += step;
+        }
+    } else {
+        int parity = 0;
+        while (true) {  // uniform per workgroup
+            run_tile(pf_off, wq0, mt0, wq0, mt0, parity);
+            tile += step;
+            if (tile >= ntiles) break;
+            load_tile(wq0, mt0, tile);
+            parity ^= 1;
+        }
+    }
+}
+
+size_t exact_mfma_lds_bytes(int K, int gs, int ks, int nu) {
+    return static_cast<size_t>(K / gs) * kMfmaCols * sizeof(float2) +
+           (gs == 128 ? static_cast<size_t>(K / 32) * kMfmaCols * sizeof(float) : 0) +
+           2 * static_cast<size_t>(ks) * 4 * 4 * kWave * sizeof(float) +
+           static_cast<size_t>(4 * ks) * nu * 4 * (256 + 16);  // per wave: nu steps of 4 padded bands
+}
+
 BatchPlan plan_batch_single(int M, int K, int gs, int cus) {
     BatchPlan p{0, 0, 8, 0, 16, false, cus};
     preq2_plan_shape(M, K, cus, &p.lks, &p.nu, &p.waves, &p.exact);
@@ -710,6 +940,102 @@ asdsl_status asdsl::preq2_batch_exact(const uint8_t* meta, const uint8_t* quant,
     return ASDSL_OK;
 }
 
+namespace asdsl {
+namespace {
+
+template <int GS, int NU, int KS>
+asdsl_status launch_exact_mfma_ks(bool pf, dim3 grid, size_t lds, hipStream_t s, const uint32_t* m, const uint8_t* q,
+                                  const uint2* img, const float2* fac, const float* us, float* Y, int M, int K,
+                                  int ncols) {
+    // K split 4 (16 waves, 128 registers): no room for the second register
+    // set; the caller gives such launches one workgroup per tile
+    if constexpr (KS < 4) {
+        if (pf)
+            return launch("preq2_batch_exact_mfma_kernel", preq2_batch_exact_mfma_kernel<GS, NU, KS, true>, grid,
+                          dim3(4 * KS * kWave), lds, s, m, q, img, fac, us, Y, M, K, ncols);
+    }
+    return launch("preq2_batch_exact_mfma_kernel", preq2_batch_exact_mfma_kernel<GS, NU, KS, false>, grid,
+                  dim3(4 * KS * kWave), lds, s, m, q, img, fac, us, Y, M, K, ncols);
+}
+
+template <int GS, int NU>
+asdsl_status launch_exact_mfma_nu(int ks, bool pf, dim3 grid, size_t lds, hipStream_t s, const uint32_t* m,
+                                  const uint8_t* q, const uint2* img, const float2* fac, const float* us, float* Y,
+                                  int M, int K, int ncols) {
+    switch (ks) {
+        case 1: return launch_exact_mfma_ks<GS, NU, 1>(pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 2: return launch_exact_mfma_ks<GS, NU, 2>(pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        default:
+            // K split 4 with K <= 8192 leaves at most 4 units per lane
+            if constexpr (NU <= 4)
+                return launch_exact_mfma_ks<GS, NU, 4>(pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+            set_error("gemv_preq2_batch_exact_mfma: no kernel for K split 4 with %d units per lane", NU);
+            return ASDSL_ERR_UNSUPPORTED;
+    }
+}
+
+template <int GS>
+asdsl_status launch_exact_mfma(int nu, int ks, bool pf, dim3 grid, size_t lds, hipStream_t s, const uint32_t* m,
+                               const uint8_t* q, const uint2* img, const float2* fac, const float* us, float* Y, int M,
+                               int K, int ncols) {
+    switch (nu) {
+        case 1: return launch_exact_mfma_nu<GS, 1>(ks, pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 2: return launch_exact_mfma_nu<GS, 2>(ks, pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 3: return launch_exact_mfma_nu<GS, 3>(ks, pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 4: return launch_exact_mfma_nu<GS, 4>(ks, pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 5: return launch_exact_mfma_nu<GS, 5>(ks, pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        default: return launch_exact_mfma_nu<GS, 6>(ks, pf, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+    }
+}
+
+}  // namespace
+}  // namespace asdsl
+
+bool asdsl::preq2_batch_exact_mfma_applies(int out_features, int in_features, int group_size, int n_cols) {
+    if ((group_size != 32 && group_size != 128) || out_features <= 0 || in_features <= 0 ||
+        in_features % group_size != 0 || in_features > 8192 || n_cols < 1 || n_cols > kMfmaCols)
+        return false;
+    const int cus = cu_count_current();
+    if (cus < 0) return false;
+    int lks = 0, nu = 0, waves = 0;
+    bool exact = false;
+    preq2_plan_shape(out_features, in_features, cus, &lks, &nu, &waves, &exact);
+    return exact && lks <= 2 && nu >= 1 && nu <= (lks == 2 ? 4 : 6);
+}
+
+asdsl_status asdsl::preq2_batch_exact_mfma_image(const uint8_t* meta, const uint8_t* quant, const void* image,
+                                                 float* Y, int out_features, int in_features, int group_size,
+                                                 int n_cols, asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(meta && quant && image && Y, "gemv_preq2_batch_exact_mfma: null pointer");
+    ASDSL_CHECK_ARG(preq2_batch_exact_mfma_applies(out_features, in_features, group_size, n_cols),
+                    "gemv_preq2_batch_exact_mfma: the form does not apply to this call");
+    ASDSL_CHECK_ARG(reinterpret_cast<uintptr_t>(image) % 16 == 0 && reinterpret_cast<uintptr_t>(quant) % 4 == 0,
+                    "gemv_preq2_batch_exact_mfma: image must be 16-byte and quant 4-byte aligned");
+    ASDSL_CU_COUNT(cus);
+    const int M = out_features, K = in_features;
+    int lks = 0, nu = 0, waves = 0;
+    bool exact = false;
+    preq2_plan_shape(M, K, cus, &lks, &nu, &waves, &exact);
+    const int ks = 1 << lks;
+    const auto* base = static_cast<const uint8_t*>(image);
+    const auto* img = reinterpret_cast<const uint2*>(base);
+    const auto* fac = reinterpret_cast<const float2*>(base + image_fac_offset(K));
+    const auto* us = reinterpret_cast<const float*>(base + image_us_offset(K));
+    // workgroups per compute unit (ASDSL_HIP_EXACT_WG_PER_CU, default 2),
+    // capped at the tile count; more tiles than workgroups: prefetch
+    static const int knob = env_knob("ASDSL_HIP_EXACT_WG_PER_CU");
+    const int per_cu = knob > 0 ? knob : 2;
+    const int tiles = (M + 15) / 16;
+    const int gridn = ks == 4 || tiles < per_cu * cus ? tiles : per_cu * cus;
+    const bool pf = tiles > gridn;
+    const dim3 grid(gridn);
+    const size_t lds = exact_mfma_lds_bytes(K, group_size, ks, nu);
+    const auto* m = reinterpret_cast<const uint32_t*>(meta);
+    hipStream_t s = as_hip(stream);
+    return group_size == 32 ? launch_exact_mfma<32>(nu, ks, pf, grid, lds, s, m, quant, img, fac, us, Y, M, K, n_cols)
+                            : launch_exact_mfma<128>(nu, ks, pf, grid, lds, s, m, quant, img, fac, us, Y, M, K, n_cols);
+}
+
 extern "C" asdsl_status asdsl_gemv_preq2_fused_batch(const uint8_t* meta, const uint8_t* quant, const float* X,
                                                      float* Y, int out_features, int in_features, int group_size,
                                                      int n_cols, asdsl_stream_t stream) {
@@ -750,7 +1076,7 @@ asdsl_status asdsl::preq2_batch_mfma_image(const uint8_t* meta, const uint8_t* q
 
 extern "C" size_t asdsl_gemv_preq2_fused_batch_work_bytes(int in_features) {
     if (in_features <= 0 || in_features % 32 != 0) return 0;
-    return static_cast<size_t>(in_features / 32) * kMfmaCols * (32 + sizeof(float2));
+    return image_bytes(in_features);  // int8 image, group (scale, sum) pairs, slice sums
 }
 
 extern "C" asdsl_status asdsl_gemv_preq2_fused_batch_ws(const uint8_t* meta, const uint8_t* quant, const float* X,

@@ -611,16 +611,18 @@ def verify_pass_us(eng, ctx: int, per_token_us, counts=(4, 8, 16), reps: int = 2
     """Multi-token verify pass (asdsl_decode_verify) of N tokens at position
     ctx, captured in a HIP graph (the token ids and the position already on
     the device) and replayed: microseconds per pass against N single-token
-    steps at the same context; the default form (dot4 in the single-token
-    GEMVs' launch shapes, bit for bit the single-token step) at the top level,
-    the MFMA form (ASDSL_HIP_VERIFY_MFMA=1) under "mfma"."""
+    steps at the same context; the default form (the exact MFMA GEMVs, bit
+    for bit the single-token step) at the top level, the dot4 exact form
+    (ASDSL_HIP_VERIFY_DOT4=1, also bit for bit) under "dot4", the MFMA form
+    in its own order (ASDSL_HIP_VERIFY_MFMA=1) under "mfma"."""
     res = {"ctx": ctx, **_verify_pass_rows(eng, ctx, per_token_us, counts, reps)}
-    os.environ["ASDSL_HIP_VERIFY_MFMA"] = "1"
-    try:
-        res["mfma"] = _verify_pass_rows(eng, ctx, per_token_us, counts, reps)
-    finally:
-        del os.environ["ASDSL_HIP_VERIFY_MFMA"]
-    res["mfma_vs_dot4"] = verify_flip_rate(eng, ctx, max(counts))
+    for key, knob in (("dot4", "ASDSL_HIP_VERIFY_DOT4"), ("mfma", "ASDSL_HIP_VERIFY_MFMA")):
+        os.environ[knob] = "1"
+        try:
+            res[key] = _verify_pass_rows(eng, ctx, per_token_us, counts, reps)
+        finally:
+            del os.environ[knob]
+    res["mfma_vs_exact"] = verify_flip_rate(eng, ctx, max(counts))
     return res
 
 
@@ -711,19 +713,18 @@ def pld_tokens_per_s(eng, new_tokens: int = 96, max_draft_k: int = 8) -> dict:
 
 
 def verify_flip_rate(eng, ctx: int, n: int) -> dict:
-    """The verify pass of tokens 1..n at ctx with the projections as the
-    dot4 forms in the single-token launch shapes (the default, bit for bit
-    the single-token step) and as MFMA batched GEMVs
-    (ASDSL_HIP_VERIFY_MFMA=1): how often the greedy tokens agree and the
-    logits' relative L2 distance, plus the dot4 pass's time (eager, one
-    pass)."""
+    """The verify pass of tokens 1..n at ctx in the default (exact) form,
+    bit for bit the single-token step, and with the projections as MFMA
+    batched GEMVs in their own order (ASDSL_HIP_VERIFY_MFMA=1): how often the
+    greedy tokens agree and the logits' relative L2 distance, plus the exact
+    pass's time (eager, one pass)."""
     import torch
 
     toks = list(range(1, n + 1))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     d4 = eng.forward_batch_all_logits(toks, ctx).float().cpu().numpy()
-    dot4_ms = 1e3 * (time.perf_counter() - t0)
+    exact_ms = 1e3 * (time.perf_counter() - t0)
     dt = eng.verify_next_tokens()
     os.environ["ASDSL_HIP_VERIFY_MFMA"] = "1"
     try:
@@ -734,7 +735,7 @@ def verify_flip_rate(eng, ctx: int, n: int) -> dict:
     errs = [float(np.linalg.norm(mf[c] - d4[c]) / np.linalg.norm(d4[c])) for c in range(n)]
     return {"columns": n, "same_token_share": sum(a == b for a, b in zip(mt, dt)) / n,
             "rel_l2_median": float(np.median(errs)), "rel_l2_max": float(max(errs)),
-            "dot4_eager_pass_ms": round(dot4_ms, 2)}
+            "exact_eager_pass_ms": round(exact_ms, 2)}
 
 
 # --------------------------------------------------------------------------- suite

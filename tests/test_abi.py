@@ -103,7 +103,8 @@ def test_work_buffer_queries_and_checks_without_gpu():
     one = ctypes.c_void_p(256)
     assert lib.asdsl_sparse_down_work_bytes(3072) == 32 * 3072 * 4
     assert lib.asdsl_sparse_down_work_bytes(0) == 0
-    assert lib.asdsl_gemv_preq2_fused_batch_work_bytes(3072) == 96 * 16 * 40
+    # per 32-element slice and column: 32 int8 codes, a (scale, sum) pair, a slice sum
+    assert lib.asdsl_gemv_preq2_fused_batch_work_bytes(3072) == 96 * 16 * 44
     assert lib.asdsl_gemv_preq2_fused_batch_work_bytes(100) == 0
     # gate_up 16384 x 3072 at group 32: 96 units, one K slab (8 waves x 12 units): image + sums only
     assert lib.asdsl_affine_batch_work_bytes(16384, 3072, 32) == 96 * 2 * 64 * 16 + 96 * 16 * 4 + 16 * 4

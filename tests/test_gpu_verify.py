@@ -343,19 +343,44 @@ def _bits_case(eng, ctx, toks):
                 torch.equal(L["v_scale"][:, ctx:ctx + n], sc_b[li][1]), li
 
 
+@pytest.mark.parametrize("form", ["exact_mfma", "dot4"])
 @pytest.mark.parametrize("kv", ["fp16", "int8"])
 @pytest.mark.parametrize("ctx,n", [(0, 3), (200, 8), (500, 16), (1000, 5)])
-def test_verify_is_the_single_token_step_bit_for_bit(gpu, kv, ctx, n):
-    """The default verify pass (dot4 GEMVs in the single-token launch
-    shapes, norms in the step's order, the attention's one-tile splits) on a 2-layer
-    model: every column equals the single-token step at its position bit for
-    bit, across the short form (below 512: o_proj merges the splits) and the
-    long form (combine kernel), 500 + 16 crossing between them."""
+def test_verify_is_the_single_token_step_bit_for_bit(gpu, kv, ctx, n, form, monkeypatch):
+    """The verify pass in both exact forms (the default: MFMA GEMVs in the
+    single-token GEMVs' fp32 order on images the norm, combine and SwiGLU
+    kernels write; ASDSL_HIP_VERIFY_DOT4=1: dot4 GEMVs in the single-token
+    launch shapes), norms in the step's order, the attention's one-tile
+    splits, on a 2-layer model (qkv/o g32 with K split 1 and 2, gate_up,
+    down and the lm_head g128): every column equals the single-token step at
+    its position bit for bit, across the short form (below 512: o_proj
+    merges the splits) and the long form (combine kernel), 500 + 16 crossing
+    between them."""
     from asdsl.engine import DecodeConfig, DecodeEngine
+
+    if form == "dot4":
+        monkeypatch.setenv("ASDSL_HIP_VERIFY_DOT4", "1")
+    else:
+        monkeypatch.setenv("ASDSL_HIP_VERIFY_EXACT_MFMA_MIN_N", "1")  # every column count
 
     eng = DecodeEngine.synthetic(DecodeConfig(n_layers=2, vocab=4096, max_seq=1100, kv_format=kv), seed=ctx + n)
     eng.prefill_kv_random(ctx, seed=5)
     toks = [int(t) for t in np.random.default_rng(ctx).integers(0, eng.cfg.vocab, n)]
+    _bits_case(eng, ctx, toks)
+
+
+@pytest.mark.parametrize("ctx,n", [(200, 8), (700, 16)])
+def test_verify_exact_forms_with_group_32_everywhere(gpu, ctx, n):
+    """The exact MFMA form's group-32 shapes beyond qkv/o: gate_up 16384x3072
+    (K split 1, 6 units per lane), down 3072x8192 (K split 4, 4 units) and
+    the lm_head at group size 32; every column the single-token step bit for
+    bit."""
+    from asdsl.engine import DecodeConfig, DecodeEngine
+
+    eng = DecodeEngine.synthetic(DecodeConfig(n_layers=2, vocab=4096, max_seq=1024, gs_ffn=32, gs_lm=32),
+                                 seed=ctx + 3)  # 8 and 16 columns: the exact MFMA form by default
+    eng.prefill_kv_random(ctx, seed=6)
+    toks = [int(t) for t in np.random.default_rng(ctx + 4).integers(0, eng.cfg.vocab, n)]
     _bits_case(eng, ctx, toks)
 
 
