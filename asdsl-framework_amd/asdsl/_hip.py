@@ -40,6 +40,12 @@ SIGNATURES: dict[str, list] = {
     "asdsl_dequant_gguf_q6k": [_P, _P, _I, _I, _P],
     "asdsl_dequant_gguf_q5k": [_P, _P, _I, _I, _P],
     "asdsl_dequant_gguf_q8_0": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q4_0": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q4_1": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q5_0": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q5_1": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q2k": [_P, _P, _I, _I, _P],
+    "asdsl_dequant_gguf_q3k": [_P, _P, _I, _I, _P],
     "asdsl_repack_gguf_q4k_to_q4km": [_P, _P, _I, _I, _P],
     "asdsl_quantize_q4_symmetric": [_P, _P, _P, _P, _I, _I, _I, _P],
     "asdsl_profile_stages_begin": [_I],

@@ -159,7 +159,8 @@ def config_from_gguf(metadata: dict, **overrides) -> DecodeConfig:
 
 def _gguf_projection(info: dict, rows: int, cols: int, gs: int, what: str):
     """One GGUF weight -> preq2 (meta, quant) on the device: decoded to fp32
-    (asdsl_dequant_gguf_q4k / _q5k / _q6k / _q8_0), requantized to symmetric Q4 at group
+    (asdsl_dequant_gguf_*: any K-quant from Q2_K to Q6_K, Q4_0, Q4_1, Q5_0,
+    Q5_1 or Q8_0), requantized to symmetric Q4 at group
     size gs (asdsl_quantize_q4_symmetric, the reference's load_from_gguf
     rule, experiments/phi4_cpu_run.py:1437-1466) and packed as preq2
     (asdsl_repack_asym_to_preq2, zero 7.5: the requantized weights exactly)."""
@@ -187,8 +188,9 @@ def layers_from_gguf(cfg: DecodeConfig, tensors: dict) -> tuple[list[dict], dict
 
     Per layer ``blk.{i}.``: attn_qkv, attn_output, the gate and up rows
     (ffn_gate_up, or ffn_up holding both as in Phi-3/4 conversions, or
-    ffn_gate + ffn_up stacked), ffn_down -- Q4_K, Q5_K, Q6_K, Q8_0 or a
-    float type, decoded and requantized on the GPU (_gguf_projection) -- and
+    ffn_gate + ffn_up stacked), ffn_down -- Q2_K..Q6_K, Q4_0, Q4_1, Q5_0,
+    Q5_1, Q8_0 or a float type, decoded and requantized on the GPU
+    (_gguf_projection) -- and
     attn_norm / ffn_norm.
     Model-wide: token_embd (decoded, stored fp16), output_norm, and output
     (the embedding when absent: tied weights) as the lm_head at cfg.gs_lm.

@@ -10,9 +10,10 @@ typed key/value metadata, tensor infos, a data section aligned to
 ``general.alignment``, default 32).  Tensor payloads are views of the map,
 never copies.
 
-Block-quantized tensors decode on the GPU (``asdsl_dequant_gguf_q4k``,
-``_q5k``, ``_q6k``, ``_q8_0``); there is no CPU decode path, and other
-types are refused.  Deviations from the reference,
+Block-quantized tensors decode on the GPU (``asdsl_dequant_gguf_q2k``,
+``_q3k``, ``_q4k``, ``_q5k``, ``_q6k``, ``_q4_0``, ``_q4_1``, ``_q5_0``,
+``_q5_1``, ``_q8_0``); there is no CPU decode path, and other types (Q8_1,
+Q8_K and the IQ types) are refused.  Deviations from the reference,
 each a fix:
 
 * ``data`` is the tensor's raw bytes for every type.  The reference converts
@@ -57,8 +58,11 @@ _K_BLOCK_BYTES: dict[str, int] = {t: GGML_BLOCK[t][1] for t in ("q2_k", "q3_k", 
 # legacy 32-weight block types whose rows are whole blocks
 _ROW_BLOCK_TYPES = ("q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "q8_1")
 # types decoded on the GPU: ggml type -> C-ABI decoder
-_DEVICE_DECODERS = {"q4_k": "asdsl_dequant_gguf_q4k", "q5_k": "asdsl_dequant_gguf_q5k",
-                    "q6_k": "asdsl_dequant_gguf_q6k", "q8_0": "asdsl_dequant_gguf_q8_0"}
+_DEVICE_DECODERS = {"q2_k": "asdsl_dequant_gguf_q2k", "q3_k": "asdsl_dequant_gguf_q3k",
+                    "q4_k": "asdsl_dequant_gguf_q4k", "q5_k": "asdsl_dequant_gguf_q5k",
+                    "q6_k": "asdsl_dequant_gguf_q6k", "q4_0": "asdsl_dequant_gguf_q4_0",
+                    "q4_1": "asdsl_dequant_gguf_q4_1", "q5_0": "asdsl_dequant_gguf_q5_0",
+                    "q5_1": "asdsl_dequant_gguf_q5_1", "q8_0": "asdsl_dequant_gguf_q8_0"}
 
 # GGUF tensor suffix -> (ASDSL projection, module), the reference's map
 GGUF_TO_ASDSL: dict[str, tuple[str, str]] = {
@@ -268,8 +272,9 @@ def _dense(info: dict[str, Any]) -> np.ndarray:
 
 def dequant_tensor_device(info: dict[str, Any]):
     """A tensor decoded to float32 on the GPU: shape (out, in) for rank-2
-    tensors (1-D otherwise).  Q4_K, Q5_K, Q6_K and Q8_0 decode in the HIP
-    kernels; F32/F16/BF16 are converted from their bytes and uploaded."""
+    tensors (1-D otherwise).  Q2_K..Q6_K, Q4_0, Q4_1, Q5_0, Q5_1 and Q8_0
+    decode in the HIP kernels; F32/F16/BF16 are converted from their bytes
+    and uploaded."""
     from asdsl import _hip
 
     torch = _hip._torch()

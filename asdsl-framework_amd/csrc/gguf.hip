@@ -1,4 +1,5 @@
-// GGUF weights on the GPU: ggml's Q4_K, Q5_K, Q6_K and Q8_0 blocks decoded to fp32, Q4_K
+// GGUF weights on the GPU: ggml's Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q4_0, Q4_1, Q5_0, Q5_1 and Q8_0
+// blocks decoded to fp32, Q4_K
 // blocks rearranged into the ASDSL Q4_K variant that asdsl_gemv_q4km_q8 reads,
 // and fp32 weights quantized to symmetric group-wise Q4 the way the
 // reference requantizes GGUF projections (experiments/phi4_cpu_run.py:1437-1466:
@@ -36,6 +37,8 @@ constexpr int kQ4kBytes = 144;
 constexpr int kQ6kBytes = 210;
 constexpr int kQ5kBytes = 176;
 constexpr int kQ80Bytes = 34;
+constexpr int kQ2kBytes = 84;
+constexpr int kQ3kBytes = 110;
 
 __device__ __forceinline__ float half_bits(uint32_t bits) {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(bits & 0xFFFFu)));
@@ -177,6 +180,92 @@ __global__ __launch_bounds__(kGgufThreads) void dequant_q8_0_kernel(const uint8_
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(static_cast<float>(static_cast<int8_t>(q[i])), d);
+    out[t * 2] = make_float4(v[0], v[1], v[2], v[3]);
+    out[t * 2 + 1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// ggml's legacy 32-weight blocks -> fp32, one thread per 8 weights (bytes
+// read one at a time: the blocks are 2-byte aligned).  Nibble byte j holds
+// weight j (low nibble) and weight j + 16 (high nibble); the Q5 forms add a
+// little-endian 32-bit word whose bit i is weight i's fifth bit.
+//   Q4_0: fp16 d | 16 B nibbles, w = (q - 8) * d                        (18 B)
+//   Q4_1: fp16 d | fp16 m | 16 B nibbles, w = d * q + m                 (20 B)
+//   Q5_0: fp16 d | 4 B high bits | 16 B nibbles, w = (q - 16) * d       (22 B)
+//   Q5_1: fp16 d | fp16 m | 4 B high bits | 16 B nibbles, w = d * q + m (24 B)
+// The offset forms round the product and then the sum, as numpy does.
+template <int BYTES>
+__global__ __launch_bounds__(kGgufThreads) void dequant_legacy_kernel(const uint8_t* __restrict__ blocks,
+                                                                      float4* __restrict__ out, size_t n_blocks) {
+    constexpr bool kMin = BYTES == 20 || BYTES == 24;
+    constexpr bool kHigh = BYTES == 22 || BYTES == 24;
+    constexpr int kHighAt = kMin ? 4 : 2;
+    constexpr int kCodesAt = kHighAt + (kHigh ? 4 : 0);
+    const size_t t = static_cast<size_t>(blockIdx.x) * kGgufThreads + threadIdx.x;
+    const size_t b = t / 4;
+    if (b >= n_blocks) return;
+    const int part = static_cast<int>(t % 4);  // weights 8 * part .. 8 * part + 7
+    const uint8_t* blk = blocks + b * BYTES;
+    auto rd16 = [&](int at) { return static_cast<uint32_t>(blk[at]) | (static_cast<uint32_t>(blk[at + 1]) << 8); };
+    const float d = half_bits(rd16(0));
+    const float m = kMin ? half_bits(rd16(2)) : 0.0f;
+    const uint32_t qh = kHigh ? rd16(kHighAt) | (rd16(kHighAt + 2) << 16) : 0u;
+    const uint8_t* qs = blk + kCodesAt + 8 * (part & 1);
+    const int shift = (part >> 1) * 4;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int wi = 8 * part + i;
+        const int q = static_cast<int>(((qs[i] >> shift) & 0x0Fu) | (((qh >> wi) & 1u) << 4));
+        if constexpr (kMin) v[i] = __fadd_rn(__fmul_rn(d, static_cast<float>(q)), m);
+        else v[i] = __fmul_rn(static_cast<float>(q - (kHigh ? 16 : 8)), d);
+    }
+    out[t * 2] = make_float4(v[0], v[1], v[2], v[3]);
+    out[t * 2 + 1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// ggml Q2_K and Q3_K -> fp32: 32 lanes per block, lane l writes weights
+// 8l..8l+7.  Both place weight 128n + 32j + 16h + i (i < 16) in bits
+// 2j..2j+1 of code byte 32n + 16h + i under scale 8n + 2j + h, so a lane's
+// eight weights share one scale and one shift.
+//   Q2_K (84 B): 16 scale bytes | 64 code bytes | fp16 d | fp16 dmin; scale
+//     byte s: w = (d * (s & 15)) * q - dmin * (s >> 4).
+//   Q3_K (110 B): 32 high-mask bytes | 64 code bytes | 12 bytes of sixteen
+//     6-bit scales | fp16 d; q -= 4 unless bit 4n + j of mask byte 16h + i
+//     is set; scale k: low 4 bits from byte k (k < 8, low nibble) or k - 8
+//     (high nibble), top 2 bits from bits 2(k/4).. of byte 8 + k % 4;
+//     w = (d * (scale - 32)) * q.
+template <bool Q3>
+__global__ __launch_bounds__(kGgufThreads) void dequant_q23k_kernel(const uint8_t* __restrict__ blocks,
+                                                                    float4* __restrict__ out, size_t n_blocks) {
+    constexpr int kBytes = Q3 ? kQ3kBytes : kQ2kBytes;
+    const size_t t = static_cast<size_t>(blockIdx.x) * kGgufThreads + threadIdx.x;
+    const size_t b = t / 32;
+    if (b >= n_blocks) return;
+    const int l = static_cast<int>(t % 32);
+    const int n = l / 16, j = (l % 16) / 4, h = (l % 4) / 2, i0 = 8 * (l % 2);
+    const int k = 8 * n + 2 * j + h;  // scale index
+    const uint8_t* blk = blocks + b * kBytes;
+    auto rd16 = [&](int at) { return static_cast<uint32_t>(blk[at]) | (static_cast<uint32_t>(blk[at + 1]) << 8); };
+    const uint8_t* qs = blk + (Q3 ? 32 : 16) + 32 * n + 16 * h + i0;
+    float v[8];
+    if constexpr (Q3) {
+        const uint8_t* sc = blk + 96;
+        const int lo = k < 8 ? (sc[k] & 15) : (sc[k - 8] >> 4);
+        const int hi = (sc[8 + k % 4] >> (2 * (k / 4))) & 3;
+        const float dl = __fmul_rn(half_bits(rd16(108)), static_cast<float>((lo | (hi << 4)) - 32));
+        const uint8_t* hm = blk + 16 * h + i0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = ((qs[i] >> (2 * j)) & 3) - (((hm[i] >> (4 * n + j)) & 1) ? 0 : 4);
+            v[i] = __fmul_rn(dl, static_cast<float>(q));
+        }
+    } else {
+        const uint8_t s = blk[k];
+        const float dl = __fmul_rn(half_bits(rd16(80)), static_cast<float>(s & 15));
+        const float ml = __fmul_rn(half_bits(rd16(82)), static_cast<float>(s >> 4));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __fsub_rn(__fmul_rn(dl, static_cast<float>((qs[i] >> (2 * j)) & 3)), ml);
+    }
     out[t * 2] = make_float4(v[0], v[1], v[2], v[3]);
     out[t * 2 + 1] = make_float4(v[4], v[5], v[6], v[7]);
 }
@@ -329,6 +418,77 @@ extern "C" asdsl_status asdsl_dequant_gguf_q8_0(const uint8_t* blocks, float* we
     const size_t n = static_cast<size_t>(rows) * (cols / 32);
     return launch("dequant_q8_0_kernel", dequant_q8_0_kernel, dim3(grid_for(n * 4)), dim3(kGgufThreads), 0,
                   as_hip(stream), blocks, reinterpret_cast<float4*>(weights), n);
+}
+
+namespace {
+
+asdsl_status dequant_legacy(const char* fn, int bytes, const uint8_t* blocks, float* weights, int rows, int cols,
+                            asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(blocks && weights, "%s: null pointer", fn);
+    if (rows <= 0 || cols <= 0 || cols % 32 != 0) {
+        set_error("%s: rows must be positive and cols a positive multiple of 32 (got %d x %d)", fn, rows, cols);
+        return ASDSL_ERR_INVALID_ARGUMENT;
+    }
+    ASDSL_CHECK_ARG(aligned(blocks, 2) && aligned(weights, 16),
+                    "%s: blocks must be 2-byte and weights 16-byte aligned", fn);
+    const size_t n = static_cast<size_t>(rows) * (cols / 32);
+    const dim3 grid(grid_for(n * 4)), block(kGgufThreads);
+    hipStream_t s = as_hip(stream);
+    float4* out = reinterpret_cast<float4*>(weights);
+    switch (bytes) {
+        case 18: return launch("dequant_legacy_kernel", dequant_legacy_kernel<18>, grid, block, 0, s, blocks, out, n);
+        case 20: return launch("dequant_legacy_kernel", dequant_legacy_kernel<20>, grid, block, 0, s, blocks, out, n);
+        case 22: return launch("dequant_legacy_kernel", dequant_legacy_kernel<22>, grid, block, 0, s, blocks, out, n);
+        default: return launch("dequant_legacy_kernel", dequant_legacy_kernel<24>, grid, block, 0, s, blocks, out, n);
+    }
+}
+
+asdsl_status dequant_q23k(const char* fn, bool q3, const uint8_t* blocks, float* weights, int rows, int cols,
+                          asdsl_stream_t stream) {
+    ASDSL_CHECK_ARG(blocks && weights, "%s: null pointer", fn);
+    const asdsl_status cs = check_k_blocks(fn, rows, cols);
+    if (cs != ASDSL_OK) return cs;
+    ASDSL_CHECK_ARG(aligned(blocks, 2) && aligned(weights, 16),
+                    "%s: blocks must be 2-byte and weights 16-byte aligned", fn);
+    const size_t n = static_cast<size_t>(rows) * (cols / 256);
+    const dim3 grid(grid_for(n * 32)), block(kGgufThreads);
+    float4* out = reinterpret_cast<float4*>(weights);
+    return q3 ? launch("dequant_q23k_kernel", dequant_q23k_kernel<true>, grid, block, 0, as_hip(stream), blocks, out,
+                       n)
+              : launch("dequant_q23k_kernel", dequant_q23k_kernel<false>, grid, block, 0, as_hip(stream), blocks,
+                       out, n);
+}
+
+}  // namespace
+
+extern "C" asdsl_status asdsl_dequant_gguf_q4_0(const uint8_t* blocks, float* weights, int rows, int cols,
+                                                asdsl_stream_t stream) {
+    return dequant_legacy("dequant_gguf_q4_0", 18, blocks, weights, rows, cols, stream);
+}
+
+extern "C" asdsl_status asdsl_dequant_gguf_q4_1(const uint8_t* blocks, float* weights, int rows, int cols,
+                                                asdsl_stream_t stream) {
+    return dequant_legacy("dequant_gguf_q4_1", 20, blocks, weights, rows, cols, stream);
+}
+
+extern "C" asdsl_status asdsl_dequant_gguf_q5_0(const uint8_t* blocks, float* weights, int rows, int cols,
+                                                asdsl_stream_t stream) {
+    return dequant_legacy("dequant_gguf_q5_0", 22, blocks, weights, rows, cols, stream);
+}
+
+extern "C" asdsl_status asdsl_dequant_gguf_q5_1(const uint8_t* blocks, float* weights, int rows, int cols,
+                                                asdsl_stream_t stream) {
+    return dequant_legacy("dequant_gguf_q5_1", 24, blocks, weights, rows, cols, stream);
+}
+
+extern "C" asdsl_status asdsl_dequant_gguf_q2k(const uint8_t* blocks, float* weights, int rows, int cols,
+                                               asdsl_stream_t stream) {
+    return dequant_q23k("dequant_gguf_q2k", false, blocks, weights, rows, cols, stream);
+}
+
+extern "C" asdsl_status asdsl_dequant_gguf_q3k(const uint8_t* blocks, float* weights, int rows, int cols,
+                                               asdsl_stream_t stream) {
+    return dequant_q23k("dequant_gguf_q3k", true, blocks, weights, rows, cols, stream);
 }
 
 extern "C" asdsl_status asdsl_repack_gguf_q4k_to_q4km(const uint8_t* gguf_blocks, uint8_t* q4km_blocks, int rows,

@@ -708,6 +708,37 @@ asdsl_status asdsl_dequant_gguf_q5k(const uint8_t* blocks, float* weights, int r
 asdsl_status asdsl_dequant_gguf_q8_0(const uint8_t* blocks, float* weights, int rows, int cols,
                                     asdsl_stream_t stream);
 
+/* ggml's legacy 32-weight blocks[rows][cols/32] -> fp32 weights[rows][cols]
+ * (cols a multiple of 32; blocks 2-byte and weights 16-byte aligned).  Nibble
+ * byte j holds weight j (low) and j + 16 (high); Q5 blocks add a 32-bit word
+ * of fifth bits (bit i: weight i).
+ *   Q4_0 (18 B): fp16 d | nibbles;                 w = (q - 8) * d
+ *   Q4_1 (20 B): fp16 d | fp16 m | nibbles;        w = d * q + m
+ *   Q5_0 (22 B): fp16 d | high bits | nibbles;     w = (q - 16) * d
+ *   Q5_1 (24 B): fp16 d | fp16 m | high bits | nibbles; w = d * q + m
+ * Replace dequant_tensor for these types (asdsl/io/gguf_loader.py:150-181). */
+asdsl_status asdsl_dequant_gguf_q4_0(const uint8_t* blocks, float* weights, int rows, int cols,
+                                    asdsl_stream_t stream);
+asdsl_status asdsl_dequant_gguf_q4_1(const uint8_t* blocks, float* weights, int rows, int cols,
+                                    asdsl_stream_t stream);
+asdsl_status asdsl_dequant_gguf_q5_0(const uint8_t* blocks, float* weights, int rows, int cols,
+                                    asdsl_stream_t stream);
+asdsl_status asdsl_dequant_gguf_q5_1(const uint8_t* blocks, float* weights, int rows, int cols,
+                                    asdsl_stream_t stream);
+
+/* ggml Q2_K blocks[rows][cols/256][84] and Q3_K blocks[rows][cols/256][110]
+ * -> fp32 weights[rows][cols] (blocks 2-byte, weights 16-byte aligned).
+ * Weight 128n + 32j + 16h + i sits in bits 2j..2j+1 of code byte
+ * 32n + 16h + i under scale 8n + 2j + h.  Q2_K (16 scale bytes | codes |
+ * fp16 d | fp16 dmin): w = (d * (s & 15)) * q - dmin * (s >> 4).  Q3_K
+ * (32 high-mask bytes | codes | 12 bytes of 6-bit scales | fp16 d): q -= 4
+ * unless mask bit 4n + j of byte 16h + i is set, w = (d * (scale - 32)) * q.
+ * Replace dequant_tensor for Q2_K and Q3_K (asdsl/io/gguf_loader.py:150-181). */
+asdsl_status asdsl_dequant_gguf_q2k(const uint8_t* blocks, float* weights, int rows, int cols,
+                                   asdsl_stream_t stream);
+asdsl_status asdsl_dequant_gguf_q3k(const uint8_t* blocks, float* weights, int rows, int cols,
+                                   asdsl_stream_t stream);
+
 /* ggml Q4_K blocks -> the ASDSL Q4_K variant blocks that asdsl_gemv_q4km_q8
  * reads (6-bit scales and mins as one linear bitstream, each sub-block's
  * codes in its own 16 bytes), losslessly, so that the GEMV computes ggml's

@@ -403,6 +403,35 @@ def dequant_gguf_q8_0(blocks, n_blocks: int) -> np.ndarray:
     return w
 
 
+# bytes per 32-weight block of ggml's legacy types
+LEGACY_BLOCK_BYTES = {"q4_0": 18, "q4_1": 20, "q5_0": 22, "q5_1": 24}
+
+
+def dequant_gguf_legacy(kind: str, blocks, n_blocks: int) -> np.ndarray:
+    """ggml Q4_0 / Q4_1 / Q5_0 / Q5_1 blocks (32 weights each) -> float32 weights."""
+    nb = LEGACY_BLOCK_BYTES[kind]
+    b = _blocks_in(blocks, n_blocks, nb)
+    w = np.empty(n_blocks * 32, np.float32)
+    lib().oracle_dequant_gguf_legacy(_p(b, _c_u8p), ctypes.c_int(nb), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
+    return w
+
+
+def dequant_gguf_q2k(blocks, n_blocks: int) -> np.ndarray:
+    """ggml Q2_K blocks (84 bytes per 256 weights) -> float32 weights."""
+    b = _blocks_in(blocks, n_blocks, 84)
+    w = np.empty(n_blocks * 256, np.float32)
+    lib().oracle_dequant_gguf_q2k(_p(b, _c_u8p), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
+    return w
+
+
+def dequant_gguf_q3k(blocks, n_blocks: int) -> np.ndarray:
+    """ggml Q3_K blocks (110 bytes per 256 weights) -> float32 weights."""
+    b = _blocks_in(blocks, n_blocks, 110)
+    w = np.empty(n_blocks * 256, np.float32)
+    lib().oracle_dequant_gguf_q3k(_p(b, _c_u8p), _p(w, _c_f32p), ctypes.c_size_t(n_blocks))
+    return w
+
+
 def repack_gguf_q4k_to_q4km(blocks, n_blocks: int) -> np.ndarray:
     """ggml Q4_K blocks -> the ASDSL Q4_K variant blocks gemv_q4km reads."""
     b = _blocks_in(blocks, n_blocks, 144)

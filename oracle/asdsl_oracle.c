@@ -736,6 +736,94 @@ EXPORT void oracle_dequant_gguf_q8_0(const uint8_t* blocks, float* w, size_t n_b
     }
 }
 
+/* The legacy 32-weight blocks (ggml's block_q4_0 / q4_1 / q5_0 / q5_1 and
+ * dequantize_row_q4_0 .. q5_1; gguf-py's Q4_0 .. Q5_1 dequantize_blocks).
+ * Byte j of the 16 nibble bytes holds weight j (low nibble) and weight
+ * j + 16 (high nibble); Q5 blocks add a little-endian 32-bit word whose bit
+ * i is weight i's fifth bit.  Q4_0: (q - 8) * d; Q5_0: (q - 16) * d; Q4_1
+ * and Q5_1: d * q + m with the product rounded before the sum (numpy's
+ * order).  Same parity status as the K-quant decoders above.
+ *   Q4_0: fp16 d | 16 B nibbles                 (18 bytes)
+ *   Q4_1: fp16 d | fp16 m | 16 B nibbles        (20 bytes)
+ *   Q5_0: fp16 d | 4 B high bits | 16 B nibbles (22 bytes)
+ *   Q5_1: fp16 d | fp16 m | 4 B high bits | 16 B nibbles (24 bytes) */
+static void legacy_block(const uint8_t* blk, int bytes, float* w) {
+    const float d = half_to_float(rd16(blk));
+    const int has_m = bytes == 20 || bytes == 24;
+    const int has_h = bytes == 22 || bytes == 24;
+    const float m = has_m ? half_to_float(rd16(blk + 2)) : 0.0f;
+    const uint8_t* hb = blk + (has_m ? 4 : 2);
+    const uint32_t qh = has_h ? (uint32_t)hb[0] | ((uint32_t)hb[1] << 8) | ((uint32_t)hb[2] << 16) |
+                                    ((uint32_t)hb[3] << 24)
+                              : 0u;
+    const uint8_t* qs = blk + (has_m ? 4 : 2) + (has_h ? 4 : 0);
+    for (int i = 0; i < 32; ++i) {
+        const int nib = i < 16 ? (qs[i] & 0x0F) : (qs[i - 16] >> 4);
+        const int q = nib | (int)(((qh >> i) & 1u) << 4);
+        if (has_m) {
+            volatile float p = d * (float)q;
+            w[i] = p + m;
+        } else {
+            w[i] = (float)(q - (has_h ? 16 : 8)) * d;
+        }
+    }
+}
+
+EXPORT void oracle_dequant_gguf_legacy(const uint8_t* blocks, int block_bytes, float* w, size_t n_blocks) {
+    for (size_t b = 0; b < n_blocks; ++b) legacy_block(blocks + b * block_bytes, block_bytes, w + b * 32);
+}
+
+/* ggml Q2_K (84 bytes per 256 weights: 16 scale bytes, 64 code bytes qs,
+ * fp16 d, fp16 dmin) and Q3_K (110 bytes: 32 high-mask bytes hmask, 64 code
+ * bytes qs, 12 bytes of sixteen 6-bit scales, fp16 d); ggml's
+ * dequantize_row_q2_K / q3_K, gguf-py's Q2_K / Q3_K dequantize_blocks.  Both
+ * place weight 128n + 32j + 16h + l (n, h in 0..1, j in 0..3, l in 0..15) in
+ * bits 2j..2j+1 of qs[32n + 16h + l] under scale 8n + 2j + h.
+ *   Q2_K: scale byte s: w = (d * (s & 15)) * q - dmin * (s >> 4).
+ *   Q3_K: q -= 4 unless bit 4n + j of hmask[16h + l] is set; scale k takes
+ *     its low 4 bits from byte k (k < 8, low nibble) or byte k - 8 (high
+ *     nibble) and its top 2 bits from bits 2(k/4).. of byte 8 + k % 4;
+ *     w = (d * (scale - 32)) * q.
+ * Same parity status as the other K-quant decoders. */
+EXPORT void oracle_dequant_gguf_q2k(const uint8_t* blocks, float* w, size_t n_blocks) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* blk = blocks + b * 84;
+        const uint8_t* sc = blk;
+        const uint8_t* qs = blk + 16;
+        const float d = half_to_float(rd16(blk + 80));
+        const float dmin = half_to_float(rd16(blk + 82));
+        for (int wi = 0; wi < 256; ++wi) {
+            const int n = wi / 128, j = (wi % 128) / 32, h = (wi % 32) / 16, l = wi % 16;
+            const uint8_t s = sc[8 * n + 2 * j + h];
+            const int q = (qs[32 * n + 16 * h + l] >> (2 * j)) & 3;
+            volatile float dl = d * (float)(s & 15);
+            volatile float ml = dmin * (float)(s >> 4);
+            volatile float p = dl * (float)q;
+            w[b * 256 + wi] = p - ml;
+        }
+    }
+}
+
+EXPORT void oracle_dequant_gguf_q3k(const uint8_t* blocks, float* w, size_t n_blocks) {
+    for (size_t b = 0; b < n_blocks; ++b) {
+        const uint8_t* blk = blocks + b * 110;
+        const uint8_t* hm = blk;
+        const uint8_t* qs = blk + 32;
+        const uint8_t* sc = blk + 96;
+        const float d = half_to_float(rd16(blk + 108));
+        for (int wi = 0; wi < 256; ++wi) {
+            const int n = wi / 128, j = (wi % 128) / 32, h = (wi % 32) / 16, l = wi % 16;
+            const int k = 8 * n + 2 * j + h;
+            const int lo = k < 8 ? (sc[k] & 15) : (sc[k - 8] >> 4);
+            const int hi = (sc[8 + k % 4] >> (2 * (k / 4))) & 3;
+            const int scale = (lo | (hi << 4)) - 32;
+            const int q = ((qs[32 * n + 16 * h + l] >> (2 * j)) & 3) - (((hm[16 * h + l] >> (4 * n + j)) & 1) ? 0 : 4);
+            volatile float dl = d * (float)scale;
+            w[b * 256 + wi] = dl * (float)q;
+        }
+    }
+}
+
 /* ggml Q4_K -> the ASDSL Q4_K variant read by oracle_gemv_q4km: the same d,
  * dmin, 6-bit fields (linear LSB-first stream, scales then mins) and codes
  * (sub-block j's 32 codes in bytes 16+16j.., low nibble first). */

@@ -1,4 +1,4 @@
-"""HIP parity for the GGUF path: ggml Q4_K / Q5_K / Q6_K / Q8_0 decoding
+"""HIP parity for the GGUF path: ggml Q2_K .. Q6_K, Q4_0, Q4_1, Q5_0, Q5_1 and Q8_0 decoding
 (random blocks against the oracle, the hand-worked known-answer blocks), the Q4_K ->
 ASDSL Q4_K rearrangement, the symmetric Q4 requantization (bit for bit
 against the oracle, up to the full Phi-4 projection shapes), the Q4_K GEMV
@@ -49,10 +49,48 @@ def q8_0_blocks(n, rng, scale=2e-4) -> np.ndarray:
     return b.reshape(-1)
 
 
+def legacy_blocks(kind, scale=2e-3):
+    """Random ggml legacy blocks with d (and m) drawn around `scale`."""
+    nb = oracle.LEGACY_BLOCK_BYTES[kind]
+
+    def make(n, rng) -> np.ndarray:
+        b = rng.integers(0, 256, (n, nb), dtype=np.uint8)
+        b[:, 0:2] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+        if nb in (20, 24):
+            b[:, 2:4] = _f16_bytes(-rng.uniform(0.5, 1.5, n) * 8 * scale)
+        return b.reshape(-1)
+    return make
+
+
+def q2k_blocks(n, rng, scale=1e-3) -> np.ndarray:
+    b = rng.integers(0, 256, (n, 84), dtype=np.uint8)
+    b[:, 80:82] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    b[:, 82:84] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    return b.reshape(-1)
+
+
+def q3k_blocks(n, rng, scale=1e-4) -> np.ndarray:
+    b = rng.integers(0, 256, (n, 110), dtype=np.uint8)
+    b[:, 108:110] = _f16_bytes(rng.uniform(0.5, 1.5, n) * scale)
+    return b.reshape(-1)
+
+
+def _legacy_decoder(kind):
+    return lambda raw, n: oracle.dequant_gguf_legacy(kind, raw, n)
+
+
 # ggml type id -> (weights per block, block maker, oracle decoder)
 KINDS = {12: (256, q4k_blocks, oracle.dequant_gguf_q4k), 13: (256, q5k_blocks, oracle.dequant_gguf_q5k),
-         14: (256, q6k_blocks, oracle.dequant_gguf_q6k), 8: (32, q8_0_blocks, oracle.dequant_gguf_q8_0)}
-TYPE_ID = {"q4_k": 12, "q5_k": 13, "q6_k": 14, "q8_0": 8}
+         14: (256, q6k_blocks, oracle.dequant_gguf_q6k), 8: (32, q8_0_blocks, oracle.dequant_gguf_q8_0),
+         10: (256, q2k_blocks, oracle.dequant_gguf_q2k), 11: (256, q3k_blocks, oracle.dequant_gguf_q3k),
+         2: (32, legacy_blocks("q4_0"), _legacy_decoder("q4_0")), 3: (32, legacy_blocks("q4_1"), _legacy_decoder("q4_1")),
+         6: (32, legacy_blocks("q5_0"), _legacy_decoder("q5_0")), 7: (32, legacy_blocks("q5_1"), _legacy_decoder("q5_1"))}
+TYPE_ID = {"q4_k": 12, "q5_k": 13, "q6_k": 14, "q8_0": 8, "q2_k": 10, "q3_k": 11, "q4_0": 2, "q4_1": 3, "q5_0": 6,
+           "q5_1": 7}
+# the decoders added beside Q4_K/Q5_K/Q6_K/Q8_0: ggml type -> C-ABI decoder
+MORE_DECODERS = {"q2_k": "asdsl_dequant_gguf_q2k", "q3_k": "asdsl_dequant_gguf_q3k",
+                 "q4_0": "asdsl_dequant_gguf_q4_0", "q4_1": "asdsl_dequant_gguf_q4_1",
+                 "q5_0": "asdsl_dequant_gguf_q5_0", "q5_1": "asdsl_dequant_gguf_q5_1"}
 
 
 def _decode(tid, raw, n_weights):
@@ -131,7 +169,33 @@ def test_dequant_q8_0_bit_exact(gpu, rows, cols):
                           oracle.dequant_gguf_q8_0(seven, 7).view(np.uint32))
 
 
-@pytest.mark.parametrize("kind", ["q4k", "q5k", "q6k", "q8_0"])
+@pytest.mark.parametrize("kind", sorted(MORE_DECODERS))
+@pytest.mark.parametrize("rows,blocks_per_row", [(1, 1), (7, 3), (3072, 12)])
+def test_dequant_more_types_bit_exact(gpu, kind, rows, blocks_per_row):
+    """Random blocks of each added type, up to the o_proj shape 3072 x 3072
+    (96 legacy or 12 K-quant blocks a row), against the oracle bit for bit;
+    and a tensor that starts 2-byte aligned."""
+    import torch
+
+    per, make, dec = KINDS[TYPE_ID[kind]]
+    if per == 32:
+        blocks_per_row *= 8  # legacy rows of 32-weight blocks: 8, 24, 96 blocks
+    cols = per * blocks_per_row
+    rng = np.random.default_rng(rows * 13 + cols + TYPE_ID[kind])
+    n = rows * blocks_per_row
+    blocks = make(n, rng)
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    _run(MORE_DECODERS[kind], gpu.ptr(_dev(blocks)), gpu.ptr(out), rows, cols)
+    want = dec(blocks, n).reshape(rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    if rows == 7:
+        buf = _dev(np.concatenate([np.zeros(2, np.uint8), blocks]))
+        out2 = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+        _run(MORE_DECODERS[kind], gpu.ptr(buf) + 2, gpu.ptr(out2), rows, cols)
+        assert np.array_equal(out2.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["q4k", "q5k", "q6k", "q8_0", "q2k", "q3k", "q4_0", "q4_1", "q5_0", "q5_1"])
 def test_known_answer_blocks_on_the_gpu(gpu, kind):
     """The hand-worked blocks of test_oracle_gguf.py through the kernels."""
     import torch
@@ -142,7 +206,8 @@ def test_known_answer_blocks_on_the_gpu(gpu, kind):
     blk, want = make()
     out = torch.empty((1, n), dtype=torch.float32, device="cuda")
     fn = {"q4k": "asdsl_dequant_gguf_q4k", "q5k": "asdsl_dequant_gguf_q5k", "q6k": "asdsl_dequant_gguf_q6k",
-          "q8_0": "asdsl_dequant_gguf_q8_0"}[kind]
+          "q8_0": "asdsl_dequant_gguf_q8_0", "q2k": "asdsl_dequant_gguf_q2k", "q3k": "asdsl_dequant_gguf_q3k",
+          **{k: MORE_DECODERS[k] for k in ("q4_0", "q4_1", "q5_0", "q5_1")}}[kind]
     _run(fn, gpu.ptr(_dev(blk.copy())), gpu.ptr(out), 1, n)
     w = out.cpu().numpy().reshape(-1)
     for i, v in want.items():
@@ -211,6 +276,12 @@ def test_argument_errors(gpu):
 
     with pytest.raises(ValueError, match="multiple of 256"):
         _run("asdsl_dequant_gguf_q4k", 16, 16, 2, 100)
+    with pytest.raises(ValueError, match="multiple of 256"):
+        _run("asdsl_dequant_gguf_q3k", 16, 16, 2, 100)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        _run("asdsl_dequant_gguf_q5_1", 16, 16, 2, 48)
+    with pytest.raises(ValueError, match="2-byte"):
+        _run("asdsl_dequant_gguf_q4_0", 17, 32, 1, 32)
     with pytest.raises(ValueError, match="group_size"):
         _run("asdsl_quantize_q4_symmetric", 16, 16, 16, 16, 2, 96, 48)
     with pytest.raises(ValueError, match="16-byte aligned"):
@@ -224,7 +295,9 @@ def test_argument_errors(gpu):
 MIXES = {"q4": {"qkv": "q4_k", "o": "q4_k", "gu": "q4_k", "gate": "q4_k", "up": "q6_k", "down": "q6_k",
                 "embd": "q6_k", "out": "q4_k"},
          "q5": {"qkv": "q5_k", "o": "q8_0", "gu": "q5_k", "gate": "q8_0", "up": "q5_k", "down": "q6_k",
-                "embd": "q8_0", "out": "q5_k"}}
+                "embd": "q8_0", "out": "q5_k"},
+         "legacy": {"qkv": "q4_0", "o": "q5_0", "gu": "q4_1", "gate": "q5_1", "up": "q3_k", "down": "q2_k",
+                    "embd": "q5_1", "out": "q4_0"}}
 
 
 def _write_model(path, cfg, rng, gate_up_split=False, mix="q4"):
@@ -274,7 +347,8 @@ def _oracle_preq2(tid, raw, rows, cols, gs):
     return oracle.repack_asym_to_preq2(p, s, b, rows, cols, gs)
 
 
-@pytest.mark.parametrize("split,mix", [(False, "q4"), (True, "q4"), (False, "q5"), (True, "q5")])
+@pytest.mark.parametrize("split,mix", [(False, "q4"), (True, "q4"), (False, "q5"), (True, "q5"), (False, "legacy"),
+                                       (True, "legacy")])
 def test_gguf_model_loads_and_decodes(gpu, tmp_path, split, mix):
     """2 Phi-4-shaped layers, vocab 4096, from a GGUF file: the config from
     its metadata; every preq2 operand, norm and the fp16 embedding equal to

@@ -1,9 +1,10 @@
 """The oracle's GGUF restatements on the CPU.
 
-ggml's Q4_K / Q6_K decoders reach the reference through the gguf package
-(asdsl/io/gguf_loader.py:150-181), which is absent here, so they are pinned
-by the layouts' invariants: each 6-bit field and each code moves exactly
-the weights the layout assigns it, with the value the formula gives.  The
+ggml's block decoders (Q2_K .. Q6_K, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0) reach
+the reference through the gguf package (asdsl/io/gguf_loader.py:150-181),
+which is absent here, so they are pinned by hand-worked blocks and by the
+layouts' invariants: each scale field, code and high bit moves exactly the
+weights the layout assigns it, with the value the formula gives.  The
 lossless Q4_K -> ASDSL Q4_K rearrangement is checked through the ASDSL GEMV
 (oracle_gemv_q4km, pinned against the reference's compiled kernel): a wrong
 field or nibble in either the decoder or the rearrangement changes the
@@ -239,8 +240,85 @@ def known_q8_0() -> tuple[np.ndarray, dict]:
     return np.frombuffer(bytes(b), np.uint8), {0: -32.0, 1: -0.25, 2: 0.0, 3: 0.25, 4: 31.75, 31: 0.0}
 
 
+def known_q4_0() -> tuple[np.ndarray, dict]:
+    """d = 0.5; nibble byte 0 = 0x3A (weight 0 code 10, weight 16 code 3),
+    byte 15 = 0xF0 (weight 15 code 0, weight 31 code 15); every other byte
+    0x88 (code 8: zero)."""
+    b = bytearray(18)
+    b[0:2] = b"\x00\x38"
+    b[2:18] = bytes([0x88] * 16)
+    b[2], b[17] = 0x3A, 0xF0
+    return np.frombuffer(bytes(b), np.uint8), {0: 1.0, 16: -2.5, 15: -4.0, 31: 3.5, 1: 0.0, 30: 0.0}
+
+
+def known_q4_1() -> tuple[np.ndarray, dict]:
+    """d = 0.25, m = -1.0; nibble byte 2 = 0x5C (weight 2 code 12, weight 18
+    code 5); every other code 0."""
+    b = bytearray(20)
+    b[0:2], b[2:4] = b"\x00\x34", b"\x00\xbc"
+    b[4 + 2] = 0x5C
+    return np.frombuffer(bytes(b), np.uint8), {2: 2.0, 18: 0.25, 0: -1.0, 31: -1.0}
+
+
+def known_q5_0() -> tuple[np.ndarray, dict]:
+    """d = 1.0; high-bit word with bits 0 and 31 set (bytes 01 00 00 80);
+    nibble byte 0 = 0x21 (weight 0: 1 | 16, weight 16: 2), byte 15 = 0xF0
+    (weight 15: 0, weight 31: 15 | 16); every other code 0, i.e. -16."""
+    b = bytearray(22)
+    b[0:2] = b"\x00\x3c"
+    b[2:6] = bytes([0x01, 0x00, 0x00, 0x80])
+    b[6], b[21] = 0x21, 0xF0
+    return np.frombuffer(bytes(b), np.uint8), {0: 1.0, 16: -14.0, 15: -16.0, 31: 15.0, 5: -16.0}
+
+
+def known_q5_1() -> tuple[np.ndarray, dict]:
+    """d = 0.5, m = 2.0; high-bit word with bit 16 set (byte 2 = 0x01);
+    nibble byte 0 = 0x37 (weight 0: 7, weight 16: 3 | 16); every other code
+    0."""
+    b = bytearray(24)
+    b[0:2], b[2:4] = b"\x00\x38", b"\x00\x40"
+    b[4 + 2] = 0x01
+    b[8] = 0x37
+    return np.frombuffer(bytes(b), np.uint8), {0: 5.5, 16: 11.5, 1: 2.0, 31: 2.0}
+
+
+def known_q2k() -> tuple[np.ndarray, dict]:
+    """d = 1.0, dmin = 0.5 (bytes 80-83).  Code byte 0 (qs at 16) = 0xE4
+    holds codes 0, 1, 2, 3 for weights 0, 32, 64, 96 (scales 0, 2, 4, 6:
+    bytes 0x21, 0x03, 0x15, 0xF2, low nibble the scale, high the min); code
+    byte 51 = 0x02 gives weight 128 + 16 + 3 = 147 code 2 under scale 9
+    (0x47).  Scale 1 is zero: weight 16 is 0."""
+    b = bytearray(84)
+    b[0], b[2], b[4], b[6], b[9] = 0x21, 0x03, 0x15, 0xF2, 0x47
+    b[16] = 0xE4
+    b[16 + 51] = 0x02
+    b[80:82], b[82:84] = b"\x00\x3c", b"\x00\x38"
+    return np.frombuffer(bytes(b), np.uint8), {
+        0: -1.0, 1: -1.0, 32: 3.0, 64: 9.5, 96: -1.5, 147: 12.0, 16: 0.0}
+
+
+def known_q3k() -> tuple[np.ndarray, dict]:
+    """d = 0.5 (bytes 108-109).  Scale 0 = 5 | 2 << 4 = 37 (byte 96 low
+    nibble 5, byte 104 bits 0-1 = 2): dl = 0.5 * 5; scale 15 = 10 | 1 << 4 =
+    26 (byte 103 high nibble 10, byte 107 bits 6-7 = 1): dl = -3; every other
+    scale 0, i.e. -32: dl = -16.  Weight 0: code byte 32 = 3, mask byte 0
+    bit 0 set: 3.  Weight 245 (n 1, j 3, h 1, l 5): code byte 32 + 53 bits
+    6-7 = 3, mask byte 21 bit 7 set: 3.  Weights 1, 241 and 16: code 0 with
+    the mask bit clear: -4."""
+    b = bytearray(110)
+    b[96], b[104], b[103], b[107] = 0x05, 0x02, 0xA0, 0x40
+    b[32], b[0] = 0x03, 0x01
+    b[32 + 53], b[21] = 0xC0, 0x80
+    b[108:110] = b"\x00\x38"
+    return np.frombuffer(bytes(b), np.uint8), {
+        0: 7.5, 1: -10.0, 2: -10.0, 245: -9.0, 241: 12.0, 16: 64.0}
+
+
 KNOWN = {"q4k": (known_q4k, oracle.dequant_gguf_q4k, 256), "q5k": (known_q5k, oracle.dequant_gguf_q5k, 256),
-         "q6k": (known_q6k, oracle.dequant_gguf_q6k, 256), "q8_0": (known_q8_0, oracle.dequant_gguf_q8_0, 32)}
+         "q6k": (known_q6k, oracle.dequant_gguf_q6k, 256), "q8_0": (known_q8_0, oracle.dequant_gguf_q8_0, 32),
+         "q2k": (known_q2k, oracle.dequant_gguf_q2k, 256), "q3k": (known_q3k, oracle.dequant_gguf_q3k, 256),
+         **{k: (f, lambda blk, n, k=k: oracle.dequant_gguf_legacy(k, blk, n), 32)
+            for k, f in (("q4_0", known_q4_0), ("q4_1", known_q4_1), ("q5_0", known_q5_0), ("q5_1", known_q5_1))}}
 
 
 @pytest.mark.parametrize("kind", sorted(KNOWN))
@@ -268,3 +346,82 @@ def test_q5k_each_high_bit_moves_its_weight(j):
         want = np.zeros(256, np.float32)
         want[32 * j + l] = 16.0
         assert np.array_equal(w, want), (j, l)
+
+
+@pytest.mark.parametrize("kind", ["q4_0", "q4_1", "q5_0", "q5_1"])
+def test_legacy_each_code_and_high_bit_moves_one_weight(kind):
+    """Nibble byte j moves weight j (low nibble) and weight j + 16 (high)
+    only, and bit i of the Q5 high-bit word moves weight i only, by d
+    times the code change (d = 1, m = 0)."""
+    nb = oracle.LEGACY_BLOCK_BYTES[kind]
+    has_m = nb in (20, 24)
+    has_h = nb in (22, 24)
+    codes_at = (4 if has_m else 2) + (4 if has_h else 0)
+    base = np.zeros(nb, np.uint8)
+    base[0:2] = _f16(1.0)
+    w0 = oracle.dequant_gguf_legacy(kind, base, 1)
+    for j in (0, 7, 15):
+        for hi in (0, 1):
+            blk = base.copy()
+            blk[codes_at + j] = 0x0B << (4 * hi)
+            diff = oracle.dequant_gguf_legacy(kind, blk, 1) - w0
+            want = np.zeros(32, np.float32)
+            want[j + 16 * hi] = 11.0
+            assert np.array_equal(diff, want), (kind, j, hi)
+    if has_h:
+        for i in (0, 9, 16, 31):
+            blk = base.copy()
+            word = np.frombuffer(np.uint32(1 << i).tobytes(), np.uint8)
+            at = 4 if has_m else 2
+            blk[at:at + 4] = word
+            diff = oracle.dequant_gguf_legacy(kind, blk, 1) - w0
+            want = np.zeros(32, np.float32)
+            want[i] = 16.0
+            assert np.array_equal(diff, want), (kind, i)
+
+
+@pytest.mark.parametrize("q3", [False, True])
+def test_q2k_q3k_each_code_field_moves_its_weight(q3):
+    """Bits 2j..2j+1 of code byte 32n + 16h + l move weight 128n + 32j + 16h
+    + l and no other; for Q3_K bit 4n + j of mask byte 16h + l moves that
+    same weight by 4 steps; each 6-bit (Q3_K) or 4-bit (Q2_K) scale moves
+    its 16 weights only."""
+    nb, dec = (110, oracle.dequant_gguf_q3k) if q3 else (84, oracle.dequant_gguf_q2k)
+    qs_at = 32 if q3 else 16
+    base = np.zeros(nb, np.uint8)
+    if q3:
+        base[108:110] = _f16(1.0)
+        base[96:104] = 0x11  # every scale's low 4 bits 1, top bits 0: scale 1 - 32 = -31
+    else:
+        base[80:82] = _f16(1.0)
+        base[0:16] = 0x01  # every scale 1, min 0
+    w0 = dec(base, 1)
+    for n in (0, 1):
+        for j in range(4):
+            for h in (0, 1):
+                for l in (0, 11):
+                    wi = 128 * n + 32 * j + 16 * h + l
+                    blk = base.copy()
+                    blk[qs_at + 32 * n + 16 * h + l] = 2 << (2 * j)
+                    diff = dec(blk, 1) - w0
+                    assert np.flatnonzero(diff).tolist() == [wi], (q3, wi)
+                    if q3:
+                        blk = base.copy()
+                        blk[16 * h + l] = 1 << (4 * n + j)
+                        diff = dec(blk, 1) - w0
+                        assert np.flatnonzero(diff).tolist() == [wi], (q3, wi, "mask")
+                        assert diff[wi] == np.float32(-31.0 * 4), (q3, wi)
+    if not q3:  # every code 1, so that a scale change shows
+        base[16:80] = 0x55
+        w0 = dec(base, 1)
+    for k in range(16):
+        blk = base.copy()
+        if q3:  # raise scale k's top 2 bits to 1: the scale moves by 16
+            blk[104 + k % 4] = 1 << (2 * (k // 4))
+        else:
+            blk[k] = 0x03
+        changed = np.flatnonzero(dec(blk, 1) != w0)
+        n, r = divmod(k, 8)
+        j, h = divmod(r, 2)
+        want = [128 * n + 32 * j + 16 * h + l for l in range(16)]
+        assert changed.tolist() == want, (q3, k)
