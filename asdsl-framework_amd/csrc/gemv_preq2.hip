@@ -18,11 +18,12 @@
 // deterministic.
 //
 // Launch shape (measured on MI355X, rotated weights): fat workgroups (8 waves,
-// 16 when K > 4096) amortize the per-workgroup activation quantization, which
-// for K=8192 reads more bytes than the workgroup's own weights when
-// workgroups are small; KS grows only while fewer than CUs/2 workgroups would
-// be launched.  o_proj 3072x3072 3.0 us (KS=2), gate_up 16384x3072 6.9 us
-// (KS=1), down 3072x8192 5.1 us (KS=4, 12 waves).
+// 16 when K > 4096 or when 16-band tiles give about one per compute unit)
+// amortize the per-workgroup activation quantization, which for K=8192 reads
+// more bytes than the workgroup's own weights when workgroups are small; KS
+// grows only while fewer than CUs/2 workgroups would be launched.  o_proj
+// 3072x3072 3.0 us (KS=2), gate_up 16384x3072 6.75 us (KS=1, 16 waves),
+// down 3072x8192 5.1 us (KS=4, 12 waves).
 //
 // The activation loads are issued before the weight loads (vmcnt retires in
 // order) and quantized while the weights are in flight; the next tile's loads
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(WAVES * kWave) void preq2_gemv_kernel(const uint32_
             }
         }
     }
-    // 16-wave workgroups (K > 4096): every wave's activation requests go
+    // 16-wave workgroups: every wave's activation requests go
     // out before any wave's weight requests.  A CU returns vector-memory data
     // in request order, so activation loads queued behind other waves' weight
     // misses wait for HBM, and the staging barrier below waits for the
@@ -597,6 +598,19 @@ Plan plan_preq2(int M, int K, int cus, int gs) {
     const int upb = K / 8;
     const int nbands = (M + 3) / 4;
     Plan p{0, 0, K > 4096 ? 16 : 8, 0, false, 0};
+    // K <= 4096 where 16-band tiles number between 3/4 of the compute units
+    // and all of them (gate_up 16384 rows: 256): 16 waves, one tile per
+    // workgroup and one workgroup per compute unit, whose waves all request
+    // the activation before any weight (see the kernel), instead of two
+    // 8-wave workgroups whose second one's activation waits behind the first
+    // one's weights (gate_up 16384x3072: 6.95 -> 6.75 and 6.86 -> 6.75 us on
+    // two boxes).  Where a workgroup walks several tiles the staging is
+    // amortized and 16 waves measured slower (lm_head 200064x3072 g128: 50.8
+    // -> 52.7 us).  ASDSL_HIP_PREQ2_WAVES (read per call) forces 8 or 16.
+    const int tiles16 = (nbands + 15) / 16;
+    if (K <= 4096 && 4 * tiles16 >= 3 * cus && tiles16 <= cus) p.waves = 16;
+    const int forced_waves = env_knob("ASDSL_HIP_PREQ2_WAVES");
+    if (forced_waves == 8 || forced_waves == 16) p.waves = forced_waves;
     auto nu_of = [&](int lks) { return (upb + (kWave << lks) - 1) / (kWave << lks); };
     auto tiles_of = [&](int lks) {
         const int bpt = p.waves >> lks;
@@ -688,6 +702,10 @@ template <int GS>
 asdsl_status launch_gateup_swiglu(const uint8_t* meta, const uint8_t* quant, const float* x, float* y, int F, int K,
                                   ProArgs pa, hipStream_t stream, int cus) {
     Plan p = plan_preq2(2 * F, K, cus, GS);
+    // 8 waves with two tiles per workgroup (below) unless forced: 16 waves
+    // with one tile each measured 957 against 939 us per 32-layer step at
+    // ctx 128 (the same bits: a row's sum does not depend on the waves)
+    if (p.waves == 16 && K <= 4096 && env_knob("ASDSL_HIP_PREQ2_WAVES") != 16) p.waves = 8;
     const int hpt = (p.waves >> p.lks) / 2;
     if (p.lks != 0 || hpt < 1 || F % 4 != 0 || (F / 4) % hpt != 0) return ASDSL_ERR_UNSUPPORTED;
     pa.fbands = F / 4;
@@ -699,8 +717,10 @@ asdsl_status launch_gateup_swiglu(const uint8_t* meta, const uint8_t* quant, con
     // per 32-layer step faster at ctx 128 and 1024 than one tile per
     // workgroup; requesting both tiles up front measured slower.
     // ASDSL_HIP_GATEUP_TILES sets the tiles per workgroup.
+    // (16-wave workgroups hold twice the bands: one tile each keeps one
+    // workgroup per compute unit.)
     static const int tpw_knob = env_knob("ASDSL_HIP_GATEUP_TILES");
-    const int tpw = tpw_knob > 0 ? tpw_knob : 2;
+    const int tpw = tpw_knob > 0 ? tpw_knob : p.waves == 16 ? 1 : 2;
     const int want = (tiles + tpw - 1) / tpw;
     p.grid = want < cap ? want : cap;
     const auto* m = reinterpret_cast<const uint32_t*>(meta);

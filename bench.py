@@ -54,13 +54,14 @@ LAYER = [("qkv", 5120, 3072), ("o_proj", 3072, 3072), ("gate_up", 16384, 3072), 
 GS = 32
 LM_HEAD = (200064, 3072, 128)
 # HBM bytes per gate_up launch measured by rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on `bench.py --pmc-probe gate_up` with the first tile's weight
-# requests split around the activation staging (median of 50 dispatches:
-# 15,442 KiB fetched, 64 KiB written), each scaled by the same counter on a
-# 64 MiB device copy (fetch x1.9993, write x1.0): 31,614,121 + 65,536 bytes;
-# see profiles/preq2_gemv_phi4_layer_g32.md.  A property of the kernel's
-# access pattern: re-measure when the kernel's loads change.
-GATE_UP_TRAFFIC_BYTES = 31_679_657
+# WRITE_SIZE on `bench.py --pmc-probe gate_up` with the instance the plan
+# picks (16 waves, one tile per workgroup, the first tile's weight requests
+# split around the activation staging; median of 50 dispatches: 15,442.5 KiB
+# fetched, 64 KiB written), each scaled by the same counter on a 64 MiB
+# device copy (fetch x1.9993, write x1.0): 31,615,145 + 65,536 bytes; see
+# profiles/preq2_gemv_phi4_layer_g32.md.  A property of the kernel's access
+# pattern: re-measure when the kernel's loads change.
+GATE_UP_TRAFFIC_BYTES = 31_680_681
 GATE_UP_BYTES = 31_535_104  # gemv_bytes(16384, 3072): the gate_up GEMV's algorithmic bytes
 
 
