@@ -36,6 +36,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import itertools
 import json
 import os
 import sys
@@ -361,10 +362,11 @@ def shape_sweep(args) -> int:
     sets) under every launch shape the tuning switches give: the K split
     (ASDSL_HIP_KSPLIT: the plan's, 1, 2, 4) times the first tile's weight
     requests split around the activation staging (ASDSL_HIP_PRE_SPLIT: the
-    plan's, 1 a third up front, 2 a half, 4 all).  The switches are read per
-    call, so each graph is captured under its own setting.  Outputs are
-    compared with the plan's launch (relative L2; the K split changes the
-    fp32 summation order only, the request split nothing)."""
+    plan's, 1 a third up front, 2 a half, 4 all) times the waves per
+    workgroup (ASDSL_HIP_PREQ2_WAVES: the plan's, 8, 16).  The switches are
+    read per call, so each graph is captured under its own setting.  Outputs
+    are compared with the plan's launch (relative L2; the K split changes the
+    fp32 summation order only, the request split and the waves nothing)."""
     import numpy as np
     import torch
 
@@ -374,37 +376,37 @@ def shape_sweep(args) -> int:
     lib = _hip.LIB
     ptrs = [{n: (_hip.ptr(m), _hip.ptr(q)) for n, (m, q) in L.items()} for L in layers]
     L = len(layers)
-    knobs = ("ASDSL_HIP_KSPLIT", "ASDSL_HIP_PRE_SPLIT")
+    knobs = ("ASDSL_HIP_KSPLIT", "ASDSL_HIP_PRE_SPLIT", "ASDSL_HIP_PREQ2_WAVES")
     saved = {k: os.environ.get(k) for k in knobs}
     try:
         for n, M, K in LAYER:
             rows, want = [], None
-            for ks in ("", "1", "2", "4"):
-                for sp in ("", "1", "2", "4"):
-                    for k, v in zip(knobs, (ks, sp)):
-                        os.environ[k] = v
-                    y = ys[n]
+            for ks, sp, wv in itertools.product(("", "1", "2", "4"), ("", "1", "2", "4"), ("", "8", "16")):
+                for k, v in zip(knobs, (ks, sp, wv)):
+                    os.environ[k] = v
+                y = ys[n]
 
-                    def calls(h, n=n, M=M, K=K):
-                        for i in range(4 * L):
-                            p = ptrs[i % L]
-                            if lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], _hip.ptr(xs[n]), _hip.ptr(y), M, K, GS,
-                                                          h):
-                                raise RuntimeError(_hip.last_error())
-                    g = capture(calls)
-                    reps = 25
-                    us = 1e3 * timed_replays(g, reps) / (reps * 4 * L)
-                    del g
-                    p0 = ptrs[0][n]
-                    if lib.asdsl_gemv_preq2_fused(p0[0], p0[1], _hip.ptr(xs[n]), _hip.ptr(y), M, K, GS,
-                                                  int(torch.cuda.current_stream().cuda_stream)):
-                        raise RuntimeError(_hip.last_error())
-                    got = y.cpu().numpy().astype(np.float64)
-                    if want is None:
-                        want = got
-                    rel = float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
-                    rows.append({"ksplit": ks or "plan", "pre_split": sp or "plan", "us": round(us, 3),
-                                 "GB/s": round(gemv_bytes(M, K) / (us * 1e-6) / 1e9, 1), "rel_l2_vs_plan": rel})
+                def calls(h, n=n, M=M, K=K):
+                    for i in range(4 * L):
+                        p = ptrs[i % L]
+                        if lib.asdsl_gemv_preq2_fused(p[n][0], p[n][1], _hip.ptr(xs[n]), _hip.ptr(y), M, K, GS,
+                                                      h):
+                            raise RuntimeError(_hip.last_error())
+                g = capture(calls)
+                reps = 25
+                us = 1e3 * timed_replays(g, reps) / (reps * 4 * L)
+                del g
+                p0 = ptrs[0][n]
+                if lib.asdsl_gemv_preq2_fused(p0[0], p0[1], _hip.ptr(xs[n]), _hip.ptr(y), M, K, GS,
+                                              int(torch.cuda.current_stream().cuda_stream)):
+                    raise RuntimeError(_hip.last_error())
+                got = y.cpu().numpy().astype(np.float64)
+                if want is None:
+                    want = got
+                rel = float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+                rows.append({"ksplit": ks or "plan", "pre_split": sp or "plan", "waves": wv or "plan",
+                             "us": round(us, 3),
+                             "GB/s": round(gemv_bytes(M, K) / (us * 1e-6) / 1e9, 1), "rel_l2_vs_plan": rel})
             print(json.dumps({"shape_sweep": n, "shape": [M, K], "bytes": gemv_bytes(M, K), "rows": rows}),
                   flush=True)
     finally:
