@@ -801,6 +801,12 @@ size_t exact_mfma_lds_bytes(int K, int gs, int ks, int nu) {
 BatchPlan plan_batch_single(int M, int K, int gs, int cus) {
     BatchPlan p{0, 0, 8, 0, 16, false, cus};
     preq2_plan_shape(M, K, cus, &p.lks, &p.nu, &p.waves, &p.exact);
+    // The single-column plan's 16-wave workgroups for K <= 4096 (one tile
+    // per compute unit) keep its K split and units per lane, so 8 waves give
+    // the same per-column bits here; the batched kernel stages every column
+    // per workgroup and measured slower at 16 (4-token verify pass at ctx
+    // 1024: 2334 against 1917 us).
+    if (p.waves == 16 && K <= 4096) p.waves = 8;
     if (!p.exact || K > 8192) {
         p.exact = false;
         return p;
