@@ -345,23 +345,25 @@ def _bits_case(eng, ctx, toks):
 
 @pytest.mark.parametrize("form", ["exact_mfma", "dot4"])
 @pytest.mark.parametrize("kv", ["fp16", "int8"])
-@pytest.mark.parametrize("ctx,n", [(0, 3), (200, 8), (500, 16), (1000, 5)])
+@pytest.mark.parametrize("ctx,n", [(0, 3), (200, 8), (500, 16), (1000, 5), (300, 2), (700, 4)])
 def test_verify_is_the_single_token_step_bit_for_bit(gpu, kv, ctx, n, form, monkeypatch):
-    """The verify pass in both exact forms (the default: MFMA GEMVs in the
-    single-token GEMVs' fp32 order on images the norm, combine and SwiGLU
-    kernels write; ASDSL_HIP_VERIFY_DOT4=1: dot4 GEMVs in the single-token
-    launch shapes), norms in the step's order, the attention's one-tile
-    splits, on a 2-layer model (qkv/o g32 with K split 1 and 2, gate_up,
-    down and the lm_head g128): every column equals the single-token step at
-    its position bit for bit, across the short form (below 512: o_proj
-    merges the splits) and the long form (combine kernel), 500 + 16 crossing
-    between them."""
+    """The verify pass in both exact forms, on a 2-layer model (qkv/o g32
+    with K split 1 and 2, gate_up, down and the lm_head g128):
+      exact_mfma: MFMA GEMVs in the single-token GEMVs' fp32 order on images
+        the norm, combine and SwiGLU kernels write (the default from 5
+        columns; here at every column count);
+      dot4 (ASDSL_HIP_VERIFY_DOT4=1): dot4 GEMVs in the single-token launch
+        shapes (the default up to 4 columns; here at every column count).
+    Norms in the step's order, the attention's one-tile splits: every column
+    equals the single-token step at its position bit for bit, across the
+    short form (below 512: o_proj merges the splits) and the long form
+    (combine kernel), 500 + 16 crossing between them."""
     from asdsl.engine import DecodeConfig, DecodeEngine
 
-    if form == "dot4":
-        monkeypatch.setenv("ASDSL_HIP_VERIFY_DOT4", "1")
-    else:
+    if form == "exact_mfma":
         monkeypatch.setenv("ASDSL_HIP_VERIFY_EXACT_MFMA_MIN_N", "1")  # every column count
+    else:
+        monkeypatch.setenv("ASDSL_HIP_VERIFY_DOT4", "1")
 
     eng = DecodeEngine.synthetic(DecodeConfig(n_layers=2, vocab=4096, max_seq=1100, kv_format=kv), seed=ctx + n)
     eng.prefill_kv_random(ctx, seed=5)
