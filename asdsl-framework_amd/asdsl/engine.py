@@ -300,6 +300,12 @@ class DecodeEngine:
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.logits = torch.empty(cfg.vocab, dtype=torch.float32, device=dev)
         self._graphs: dict[int, object] = {}
+        # HIP graphs of the reference-signature calls (forward_token per
+        # position range, forward_batch_all_logits per token count), keyed
+        # with the ASDSL_HIP_* switches in force when captured; off with
+        # ASDSL_ENGINE_EAGER=1
+        self._call_graphs: dict[tuple, object] = {}
+        self.graph_calls = os.environ.get("ASDSL_ENGINE_EAGER", "") in ("", "0")
         self._host_pos = 0  # the device position as the host last set or advanced it
         # committed KV length and its snapshot stack (UnifiedEngine::kv_seq_len_,
         # kv_snapshot_stack_), host-side like the reference's
@@ -425,7 +431,7 @@ class DecodeEngine:
         if self._profile_due():
             self._report(self.profile_step(limit))
         else:
-            self._queue_step(_hip.stream_handle(), limit)
+            self._graph_call(("step", limit), lambda h: self._queue_step(h, limit))
         self._host_pos = pos + 1
         self.kv_seq_len = max(self.kv_seq_len, pos + 1)
         return self.logits
@@ -463,6 +469,32 @@ class DecodeEngine:
         if flags:
             self.check_device_flags()
         return int(tok)
+
+    def decode_steps(self, k: int) -> list[int]:
+        """k greedy steps (step(), captured graphs) queued back to back from
+        the device token at the device position, each step's token copied to
+        a device history; returns the k tokens with one read, where k calls
+        of next_token() and step() would read the device k times.  The host
+        position advances by k; the caller's position must not pass max_seq."""
+        import torch
+
+        k = int(k)
+        if k < 1:
+            return []
+        if self._host_pos + k > self.cfg.max_seq:
+            raise ValueError("decode_steps: positions out of kv-cache range")
+        hist = getattr(self, "_hist", None)
+        if hist is None or hist.numel() < k + 1:
+            hist = self._hist = torch.empty(max(k + 1, 64), dtype=torch.int32, device=self.token.device)
+        for j in range(k):
+            self.step()
+            hist[j:j + 1].copy_(self.token)
+        hist[k:k + 1].copy_(self._flags)
+        out = hist[:k + 1].tolist()  # one device read
+        self.kv_seq_len = max(self.kv_seq_len, self._host_pos)
+        if out[k]:
+            self.check_device_flags()
+        return [int(t) for t in out[:k]]
 
     def capture(self) -> None:
         """HIP graph of one step (token and position advance on the device)
@@ -512,6 +544,29 @@ class DecodeEngine:
             self.capture()
         self._graph.replay()
         self._host_pos += 1
+
+    def _graph_call(self, key: tuple, queue) -> None:
+        """queue(stream) on the current stream: replayed from a HIP graph
+        when one was captured for `key` under the same ASDSL_HIP_* switches;
+        otherwise queued eagerly and then captured for the next call (the
+        capture records the launches without running them).  The launches
+        read their token(s) and position from device buffers, so one graph
+        serves every call with the same key, with the eager call's bits."""
+        import torch
+
+        if not self.graph_calls or torch.cuda.is_current_stream_capturing():
+            queue(_hip.stream_handle())
+            return
+        full = key + tuple(sorted((k, v) for k, v in os.environ.items() if k.startswith("ASDSL_HIP_")))
+        g = self._call_graphs.get(full)
+        if g is not None:
+            g.replay()
+            return
+        queue(_hip.stream_handle())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            queue(int(torch.cuda.current_stream().cuda_stream))
+        self._call_graphs[full] = g
 
     # ------------------------------------------------------------ profiling
     STAGES = ("embed", "qkv", "attention", "attention_combine", "o_proj", "gate_up", "down", "lm_head", "finalize")
@@ -598,10 +653,13 @@ class DecodeEngine:
         v = self._verify
         v["tokens"][:n].copy_(torch.tensor(toks, dtype=torch.int32))
         self.pos.fill_(start_pos)
-        _hip.check(_hip.LIB.asdsl_decode_verify(ctypes.byref(self._model), _hip.ptr(v["tokens"]), n,
-                                                _hip.ptr(self.pos), _hip.ptr(v["logits"]), _hip.ptr(v["next"]),
-                                                _hip.ptr(v["work"]), _hip.stream_handle()),
-                   "asdsl_decode_verify")
+
+        def queue(h, n=n, v=v):
+            _hip.check(_hip.LIB.asdsl_decode_verify(ctypes.byref(self._model), _hip.ptr(v["tokens"]), n,
+                                                    _hip.ptr(self.pos), _hip.ptr(v["logits"]), _hip.ptr(v["next"]),
+                                                    _hip.ptr(v["work"]), h),
+                       "asdsl_decode_verify")
+        self._graph_call(("verify", n), queue)
         self.pos.fill_(start_pos + n)
         self._host_pos = start_pos + n
         self.kv_seq_len = max(self.kv_seq_len, start_pos + n)

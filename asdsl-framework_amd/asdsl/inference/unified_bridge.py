@@ -235,12 +235,28 @@ def cpp_generate(store: Any, prompt_ids: list[int], max_new_tokens: int,
     out: list[int] = []
     if not prompt:
         return out
-    for _ in range(int(max_new_tokens)):
-        best = eng.next_token()
+    # the device keeps the token: steps run in chunks (decode_steps), each
+    # read once; the engine ends as one step per token leaves it
+    pending = [eng.next_token()]
+    stepped = len(prompt)
+    while len(out) < int(max_new_tokens):
+        if not pending:
+            k = min(_GREEDY_CHUNK, int(max_new_tokens) - len(out), eng.cfg.max_seq - stepped)
+            if k <= 0:
+                break
+            pending = eng.decode_steps(k)
+            stepped += k
+        best = pending.pop(0)
         out.append(best)
         if best in stop or len(prompt) + len(out) > eng.cfg.max_seq:
             break
-        eng.step()  # consumes the device token at the device position
+    n = len(prompt) + len(out)
+    # the per-token loop steps every generated token but a final stop token
+    # (or one past the cache)
+    if out and (out[-1] in stop or n > eng.cfg.max_seq):
+        _settle(eng, n - 1, out[-2] if len(out) > 1 else prompt[-1], stepped, out[-1])
+    elif out:
+        _settle(eng, n, out[-1], stepped, pending[0] if pending else None)
     return out
 
 
@@ -272,15 +288,46 @@ def greedy_generate(store: Any, prompt_ids: list[int], max_new_tokens: int, eos=
     prompt_len = len(tokens)
     for i, t in enumerate(tokens):
         engine.forward_token(t, i)
-    pos = len(tokens)
+    if not tokens:
+        return tokens
+    # Steps run in chunks on the device (decode_steps: one read per chunk);
+    # the engine ends as the one-step-per-token loop leaves it.
+    pending = [engine.next_token()]
+    stepped = len(tokens)  # positions whose step has run
+    stop_tok = None
     while len(tokens) - prompt_len < max_new_tokens:
-        cur = engine.next_token()
+        if not pending:
+            k = min(_GREEDY_CHUNK, max_new_tokens - (len(tokens) - prompt_len), engine.cfg.max_seq - stepped)
+            if k <= 0:
+                break
+            pending = engine.decode_steps(k)
+            stepped += k
+        cur = pending.pop(0)
         if cur in eos:
+            stop_tok = cur
             break
         tokens.append(cur)
-        engine.forward_token(cur, pos)
-        pos += 1
+    # the per-token loop steps every position 0 .. len(tokens) - 1
+    _settle(engine, len(tokens), tokens[-1], stepped, stop_tok if stop_tok is not None else
+            (pending[0] if pending else None))
     return tokens
+
+
+# greedy steps per device read in greedy_generate and cpp_generate
+_GREEDY_CHUNK = 16
+
+
+def _settle(engine: Any, n: int, last: int, stepped: int, after: int | None) -> None:
+    """Leave the engine as a loop of one step per token leaves it: the steps
+    of positions 0 .. n - 1 run and no other, the device token the one the
+    step at n - 1 gives, the position n.  last: the token at position n - 1;
+    stepped: positions whose step ran (a chunk may run past the last token
+    taken); after: the token the step at n - 1 gave, when known."""
+    if stepped < n:  # the last token's own step
+        engine.forward_token(last, n - 1)
+    elif stepped > n:  # steps past it: drop their K/V rows, restore its successor
+        engine.truncate_kv(n)
+        engine.token.fill_(int(after))
 
 
 def pld_generate(store: Any, prompt_ids: list[int], max_new_tokens: int, max_draft_k: int = 6,

@@ -111,3 +111,63 @@ def test_cpp_generate_stops_after_a_stop_token(gpu):
     first = free.index(stop)
     got = ub.cpp_generate(store, PROMPT, 20, stop_ids=[stop])
     assert got == free[:first + 1]
+
+
+def _state(eng):
+    """Position, KV length, device token and every layer's K/V rows."""
+    return (eng._host_pos, int(eng.pos.item()), eng.get_kv_seq_len(), int(eng.token.item()),
+            [(L["k_cache"].clone(), L["v_cache"].clone()) for L in eng.layers])
+
+
+def _same_state(a, b):
+    import torch
+
+    assert a[:4] == b[:4], (a[:4], b[:4])
+    for (ka, va), (kb, vb) in zip(a[4], b[4]):
+        assert torch.equal(ka, kb) and torch.equal(va, vb)
+
+
+@pytest.mark.parametrize("max_new,stop_at", [(1, None), (16, None), (17, None), (40, None), (40, 5), (40, 21),
+                                             (40, 0)])
+def test_chunked_generation_is_the_per_token_loop(gpu, max_new, stop_at):
+    """greedy_generate and cpp_generate run their steps in chunks of 16 on
+    the device (decode_steps, one read per chunk).  Against the one step per
+    token loop (forward_token, next_token): the same tokens, and the engine
+    left in the same state (position, KV length, device token, K/V rows),
+    whether the generation ends on max_new_tokens inside or on a chunk's
+    end, or on a stop token inside a chunk (stop_at: index of the free run's
+    token used as the stop token)."""
+    from asdsl.inference import unified_bridge as ub
+
+    store = _store(8)
+    eng = ub.get_or_build_unified_engine(store)
+    free = ub.cpp_generate(store, PROMPT, 45, stop_ids=[])
+    stop = [] if stop_at is None else [free[stop_at]]
+
+    def per_token(include_stop: bool):
+        eng.reset_session()
+        for i, t in enumerate(PROMPT):
+            eng.forward_token(t, i)
+        out, pos = [], len(PROMPT)
+        for _ in range(max_new):
+            cur = eng.next_token()
+            if cur in stop:
+                if include_stop:
+                    out.append(cur)
+                break
+            out.append(cur)
+            eng.forward_token(cur, pos)
+            pos += 1
+        return out
+
+    want_g = per_token(False)
+    st_g = _state(eng)
+    got_g = ub.greedy_generate(store, PROMPT, max_new, eos=stop)
+    assert got_g[len(PROMPT):] == want_g
+    _same_state(_state(eng), st_g)
+
+    want_c = per_token(True)
+    st_c = _state(eng)
+    got_c = ub.cpp_generate(store, PROMPT, max_new, stop_ids=stop or [-1])
+    assert got_c == want_c
+    _same_state(_state(eng), st_c)

@@ -400,3 +400,42 @@ def test_verify_is_the_single_token_step_bit_for_bit_full_size(full32, ctx, n):
     full32.prefill_kv_random(ctx, seed=ctx)
     toks = [int(t) for t in np.random.default_rng(ctx + 1).integers(0, full32.cfg.vocab, n)]
     _bits_case(full32, ctx, toks)
+
+
+def test_reference_calls_replay_graphs_with_the_eager_bits(gpu, monkeypatch):
+    """forward_token and forward_batch_all_logits replay a HIP graph per
+    position range / token count after their first call: over a sequence of
+    calls at several positions and counts the logits, tokens and K/V rows
+    equal those of the same calls queued eagerly (ASDSL_ENGINE_EAGER=1),
+    bit for bit; and a switch changed between calls is captured anew."""
+    import torch
+    from asdsl.engine import DecodeConfig, DecodeEngine
+
+    def run(eager: bool):
+        if eager:
+            monkeypatch.setenv("ASDSL_ENGINE_EAGER", "1")
+        else:
+            monkeypatch.delenv("ASDSL_ENGINE_EAGER", raising=False)
+        eng = DecodeEngine.synthetic(DecodeConfig(n_layers=2, vocab=4096, max_seq=700), seed=12)
+        eng.prefill_kv_random(100, seed=3)
+        out = []
+        for pos, tok in ((100, 5), (101, 9), (102, 5), (300, 7), (301, 8)):
+            out.append((eng.forward_token(tok, pos).clone(), eng.next_token()))
+        for toks, pos in (([3, 4, 5], 302), ([6, 7, 8], 305), ([1, 2], 308), ([9, 10, 11], 310)):
+            out.append((eng.forward_batch_all_logits(toks, pos).clone(), tuple(eng.verify_next_tokens())))
+        monkeypatch.setenv("ASDSL_HIP_VERIFY_MFMA", "1")  # another form: its own graph
+        out.append((eng.forward_batch_all_logits([1, 2, 3], 320).clone(), tuple(eng.verify_next_tokens())))
+        monkeypatch.delenv("ASDSL_HIP_VERIFY_MFMA")
+        out.append((eng.forward_batch_all_logits([1, 2, 3], 320).clone(), tuple(eng.verify_next_tokens())))
+        kv = [(L["k_cache"][:, :330].clone(), L["v_cache"][:, :330].clone()) for L in eng.layers]
+        graphs = len(eng._call_graphs)
+        return out, kv, graphs
+
+    (oe, kve, ge), (og, kvg, gg) = run(True), run(False)
+    assert ge == 0 and gg == 5  # two position ranges, counts 3 and 2, 3 again under the switch
+    for (a, ta), (b, tb) in zip(oe, og):
+        assert torch.equal(a, b) and ta == tb
+    for (ka, va), (kb, vb) in zip(kve, kvg):
+        assert torch.equal(ka, kb) and torch.equal(va, vb)
+    mf, ex = og[-2][0], og[-1][0]  # the MFMA form: the same columns to fp32 rounding
+    assert rel_l2(_host(mf), _host(ex)) < LOOSE
