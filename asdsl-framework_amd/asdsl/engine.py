@@ -470,6 +470,31 @@ class DecodeEngine:
             self.check_device_flags()
         return int(tok)
 
+    # Below this position the verify pass's columns are the single-token
+    # step bit for bit (its attention splits coincide with the step's); from
+    # it on the step's deep attention form splits differently.
+    EXACT_BATCH_LIMIT = 2048
+
+    def prefill(self, tokens) -> None:
+        """The prompt tokens at positions 0, 1, ...: the K/V rows, the device
+        token (the greedy token after the last one), the logits of the last
+        token and the position that forward_token on each in turn leaves,
+        bit for bit; below EXACT_BATCH_LIMIT positions as verify passes of up
+        to MAX_VERIFY_TOKENS tokens (one pass instead of one step per token),
+        the rest as single steps."""
+        toks = [int(t) for t in tokens]
+        pos = 0
+        while pos < len(toks):
+            n = min(self.MAX_VERIFY_TOKENS, len(toks) - pos, self.EXACT_BATCH_LIMIT - pos)
+            if n >= 2:
+                logits = self.forward_batch_all_logits(toks[pos:pos + n], pos)
+                self.logits.copy_(logits[n - 1])
+                self.token.copy_(self._verify["next"][n - 1:n])
+                pos += n
+            else:
+                self.forward_token(toks[pos], pos)
+                pos += 1
+
     def decode_steps(self, k: int) -> list[int]:
         """k greedy steps (step(), captured graphs) queued back to back from
         the device token at the device position, each step's token copied to

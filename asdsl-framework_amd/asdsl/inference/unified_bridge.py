@@ -230,8 +230,7 @@ def cpp_generate(store: Any, prompt_ids: list[int], max_new_tokens: int,
     eng.reset_session()
     stop = set() if _env_yes("ASDSL_IGNORE_EOS", "") else {int(t) for t in (stop_ids or PHI4_EOS)}
     prompt = [int(t) for t in prompt_ids]
-    for i, t in enumerate(prompt):
-        eng.forward_token(t, i)
+    eng.prefill(prompt)  # as forward_token on each prompt token, in verify passes
     out: list[int] = []
     if not prompt:
         return out
@@ -286,8 +285,7 @@ def greedy_generate(store: Any, prompt_ids: list[int], max_new_tokens: int, eos=
     eos = set(eos)
     tokens = [int(t) for t in prompt_ids]
     prompt_len = len(tokens)
-    for i, t in enumerate(tokens):
-        engine.forward_token(t, i)
+    engine.prefill(tokens)  # as forward_token on each prompt token, in verify passes
     if not tokens:
         return tokens
     # Steps run in chunks on the device (decode_steps: one read per chunk);
@@ -362,8 +360,7 @@ def pld_generate(store: Any, prompt_ids: list[int], max_new_tokens: int, max_dra
     prompt_len = len(tokens)
     max_seq = int(engine.cfg.max_seq)
     counts = {"verify_passes": 0, "drafted": 0, "accepted": 0, "withdrawn": 0}
-    for i, t in enumerate(tokens):
-        engine.forward_token(t, i)
+    engine.prefill(tokens)  # as forward_token on each prompt token, in verify passes
     pos = len(tokens)
     cur = engine.next_token()
 

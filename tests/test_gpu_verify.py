@@ -439,3 +439,34 @@ def test_reference_calls_replay_graphs_with_the_eager_bits(gpu, monkeypatch):
         assert torch.equal(ka, kb) and torch.equal(va, vb)
     mf, ex = og[-2][0], og[-1][0]  # the MFMA form: the same columns to fp32 rounding
     assert rel_l2(_host(mf), _host(ex)) < LOOSE
+
+
+@pytest.mark.parametrize("kv", ["fp16", "int8"])
+def test_prefill_is_forward_token_on_each_token(gpu, kv):
+    """DecodeEngine.prefill runs a prompt as verify passes of up to 16
+    tokens: K/V rows, logits of the last token, device token, position and
+    KV length as forward_token on each prompt token in turn leaves them, bit
+    for bit, for prompts of 1 to 40 tokens (single step, a 2-token pass, 16,
+    16 + 1 single step, 16 + 16 + 8)."""
+    import torch
+    from asdsl.engine import DecodeConfig, DecodeEngine
+
+    eng = DecodeEngine.synthetic(DecodeConfig(n_layers=2, vocab=4096, max_seq=256, kv_format=kv), seed=21)
+    rng = np.random.default_rng(22)
+    for plen in (1, 2, 16, 17, 40):
+        prompt = [int(t) for t in rng.integers(0, eng.cfg.vocab, plen)]
+        states = []
+        for batched in (True, False):
+            eng.reset_session()
+            if batched:
+                eng.prefill(prompt)
+            else:
+                for i, t in enumerate(prompt):
+                    eng.forward_token(t, i)
+            states.append((eng.logits.clone(), eng.next_token(), int(eng.pos.item()), eng._host_pos,
+                           eng.get_kv_seq_len(),
+                           [(L["k_cache"].clone(), L["v_cache"].clone()) for L in eng.layers]))
+        (la, ta, pa, ha, ka, kva), (lb, tb, pb, hb, kb, kvb) = states
+        assert torch.equal(la, lb) and (ta, pa, ha, ka) == (tb, pb, hb, kb) == (ta, plen, plen, plen), plen
+        for (k1, v1), (k2, v2) in zip(kva, kvb):
+            assert torch.equal(k1, k2) and torch.equal(v1, v2), plen
