@@ -180,8 +180,10 @@ asdsl_status preq2_embed_rmsnorm(const uint8_t* meta, const uint8_t* quant, cons
                                  asdsl_stream_t stream);
 
 #ifdef ASDSL_WG_TIMELINE
-// Timing build: the preq2 GEMVs' timeline buffer (see device_common.hpp).
+// Timing build: the preq2 GEMVs' and the sparse down-projection's timeline
+// buffers (see device_common.hpp).
 asdsl_status timeline_set_preq2(void* buf);
+asdsl_status timeline_set_sparse(void* buf);
 #endif
 
 // Workgroups for a streaming kernel: enough tiles for every wave, capped at

@@ -1617,6 +1617,7 @@ extern "C" asdsl_status asdsl_timeline_set_buffer(void* buf) {
         asdsl::set_error("timeline: %s", hipGetErrorString(e));
         return ASDSL_ERR_HIP;
     }
-    return asdsl::timeline_set_preq2(buf);
+    const asdsl_status st = asdsl::timeline_set_preq2(buf);
+    return st != ASDSL_OK ? st : asdsl::timeline_set_sparse(buf);
 }
 #endif

@@ -368,7 +368,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
 // asdsl_timeline_set_buffer.  Slots: 0 o_proj with the split merge, 1 gate_up
 // with SwiGLU, 2 norm-fed GEMV (qkv), 3 plain 16-wave GEMV (down), 4 the
 // step's attention, 6 attention combine, 7 plain 8-wave GEMV (o_proj beyond
-// 512 positions); 5 is unused.
+// 512 positions), 5 the sparse down-projection's partial kernel.
 constexpr int kTimelineSlots = 8;
 constexpr int kTimelineWgs = 1024;
 #ifdef ASDSL_WG_TIMELINE

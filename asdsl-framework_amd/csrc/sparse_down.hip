@@ -32,6 +32,9 @@
 #include "device_common.hpp"
 
 namespace asdsl {
+
+ASDSL_TIMELINE_BUFFER
+
 namespace {
 
 constexpr int kWaves = 4;
@@ -57,6 +60,7 @@ __global__ __launch_bounds__(kWaves * kWave) void sparse_down_kernel(
     const int per_xcd = static_cast<int>(gridDim.x) / kXcds;
     const int t = (bid % kXcds) * per_xcd + bid / kXcds;
     if (t >= nslices * nparts) return;  // padding workgroup: the whole workgroup leaves
+    ASDSL_TIMELINE_STAMP(5, t, 0);
     const int slice = t % nslices;
     const int p = t / nslices;
 
@@ -112,6 +116,7 @@ __global__ __launch_bounds__(kWaves * kWave) void sparse_down_kernel(
                 }
             }
         }
+        ASDSL_TIMELINE_STAMP(5, t, 1);  // the row indices arrived, the rows requested
 #pragma unroll
         for (int d = 0; d < kDepth; ++d) {
             if (ok[d] && xv[d] != 0.0f) {
@@ -128,6 +133,7 @@ __global__ __launch_bounds__(kWaves * kWave) void sparse_down_kernel(
         }
     }
 
+    ASDSL_TIMELINE_STAMP(5, t, 2);  // the rows arrived and were accumulated
     // fold the 8 rows of a wave load: lanes that agree in bits 0-2 (the unit j)
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
@@ -137,6 +143,7 @@ __global__ __launch_bounds__(kWaves * kWave) void sparse_down_kernel(
         v += __shfl_xor(v, 32, kWave);  // bit 5
         acc[e] = v;
     }
+    ASDSL_TIMELINE_STAMP(5, t, 3);
     if (sub == 0) {
         float* dst = &red[wave][j * 32];
 #pragma unroll
@@ -153,6 +160,7 @@ __global__ __launch_bounds__(kWaves * kWave) void sparse_down_kernel(
             out[static_cast<size_t>(p) * out_dim + og] = sum;
         }
     }
+    ASDSL_TIMELINE_STAMP(5, t, 4);
 }
 
 // y[o] = part[0][o] + part[1][o] + ... + part[P-1][o], in that order.  All P
@@ -172,6 +180,17 @@ __global__ __launch_bounds__(64) void sparse_down_sum_parts(const float* __restr
 }
 
 }  // namespace
+
+#ifdef ASDSL_WG_TIMELINE
+asdsl_status timeline_set_sparse(void* buf) {
+    const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), &buf, sizeof(buf));
+    if (e != hipSuccess) {
+        set_error("timeline: %s", hipGetErrorString(e));
+        return ASDSL_ERR_HIP;
+    }
+    return ASDSL_OK;
+}
+#endif
 }  // namespace asdsl
 
 using namespace asdsl;

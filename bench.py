@@ -1387,6 +1387,63 @@ def decode_timeline(ctx: int, n_layers: int = 32, steps: int = 8, seed: int = 11
             "kernels": kernels}
 
 
+def sparse_timeline(launches: int = 16) -> dict:
+    """Per-workgroup timeline of the FATReLU sparse down-projection's partial
+    kernel (down 8192 -> 3072, group 32, 80 % zeros) in the last of
+    `launches` graph-replayed calls over 8 rotated weight sets.  Needs the
+    timing build.  Stamps per workgroup (thread 0): start, row indices
+    arrived (rows requested), rows arrived and accumulated, fold done, end;
+    percentiles over workgroups of each stamp's time from the first start
+    (the parts' sum is a launch of its own, not stamped)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from asdsl import _hip
+
+    try:
+        setter = _hip.LIB.asdsl_timeline_set_buffer
+    except AttributeError:
+        raise SystemExit("--sparse-timeline needs the timing build: "
+                         "ASDSL_HIP_LIB=asdsl-framework_amd/lib/libasdsl_hip_timeline.so") from None
+    setter.argtypes = [ctypes.c_void_p]
+    setter.restype = ctypes.c_int
+    lib = _hip.LIB
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    IN, OUT = 8192, 3072
+    xs_ = torch.clamp(torch.randn(IN, generator=gen, device="cuda") - 0.841621, min=0.0)
+    rows = torch.nonzero(xs_).to(torch.int32).view(-1).contiguous()
+    na = int(rows.numel())
+    copies = [{"w": _dev_bytes(IN * OUT // 2, gen), "s": _dev_f32(IN * OUT // 32, gen, 0.01, 1e-3),
+               "b": _dev_f32(IN * OUT // 32, gen, -0.08, 0.0)} for _ in range(8)]
+    y = torch.empty(OUT, device="cuda")
+    work = torch.empty(lib.asdsl_sparse_down_work_bytes(OUT), dtype=torch.uint8, device="cuda")
+    P = _hip.ptr
+
+    def calls(h):
+        for i in range(launches):
+            c = copies[i % len(copies)]
+            _hip.check(lib.asdsl_sparse_down_proj_T_ws(P(c["w"]), P(c["s"]), P(c["b"]), P(xs_), P(rows), na, P(y),
+                                                       IN, OUT, 32, P(work), work.numel(), h),
+                       "asdsl_sparse_down_proj_T_ws")
+    g = capture(calls)
+    buf = torch.zeros(8 * 1024 * 8, dtype=torch.int64, device="cuda")
+    _hip.check(setter(ctypes.c_void_p(buf.data_ptr())), "asdsl_timeline_set_buffer")
+    g.replay()
+    torch.cuda.synchronize()
+    _hip.check(setter(None), "asdsl_timeline_set_buffer")
+    del g
+    a = buf.cpu().numpy().reshape(8, 1024, 8)[5].astype(np.float64)
+    a = a[(a[:, 0] > 0) & (a[:, 4] > 0)]
+    base = a[:, 0].min()
+    names = ("start", "indices arrived", "rows accumulated", "folded", "end")
+    pct = {n: [round(float(np.percentile((a[:, k] - base) * 0.01, q)), 2) for q in (0, 10, 50, 90, 100)]
+           for k, n in enumerate(names)}
+    return {"sparse_timeline": {"shape": [IN, OUT], "active_rows": na, "launches": launches,
+                                "workgroups": int(len(a)), "stamps_us_p0_p10_p50_p90_p100": pct}}
+
+
 def gemv_timeline(name: str, launches: int = 16) -> dict:
     """Per-workgroup timeline of one layer GEMV (preq2 g32, one of the
     headline's four shapes) in the last of `launches` graph-replayed launches
@@ -1462,6 +1519,8 @@ def main() -> int:
     ap.add_argument("--timeline-layers", type=int, default=32, help="--decode-timeline: layers of the model")
     ap.add_argument("--gemv-timeline", nargs="+", default=None, choices=[n for n, _, _ in LAYER],
                     help="per-workgroup timeline of these layer GEMVs (the timing build, as --decode-timeline)")
+    ap.add_argument("--sparse-timeline", action="store_true",
+                    help="per-workgroup timeline of the sparse down-projection (timing build)")
     ap.add_argument("--ceiling", action="store_true",
                     help="only the single-launch read ceiling sweep (asdsl_stream_read_ex) against byte count")
     ap.add_argument("--ceiling-out", default="", help="--ceiling: also write every configuration to this JSON file")
@@ -1497,6 +1556,9 @@ def main() -> int:
         rows = ceiling_sweep(_hip.LIB, oneshot_only=args.ceiling_oneshot)
         if args.ceiling_out:
             Path(args.ceiling_out).write_text(json.dumps(rows, indent=1))
+        return 0
+    if args.sparse_timeline:
+        print(json.dumps(sparse_timeline()), flush=True)
         return 0
     if args.gemv_timeline:
         for name in args.gemv_timeline:
