@@ -569,6 +569,22 @@ asdsl_status launch_batch_waves(const BatchPlan& p, const uint32_t* m, const uin
 // plan_batch's column count and grid on the single-column GEMV's launch
 // shape (preq2_plan_shape): K split, units per lane and waves (8, 12 or 16).
 // ------------------------------------------------------- exact MFMA form
+// Copies n <= PER * THREADS 16-byte units from global memory to LDS, thread
+// tid taking units tid, tid + THREADS, ...  All of a thread's loads are
+// requested before its first LDS write, so the copy costs one memory round
+// trip; a strided copy loop waits for each load before requesting the next.
+// Indexes past n are clamped to unit n - 1 (a repeated load and an identical
+// write), which keeps the copy free of branches and of a loop, whose back
+// edge would make the compiler wait for every earlier load at its head.
+template <int THREADS, int PER>
+__device__ __forceinline__ void copy_to_lds(uint4* __restrict__ dst, const uint4* __restrict__ src, int n, int tid) {
+    uint4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = src[min(i * THREADS + tid, n - 1)];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) dst[min(i * THREADS + tid, n - 1)] = v[i];
+}
+
 // The batched GEMV with the single-column GEMV's fp32 order (plan_preq2's
 // shape: K split KS = 1 << lks, NU units per lane), on an activation image
 // that carries the per-slice sums (image_store8 with `us`).  In the
@@ -674,10 +690,16 @@ __global__ __launch_bounds__(4 * KS * kWave) void preq2_batch_exact_mfma_kernel(
     constexpr int kStepBytes = 4 * kBandStride;
     uint8_t* stage = stage_all + static_cast<size_t>(wave) * NU * kStepBytes;
     uint32_t mt0[NU][kStepGroups], mt1[PF ? NU : 1][kStepGroups];
-    load_tile(wq0, mt0, tile);  // the grid never exceeds the tile count
-    for (int e = tid; e < G * kMfmaCols; e += 4 * KS * kWave) sfac[e] = fac[e];
+    // the scale tables first, all of a thread's loads in flight together:
+    // the LDS writes then wait for these alone, not for the weights
+    // (K <= 8192: at most 8192 / GS * 8 pair units and 1024 sum units)
+    constexpr int kThreads = 4 * KS * kWave;
+    copy_to_lds<kThreads, (8192 / GS * 8 + kThreads - 1) / kThreads>(
+        reinterpret_cast<uint4*>(sfac), reinterpret_cast<const uint4*>(fac), G * kMfmaCols / 2, tid);
     if constexpr (GS == 128)
-        for (int e = tid; e < (K / 32) * kMfmaCols; e += 4 * KS * kWave) sus[e] = us[e];
+        copy_to_lds<kThreads, (1024 + kThreads - 1) / kThreads>(
+            reinterpret_cast<uint4*>(sus), reinterpret_cast<const uint4*>(us), (K / 32) * kMfmaCols / 4, tid);
+    load_tile(wq0, mt0, tile);  // the grid never exceeds the tile count
     __syncthreads();
 
     const v4i32 zero = {0, 0, 0, 0};
