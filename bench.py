@@ -1512,6 +1512,9 @@ def main() -> int:
     ap.add_argument("--decode", action="store_true", help="only the decode tokens/s measurement (one JSON line)")
     ap.add_argument("--decode-steps", type=int, default=64, help="captured steps per context in the decode phase")
     ap.add_argument("--no-verify", action="store_true", help="decode phase: skip the verify pass, PLD rows")
+    ap.add_argument("--verify-pass", type=int, nargs="+", default=None, metavar="N",
+                    help="only the verify pass of N tokens at ctx 1024 on the 32-layer model, graph-replayed "
+                         "(one JSON line; the workload of the verify profiles)")
     ap.add_argument("--no-int8-kv", action="store_true", help="decode phase: skip the int8 KV cache rows")
     ap.add_argument("--decode-timeline", type=int, nargs="+", default=None, metavar="CTX",
                     help="per-workgroup timeline of one decode layer at these contexts (needs the timing "
@@ -1570,6 +1573,13 @@ def main() -> int:
         return 0
     if args.pmc_probe and args.pmc_probe != "gate_up":
         return pmc_probe(args.pmc_probe)
+    if args.verify_pass:
+        from asdsl.engine import DecodeConfig, DecodeEngine
+
+        eng = DecodeEngine.synthetic(DecodeConfig(n_layers=32, max_seq=1100), seed=11)
+        rows = _verify_pass_rows(eng, 1024, None, tuple(args.verify_pass), 20)
+        print(json.dumps({"verify_pass": {"ctx": 1024, "reps": 20, **rows}}), flush=True)
+        return 0
     if args.decode:
         import torch  # noqa: F401
 
