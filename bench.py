@@ -1444,6 +1444,45 @@ def sparse_timeline(launches: int = 16) -> dict:
                                 "workgroups": int(len(a)), "stamps_us_p0_p10_p50_p90_p100": pct}}
 
 
+def residency_sweep(launches: int = 64, reps: int = 10) -> dict:
+    """Each layer GEMV (preq2 g32) against where its weights live: graphs of
+    `launches` launches rotating over R weight sets, with R sets x bytes above
+    the 256 MB last-level cache (HBM), about 100 MB (cache-resident, L2-cold),
+    2 sets and 1 set (L2/cache-hot).  Per-launch average over `reps` replays."""
+    import torch
+
+    from asdsl import _hip
+
+    layers, xs, ys = build_layers(32, seed=42)
+    lib = _hip.LIB
+    rows = []
+    for name, M, K in LAYER:
+        nbytes = gemv_bytes(M, K)
+        for R in (32, max(1, int(100e6 // nbytes)), 2, 1):
+            ptrs = [(_hip.ptr(layers[i][name][0]), _hip.ptr(layers[i][name][1])) for i in range(R)]
+
+            def calls(h, ptrs=ptrs, R=R, name=name, M=M, K=K):
+                for i in range(launches):
+                    p = ptrs[i % R]
+                    if lib.asdsl_gemv_preq2_fused(p[0], p[1], _hip.ptr(xs[name]), _hip.ptr(ys[name]), M, K, GS, h):
+                        raise RuntimeError(_hip.last_error())
+            g = capture(calls)
+            for _ in range(3):
+                g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = 1e3 * e0.elapsed_time(e1) / (reps * launches)
+            rows.append({"gemv": name, "sets": R, "set_bytes": nbytes, "rotated_bytes": R * nbytes,
+                         "us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1)})
+            del g
+    return {"residency": rows}
+
+
 def gemv_timeline(name: str, launches: int = 16) -> dict:
     """Per-workgroup timeline of one layer GEMV (preq2 g32, one of the
     headline's four shapes) in the last of `launches` graph-replayed launches
@@ -1528,6 +1567,8 @@ def main() -> int:
                     help="only the single-launch read ceiling sweep (asdsl_stream_read_ex) against byte count")
     ap.add_argument("--ceiling-out", default="", help="--ceiling: also write every configuration to this JSON file")
     ap.add_argument("--ceiling-oneshot", action="store_true", help="--ceiling: only the one-shot (slab 2) reads")
+    ap.add_argument("--residency", action="store_true",
+                    help="only the layer GEMVs with their weights in HBM, cache-resident or cache-hot")
     ap.add_argument("--shape-sweep", action="store_true",
                     help="only the layer GEMVs under each launch shape the tuning switches select "
                          "(ASDSL_HIP_KSPLIT x ASDSL_HIP_PRE_SPLIT), one JSON line per GEMV")
@@ -1573,6 +1614,9 @@ def main() -> int:
         return 0
     if args.pmc_probe and args.pmc_probe != "gate_up":
         return pmc_probe(args.pmc_probe)
+    if args.residency:
+        print(json.dumps(residency_sweep()), flush=True)
+        return 0
     if args.verify_pass:
         from asdsl.engine import DecodeConfig, DecodeEngine
 
