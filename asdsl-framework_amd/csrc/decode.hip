@@ -299,6 +299,16 @@ __device__ __forceinline__ void kv_quantize_new(float (*kv_new)[kHeadDim], const
 // partials and output follow column c - 1's); the decode step runs one column.
 constexpr int kCombineGroups = 8;
 constexpr int kCombineThreads = kCombineGroups * kHeadDim;
+constexpr int kCombineChunk = 16;  // splits whose loads a group issues together
+
+// Threads of a combine launch whose positions have at most max_ns splits:
+// one group of 128 per kCombineChunk splits, so that no wave of the
+// workgroup idles (the kernel's grouping, and with it its fp32 order,
+// depends on the position's split count alone).
+inline int combine_threads(int max_ns) {
+    const int groups = (max_ns + kCombineChunk - 1) / kCombineChunk;
+    return kHeadDim * (groups < 1 ? 1 : groups > kCombineGroups ? kCombineGroups : groups);
+}
 
 // IMG_GS (32 or 128): the head's 128 outputs of column c are also quantized
 // into the o_proj batched GEMV's int8 image (image_store8, 16 chunks per
@@ -313,7 +323,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
                                                                       uint2* __restrict__ img,
                                                                       float2* __restrict__ fac,
                                                                       float* __restrict__ us) {
-    constexpr int kChunk = 16;
+    constexpr int kChunk = kCombineChunk;
     constexpr int kHeadChunks = kHeadDim / 8;
     __shared__ float gml[kCombineGroups][2];
     __shared__ float go[kCombineGroups][kHeadDim];
@@ -348,7 +358,9 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
     if (ns <= fold) return;  // the consuming GEMV's prologue merges these splits itself
     const int tl_slot = col == 0 ? 6 : -1;
     ASDSL_TIMELINE_STAMP(tl_slot, h, 0);
-    const int ng = min(kCombineGroups, (ns + kChunk - 1) / kChunk);  // groups with splits
+    // groups with splits (the launch gives every one of them its 128 threads:
+    // combine_threads of the most splits its positions can have)
+    const int ng = min(kCombineGroups, (ns + kChunk - 1) / kChunk);
     const int per = (ns + ng - 1) / ng;
     const int s_begin = min(ns, g * per);
     const int s_end = min(ns, s_begin + per);
@@ -742,7 +754,7 @@ asdsl_status launch_attention_decode(const float* qkv, const KvCache& kv, bool q
                                  : with_attn_kernel<DecodeAttnK>(n_heads / n_kv, q8, go);
     if (st != ASDSL_OK || fold) return st;
     const StageScope stage("attention_combine");
-    return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(kCombineThreads), 0, s,
+    return launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(n_heads), dim3(combine_threads(grid.x)), 0, s,
                   static_cast<const float*>(work), pos, att, kMaxSplits, max_seq, limit, 0, 1, f.tile, f.max_splits,
                   static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr), static_cast<float*>(nullptr));
 }
@@ -1529,12 +1541,12 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
         const int o_form = image_form(L.o_meta, L.o_quant, m.hidden, q_dim, m.gs_attn);
         if (o_form != 0) {
             st = launch("attn_combine_kernel", m.gs_attn == 32 ? attn_combine_kernel<32> : attn_combine_kernel<128>,
-                        dim3(m.n_heads, kImageCols), dim3(kCombineThreads), 0, s, static_cast<const float*>(part), pos,
+                        dim3(m.n_heads, kImageCols), dim3(combine_threads(nsplit)), 0, s, static_cast<const float*>(part), pos,
                         att, nsplit, m.max_seq, m.max_seq, 0, n, 0, 0, img, fac_of(q_dim), us_of(q_dim));
             if (st != ASDSL_OK) return st;
             st = image_gemv(o_form, L.o_meta, L.o_quant, O, m.hidden, q_dim, m.gs_attn);
         } else {
-            st = launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(m.n_heads, n), dim3(kCombineThreads), 0, s,
+            st = launch("attn_combine_kernel", attn_combine_kernel<0>, dim3(m.n_heads, n), dim3(combine_threads(nsplit)), 0, s,
                         static_cast<const float*>(part), pos, att, nsplit, m.max_seq, m.max_seq, 0, n, 0, 0,
                         static_cast<uint2*>(nullptr), static_cast<float2*>(nullptr), static_cast<float*>(nullptr));
             if (st != ASDSL_OK) return st;
