@@ -1114,15 +1114,31 @@ __global__ __launch_bounds__(256) void verify_swiglu_kernel(const float* __restr
 
 // keys[c] = max over rows of argmax_key(logits[c][row], row): the largest
 // logit, the first row among equals (argmax_f32_avx2, unified_engine.cpp:207-233).
+// A thread takes kArgmaxRows rows 256 apart per step, all loaded before any
+// is compared.  kArgmaxWgs workgroups per column: each ends in one atomicMax
+// on the column's key, and those serialize (196 per key measured 30 us
+// against 12 for 64).
+constexpr int kArgmaxRows = 8;
+constexpr int kArgmaxWgs = 64;
 __global__ __launch_bounds__(256) void verify_argmax_kernel(const float* __restrict__ logits, int vocab,
                                                             unsigned long long* __restrict__ keys) {
     __shared__ unsigned long long red[256 / kWave];
     const size_t c = blockIdx.y;
     unsigned long long best = 0ull;
-    for (int r = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); r < vocab;
-         r += static_cast<int>(gridDim.x * blockDim.x)) {
-        const unsigned long long k = argmax_key(logits[c * vocab + r], r);
-        best = k > best ? k : best;
+    for (int r0 = static_cast<int>(blockIdx.x * blockDim.x * kArgmaxRows + threadIdx.x); r0 < vocab;
+         r0 += static_cast<int>(gridDim.x * blockDim.x * kArgmaxRows)) {
+        float v[kArgmaxRows];
+#pragma unroll
+        for (int j = 0; j < kArgmaxRows; ++j) {
+            const int r = r0 + j * static_cast<int>(blockDim.x);
+            v[j] = logits[c * vocab + (r < vocab ? r : r0)];  // past the vocabulary: row r0 again
+        }
+#pragma unroll
+        for (int j = 0; j < kArgmaxRows; ++j) {
+            const int r = r0 + j * static_cast<int>(blockDim.x);
+            const unsigned long long k = r < vocab ? argmax_key(v[j], r) : 0ull;
+            best = k > best ? k : best;
+        }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -1579,7 +1595,7 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     }
     st = norm_then_gemv(pending, m.rms_out, m.lm_meta, m.lm_quant, logits, m.vocab, m.gs_lm);
     if (st != ASDSL_OK) return st;
-    st = launch("verify_argmax_kernel", verify_argmax_kernel, dim3(64, n), dim3(256), 0, s,
+    st = launch("verify_argmax_kernel", verify_argmax_kernel, dim3(kArgmaxWgs, n), dim3(256), 0, s,
                 static_cast<const float*>(logits), m.vocab, keys);
     if (st != ASDSL_OK) return st;
     return launch("verify_tokens_kernel", verify_tokens_kernel, dim3(1), dim3(kWave), 0, s,
