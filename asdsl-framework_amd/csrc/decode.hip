@@ -185,14 +185,6 @@ __device__ __forceinline__ void merge_position_groups(const float (&m)[G], const
     }
 }
 
-// e^x for a position's softmax weight (x = score - running max <= 0): 2^(x
-// log2 e) on the hardware exp2, two instructions where expf's range
-// reduction and special cases take about ten.  Near x = 0, where the weights
-// that matter lie, it is within ~1 ulp of e^x; the relative error grows as
-// |x| 2^-24 for the far smaller weights below.  Every attention form and the
-// verify pass take their weights from it, so they still agree bit for bit.
-__device__ __forceinline__ float attn_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
-
 // Scores, split-local softmax and P.V of one split for the G query heads of a
 // KV head, then the merge of the four waves: lane (wave, pg, dc) holds the
 // K/V rows of positions p0 + 4*wave + pg + 16*it in kraw/vraw (dims
@@ -268,7 +260,7 @@ __device__ __forceinline__ void attn_split_core(const uint4 (&kraw)[kSplit / 16]
         row_of(vraw[it], 1, p, v8);
 #pragma unroll
         for (int hh = 0; hh < G; ++hh) {
-            const float w = p < p1 ? attn_exp(sr[it][hh] - m[hh]) : 0.0f;
+            const float w = p < p1 ? expf(sr[it][hh] - m[hh]) : 0.0f;
             l[hh] += w;
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[hh][e] = fmaf(w, v8[e], acc[hh][e]);
@@ -679,7 +671,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_decode_kernel(
             row_of(vraw[it], 1, p, v8);
 #pragma unroll
             for (int hh = 0; hh < G; ++hh) {
-                const float w = p < p1 ? attn_exp(sr[it][hh] - m[hh]) : 0.0f;
+                const float w = p < p1 ? expf(sr[it][hh] - m[hh]) : 0.0f;
                 l[hh] += w;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[hh][e] = fmaf(w, v8[e], acc[hh][e]);
