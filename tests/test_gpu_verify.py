@@ -72,11 +72,12 @@ def _oracle_model(eng):
             "rope_cos": _host(eng.rope_cos), "rope_sin": _host(eng.rope_sin)}
 
 
-@pytest.mark.parametrize("ctx,n", [(100, 1), (100, 4), (124, 9), (300, 16)])
+@pytest.mark.parametrize("ctx,n", [(100, 1), (100, 4), (124, 9), (300, 16), (2100, 8)])
 def test_verify_matches_serial_oracle(gpu, ctx, n):
     """n tokens at ctx .. ctx + n - 1 (124 + 9 crosses the 128-position
-    split boundary; 300 + 16 spans five 64-position splits)."""
-    eng = _engine(seed=ctx + n, n_layers=2 if n == 4 else 1)
+    split boundary; 300 + 16 spans five 64-position splits; at 2100 the
+    combine folds 33-34 splits in three groups of 128 threads)."""
+    eng = _engine(seed=ctx + n, n_layers=2 if n == 4 else 1, max_seq=512 if ctx + n <= 512 else 2240)
     eng.prefill_kv_random(ctx, seed=3)
     model = _oracle_model(eng)
     kc = [_host(L["k_cache"]) for L in eng.layers]
