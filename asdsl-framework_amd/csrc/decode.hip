@@ -1461,13 +1461,14 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     // reduced rows): below 2048 positions, where the attention splits
     // coincide too, every column then gives the single-token step's logits,
     // K/V rows and token bit for bit, as lossless speculative decoding needs.
-    // From 5 columns (ASDSL_HIP_VERIFY_EXACT_MFMA_MIN_N, read per call), where
+    // From 4 columns (ASDSL_HIP_VERIFY_EXACT_MFMA_MIN_N, read per call), where
     // the single-token shape allows (preq2_batch_exact_mfma_applies), the
     // projection is the exact MFMA form on an activation image that the
     // kernel before it writes (the norm, the combine, the SwiGLU): the weights
-    // stream once for up to 16 columns (32-layer pass at ctx 1024: 2.23 ms
-    // against 2.70 for the dot4 form at 8 columns, 2.52 against 4.81 at 16;
-    // at 4 columns dot4 measured 2.01 against 2.15).  Otherwise, with the
+    // stream once for up to 16 columns (32-layer pass at ctx 1024, against
+    // the dot4 form: 1.94 against 1.97 ms at 4 columns, 1.95 against 2.18 at
+    // 5, 2.06 against 2.70 at 8, 2.29 against 4.73 at 16; at 2 and 3 columns
+    // dot4 is faster, 1.53 against 1.89 and 1.79 against 1.90).  Otherwise, with the
     // factored norm or ASDSL_HIP_VERIFY_DOT4=1 (read per call), the dot4
     // batched GEMV in the single-token launch shape (preq2_batch_exact).
     // ASDSL_HIP_VERIFY_MFMA=1 (read per call) takes the MFMA batched GEMV in
@@ -1477,7 +1478,7 @@ extern "C" asdsl_status asdsl_decode_verify(const asdsl_decode_model* model, con
     const bool factored_norm = !mfma && preq2_norm_factored();
     const int exact_min_n = env_knob("ASDSL_HIP_VERIFY_EXACT_MFMA_MIN_N");
     const bool exact_mfma = !mfma && !factored_norm && env_knob("ASDSL_HIP_VERIFY_DOT4") == 0 &&
-                            n >= (exact_min_n > 0 ? exact_min_n : 5);
+                            n >= (exact_min_n > 0 ? exact_min_n : 4);
     // dot4 in the single-token launch shape, else (a shape whose split masks
     // units) the batched GEMV's own dot4 plan
     auto gemv_exact = [&](const uint8_t* meta, const uint8_t* quant, const float* Xin, const float* inv, float* Y,

@@ -351,10 +351,10 @@ def test_verify_is_the_single_token_step_bit_for_bit(gpu, kv, ctx, n, form, monk
     """The verify pass in both exact forms, on a 2-layer model (qkv/o g32
     with K split 1 and 2, gate_up, down and the lm_head g128):
       exact_mfma: MFMA GEMVs in the single-token GEMVs' fp32 order on images
-        the norm, combine and SwiGLU kernels write (the default from 5
+        the norm, combine and SwiGLU kernels write (the default from 4
         columns; here at every column count);
       dot4 (ASDSL_HIP_VERIFY_DOT4=1): dot4 GEMVs in the single-token launch
-        shapes (the default up to 4 columns; here at every column count).
+        shapes (the default up to 3 columns; here at every column count).
     Norms in the step's order, the attention's one-tile splits: every column
     equals the single-token step at its position bit for bit, across the
     short form (below 512: o_proj merges the splits) and the long form
