@@ -568,6 +568,9 @@ asdsl_status launch_batch_waves(const BatchPlan& p, const uint32_t* m, const uin
 
 // plan_batch's column count and grid on the single-column GEMV's launch
 // shape (preq2_plan_shape): K split, units per lane and waves (8, 12 or 16).
+// columns from which the batched GEMV takes the MFMA form (dot4 below)
+constexpr int kBatchMfmaMinN = 5;
+
 // ------------------------------------------------------- exact MFMA form
 // Copies n <= PER * THREADS 16-byte units from global memory to LDS, thread
 // tid taking units tid, tid + THREADS, ...  All of a thread's loads are
@@ -872,11 +875,12 @@ asdsl_status asdsl::preq2_fused_batch(const uint8_t* meta, const uint8_t* quant,
     const int M = out_features, K = in_features;
     const auto* m = reinterpret_cast<const uint32_t*>(meta);
     // At least ASDSL_HIP_BATCH_MFMA_MIN_N columns: 16 columns per pass.
-    // Default where the MFMA path was measured to overtake the dot4 kernel:
-    // N >= 4 (gate_up 16384x3072 g32: 13.0 vs 13.9 us; N = 3: 12.9 vs 12.1),
-    // N >= 3 once K >= 4096 (down 3072x8192, N = 3: 10.9 vs 12.2 us).
+    // Default where the MFMA path was measured to overtake the dot4 kernel
+    // (graph-replayed over rotated weights, pre-pass included): N >= 5
+    // (gate_up 16384x3072 g32: N = 4 12.6 vs 11.6 us, N = 5 12.2 vs 13.8;
+    // down 3072x8192: N = 4 10.6 vs 10.3, N = 5 10.6 vs 12.6).
     static const int mfma_knob = env_knob("ASDSL_HIP_BATCH_MFMA_MIN_N");
-    const int mfma_min = mfma_knob > 0 ? mfma_knob : (in_features >= 4096 ? 3 : 4);
+    const int mfma_min = mfma_knob > 0 ? mfma_knob : kBatchMfmaMinN;
     const MfmaPlan mp = plan_mfma(M, K, group_size, cus);
     if (allow_mfma && n_cols >= mfma_min && mp.ok && reinterpret_cast<uintptr_t>(meta) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(quant) % 4 == 0) {
@@ -1081,7 +1085,7 @@ bool asdsl::preq2_batch_image_applies(const uint8_t* meta, const uint8_t* quant,
     const int cus = cu_count_current();
     if (cus < 0) return false;
     static const int mfma_knob = env_knob("ASDSL_HIP_BATCH_MFMA_MIN_N");
-    const int mfma_min = mfma_knob > 0 ? mfma_knob : (in_features >= 4096 ? 3 : 4);
+    const int mfma_min = mfma_knob > 0 ? mfma_knob : kBatchMfmaMinN;
     return n_cols >= mfma_min && plan_mfma(out_features, in_features, group_size, cus).ok &&
            reinterpret_cast<uintptr_t>(meta) % 16 == 0 && reinterpret_cast<uintptr_t>(quant) % 4 == 0;
 }

@@ -176,11 +176,10 @@ def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
     """Batched verification GEMV: column n == gemv_preq2_fused(x_n) (each column
     quantized on its own), against the oracle per column.  Covers every
     kernel instance the speculative-verify shapes reach: the 8-wave dot4
-    kernel (K = 3072, N <= 3), the 16-wave dot4 kernel (K = 8192, N = 2),
+    kernel (K = 3072, N <= 4), the 16-wave dot4 kernel (K = 8192, N <= 4),
     8192 x 8192 at N = 2, whose 1024 tiles exceed the resident workgroups
-    so each workgroup loops over several, and the MFMA kernels (N >= 4,
-    N >= 3 once K >= 4096; at g128 four 32-element slices per group in one
-    int32 accumulator)."""
+    so each workgroup loops over several, and the MFMA kernels (N >= 5; at
+    g128 four 32-element slices per group in one int32 accumulator)."""
     if K % gs:
         pytest.skip("K not a multiple of the group size")
     import torch
@@ -204,9 +203,9 @@ def test_preq2_batch_each_column_is_the_single_gemv(gpu, gs, M, K, N):
 @pytest.mark.parametrize("M,K", [(16384, 3072), (3072, 8192), (1000, 5120)])
 def test_preq2_batch_columns_do_not_depend_on_the_column_count(gpu, M, K):
     """g128 batch: a column's result does not depend on how many columns
-    share the call: the shared columns of 4, 9 and 16-column calls (the MFMA
-    kernel, 16-column passes) are bit for bit equal, and a 3-column call
-    (the dot4 kernel at K = 3072, another fp32 summation order) agrees to
+    share the call: the shared columns of 5, 9 and 16-column calls (the MFMA
+    kernel, 16-column passes) are bit for bit equal, and 3 and 4-column
+    calls (the dot4 kernel, another fp32 summation order) agree with them to
     1e-5 relative."""
     import torch
     from asdsl.kernels import _native_gemv as ng
@@ -217,16 +216,17 @@ def test_preq2_batch_columns_do_not_depend_on_the_column_count(gpu, M, K):
     del w
     X = torch.from_numpy(syn.activation(K, 16, batch=16)).cuda()
     outs = {}
-    for n in (3, 4, 9, 16):
+    for n in (3, 4, 5, 9, 16):
         Y = torch.empty((n, M), dtype=torch.float32, device="cuda")
         ng.gemv_preq2_fused_avx2(meta, quant, X[:n].contiguous(), Y, M, K, 128)
         torch.cuda.synchronize()
         outs[n] = Y.cpu().numpy()
     for n in (9, 16):
-        assert np.array_equal(outs[n][:4], outs[4]), n
+        assert np.array_equal(outs[n][:5], outs[5]), n
     assert np.array_equal(outs[16][:9], outs[9])
-    for c in range(3):
-        assert rel_l2(outs[4][c], outs[3][c]) < 1e-5, c
+    for n in (3, 4):
+        for c in range(n):
+            assert rel_l2(outs[n][c], outs[5][c]) < 1e-5, (n, c)
 
 
 def test_forced_ksplit_still_covers_every_unit(gpu, monkeypatch):
