@@ -1084,8 +1084,12 @@ bool asdsl::preq2_batch_image_applies(const uint8_t* meta, const uint8_t* quant,
         return false;
     const int cus = cu_count_current();
     if (cus < 0) return false;
+    // The image comes from the kernel before (no quantize pre-pass), so the
+    // MFMA form pays from fewer columns than in the standalone batched GEMV:
+    // 4, or 3 once K >= 4096 (the verify pass's own-order form measured 1713
+    // against 1973 us per 4-token pass with the dot4 kernel instead).
     static const int mfma_knob = env_knob("ASDSL_HIP_BATCH_MFMA_MIN_N");
-    const int mfma_min = mfma_knob > 0 ? mfma_knob : kBatchMfmaMinN;
+    const int mfma_min = mfma_knob > 0 ? mfma_knob : (in_features >= 4096 ? 3 : 4);
     return n_cols >= mfma_min && plan_mfma(out_features, in_features, group_size, cus).ok &&
            reinterpret_cast<uintptr_t>(meta) % 16 == 0 && reinterpret_cast<uintptr_t>(quant) % 4 == 0;
 }
