@@ -11,6 +11,7 @@
 // the fp32 epilogue acc_n += D*(s*xs_n) - (z*s)*(X_n*xs_n).  Column chunks of
 // up to 16 (8 when K > 4096, LDS-bound) run as separate launches over the
 // same weights.  Deterministic: no atomics, fixed-order K-split combine.
+#include <cstdlib>
 #include <type_traits>
 
 #include "abi_util.hpp"
@@ -816,11 +817,197 @@ __global__ __launch_bounds__(4 * KS * kWave) void preq2_batch_exact_mfma_kernel(
     }
 }
 
-size_t exact_mfma_lds_bytes(int K, int gs, int ks, int nu) {
+// The exact MFMA form for at most 8 columns, two 16-row tiles per step.
+// With 8 columns half of each MFMA's 16 columns is padding, and the fp32
+// steps run over all 64 lanes anyway.  Here the activation operands carry
+// columns 0..7 twice (operand rows c and c + 8), one MFMA runs per tile of
+// the pair, and lanes q < 2 take tile A's dots (columns 4q + v) while lanes
+// q >= 2 take tile B's (columns 4(q - 2) + v): one pass of fp32 steps
+// serves both tiles.  Every (row, column) accumulator still sees the
+// single-column GEMV's steps in its order, so the results are those of the
+// one-tile kernel bit for bit.  Tile pair p is tiles 2p and 2p + 1 (rows
+// past M read the last row and are never stored); workgroups loop over pairs.
+template <int GS, int NU, int KS>
+__global__ __launch_bounds__(4 * KS * kWave) void preq2_batch_exact_mfma_pair_kernel(
+    const uint32_t* __restrict__ meta, const uint8_t* __restrict__ quant, const uint2* __restrict__ img,
+    const float2* __restrict__ fac, const float* __restrict__ us, float* __restrict__ Y, int M, int K, int ncols) {
+#pragma clang fp contract(off)
+    constexpr int UPS = GS / 32;
+    constexpr int kGroupBytes = GS * 2;
+    constexpr int kStepGroups = GS == 32 ? 4 : 1;
+    constexpr int kRangeGroups = GS == 32 ? 16 * NU : 4 * NU;
+    extern __shared__ __align__(16) uint32_t lds_words[];
+    const int G = K / GS;
+    float2* sfac = reinterpret_cast<float2*>(lds_words);                                  // [G][16]
+    float* sus = reinterpret_cast<float*>(sfac + static_cast<size_t>(G) * kMfmaCols);    // [K/32][16] (GS 128)
+    float* red = sus + (GS == 128 ? static_cast<size_t>(K / 32) * kMfmaCols : 0);        // [2][KS][4][4][kWave]
+    uint8_t* stage_all = reinterpret_cast<uint8_t*>(red + 2 * static_cast<size_t>(KS) * 16 * kWave);
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWave - 1);
+    const int wave = tid >> 6;
+    const int ks = wave >> 2;
+    const int w = wave & 3;
+    const int r16 = lane & 15;
+    const int q = lane >> 4;
+    const bool upper = q >= 2;  // this lane takes tile B of the pair
+    const int qc = q & 1;       // its columns: 4 qc .. 4 qc + 3
+    const int ntiles = (M + 15) >> 4;
+    const int npairs = (ntiles + 1) >> 1;
+    const int nbands = (M + 3) >> 2;
+
+    auto first_group = [&](int st) {
+        return GS == 32 ? ks * kRangeGroups + 16 * st + 4 * w : ks * kRangeGroups + 4 * st + w;
+    };
+    // a tile's weights, staged by the whole wave
+    auto load_weights = [&](uint4 (&wq)[NU], int tile) {
+        const int lband = min(tile * 4 + (lane >> 4), nbands - 1);
+#pragma unroll
+        for (int st = 0; st < NU; ++st)
+            wq[st] = load_stream16(
+                reinterpret_cast<const uint4*>(quant + (static_cast<size_t>(lband) * G + first_group(st)) * kGroupBytes) +
+                (lane & 15));
+    };
+    // the (s, z) pairs of row r16 of this lane's own tile of the pair
+    auto load_meta = [&](uint32_t (&mt)[NU][kStepGroups], int tile) {
+        const int row = min(tile * 16 + r16, M - 1);
+#pragma unroll
+        for (int st = 0; st < NU; ++st) {
+            const uint32_t* mp = meta + static_cast<size_t>(row) * G + first_group(st);
+            if constexpr (kStepGroups == 4) {
+                const uint4 m4 = *reinterpret_cast<const uint4*>(mp);
+                mt[st][0] = m4.x;
+                mt[st][1 % kStepGroups] = m4.y;
+                mt[st][2 % kStepGroups] = m4.z;
+                mt[st][3 % kStepGroups] = m4.w;
+            } else {
+                mt[st][0] = mp[0];
+            }
+        }
+    };
+
+    // activation operands: operand row r16 holds column r16 & 7
+    long av[NU][4];
+#pragma unroll
+    for (int st = 0; st < NU; ++st)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int slice = GS == 32 ? first_group(st) + k : first_group(st) * UPS + k;
+            const uint2 v = img[(static_cast<size_t>(slice) * kMfmaCols + (r16 & 7)) * 4 + q];
+            av[st][k] = static_cast<long>(static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32));
+        }
+    int pair = static_cast<int>(blockIdx.x);
+    const int step = static_cast<int>(gridDim.x);
+    uint4 wa[NU], wb[NU];
+    uint32_t mt[NU][kStepGroups];
+    constexpr int kBandStride = 256 + 16;
+    constexpr int kStepBytes = 4 * kBandStride;
+    uint8_t* stage_a = stage_all + static_cast<size_t>(wave) * 2 * NU * kStepBytes;
+    uint8_t* stage_b = stage_a + NU * kStepBytes;
+    constexpr int kThreads = 4 * KS * kWave;
+    copy_to_lds<kThreads, (8192 / GS * 8 + kThreads - 1) / kThreads>(
+        reinterpret_cast<uint4*>(sfac), reinterpret_cast<const uint4*>(fac), G * kMfmaCols / 2, tid);
+    if constexpr (GS == 128)
+        copy_to_lds<kThreads, (1024 + kThreads - 1) / kThreads>(
+            reinterpret_cast<uint4*>(sus), reinterpret_cast<const uint4*>(us), (K / 32) * kMfmaCols / 4, tid);
+    load_weights(wa, 2 * pair);  // the grid never exceeds the pair count
+    load_weights(wb, 2 * pair + 1);
+    load_meta(mt, 2 * pair + (upper ? 1 : 0));
+    __syncthreads();
+
+    const v4i32 zero = {0, 0, 0, 0};
+    int parity = 0;
+    while (true) {  // uniform per workgroup
+#pragma unroll
+        for (int st = 0; st < NU; ++st) {
+            const int off = st * kStepBytes + (lane >> 4) * kBandStride + (lane & 15) * 16;
+            *reinterpret_cast<uint4*>(stage_a + off) = wa[st];
+            *reinterpret_cast<uint4*>(stage_b + off) = wb[st];
+        }
+        float sf[NU][kStepGroups], zs[NU][kStepGroups];
+#pragma unroll
+        for (int st = 0; st < NU; ++st)
+#pragma unroll
+            for (int k = 0; k < kStepGroups; ++k) {
+                sf[st][k] = half_bits_to_float(mt[st][k]);
+                zs[st][k] = -(half_bits_to_float(mt[st][k] >> 16) * sf[st][k]);
+            }
+        float acc[4][4];  // [column 4 qc + v][accumulator j of this wave]
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[v][j] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < NU; ++st) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int unit = GS == 32 ? 4 * k + (r16 & 3) : 4 * (r16 & 3) + k;
+                const int rd = st * kStepBytes + (r16 >> 2) * kBandStride + unit * 16 + q * 4;
+                const uint32_t wsa = *reinterpret_cast<const uint32_t*>(stage_a + rd);
+                const uint32_t wsb = *reinterpret_cast<const uint32_t*>(stage_b + rd);
+                const uint64_t ba = static_cast<uint64_t>(wsa & 0x0F0F0F0Fu) |
+                                    (static_cast<uint64_t>((wsa >> 4) & 0x0F0F0F0Fu) << 32);
+                const uint64_t bb = static_cast<uint64_t>(wsb & 0x0F0F0F0Fu) |
+                                    (static_cast<uint64_t>((wsb >> 4) & 0x0F0F0F0Fu) << 32);
+                const v4i32 da = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[st][k], static_cast<long>(ba), zero, 0, 0, 0);
+                const v4i32 db = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[st][k], static_cast<long>(bb), zero, 0, 0, 0);
+                const int g = GS == 32 ? first_group(st) + k : first_group(st);
+                const int mk = GS == 32 ? k : 0;
+                const float4 f0 = reinterpret_cast<const float4*>(sfac + static_cast<size_t>(g) * kMfmaCols + 4 * qc)[0];
+                const float4 f1 = reinterpret_cast<const float4*>(sfac + static_cast<size_t>(g) * kMfmaCols + 4 * qc)[1];
+                const float xs[4] = {f0.x, f0.z, f1.x, f1.z};
+                float xu[4] = {f0.y, f0.w, f1.y, f1.w};
+                if constexpr (GS == 128) {
+                    const float4 u = reinterpret_cast<const float4*>(
+                        sus + static_cast<size_t>(g * UPS + k) * kMfmaCols + 4 * qc)[0];
+                    xu[0] = u.x; xu[1] = u.y; xu[2] = u.z; xu[3] = u.w;
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int d = upper ? db[v] : da[v];
+                    acc[v][k] = fmaf(static_cast<float>(d), sf[st][mk] * xs[v], acc[v][k]);
+                    acc[v][k] = fmaf(zs[st][mk], xu[v], acc[v][k]);
+                }
+            }
+        }
+        const int tile = 2 * pair + (upper ? 1 : 0);
+        pair += step;
+        const bool more = pair < npairs;  // uniform
+        float* rb = red + static_cast<size_t>(parity) * KS * 16 * kWave;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float r = GS == 32 ? (acc[v][0] + acc[v][3]) + (acc[v][2] + acc[v][1])
+                                     : (acc[v][0] + acc[v][1]) + (acc[v][2] + acc[v][3]);
+            rb[((ks * 4 + w) * 4 + v) * kWave + lane] = r;
+        }
+        __syncthreads();
+        if (wave < 4) {  // wave w stores column 4 qc + w of its lane's tile
+            const int v = w;
+            float sum = 0.0f;
+#pragma unroll
+            for (int k2 = 0; k2 < KS; ++k2) {
+                const float* rr = rb + static_cast<size_t>(k2) * 16 * kWave;
+                const float p = (rr[(0 * 4 + v) * kWave + lane] + rr[(1 * 4 + v) * kWave + lane]) +
+                                (rr[(2 * 4 + v) * kWave + lane] + rr[(3 * 4 + v) * kWave + lane]);
+                sum = k2 == 0 ? p : sum + p;
+            }
+            const int n = 4 * qc + v;
+            const int orow = tile * 16 + r16;
+            if (n < ncols && orow < M) Y[static_cast<size_t>(n) * M + orow] = sum;
+        }
+        if (!more) break;
+        load_weights(wa, 2 * pair);
+        load_weights(wb, 2 * pair + 1);
+        load_meta(mt, 2 * pair + (upper ? 1 : 0));
+        parity ^= 1;
+    }
+}
+
+size_t exact_mfma_lds_bytes(int K, int gs, int ks, int nu, bool pair = false) {
     return static_cast<size_t>(K / gs) * kMfmaCols * sizeof(float2) +
            (gs == 128 ? static_cast<size_t>(K / 32) * kMfmaCols * sizeof(float) : 0) +
            2 * static_cast<size_t>(ks) * 4 * 4 * kWave * sizeof(float) +
-           static_cast<size_t>(4 * ks) * nu * 4 * (256 + 16);  // per wave: nu steps of 4 padded bands
+           static_cast<size_t>(4 * ks) * nu * 4 * (256 + 16) * (pair ? 2 : 1);  // per wave: nu steps of 4 padded bands (per tile)
 }
 
 BatchPlan plan_batch_single(int M, int K, int gs, int cus) {
@@ -1006,6 +1193,31 @@ asdsl_status launch_exact_mfma_nu(int ks, bool pf, dim3 grid, size_t lds, hipStr
     }
 }
 
+template <int GS, int NU>
+asdsl_status launch_exact_mfma_pair(int ks, dim3 grid, size_t lds, hipStream_t s, const uint32_t* m,
+                                   const uint8_t* q, const uint2* img, const float2* fac, const float* us, float* Y,
+                                   int M, int K, int ncols) {
+    if (ks == 1)
+        return launch("preq2_batch_exact_mfma_pair_kernel", preq2_batch_exact_mfma_pair_kernel<GS, NU, 1>, grid,
+                      dim3(4 * kWave), lds, s, m, q, img, fac, us, Y, M, K, ncols);
+    return launch("preq2_batch_exact_mfma_pair_kernel", preq2_batch_exact_mfma_pair_kernel<GS, NU, 2>, grid,
+                  dim3(8 * kWave), lds, s, m, q, img, fac, us, Y, M, K, ncols);
+}
+
+template <int GS>
+asdsl_status launch_exact_mfma_pairs(int nu, int ks, dim3 grid, size_t lds, hipStream_t s, const uint32_t* m,
+                                     const uint8_t* q, const uint2* img, const float2* fac, const float* us,
+                                     float* Y, int M, int K, int ncols) {
+    switch (nu) {
+        case 1: return launch_exact_mfma_pair<GS, 1>(ks, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 2: return launch_exact_mfma_pair<GS, 2>(ks, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 3: return launch_exact_mfma_pair<GS, 3>(ks, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 4: return launch_exact_mfma_pair<GS, 4>(ks, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        case 5: return launch_exact_mfma_pair<GS, 5>(ks, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+        default: return launch_exact_mfma_pair<GS, 6>(ks, grid, lds, s, m, q, img, fac, us, Y, M, K, ncols);
+    }
+}
+
 template <int GS>
 asdsl_status launch_exact_mfma(int nu, int ks, bool pf, dim3 grid, size_t lds, hipStream_t s, const uint32_t* m,
                                const uint8_t* q, const uint2* img, const float2* fac, const float* us, float* Y, int M,
@@ -1058,6 +1270,24 @@ asdsl_status asdsl::preq2_batch_exact_mfma_image(const uint8_t* meta, const uint
     static const int knob = env_knob("ASDSL_HIP_EXACT_WG_PER_CU");
     const int per_cu = knob > 0 ? knob : 2;
     const int tiles = (M + 15) / 16;
+    const auto* base_m = reinterpret_cast<const uint32_t*>(meta);
+    // up to 8 columns: two tiles per step (ASDSL_HIP_EXACT_PAIR=0, read per
+    // call, turns it off).  Not at K split 4, whose 16 waves have no room for
+    // the second tile's registers, nor with fewer pairs than half the compute
+    // units (o_proj 3072x3072, 96 pairs: 6.7 against 5.7 us at 8 columns;
+    // qkv 5120x3072, 160 pairs: 8.0 against 9.0; gate_up 10.8 against 12.4;
+    // lm_head 72.6 against 84.3)
+    const char* pair_env = std::getenv("ASDSL_HIP_EXACT_PAIR");
+    const int pairs = (tiles + 1) / 2;
+    if (n_cols <= 8 && ks < 4 && 2 * pairs >= cus && !(pair_env && pair_env[0] == '0')) {
+        const dim3 pgrid(pairs < per_cu * cus ? pairs : per_cu * cus);
+        const size_t plds = exact_mfma_lds_bytes(K, group_size, ks, nu, true);
+        hipStream_t ps = as_hip(stream);
+        return group_size == 32
+                   ? launch_exact_mfma_pairs<32>(nu, ks, pgrid, plds, ps, base_m, quant, img, fac, us, Y, M, K, n_cols)
+                   : launch_exact_mfma_pairs<128>(nu, ks, pgrid, plds, ps, base_m, quant, img, fac, us, Y, M, K,
+                                                  n_cols);
+    }
     const int gridn = ks == 4 || tiles < per_cu * cus ? tiles : per_cu * cus;
     const bool pf = tiles > gridn;
     const dim3 grid(gridn);
